@@ -1,0 +1,416 @@
+/*
+ * CPU ORACLE for the Q4_K matvec path -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of the reference's Q4_K format code, quantizer,
+ * seeded RNG, f64 dequant-dot GEMV and CPU fused GEMV. It exists to check the
+ * HIP kernels and to time the reference CPU path; the product library never
+ * links it. Build flags (oracle/Makefile): -O2 -ffp-contract=off
+ * -fno-fast-math, so every f32 multiply and subtract rounds on its own, as
+ * the Rust reference does.
+ *
+ * Parity pins for each function live in tests/test_oracle_pins.py; see the
+ * per-function notes below for what pins it.
+ */
+#include "q4k_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+#if defined(__x86_64__)
+#include <immintrin.h>
+#endif
+
+/* ---------------------------------------------------------------- f16 ---- */
+
+static inline float bits_to_f32(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static inline uint32_t f32_to_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+
+/* gguf.rs:281-292. Subnormals are exact (mant/1024 * 2^-14, both exact);
+ * exponent 31 (Inf and NaN alike) decodes to NaN. */
+float orq_f16_to_f32(uint16_t h) {
+    uint32_t sign = (h >> 15) & 1u;
+    uint32_t exp = (h >> 10) & 0x1Fu;
+    uint32_t mant = h & 0x3FFu;
+    if (exp == 0) {
+        if (mant == 0) return sign ? -0.0f : 0.0f;
+        float m = (float)mant / 1024.0f * (1.0f / 16384.0f);
+        return sign ? -m : m;
+    }
+    if (exp == 31) return bits_to_f32(0x7FC00000u);
+    return bits_to_f32((sign << 31) | ((exp + 112u) << 23) | (mant << 13));
+}
+
+/* gguf.rs:297-328. NOTE: truncates the mantissa (mant >> 13) rather than
+ * rounding to nearest; subnormal results are truncated too. */
+uint16_t orq_f32_to_f16(float f) {
+    uint32_t bits = f32_to_bits(f);
+    uint16_t sign = (uint16_t)((bits >> 31) & 1u);
+    int32_t exp = (int32_t)((bits >> 23) & 0xFFu);
+    uint32_t mant = bits & 0x7FFFFFu;
+    if (exp == 0xFF) {
+        uint16_t m = (uint16_t)(mant >> 13);
+        uint16_t payload = mant != 0 ? (m > 1 ? m : 1) : 0;
+        return (uint16_t)((sign << 15) | (0x1Fu << 10) | payload);
+    }
+    int32_t unbiased = exp - 127 + 15;
+    if (unbiased >= 0x1F) return (uint16_t)((sign << 15) | (0x1Fu << 10));
+    if (unbiased <= 0) {
+        if (unbiased < -10) return (uint16_t)(sign << 15);
+        uint32_t with_lead = mant | 0x800000u;
+        uint32_t shift = (uint32_t)(14 - unbiased);
+        return (uint16_t)((sign << 15) | (uint16_t)(with_lead >> shift));
+    }
+    return (uint16_t)((sign << 15) | ((uint16_t)unbiased << 10) | (uint16_t)(mant >> 13));
+}
+
+/* ------------------------------------------------------ scales / mins ---- */
+
+/* gguf.rs:334-342 (6-bit scale/min of sub-block j from the 12-byte header). */
+void orq_get_scale_min_k4(int j, const uint8_t *s, uint8_t *sc, uint8_t *m) {
+    if (j < 4) {
+        *sc = s[j] & 63;
+        *m = s[j + 4] & 63;
+    } else {
+        *sc = (uint8_t)((s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4));
+        *m = (uint8_t)((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+    }
+}
+
+/* gguf.rs:349-358 (inverse of the above for values < 64). */
+void orq_pack_scales_mins(const uint8_t sc[8], const uint8_t m[8], uint8_t s[12]) {
+    for (int i = 0; i < 4; ++i) {
+        s[i] = (uint8_t)((sc[i] & 0x3F) | (((sc[i + 4] >> 4) & 0x3) << 6));
+        s[i + 4] = (uint8_t)((m[i] & 0x3F) | (((m[i + 4] >> 4) & 0x3) << 6));
+        s[i + 8] = (uint8_t)((sc[i + 4] & 0x0F) | ((m[i + 4] & 0x0F) << 4));
+    }
+}
+
+/* ------------------------------------------------------------ dequant ---- */
+
+static inline float finite_or_zero(float v) { return isfinite(v) ? v : 0.0f; }
+
+/* gguf.rs:364-404, canonical order: for each 32-byte group j of qs, 32
+ * low-nibble outputs (sub-block 2j/32) then 32 high-nibble outputs. Each
+ * weight is fl(fl(d*sc)*q) - fl(dmin*m): two roundings, never fused. */
+void orq_dequantize_row_q4_k(const uint8_t *data, float *out, size_t out_len,
+                             size_t n_blocks) {
+    for (size_t blk = 0; blk < n_blocks; ++blk) {
+        const uint8_t *b = data + blk * ORQ_BLOCK_BYTES;
+        float d = finite_or_zero(orq_f16_to_f32((uint16_t)(b[0] | (b[1] << 8))));
+        float dmin = finite_or_zero(orq_f16_to_f32((uint16_t)(b[2] | (b[3] << 8))));
+        const uint8_t *scales = b + 4;
+        const uint8_t *qs = b + 16;
+        size_t out_idx = blk * ORQ_BLOCK_ELEMS;
+        int is = 0;
+        for (int j = 0; j < 128; j += 32) {
+            uint8_t sc, m;
+            orq_get_scale_min_k4(is, scales, &sc, &m);
+            float d1 = d * (float)sc, m1 = dmin * (float)m;
+            for (int l = 0; l < 32; ++l, ++out_idx)
+                if (out_idx < out_len) out[out_idx] = d1 * (float)(qs[j + l] & 0xF) - m1;
+            ++is;
+            orq_get_scale_min_k4(is, scales, &sc, &m);
+            float d2 = d * (float)sc, m2 = dmin * (float)m;
+            for (int l = 0; l < 32; ++l, ++out_idx)
+                if (out_idx < out_len) out[out_idx] = d2 * (float)(qs[j + l] >> 4) - m2;
+            ++is;
+        }
+    }
+}
+
+/* ----------------------------------------------------------- quantize ---- */
+
+/* Rust `f32::round().clamp(0,hi) as u8`: round half away from zero, clamp,
+ * saturating cast (NaN -> 0). */
+static inline uint8_t round_clamp_u8(float v, float hi) {
+    float r = roundf(v);
+    if (isnan(r)) return 0;
+    if (r < 0.0f) r = 0.0f;
+    if (r > hi) r = hi;
+    return (uint8_t)r;
+}
+
+/* gguf.rs:509-529 (q4k_sub_block_local_scale_min). */
+static void local_scale_min(const float *x, float *local_d, float *local_dmin) {
+    float x_min = x[0], x_max = x[0];
+    for (int i = 1; i < 32; ++i) {
+        if (x[i] < x_min) x_min = x[i];
+        if (x[i] > x_max) x_max = x[i];
+    }
+    if (x_min > 0.0f) x_min = 0.0f;
+    *local_d = (x_max - x_min) / 15.0f;
+    *local_dmin = -x_min;
+}
+
+/* gguf.rs:534-566 (quantize_sub_block). */
+static void quantize_sub_block(const float *x, uint8_t *sc, uint8_t *m, uint8_t *q,
+                               float super_d, float super_dmin) {
+    float local_d, local_dmin;
+    local_scale_min(x, &local_d, &local_dmin);
+    float sc_f = super_d > 0.0f ? local_d / super_d : 0.0f;
+    float m_f = super_dmin > 0.0f ? local_dmin / super_dmin : 0.0f;
+    uint8_t sc_q = round_clamp_u8(sc_f, 63.0f), m_q = round_clamp_u8(m_f, 63.0f);
+    *sc = sc_q;
+    *m = m_q;
+    float d1 = super_d * (float)sc_q;
+    float m1 = super_dmin * (float)m_q;
+    for (int i = 0; i < 32; ++i)
+        q[i] = d1 > 0.0f ? round_clamp_u8((x[i] + m1) / d1, 15.0f) : 0;
+}
+
+/* gguf.rs:581-663. Sub-block `is` reads x[OFFS[is] .. +32] (the reference's
+ * all-low-then-all-high table at gguf.rs:590-601), so its bytes decode, in the
+ * canonical order above, to a 32-element-chunk permutation of x. */
+size_t orq_quantize_row_q4_k(const float *x, size_t n, uint8_t *out) {
+    static const int OFFS[8] = {0, 128, 32, 160, 64, 192, 96, 224};
+    if (n % ORQ_BLOCK_ELEMS != 0) return 0;
+    size_t n_blocks = n / ORQ_BLOCK_ELEMS;
+    for (size_t blk = 0; blk < n_blocks; ++blk) {
+        const float *bx = x + blk * ORQ_BLOCK_ELEMS;
+        float super_d = 0.0f, super_dmin = 0.0f;
+        for (int is = 0; is < 8; ++is) {
+            float ld, ldm;
+            local_scale_min(bx + OFFS[is], &ld, &ldm);
+            if (ld > super_d) super_d = ld;
+            if (ldm > super_dmin) super_dmin = ldm;
+        }
+        float sd = orq_f16_to_f32(orq_f32_to_f16(super_d / 63.0f));
+        float sdm = orq_f16_to_f32(orq_f32_to_f16(super_dmin / 63.0f));
+        uint8_t sc[8], m[8], nib[8][32];
+        for (int is = 0; is < 8; ++is)
+            quantize_sub_block(bx + OFFS[is], &sc[is], &m[is], nib[is], sd, sdm);
+        uint8_t *dst = out + blk * ORQ_BLOCK_BYTES;
+        uint16_t dh = orq_f32_to_f16(sd), dmh = orq_f32_to_f16(sdm);
+        dst[0] = (uint8_t)(dh & 0xFF); dst[1] = (uint8_t)(dh >> 8);
+        dst[2] = (uint8_t)(dmh & 0xFF); dst[3] = (uint8_t)(dmh >> 8);
+        orq_pack_scales_mins(sc, m, dst + 4);
+        for (int j = 0; j < 128; ++j) {
+            int lo = (j / 32) * 2;
+            dst[16 + j] = (uint8_t)((nib[lo][j % 32] & 0xF) | ((nib[lo + 1][j % 32] & 0xF) << 4));
+        }
+    }
+    return n_blocks * ORQ_BLOCK_BYTES;
+}
+
+/* ---------------------------------------------------------------- RNG ---- */
+
+/* neuron.rs:1345-1367. Box-Muller in f32 with the C library's logf/cosf/sqrtf
+ * (what Rust's f32::ln/cos/sqrt lower to on Linux). */
+void orq_rng_init(orq_rng *r, uint64_t seed) { r->s = seed + 1u; }
+uint64_t orq_rng_next_u64(orq_rng *r) {
+    r->s = r->s * 6364136223846793005ull + 1442695040888963407ull;
+    return r->s;
+}
+float orq_rng_next_f32(orq_rng *r) {
+    return (float)(orq_rng_next_u64(r) >> 40) / 16777216.0f;
+}
+float orq_rng_next_normal(orq_rng *r) {
+    float u1 = orq_rng_next_f32(r);
+    if (u1 < 1e-10f) u1 = 1e-10f;
+    float u2 = orq_rng_next_f32(r);
+    const float two_pi = 2.0f * 3.14159265358979323846f;
+    return sqrtf(-2.0f * logf(u1)) * cosf(two_pi * u2);
+}
+void orq_fill_normal(uint64_t seed, float scale, float *out, size_t n) {
+    orq_rng r;
+    orq_rng_init(&r, seed);
+    for (size_t i = 0; i < n; ++i) out[i] = orq_rng_next_normal(&r) * scale;
+}
+
+/* --------------------------------------------------------------- GEMV ---- */
+
+/* rocm_matvec_check.rs:38-47: dequantize the row, accumulate w*x in f64,
+ * round once to f32. absdot[r] = sum |w||x| (f64). */
+void orq_gemv_f64_abs(const uint8_t *w, const float *x, float *y, double *absdot,
+                      int out_dim, int bpr) {
+    size_t k = (size_t)bpr * ORQ_BLOCK_ELEMS;
+    float *wr = (float *)malloc(k * sizeof(float));
+    for (int r = 0; r < out_dim; ++r) {
+        orq_dequantize_row_q4_k(w + (size_t)r * bpr * ORQ_BLOCK_BYTES, wr, k, (size_t)bpr);
+        double acc = 0.0, aabs = 0.0;
+        for (size_t i = 0; i < k; ++i) {
+            acc += (double)wr[i] * (double)x[i];
+            aabs += fabs((double)wr[i]) * fabs((double)x[i]);
+        }
+        y[r] = (float)acc;
+        if (absdot) absdot[r] = aabs;
+    }
+    free(wr);
+}
+void orq_gemv_f64(const uint8_t *w, const float *x, float *y, int out_dim, int bpr) {
+    orq_gemv_f64_abs(w, x, y, NULL, out_dim, bpr);
+}
+
+void orq_gemv_flat_f64_abs(const uint8_t *w, const float *x, float *y,
+                           double *absdot, int out_dim, int k_elems) {
+    float blk[ORQ_BLOCK_ELEMS];
+    long cur = -1;
+    for (int r = 0; r < out_dim; ++r) {
+        double acc = 0.0, aabs = 0.0;
+        for (int c = 0; c < k_elems; ++c) {
+            size_t f = (size_t)r * (size_t)k_elems + (size_t)c;
+            long b = (long)(f / ORQ_BLOCK_ELEMS);
+            if (b != cur) {
+                orq_dequantize_row_q4_k(w + (size_t)b * ORQ_BLOCK_BYTES, blk,
+                                        ORQ_BLOCK_ELEMS, 1);
+                cur = b;
+            }
+            double wv = blk[f % ORQ_BLOCK_ELEMS];
+            acc += wv * (double)x[c];
+            aabs += fabs(wv) * fabs((double)x[c]);
+        }
+        y[r] = (float)acc;
+        if (absdot) absdot[r] = aabs;
+    }
+}
+
+void orq_gemv_batched_f64_abs(const uint8_t *w, const float *X, float *Y,
+                              double *absdot, int out_dim, int bpr, int batch) {
+    size_t k = (size_t)bpr * ORQ_BLOCK_ELEMS;
+    float *wr = (float *)malloc(k * sizeof(float));
+    for (int r = 0; r < out_dim; ++r) {
+        orq_dequantize_row_q4_k(w + (size_t)r * bpr * ORQ_BLOCK_BYTES, wr, k, (size_t)bpr);
+        for (int b = 0; b < batch; ++b) {
+            const float *xb = X + (size_t)b * k;
+            double acc = 0.0, aabs = 0.0;
+            for (size_t i = 0; i < k; ++i) {
+                acc += (double)wr[i] * (double)xb[i];
+                aabs += fabs((double)wr[i]) * fabs((double)xb[i]);
+            }
+            Y[(size_t)b * out_dim + r] = (float)acc;
+            if (absdot) absdot[(size_t)b * out_dim + r] = aabs;
+        }
+    }
+    free(wr);
+}
+
+void orq_gemm_f16_f64(const uint8_t *w, const uint16_t *a_f16, float *c,
+                      double *absdot, int out_dim, int bpr, int m_tokens,
+                      const int *rows, int n_rows) {
+    size_t k = (size_t)bpr * ORQ_BLOCK_ELEMS;
+    float *wr = (float *)malloc(k * sizeof(float));
+    int nr = rows ? n_rows : out_dim;
+    for (int ii = 0; ii < nr; ++ii) {
+        int r = rows ? rows[ii] : ii;
+        orq_dequantize_row_q4_k(w + (size_t)r * bpr * ORQ_BLOCK_BYTES, wr, k, (size_t)bpr);
+        for (int m = 0; m < m_tokens; ++m) {
+            const uint16_t *am = a_f16 + (size_t)m * k;
+            double acc = 0.0, aabs = 0.0;
+            for (size_t i = 0; i < k; ++i) {
+                double av = orq_f16_to_f32(am[i]);
+                acc += (double)wr[i] * av;
+                aabs += fabs((double)wr[i]) * fabs(av);
+            }
+            c[(size_t)m * nr + ii] = (float)acc;
+            if (absdot) absdot[(size_t)m * nr + ii] = aabs;
+        }
+    }
+    free(wr);
+}
+
+/* ------------------------------------------------ CPU timing baseline ---- */
+
+/* llm.rs:695-735 (dot_q4k_row_scalar): one sequential f32 accumulator over
+ * the row, canonical order, dequantized weight then multiply-add (unfused). */
+static float dot_row_scalar(const uint8_t *row, const float *x, int nb) {
+    float acc = 0.0f;
+    for (int blk = 0; blk < nb; ++blk) {
+        const uint8_t *b = row + (size_t)blk * ORQ_BLOCK_BYTES;
+        float d = finite_or_zero(orq_f16_to_f32((uint16_t)(b[0] | (b[1] << 8))));
+        float dmin = finite_or_zero(orq_f16_to_f32((uint16_t)(b[2] | (b[3] << 8))));
+        const float *xb = x + (size_t)blk * ORQ_BLOCK_ELEMS;
+        for (int g = 0; g < 4; ++g) {
+            for (int half = 0; half < 2; ++half) {
+                uint8_t sc, m;
+                orq_get_scale_min_k4(2 * g + half, b + 4, &sc, &m);
+                float d1 = d * (float)sc, m1 = dmin * (float)m;
+                const float *xs = xb + g * 64 + half * 32;
+                for (int l = 0; l < 32; ++l) {
+                    uint8_t byte = b[16 + g * 32 + l];
+                    float wv = d1 * (float)(half ? (byte >> 4) : (byte & 0xF)) - m1;
+                    acc += wv * xs[l];
+                }
+            }
+        }
+    }
+    return acc;
+}
+
+#if defined(__x86_64__)
+/* llm.rs:748-806 (dot_q4k_row_avx512): per sub-block, 32 nibbles widened to
+ * two 16-lane f32 vectors, weights by fused q*scale - offset, then fused
+ * multiply-add into two 16-lane accumulators; horizontal sum at the end. */
+__attribute__((target("avx512f,avx512bw,fma")))
+static float dot_row_avx512(const uint8_t *row, const float *x, int nb) {
+    __m512 acc0 = _mm512_setzero_ps(), acc1 = _mm512_setzero_ps();
+    const __m256i low4 = _mm256_set1_epi8(0x0F);
+    for (int blk = 0; blk < nb; ++blk) {
+        const uint8_t *b = row + (size_t)blk * ORQ_BLOCK_BYTES;
+        float d = finite_or_zero(orq_f16_to_f32((uint16_t)(b[0] | (b[1] << 8))));
+        float dmin = finite_or_zero(orq_f16_to_f32((uint16_t)(b[2] | (b[3] << 8))));
+        const float *xb = x + (size_t)blk * ORQ_BLOCK_ELEMS;
+        for (int g = 0; g < 4; ++g) {
+            __m256i bytes = _mm256_loadu_si256((const __m256i *)(b + 16 + 32 * g));
+            __m256i nibs[2] = {_mm256_and_si256(bytes, low4),
+                               _mm256_and_si256(_mm256_srli_epi16(bytes, 4), low4)};
+            for (int half = 0; half < 2; ++half) {
+                uint8_t sc, m;
+                orq_get_scale_min_k4(2 * g + half, b + 4, &sc, &m);
+                __m512 vs = _mm512_set1_ps(d * (float)sc);
+                __m512 vo = _mm512_set1_ps(dmin * (float)m);
+                __m512 q0 = _mm512_cvtepi32_ps(_mm512_cvtepu8_epi32(_mm256_castsi256_si128(nibs[half])));
+                __m512 q1 = _mm512_cvtepi32_ps(_mm512_cvtepu8_epi32(_mm256_extracti128_si256(nibs[half], 1)));
+                const float *xs = xb + 64 * g + 32 * half;
+                acc0 = _mm512_fmadd_ps(_mm512_fmsub_ps(q0, vs, vo), _mm512_loadu_ps(xs), acc0);
+                acc1 = _mm512_fmadd_ps(_mm512_fmsub_ps(q1, vs, vo), _mm512_loadu_ps(xs + 16), acc1);
+            }
+        }
+    }
+    return _mm512_reduce_add_ps(_mm512_add_ps(acc0, acc1));
+}
+#endif
+
+int orq_cpu_has_avx512(void) {
+#if defined(__x86_64__)
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+           __builtin_cpu_supports("fma");
+#else
+    return 0;
+#endif
+}
+
+/* llm.rs:468-534: y[r] = dot(row r) for every row, rows in parallel (rayon
+ * par_iter there, OpenMP static schedule here). */
+int orq_cpu_matvec_q4k(const uint8_t *w, const float *x, float *y, int out_dim,
+                       int bpr, int threads) {
+    int avx = orq_cpu_has_avx512();
+    size_t row_bytes = (size_t)bpr * ORQ_BLOCK_BYTES;
+#ifdef _OPENMP
+    int nt = threads > 0 ? threads : omp_get_num_procs();
+#pragma omp parallel for schedule(static) num_threads(nt)
+#endif
+    for (int r = 0; r < out_dim; ++r) {
+        const uint8_t *row = w + (size_t)r * row_bytes;
+#if defined(__x86_64__)
+        y[r] = avx ? dot_row_avx512(row, x, bpr) : dot_row_scalar(row, x, bpr);
+#else
+        y[r] = dot_row_scalar(row, x, bpr);
+#endif
+    }
+    (void)threads;
+    return avx;
+}
+
+/* The smooth test signal of the reference's own Q4_K tests
+ * (gguf.rs:703-738 and tests/dequant_q4k.rs:70-78):
+ * t = i/n (f32); v = sin(7.3 t)*0.5 + cos(17.1 t)*0.2, all in f32. */
+void orq_fill_smooth(float *out, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        float t = (float)i / (float)n;
+        out[i] = sinf(t * 7.3f) * 0.5f + cosf(t * 17.1f) * 0.2f;
+    }
+}

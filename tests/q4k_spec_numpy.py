@@ -1,0 +1,46 @@
+"""Independent numpy restatement of the Q4_K block format, written from the
+format description (not from the C oracle), used to cross-check the oracle.
+
+Block (144 B, little-endian): +0 d:f16, +2 dmin:f16, +4 scales[12], +16 qs[128].
+Sub-block j in 0..8 has a 6-bit scale sc[j] and min m[j]:
+  j < 4:  sc = s[j] & 63,                         m = s[j+4] & 63
+  j >= 4: sc = (s[j+4] & 15) | ((s[j-4] >> 6) << 4), m = (s[j+4] >> 4) | ((s[j] >> 6) << 4)
+Output position p in 0..256 (ggml order): sub-block p // 32; byte
+qs[32*(p // 64) + p % 32]; low nibble when (p // 32) is even, else high.
+w[p] = f32(f32(d*sc) * q) - f32(dmin*m); d or dmin with exponent 31 -> 0.
+"""
+import numpy as np
+
+
+def unpack_scales(s: np.ndarray):
+    """s: uint8 [nb, 12] -> (sc, m) uint8 [nb, 8]."""
+    s = s.astype(np.uint16)
+    sc = np.empty((s.shape[0], 8), np.uint16)
+    m = np.empty((s.shape[0], 8), np.uint16)
+    sc[:, :4] = s[:, 0:4] & 63
+    m[:, :4] = s[:, 4:8] & 63
+    sc[:, 4:] = (s[:, 8:12] & 15) | ((s[:, 0:4] >> 6) << 4)
+    m[:, 4:] = (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)
+    return sc.astype(np.uint8), m.astype(np.uint8)
+
+
+def half_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    f = h.astype(np.uint16).view(np.float16).astype(np.float32)
+    return np.where(np.isfinite(f), f, np.float32(0.0)).astype(np.float32)
+
+
+def dequantize(data: np.ndarray) -> np.ndarray:
+    blocks = np.asarray(data, np.uint8).reshape(-1, 144)
+    nb = blocks.shape[0]
+    d = half_bits_to_f32(blocks[:, 0:2].copy().view(np.uint16)[:, 0])
+    dmin = half_bits_to_f32(blocks[:, 2:4].copy().view(np.uint16)[:, 0])
+    sc, m = unpack_scales(blocks[:, 4:16])
+    qs = blocks[:, 16:144]
+    p = np.arange(256)
+    sub = p // 32
+    byte = qs[:, 32 * (p // 64) + p % 32]
+    q = np.where(sub % 2 == 0, byte & 15, byte >> 4).astype(np.float32)
+    d1 = (d[:, None] * sc.astype(np.float32))[:, sub]          # f32 product
+    m1 = (dmin[:, None] * m.astype(np.float32))[:, sub]
+    out = (d1 * q).astype(np.float32) - m1                      # two roundings
+    return out.astype(np.float32).reshape(nb * 256)

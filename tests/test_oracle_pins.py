@@ -1,0 +1,349 @@
+"""Pins for the CPU oracle (oracle/q4k_oracle.c): closed forms, invariants and
+an independent numpy restatement, chosen so that a plausible transcription
+mistake (dropped term, wrong shift, swapped operand, wrong sub-block order)
+fails at least one of them. CPU only."""
+import math
+import struct
+
+import numpy as np
+import pytest
+
+from tests import q4k_spec_numpy as spec
+
+OFFS = [0, 128, 32, 160, 64, 192, 96, 224]  # gguf.rs:590-601
+
+
+def f32(v):
+    return np.float32(v)
+
+
+def trunc_f16_bits(x: np.float32) -> int:
+    """Truncation toward zero computed a different way than the oracle:
+    numpy's round-to-nearest-even, then one ulp toward zero if it overshot."""
+    h = np.array([x], np.float32).astype(np.float16)
+    hb = int(h.view(np.uint16)[0])
+    if np.isinf(h[0]) and abs(x) < 65536.0:
+        return (hb & 0x8000) | 0x7BFF
+    if abs(np.float32(h[0])) > abs(x) and (hb & 0x7FFF) != 0:
+        hb -= 1
+    return hb
+
+
+# ------------------------------------------------------------ f16 helpers ---
+def test_f16_to_f32_exhaustive(orc):
+    L = orc.lib()
+    for h in range(65536):
+        got = L.orq_f16_to_f32(h)
+        ref = np.array([h], np.uint16).view(np.float16).astype(np.float32)[0]
+        if (h >> 10) & 0x1F == 31:
+            assert math.isnan(got), hex(h)  # gguf.rs:291: Inf and NaN -> NaN
+        else:
+            assert struct.pack("<f", got) == struct.pack("<f", ref), hex(h)
+
+
+def test_f32_to_f16_truncates(orc):
+    L = orc.lib()
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 2**32, size=200_000, dtype=np.uint64).astype(np.uint32)
+    vals = bits.view(np.float32)
+    vals = vals[np.isfinite(vals) & (np.abs(vals) < 65504.0)]
+    dense = np.linspace(-70000, 70000, 20001, dtype=np.float32)
+    tiny = (np.arange(-2000, 2000, dtype=np.float32) * np.float32(2.0**-30))
+    for x in np.concatenate([vals[:50_000], dense, tiny]):
+        h = L.orq_f32_to_f16(float(x))
+        if abs(x) >= 65536.0:
+            assert h & 0x7FFF == 0x7C00
+            continue
+        assert h == trunc_f16_bits(x), (x, hex(h))
+        back = np.array([h], np.uint16).view(np.float16).astype(np.float32)[0]
+        assert abs(back) <= abs(x)
+        nxt = np.array([(h & 0x7FFF) + 1], np.uint16).view(np.float16).astype(np.float32)[0]
+        assert abs(x) < nxt or h & 0x7FFF == 0x7BFF
+
+
+def test_f32_to_f16_specials(orc):
+    L = orc.lib()
+    assert L.orq_f32_to_f16(65504.0) == 0x7BFF
+    assert L.orq_f32_to_f16(65535.0) == 0x7BFF          # truncation, not Inf
+    assert L.orq_f32_to_f16(65536.0) == 0x7C00
+    assert L.orq_f32_to_f16(-1e30) == 0xFC00
+    assert L.orq_f32_to_f16(float("inf")) == 0x7C00
+    assert L.orq_f32_to_f16(float("nan")) & 0x7C00 == 0x7C00
+    assert L.orq_f32_to_f16(float("nan")) & 0x3FF != 0
+    assert L.orq_f32_to_f16(2.0**-25) == 0x0000          # below half-ulp of subnormal
+    assert L.orq_f32_to_f16(2.0**-24) == 0x0001
+    assert L.orq_f32_to_f16(-(2.0**-24) * 3.9) == 0x8003
+    assert L.orq_f32_to_f16(1.0) == 0x3C00
+    assert L.orq_f32_to_f16(1.0 + 2.0**-11) == 0x3C00    # RNE would give 0x3C00 too
+    assert L.orq_f32_to_f16(1.0 + 3 * 2.0**-11) == 0x3C01  # RNE would give 0x3C02
+    assert L.orq_f32_to_f16(1.0 + 3 * 2.0**-12) == 0x3C00  # RNE would give 0x3C01
+
+
+# ------------------------------------------------------------ scales -------
+def test_scale_pack_unpack_exhaustive(orc):
+    rng = np.random.default_rng(2)
+    for j in range(8):
+        for sc in range(64):
+            for m in range(64):
+                scs = rng.integers(0, 64, 8)
+                ms = rng.integers(0, 64, 8)
+                scs[j], ms[j] = sc, m
+                packed = orc.pack_scales_mins(scs, ms)
+                got = [orc.get_scale_min_k4(i, packed) for i in range(8)]
+                assert got == list(zip(scs.tolist(), ms.tolist()))
+
+
+def test_scale_unpack_matches_spec(orc):
+    rng = np.random.default_rng(3)
+    s = rng.integers(0, 256, size=(500, 12), dtype=np.uint8)
+    sc, m = spec.unpack_scales(s)
+    for b in range(500):
+        for j in range(8):
+            assert orc.get_scale_min_k4(j, s[b].tobytes()) == (sc[b, j], m[b, j])
+
+
+# ------------------------------------------------------------ dequant ------
+def _block(d_bits, dmin_bits, sc, m, qs):
+    head = struct.pack("<HH", d_bits, dmin_bits)
+    from oracle.oracle import pack_scales_mins
+    return np.frombuffer(head + pack_scales_mins(sc, m) + bytes(qs), np.uint8).copy()
+
+
+def test_dequant_positions_closed_form(orc):
+    # d = 1, dmin = 0, every scale 1: output p is its own nibble.
+    qs = [(j % 16) | ((15 - j % 16) << 4) for j in range(128)]
+    out = orc.dequantize(_block(0x3C00, 0, [1] * 8, [0] * 8, qs))
+    p = np.arange(256)
+    want = np.where((p // 32) % 2 == 0, p % 16, 15 - p % 16).astype(np.float32)
+    assert np.array_equal(out, want)
+
+
+def test_dequant_subblock_to_position(orc):
+    # q = 0, d = 0, dmin = 1, m[is] = is+1: out[p] = -(p//32 + 1).
+    out = orc.dequantize(_block(0x0000, 0x3C00, [5] * 8, list(range(1, 9)), [0] * 128))
+    assert np.array_equal(out, -(np.arange(256) // 32 + 1).astype(np.float32))
+
+
+def test_dequant_nonfinite_scale_is_zero(orc):
+    qs = list(range(128))
+    for bad in (0x7C00, 0xFC00, 0x7E00):
+        out = orc.dequantize(_block(bad, 0x3800, [7] * 8, [3] * 8, qs))
+        assert np.array_equal(out, np.full(256, -0.5 * 3, np.float32))
+        out = orc.dequantize(_block(0x3800, bad, [7] * 8, [3] * 8, qs))
+        assert np.all(out >= 0)
+
+
+def test_dequant_matches_numpy_spec_random_bytes(orc):
+    rng = np.random.default_rng(4)
+    data = rng.integers(0, 256, size=144 * 400, dtype=np.uint8)
+    # force some non-finite, subnormal and zero scales
+    blocks = data.reshape(400, 144)
+    blocks[0, 0:2] = [0x00, 0x7C]
+    blocks[1, 2:4] = [0x01, 0x7E]
+    blocks[2, 0:2] = [0x03, 0x00]
+    blocks[3, 0:4] = 0
+    got = orc.dequantize(data)
+    want = spec.dequantize(data)
+    assert got.view(np.uint32).tolist() == want.view(np.uint32).tolist()
+
+
+def test_dequant_is_pure_function_of_bytes(orc):
+    # gguf.rs:745-760
+    x = np.sin(np.arange(512, dtype=np.float32) * np.float32(0.013)).astype(np.float32)
+    q = orc.quantize(x)
+    assert np.array_equal(orc.dequantize(q).view(np.uint32), orc.dequantize(q).view(np.uint32))
+
+
+def test_dequant_respects_out_len(orc):
+    q = orc.quantize(orc.normal(5, 512, 0.02))
+    full = orc.dequantize(q)
+    part = orc.dequantize(q, n_blocks=2, out_len=300)
+    assert np.array_equal(part, full[:300])
+
+
+# ------------------------------------------------------------ quantizer ----
+def _legacy_decode(q: np.ndarray) -> np.ndarray:
+    """Decode with the quantizer's own (legacy) sub-block order."""
+    blocks = q.reshape(-1, 144)
+    out = np.zeros((blocks.shape[0], 256), np.float32)
+    d = spec.half_bits_to_f32(blocks[:, 0:2].copy().view(np.uint16)[:, 0])
+    dm = spec.half_bits_to_f32(blocks[:, 2:4].copy().view(np.uint16)[:, 0])
+    sc, m = spec.unpack_scales(blocks[:, 4:16])
+    for b in range(blocks.shape[0]):
+        for i in range(8):
+            byt = blocks[b, 16 + 32 * (i // 2): 16 + 32 * (i // 2) + 32]
+            nib = (byt & 15) if i % 2 == 0 else (byt >> 4)
+            out[b, OFFS[i]:OFFS[i] + 32] = (d[b] * f32(sc[b, i])) * nib.astype(np.float32) - dm[b] * f32(m[b, i])
+    return out.ravel()
+
+
+def test_quantize_constant_closed_form(orc):
+    q = orc.quantize(np.ones(256, np.float32))
+    sd = trunc_f16_bits(np.float32(np.float32(1.0) / np.float32(15.0)) / np.float32(63.0))
+    want = struct.pack("<HH", sd, 0) + bytes([0xFF] * 4 + [0x00] * 4 + [0x0F] * 4) + bytes([0xFF] * 128)
+    assert q.tobytes() == want
+
+
+def test_quantize_uses_legacy_subblock_order(orc):
+    # Sub-block is (legacy positions OFFS[is]..+32) holds the constant 0.1*(is+1):
+    # its scale must then grow with is like 63*(is+1)/8. A quantizer using the
+    # canonical order would see [0.1,0.3,0.5,0.7,0.2,0.4,0.6,0.8] instead.
+    x = np.zeros(256, np.float32)
+    for i in range(8):
+        x[OFFS[i]:OFFS[i] + 32] = np.float32(0.1 * (i + 1))
+    q = orc.quantize(x)
+    scs = [orc.get_scale_min_k4(i, q[4:16].tobytes())[0] for i in range(8)]
+    want = [round(63 * (i + 1) / 8) for i in range(8)]
+    assert all(abs(a - b) <= 1 for a, b in zip(scs, want)), scs
+    assert np.max(np.abs(_legacy_decode(q) - x)) < 0.01
+
+
+@pytest.mark.parametrize("seed", [11, 12, 13])
+def test_quantize_error_bound_legacy_order(orc, seed):
+    x = orc.normal(seed, 256 * 64, 0.02)
+    x[:256] = np.abs(x[:256])                    # all-positive block: x_min clamps to 0
+    x[256:512] = 0.0                             # all-zero block
+    q = orc.quantize(x)
+    blocks = q.reshape(-1, 144)
+    sd = spec.half_bits_to_f32(blocks[:, 0:2].copy().view(np.uint16)[:, 0])
+    sdm = spec.half_bits_to_f32(blocks[:, 2:4].copy().view(np.uint16)[:, 0])
+    # d, dmin are the truncated f16 of (max local)/63
+    for b in range(blocks.shape[0]):
+        xb = x[256 * b: 256 * b + 256]
+        loc = []
+        for o in OFFS:
+            s = xb[o:o + 32]
+            mn = min(s.min(), np.float32(0.0))
+            loc.append((np.float32(np.float32(s.max() - mn) / np.float32(15.0)), -mn))
+        super_d = super_dm = np.float32(0.0)   # +0 start, strict '>' as gguf.rs:609-613
+        for a, c in loc:
+            super_d = a if a > super_d else super_d
+            super_dm = c if c > super_dm else super_dm
+        assert blocks[b, 0:2].view(np.uint16)[0] == trunc_f16_bits(np.float32(super_d / np.float32(63.0)))
+        assert blocks[b, 2:4].view(np.uint16)[0] == trunc_f16_bits(np.float32(super_dm / np.float32(63.0)))
+    v = _legacy_decode(q).reshape(-1, 256)
+    xr = x.reshape(-1, 256)
+    sc, m = spec.unpack_scales(blocks[:, 4:16])
+    for b in range(blocks.shape[0]):
+        for i in range(8):
+            d1 = sd[b] * sc[b, i]
+            bound = max(d1 / 2, sdm[b] / 2 + 7.5 * sd[b]) * 1.0001 + 1e-7
+            e = np.abs(xr[b, OFFS[i]:OFFS[i] + 32] - v[b, OFFS[i]:OFFS[i] + 32])
+            assert e.max() <= bound, (b, i, e.max(), bound)
+
+
+def test_reference_round_trip_test_fails_in_canonical_order(orc):
+    # gguf.rs:703-738 gates rms_rel < 0.05 for quantize -> dequantize_row_q4_k.
+    # The quantizer writes legacy order and the dequant reads canonical order,
+    # so that round trip is a chunk permutation and the gate fails; the same
+    # bytes decoded in the quantizer's own order pass it.
+    x = orc.smooth(4 * 256)
+    q = orc.quantize(x)
+    canon = orc.dequantize(q)
+    leg = _legacy_decode(q)
+    rms = lambda y: math.sqrt(float(np.sum((x - y) ** 2)) / float(np.sum(x * x)))
+    assert rms(canon) > 0.05
+    assert rms(leg) < 0.05
+
+
+# ------------------------------------------------------------ SimpleRng ----
+def test_rng_integer_core(orc):
+    r = orc.SimpleRng(0xCAFEBABE)
+    s = (0xCAFEBABE + 1) & (2**64 - 1)
+    for _ in range(1000):
+        s = (s * 6364136223846793005 + 1442695040888963407) & (2**64 - 1)
+        assert r.next_u64() == s
+    r = orc.SimpleRng(7)
+    s = 8
+    for _ in range(1000):
+        s = (s * 6364136223846793005 + 1442695040888963407) & (2**64 - 1)
+        assert r.next_f32() == np.float32((s >> 40) / 2.0**24)
+
+
+def test_rng_normal_box_muller(orc):
+    r = orc.SimpleRng(0xC0FFEEFE)
+    s = (0xC0FFEEFE + 1) & (2**64 - 1)
+    for _ in range(2000):
+        s = (s * 6364136223846793005 + 1442695040888963407) & (2**64 - 1)
+        u1 = max(float(np.float32((s >> 40) / 2.0**24)), float(np.float32(1e-10)))
+        s = (s * 6364136223846793005 + 1442695040888963407) & (2**64 - 1)
+        u2 = float(np.float32((s >> 40) / 2.0**24))
+        ref = math.sqrt(-2.0 * math.log(u1)) * math.cos(2.0 * math.pi * u2)
+        got = r.next_normal()
+        assert abs(got - ref) <= 4e-6 * max(1.0, abs(ref)), (got, ref)
+    v = orc.normal(123, 200_000)
+    assert abs(float(v.mean())) < 0.01 and abs(float(v.std()) - 1.0) < 0.01
+
+
+# ------------------------------------------------------------ GEMV ---------
+def test_gemv_unit_vector_returns_column(orc):
+    n, bpr = 24, 3
+    w = orc.seeded_weight(21, n, bpr * 256)
+    wd = spec.dequantize(w).reshape(n, bpr * 256)
+    for k in (0, 1, 31, 32, 255, 256, 700, 767):
+        x = np.zeros(bpr * 256, np.float32)
+        x[k] = 1.0
+        y, _ = orc.gemv(w, x, n, bpr)
+        assert np.array_equal(y, wd[:, k])
+
+
+def test_gemv_ones_gives_row_sums_and_matches_numpy(orc):
+    n, bpr = 40, 4
+    w = orc.seeded_weight(22, n, bpr * 256)
+    wd = spec.dequantize(w).reshape(n, bpr * 256).astype(np.float64)
+    y, a = orc.gemv(w, np.ones(bpr * 256, np.float32), n, bpr)
+    assert np.array_equal(y, wd.sum(axis=1).astype(np.float32))
+    x = orc.normal(23, bpr * 256)
+    y, a = orc.gemv(w, x, n, bpr)
+    ref = wd @ x.astype(np.float64)
+    assert np.allclose(y, ref.astype(np.float32), rtol=0, atol=1e-6 * np.abs(wd) @ np.abs(x))
+    assert np.allclose(a, np.abs(wd) @ np.abs(x.astype(np.float64)), rtol=1e-12)
+
+
+def test_gemv_flat_matches_row_aligned_and_numpy(orc):
+    n, k = 16, 512
+    w = orc.seeded_weight(24, n, k)
+    x = orc.normal(25, k)
+    y1, a1 = orc.gemv(w, x, n, k // 256)
+    y2, a2 = orc.gemv_flat(w, x, n, k)
+    assert np.array_equal(y1, y2) and np.allclose(a1, a2, rtol=1e-12)
+    n, k = 8, 96             # 768 elements = 3 blocks, rows straddle blocks
+    w = orc.seeded_weight(26, n, k)
+    x = orc.normal(27, k)
+    y, a = orc.gemv_flat(w, x, n, k)
+    wd = spec.dequantize(w).reshape(n, k).astype(np.float64)
+    assert np.allclose(y, (wd @ x).astype(np.float32), rtol=0, atol=1e-6 * (np.abs(wd) @ np.abs(x)))
+
+
+def test_gemv_batched_is_rowwise_gemv(orc):
+    n, bpr, B = 10, 2, 5
+    w = orc.seeded_weight(28, n, bpr * 256)
+    X = orc.normal(29, B * bpr * 256).reshape(B, -1)
+    Y, A = orc.gemv_batched(w, X, n, bpr)
+    for b in range(B):
+        y, a = orc.gemv(w, X[b], n, bpr)
+        assert np.array_equal(Y[b], y) and np.array_equal(A[b], a)
+
+
+def test_gemm_f16_matches_numpy(orc):
+    n, bpr, M = 12, 2, 6
+    w = orc.seeded_weight(30, n, bpr * 256)
+    a = orc.normal(31, M * bpr * 256).astype(np.float16).reshape(M, -1)
+    C, _ = orc.gemm_f16(w, a.view(np.uint16), n, bpr)
+    wd = spec.dequantize(w).reshape(n, -1).astype(np.float64)
+    ref = a.astype(np.float64) @ wd.T
+    assert np.allclose(C, ref.astype(np.float32), rtol=1e-6, atol=1e-6)
+    rows = np.array([3, 0, 11])
+    Cs, _ = orc.gemm_f16(w, a.view(np.uint16), n, bpr, rows=rows)
+    assert np.array_equal(Cs, C[:, rows])
+
+
+def test_cpu_baseline_matches_oracle(orc):
+    n, bpr = 300, 14
+    w = orc.seeded_weight(32, n, bpr * 256)
+    x = orc.normal(33, bpr * 256)
+    y_ref, a = orc.gemv(w, x, n, bpr)
+    for threads in (1, 0):
+        y = np.empty(n, np.float32)
+        orc.cpu_matvec(w, x, y, n, bpr, threads)
+        assert np.all(np.abs(y - y_ref) <= 1e-5 * a)
