@@ -1,0 +1,118 @@
+/*
+ * modgrad_q4k -- MI355X (gfx950) Q4_K quantized matvec, C ABI.
+ *
+ * Drop-in for the Q4_K kernel ABI of rotkonetworks/modgrad: the first group of
+ * entry points has exactly the names, argument order and types that the
+ * reference's Rust host declares in its `unsafe extern "C"` block
+ * (crates/modgrad-device/src/backend/rocm.rs:433-563), so that block links
+ * against libmodgrad_q4k unchanged. The remaining entry points are additive.
+ *
+ * Conventions (kept from the reference, matvec_q4k.hip:110-124):
+ *   - every pointer is a device pointer owned by the caller; launchers never
+ *     allocate caller-visible memory and never synchronize;
+ *   - reference-compatible launchers enqueue on the null stream; the *_ex
+ *     variants take an explicit hipStream_t;
+ *   - the return value is a hipError_t (0 = hipSuccess); non-positive sizes
+ *     return hipErrorInvalidValue and enqueue nothing.
+ *
+ * Q4_K super-block (144 bytes, 256 weights): +0 d:f16, +2 dmin:f16,
+ * +4 scales[12] (6-bit scale/min pairs), +16 qs[128] (4-bit quants).
+ * Element order is ggml's (canonical): position p of a block belongs to
+ * sub-block p/32 and reads the low (p/32 even) or high nibble of
+ * qs[32*(p/64) + p%32]; w = d*sc*q - dmin*m.
+ */
+#ifndef MODGRAD_Q4K_H
+#define MODGRAD_Q4K_H
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------------------
+ * Reference-compatible entry points
+ * ------------------------------------------------------------------------ */
+
+/* Replaces launch_dequant_q4k (decl rocm.rs:447-451, def
+ * kernels/dequant_q4k.hip:147-157). Dequantizes n_blocks*144 bytes into
+ * n_blocks*256 floats in canonical order, bit-identical to the reference host
+ * dequantizer dequantize_row_q4_k (kfd/gguf.rs:364-404): each weight is
+ * fl(fl(d*sc)*q) - fl(dmin*m), never fused. (The reference's own GPU kernel
+ * writes the legacy all-low-then-all-high order instead; this one follows the
+ * host spec.) n_blocks <= 0 -> hipErrorInvalidValue. */
+hipError_t launch_dequant_q4k(const unsigned char *q4k, int n_blocks, float *fp32_out);
+
+/* Replaces launch_matvec_q4k (decl rocm.rs:457-463, def
+ * kernels/matvec_q4k.hip:111-124). y[r] = sum_k dequant(W)[r][k] * x[k],
+ * W row-aligned: row r starts at byte r*blocks_per_row*144, x has
+ * blocks_per_row*256 floats, y has out_dim floats. f32 accumulation;
+ * |y - y_f64| <= 1e-4 * sum_k |w_rk||x_k| per row.
+ * out_dim <= 0 or blocks_per_row <= 0 -> hipErrorInvalidValue. */
+hipError_t launch_matvec_q4k(const unsigned char *w_q4, const float *x, float *y,
+                             int out_dim, int blocks_per_row);
+
+/* ---------------------------------------------------------------------------
+ * Additive entry points (no counterpart in the reference unless noted)
+ * ------------------------------------------------------------------------ */
+
+/* Layout of the weight bytes for launch_matvec_q4k_ex. */
+#define MGQ_LAYOUT_ROWS 0 /* GGUF row-aligned: k_elems % 256 == 0 */
+#define MGQ_LAYOUT_FLAT 1 /* flattened [out_dim x k_elems] tensor quantized as one
+                             stream (LinearResidentQuantized, neuron.rs:931-951):
+                             element (r,c) is flat index r*k_elems+c, in block
+                             idx/256 at position idx%256; needs
+                             out_dim*k_elems % 256 == 0 */
+
+/* launch_matvec_q4k with an explicit stream and either layout. For
+ * MGQ_LAYOUT_ROWS it computes the same function as launch_matvec_q4k with
+ * blocks_per_row = k_elems/256. */
+hipError_t launch_matvec_q4k_ex(const unsigned char *w_q4, const float *x, float *y,
+                                int out_dim, int k_elems, int layout,
+                                hipStream_t stream);
+
+/* launch_dequant_q4k with an explicit stream. */
+hipError_t launch_dequant_q4k_ex(const unsigned char *q4k, int n_blocks, float *fp32_out,
+                                 hipStream_t stream);
+
+/* Batched matvec for multi-sequence decode: Y[b][r] = dequant(W)[r] . X[b] for
+ * b < batch (1..16). X is [batch][blocks_per_row*256] f32 row-major, Y is
+ * [batch][out_dim] f32. Each super-block is decoded once and reused across
+ * the batch. Same per-(b,r) tolerance as launch_matvec_q4k. */
+hipError_t launch_matvec_q4k_batched(const unsigned char *w_q4, const float *X, float *Y,
+                                     int out_dim, int blocks_per_row, int batch,
+                                     hipStream_t stream);
+
+/* Prefill dequant-GEMM: C[m][r] = sum_k dequant(W)[r][k] * A[m][k] for
+ * m < m_tokens, with A f16 [m_tokens][blocks_per_row*256] (IEEE half bits)
+ * and C f32 [m_tokens][out_dim]. Weights are dequantized to f16 tiles and
+ * multiplied on the gfx950 matrix cores with f32 accumulation. */
+hipError_t launch_gemm_q4k_f16(const unsigned char *w_q4, const uint16_t *a_f16, float *c,
+                               int out_dim, int blocks_per_row, int m_tokens,
+                               hipStream_t stream);
+
+/* One matvec of a decode-step chain. */
+typedef struct mgq_gemv_desc {
+    const unsigned char *w_q4; /* row-aligned Q4_K bytes */
+    const float *x;            /* blocks_per_row*256 f32 */
+    float *y;                  /* out_dim f32 */
+    int out_dim;
+    int blocks_per_row;
+} mgq_gemv_desc;
+
+/* Records the n matvecs, in order, into a HIP graph (stream capture on a
+ * private stream), so a whole decode step replays with one launch. The graph
+ * keeps the descriptors' pointers: buffers must outlive the chain. */
+hipError_t mgq_chain_create(const mgq_gemv_desc *descs, int n, void **chain_out);
+/* Replays the chain on `stream`; ordered after prior work on that stream. */
+hipError_t mgq_chain_launch(void *chain, hipStream_t stream);
+hipError_t mgq_chain_destroy(void *chain);
+
+/* Library version string, e.g. "modgrad_q4k 0.1.0 gfx950". */
+const char *mgq_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MODGRAD_Q4K_H */

@@ -1,0 +1,79 @@
+"""ctypes binding of libmodgrad_q4k.so (the C ABI in include/modgrad_q4k.h).
+
+There is no fallback: if the library is missing or does not export every
+declared symbol, loading raises. Build it with `python -m modgrad_amd.build`.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmodgrad_q4k.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "modgrad_q4k.h")
+
+hipSuccess = 0
+hipErrorInvalidValue = 1
+hipErrorNotSupported = 801
+
+P = ctypes.c_void_p
+I = ctypes.c_int
+
+SIGNATURES = {
+    "launch_dequant_q4k": (I, [P, I, P]),
+    "launch_matvec_q4k": (I, [P, P, P, I, I]),
+    "launch_matvec_q4k_ex": (I, [P, P, P, I, I, I, P]),
+    "launch_dequant_q4k_ex": (I, [P, I, P, P]),
+    "launch_matvec_q4k_batched": (I, [P, P, P, I, I, I, P]),
+    "launch_gemm_q4k_f16": (I, [P, P, P, I, I, I, P]),
+    "mgq_chain_create": (I, [P, I, P]),
+    "mgq_chain_launch": (I, [P, P]),
+    "mgq_chain_destroy": (I, [P]),
+    "mgq_version": (ctypes.c_char_p, []),
+}
+
+LAYOUT_ROWS = 0
+LAYOUT_FLAT = 1
+
+
+class GemvDesc(ctypes.Structure):
+    """mgq_gemv_desc."""
+    _fields_ = [("w_q4", P), ("x", P), ("y", P), ("out_dim", I), ("blocks_per_row", I)]
+
+
+class HipError(RuntimeError):
+    def __init__(self, fn: str, code: int):
+        super().__init__(f"{fn} returned hipError {code}")
+        self.code = code
+
+
+_lib = None
+
+
+def declared_symbols() -> list[str]:
+    """Function names declared in include/modgrad_q4k.h."""
+    text = open(HEADER).read()
+    return re.findall(r"^\s*(?:hipError_t|const char \*)\s*\*?\s*(\w+)\s*\(", text, re.M)
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -m modgrad_amd.build` "
+            "(there is no CPU fallback)")
+    L = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(L, name)  # AttributeError if the symbol is not exported
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def check(fn: str, code: int) -> None:
+    if code != hipSuccess:
+        raise HipError(fn, code)

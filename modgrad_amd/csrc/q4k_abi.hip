@@ -1,0 +1,146 @@
+// C ABI of libmodgrad_q4k (declarations and contracts: include/modgrad_q4k.h).
+//
+// Reference-compatible launchers keep the reference's conventions
+// (matvec_q4k.hip:110-124, dequant_q4k.hip:147-157): null stream, no
+// synchronization, hipErrorInvalidValue on non-positive sizes, otherwise the
+// launch status from hipGetLastError().
+#include "../../include/modgrad_q4k.h"
+#include "q4k_launch.hpp"
+
+#include <new>
+#include <vector>
+
+namespace {
+
+constexpr int64_t kMaxI32 = 0x7FFFFFFF;
+
+bool misaligned4(const void *p) { return ((uintptr_t)p & 3u) != 0; }
+
+}  // namespace
+
+extern "C" {
+
+hipError_t launch_dequant_q4k_ex(const unsigned char *q4k, int n_blocks, float *fp32_out,
+                                 hipStream_t stream) {
+    if (n_blocks <= 0 || !q4k || !fp32_out) return hipErrorInvalidValue;
+    if (misaligned4(q4k) || misaligned4(fp32_out)) return hipErrorInvalidValue;
+    if ((int64_t)n_blocks * 32 > kMaxI32 * 256LL) return hipErrorInvalidValue;
+    return mgq::dequant_launch(q4k, n_blocks, fp32_out, stream);
+}
+
+hipError_t launch_dequant_q4k(const unsigned char *q4k, int n_blocks, float *fp32_out) {
+    return launch_dequant_q4k_ex(q4k, n_blocks, fp32_out, nullptr);
+}
+
+hipError_t launch_matvec_q4k_ex(const unsigned char *w_q4, const float *x, float *y,
+                                int out_dim, int k_elems, int layout, hipStream_t stream) {
+    if (out_dim <= 0 || k_elems <= 0 || !w_q4 || !x || !y) return hipErrorInvalidValue;
+    if (misaligned4(w_q4) || misaligned4(x) || misaligned4(y)) return hipErrorInvalidValue;
+    if (layout == MGQ_LAYOUT_ROWS) {
+        if (k_elems % 256 != 0) return hipErrorInvalidValue;
+        return mgq::gemv_rows_launch(w_q4, x, y, out_dim, k_elems / 256, stream);
+    }
+    if (layout == MGQ_LAYOUT_FLAT) {
+        if (((int64_t)out_dim * k_elems) % 256 != 0) return hipErrorInvalidValue;
+        if (k_elems % 256 == 0)
+            return mgq::gemv_rows_launch(w_q4, x, y, out_dim, k_elems / 256, stream);
+        return mgq::gemv_generic_launch(w_q4, x, y, out_dim, k_elems, stream);
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_matvec_q4k(const unsigned char *w_q4, const float *x, float *y, int out_dim,
+                             int blocks_per_row) {
+    if (out_dim <= 0 || blocks_per_row <= 0) return hipErrorInvalidValue;
+    if ((int64_t)blocks_per_row * 256 > kMaxI32) return hipErrorInvalidValue;
+    return launch_matvec_q4k_ex(w_q4, x, y, out_dim, blocks_per_row * 256, MGQ_LAYOUT_ROWS,
+                                nullptr);
+}
+
+hipError_t launch_matvec_q4k_batched(const unsigned char *w_q4, const float *X, float *Y,
+                                     int out_dim, int blocks_per_row, int batch,
+                                     hipStream_t stream) {
+    if (out_dim <= 0 || blocks_per_row <= 0 || batch <= 0 || batch > 16) return hipErrorInvalidValue;
+    if (!w_q4 || !X || !Y || misaligned4(w_q4) || misaligned4(X) || misaligned4(Y))
+        return hipErrorInvalidValue;
+    if ((int64_t)blocks_per_row * 256 > kMaxI32) return hipErrorInvalidValue;
+    return mgq::gemv_batched_launch(w_q4, X, Y, out_dim, blocks_per_row, batch, stream);
+}
+
+hipError_t launch_gemm_q4k_f16(const unsigned char *w_q4, const uint16_t *a_f16, float *c,
+                               int out_dim, int blocks_per_row, int m_tokens,
+                               hipStream_t stream) {
+    if (out_dim <= 0 || blocks_per_row <= 0 || m_tokens <= 0) return hipErrorInvalidValue;
+    if (!w_q4 || !a_f16 || !c || misaligned4(w_q4) || misaligned4(a_f16) || misaligned4(c))
+        return hipErrorInvalidValue;
+    if ((int64_t)blocks_per_row * 256 > kMaxI32) return hipErrorInvalidValue;
+    return mgq::gemm_f16_launch(w_q4, a_f16, c, out_dim, blocks_per_row, m_tokens, stream);
+}
+
+// ------------------------------------------------------ decode-step chain --
+
+struct mgq_chain {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+hipError_t mgq_chain_create(const mgq_gemv_desc *descs, int n, void **chain_out) {
+    if (!chain_out || !descs || n <= 0) return hipErrorInvalidValue;
+    *chain_out = nullptr;
+    for (int i = 0; i < n; ++i) {
+        const mgq_gemv_desc &d = descs[i];
+        if (d.out_dim <= 0 || d.blocks_per_row <= 0 || !d.w_q4 || !d.x || !d.y)
+            return hipErrorInvalidValue;
+    }
+    hipError_t e = mgq::gemv_prepare();  // not allowed to happen mid-capture
+    if (e != hipSuccess) return e;
+    hipStream_t s = nullptr;
+    e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e != hipSuccess) return e;
+    auto *ch = new (std::nothrow) mgq_chain;
+    if (!ch) {
+        hipStreamDestroy(s);
+        return hipErrorOutOfMemory;
+    }
+    e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    hipError_t launch_err = hipSuccess;
+    if (e == hipSuccess) {
+        for (int i = 0; i < n && launch_err == hipSuccess; ++i) {
+            const mgq_gemv_desc &d = descs[i];
+            launch_err = launch_matvec_q4k_ex(d.w_q4, d.x, d.y, d.out_dim, d.blocks_per_row * 256,
+                                              MGQ_LAYOUT_ROWS, s);
+        }
+        hipGraph_t g = nullptr;
+        e = hipStreamEndCapture(s, &g);
+        ch->graph = g;
+        if (e == hipSuccess) e = launch_err;
+        if (e == hipSuccess) e = hipGraphInstantiate(&ch->exec, ch->graph, nullptr, nullptr, 0);
+    }
+    hipStreamDestroy(s);
+    if (e != hipSuccess) {
+        if (ch->exec) hipGraphExecDestroy(ch->exec);
+        if (ch->graph) hipGraphDestroy(ch->graph);
+        delete ch;
+        return e;
+    }
+    *chain_out = ch;
+    return hipSuccess;
+}
+
+hipError_t mgq_chain_launch(void *chain, hipStream_t stream) {
+    if (!chain) return hipErrorInvalidValue;
+    return hipGraphLaunch(static_cast<mgq_chain *>(chain)->exec, stream);
+}
+
+hipError_t mgq_chain_destroy(void *chain) {
+    if (!chain) return hipErrorInvalidValue;
+    auto *ch = static_cast<mgq_chain *>(chain);
+    hipError_t e1 = ch->exec ? hipGraphExecDestroy(ch->exec) : hipSuccess;
+    hipError_t e2 = ch->graph ? hipGraphDestroy(ch->graph) : hipSuccess;
+    delete ch;
+    return e1 != hipSuccess ? e1 : e2;
+}
+
+const char *mgq_version(void) { return "modgrad_q4k 0.1.0 gfx950"; }
+
+}  // extern "C"

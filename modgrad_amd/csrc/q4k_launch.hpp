@@ -1,0 +1,36 @@
+// Internal (C++) launchers behind the C ABI. Arguments are validated by the
+// ABI layer (q4k_abi.hip) before any of these is called.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mgq {
+
+// Bit-exact canonical dequant of n_blocks super-blocks; q must be 4-B aligned.
+hipError_t dequant_launch(const uint8_t *q, int n_blocks, float *out, hipStream_t stream);
+
+// Generic GEMV over the flat-stream layout (element (r,c) at flat r*k+c);
+// any k with n*k % 256 == 0; w 4-B aligned. Also serves the row-aligned
+// layout (k % 256 == 0) when the fast kernel does not apply.
+hipError_t gemv_generic_launch(const uint8_t *w, const float *x, float *y, int n, int k,
+                               hipStream_t stream);
+
+// Matrix-core GEMV for the row-aligned layout. Returns hipErrorNotSupported
+// when the shape or alignment does not fit it (caller then uses generic).
+hipError_t gemv_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                            hipStream_t stream);
+
+// One-time kernel attribute setup (dynamic LDS limit); safe to call often.
+hipError_t gemv_prepare();
+
+// Row-aligned GEMV: picks the matrix-core kernel when it applies.
+hipError_t gemv_rows_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                            hipStream_t stream);
+
+hipError_t gemv_batched_launch(const uint8_t *w, const float *X, float *Y, int n, int bpr,
+                               int batch, hipStream_t stream);
+
+hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n, int bpr,
+                           int m_tokens, hipStream_t stream);
+
+}  // namespace mgq

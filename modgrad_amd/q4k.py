@@ -1,0 +1,271 @@
+"""Host-side mirror of the reference's Q4_K device interface, over the C ABI.
+
+Names, argument meaning and error behaviour follow the reference's Rust host
+(crates/modgrad-device/src/backend/rocm.rs, ops.rs and
+crates/modgrad-compute/src/neuron.rs), so tests read like the reference's:
+
+  HipBuffer           rocm.rs:603-935  (RAII device buffer; here a torch
+                                        uint8 CUDA tensor holds the memory)
+  HipBuffer.matvec_q4k / matvec_q4k_into   rocm.rs:681-738
+  kern.matvec_q4k, kern.hip_sync           rocm.rs:942-963
+  ops.dequant_q4k_resident                 ops.rs:531-539
+  LinearResidentQuantized                  neuron.rs:897-1108
+
+PyTorch is only the device-memory allocator here; every computation goes
+through libmodgrad_q4k.so (modgrad_amd._lib), with no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+
+Q4K_BLOCK_BYTES = 144
+Q4K_BLOCK_ELEMS = 256
+
+
+class BackendError(RuntimeError):
+    """backend/mod.rs:107-123 (Runtime / Unsupported / OutOfMemory)."""
+
+    def __init__(self, kind: str, msg: str):
+        super().__init__(f"{kind}: {msg}")
+        self.kind = kind
+
+
+def _torch():
+    import torch
+    if not torch.cuda.is_available():
+        raise BackendError("Unsupported", "no HIP device visible")
+    return torch
+
+
+def _chk(code: int, what: str) -> None:
+    if code != 0:
+        raise BackendError("Runtime", f"{what}: hip error {code}")
+
+
+def _stream_ptr(stream) -> ctypes.c_void_p:
+    if stream is None:
+        return ctypes.c_void_p(0)
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+class HipBuffer:
+    """A device allocation of `nbytes` bytes (rocm.rs:620-635)."""
+
+    def __init__(self, nbytes: int):
+        torch = _torch()
+        # round up to 16 B so 128-bit loads of the tail stay in the allocation
+        self._t = torch.empty(max(16, (nbytes + 15) // 16 * 16), dtype=torch.uint8, device="cuda")
+        self._bytes = nbytes
+
+    @classmethod
+    def new(cls, nbytes: int) -> "HipBuffer":
+        return cls(nbytes)
+
+    def device_ptr(self) -> int:
+        return self._t.data_ptr()
+
+    def bytes(self) -> int:
+        return self._bytes
+
+    def len_f32(self) -> int:
+        return self._bytes // 4
+
+    def tensor(self):
+        return self._t[: self._bytes]
+
+    def u8_at(self, offset: int) -> int:
+        """Device pointer `offset` bytes in (rocm.rs:913-934)."""
+        if offset > self._bytes:
+            raise BackendError("Runtime", f"u8_at: offset {offset} > buf {self._bytes}")
+        return self.device_ptr() + offset
+
+    def f32_at(self, index: int) -> int:
+        return self.u8_at(4 * index)
+
+    def copy_from_host_bytes(self, src) -> None:
+        torch = _torch()
+        a = np.frombuffer(bytes(src), dtype=np.uint8) if not isinstance(src, np.ndarray) else src
+        a = np.ascontiguousarray(a, dtype=np.uint8).ravel()
+        if a.size > self._bytes:
+            raise BackendError("Runtime", f"copy_from_host_bytes: src {a.size} > buf {self._bytes}")
+        self._t[: a.size].copy_(torch.from_numpy(a))
+
+    def copy_from_host(self, src) -> None:
+        a = np.ascontiguousarray(src, dtype=np.float32).ravel()
+        if a.nbytes > self._bytes:
+            raise BackendError("Runtime", f"copy_from_host: src {a.nbytes} > buf {self._bytes}")
+        self.copy_from_host_bytes(a.view(np.uint8))
+
+    def copy_to_host(self, n_f32: int | None = None) -> np.ndarray:
+        _torch().cuda.synchronize()
+        n = self.len_f32() if n_f32 is None else n_f32
+        return self._t[: 4 * n].cpu().numpy().view(np.float32).copy()
+
+    def matvec_q4k(self, x, out_dim: int, blocks_per_row: int) -> np.ndarray:
+        """y = dequant(self) @ x with host x in and host y out (rocm.rs:681-709)."""
+        in_dim = blocks_per_row * Q4K_BLOCK_ELEMS
+        x_dev = HipBuffer(in_dim * 4)
+        x_dev.copy_from_host(np.asarray(x, np.float32)[:in_dim])
+        y_dev = HipBuffer(out_dim * 4)
+        self.matvec_q4k_into(x_dev, y_dev, out_dim, blocks_per_row)
+        return y_dev.copy_to_host(out_dim)
+
+    def matvec_q4k_into(self, x_dev: "HipBuffer", y_dev: "HipBuffer", out_dim: int,
+                        blocks_per_row: int) -> None:
+        """Launch + device sync, resident x/y (rocm.rs:711-738)."""
+        kern.matvec_q4k(self.device_ptr(), x_dev.device_ptr(), y_dev.device_ptr(), out_dim,
+                        blocks_per_row)
+        kern.hip_sync()
+
+
+class kern:
+    """Launch-only wrappers, null stream, no sync (rocm.rs:942-979)."""
+
+    @staticmethod
+    def hip_sync() -> None:
+        _torch().cuda.synchronize()
+
+    @staticmethod
+    def matvec_q4k(w: int, x: int, y: int, out_dim: int, bpr: int) -> None:
+        _chk(_lib.load().launch_matvec_q4k(w, x, y, out_dim, bpr), "matvec_q4k")
+
+    # additive entry points -------------------------------------------------
+    @staticmethod
+    def matvec_q4k_ex(w: int, x: int, y: int, out_dim: int, k_elems: int,
+                      layout: int = _lib.LAYOUT_ROWS, stream=None) -> None:
+        _chk(_lib.load().launch_matvec_q4k_ex(w, x, y, out_dim, k_elems, layout,
+                                              _stream_ptr(stream)), "matvec_q4k_ex")
+
+    @staticmethod
+    def matvec_q4k_batched(w: int, X: int, Y: int, out_dim: int, bpr: int, batch: int,
+                           stream=None) -> None:
+        _chk(_lib.load().launch_matvec_q4k_batched(w, X, Y, out_dim, bpr, batch,
+                                                   _stream_ptr(stream)), "matvec_q4k_batched")
+
+    @staticmethod
+    def gemm_q4k_f16(w: int, a: int, c: int, out_dim: int, bpr: int, m_tokens: int,
+                     stream=None) -> None:
+        _chk(_lib.load().launch_gemm_q4k_f16(w, a, c, out_dim, bpr, m_tokens,
+                                             _stream_ptr(stream)), "gemm_q4k_f16")
+
+    @staticmethod
+    def dequant_q4k(q: int, n_blocks: int, out: int, stream=None) -> None:
+        _chk(_lib.load().launch_dequant_q4k_ex(q, n_blocks, out, _stream_ptr(stream)),
+             "dequant_q4k")
+
+
+class ops:
+    """ops.rs façade for the Q4_K op."""
+
+    @staticmethod
+    def dequant_q4k_resident(q4k_dev: int, fp32_dev: int, n_blocks: int) -> None:
+        """ops.rs:531-539 -> Op::DequantQ4KResident (rocm.rs:2988-3005)."""
+        if n_blocks <= 0:
+            raise BackendError("Runtime", "dequant_q4k_resident: n_blocks must be > 0")
+        _chk(_lib.load().launch_dequant_q4k(q4k_dev, n_blocks, fp32_dev), "launch_dequant_q4k")
+
+
+class Chain:
+    """A recorded sequence of row-aligned matvecs replayed as one HIP graph."""
+
+    def __init__(self, descs):
+        arr = (_lib.GemvDesc * len(descs))()
+        for i, (w, x, y, out_dim, bpr) in enumerate(descs):
+            arr[i] = _lib.GemvDesc(w, x, y, out_dim, bpr)
+        h = ctypes.c_void_p()
+        _chk(_lib.load().mgq_chain_create(arr, len(descs), ctypes.byref(h)), "mgq_chain_create")
+        self._h = h
+        self.n = len(descs)
+
+    def launch(self, stream=None) -> None:
+        _chk(_lib.load().mgq_chain_launch(self._h, _stream_ptr(stream)), "mgq_chain_launch")
+
+    def close(self) -> None:
+        if self._h:
+            _chk(_lib.load().mgq_chain_destroy(self._h), "mgq_chain_destroy")
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class LinearResidentQuantized:
+    """Q4_K-quantised resident linear layer (neuron.rs:897-1108).
+
+    Host keeps the Q4_K bytes of the flattened [out x in] weight plus an f32
+    bias. Unlike the reference, forward() runs the fused Q4_K GEMV directly on
+    the resident Q4_K bytes (0.5625 B/weight) instead of dequantising to an f32
+    weight and calling hipblasSgemv (4 B/weight); ensure_resident() still
+    materialises the f32 weight via the dequant kernel so dequant-based
+    callers and the evict/re-dequant determinism check keep working.
+    """
+
+    Q4K_BLOCK_ELEMS = Q4K_BLOCK_ELEMS
+
+    def __init__(self, q4k_bytes: np.ndarray, bias: np.ndarray, in_dim: int, out_dim: int):
+        self.host_weight_q4k = np.ascontiguousarray(q4k_bytes, dtype=np.uint8)
+        self.host_bias = np.ascontiguousarray(bias, dtype=np.float32)
+        self._in, self._out = in_dim, out_dim
+        self.weight_q4k_dev = None
+        self.weight_dev = None
+        self.bias_dev = None
+
+    @classmethod
+    def from_q4k(cls, q4k_bytes, bias, in_dim: int, out_dim: int) -> "LinearResidentQuantized":
+        """Wrap already-quantized bytes (the reference's from_linear quantizes on
+        the host with quantize_row_q4_k, gguf.rs:581-663, neuron.rs:931-951)."""
+        if (in_dim * out_dim) % Q4K_BLOCK_ELEMS:
+            raise BackendError("WrongVariant", "weight len not aligned to Q4_K block")
+        if np.asarray(q4k_bytes).size != in_dim * out_dim // 256 * Q4K_BLOCK_BYTES:
+            raise BackendError("WrongVariant", "q4k byte count does not match dims")
+        return cls(q4k_bytes, bias, in_dim, out_dim)
+
+    def in_dim(self) -> int:
+        return self._in
+
+    def out_dim(self) -> int:
+        return self._out
+
+    def is_resident(self) -> bool:
+        return (self.weight_dev is not None and self.bias_dev is not None
+                and self.weight_q4k_dev is not None)
+
+    def host_size_bytes(self) -> int:
+        return self.host_weight_q4k.size + self.host_bias.size * 4
+
+    def dequant_size_bytes(self) -> int:
+        return self.host_weight_q4k.size + self._in * self._out * 4 + self.host_bias.size * 4
+
+    def ensure_resident(self) -> None:
+        if self.is_resident():
+            return
+        q = HipBuffer(self.host_weight_q4k.size)
+        q.copy_from_host_bytes(self.host_weight_q4k)
+        wf = HipBuffer(self._in * self._out * 4)
+        ops.dequant_q4k_resident(q.device_ptr(), wf.device_ptr(),
+                                 self.host_weight_q4k.size // Q4K_BLOCK_BYTES)
+        b = HipBuffer(self.host_bias.size * 4)
+        b.copy_from_host(self.host_bias)
+        self.weight_q4k_dev, self.weight_dev, self.bias_dev = q, wf, b
+
+    def evict(self) -> None:
+        self.weight_q4k_dev = self.weight_dev = self.bias_dev = None
+
+    def forward(self, x_dev: HipBuffer, out_dev: HipBuffer, auto_evict: bool = False,
+                stream=None) -> None:
+        """out = W x + b, W the canonical dequant of the resident Q4_K bytes."""
+        self.ensure_resident()
+        kern.matvec_q4k_ex(self.weight_q4k_dev.device_ptr(), x_dev.device_ptr(),
+                           out_dev.device_ptr(), self._out, self._in, _lib.LAYOUT_FLAT, stream)
+        torch = _torch()
+        y = out_dev.tensor()[: 4 * self._out].view(torch.float32)
+        y.add_(self.bias_dev.tensor()[: 4 * self._out].view(torch.float32))
+        if auto_evict:
+            self.evict()

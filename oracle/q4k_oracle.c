@@ -214,10 +214,33 @@ float orq_rng_next_normal(orq_rng *r) {
     const float two_pi = 2.0f * 3.14159265358979323846f;
     return sqrtf(-2.0f * logf(u1)) * cosf(two_pi * u2);
 }
+/* State after `steps` LCG steps from s (affine map composed by squaring), so
+ * a long fill can be split across threads and still be the one sequential
+ * stream SimpleRng produces. */
+static uint64_t lcg_skip(uint64_t s, uint64_t steps) {
+    uint64_t A = 1, C = 0, a = 6364136223846793005ull, c = 1442695040888963407ull;
+    while (steps) {
+        if (steps & 1) { A = a * A; C = a * C + c; }
+        c = a * c + c;
+        a = a * a;
+        steps >>= 1;
+    }
+    return A * s + C;
+}
+
 void orq_fill_normal(uint64_t seed, float scale, float *out, size_t n) {
-    orq_rng r;
-    orq_rng_init(&r, seed);
-    for (size_t i = 0; i < n; ++i) out[i] = orq_rng_next_normal(&r) * scale;
+    const size_t chunk = 1u << 16;
+    const long long nchunks = (long long)((n + chunk - 1) / chunk);
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (long long ci = 0; ci < nchunks; ++ci) {
+        size_t i0 = (size_t)ci * chunk, i1 = i0 + chunk < n ? i0 + chunk : n;
+        orq_rng r;
+        orq_rng_init(&r, seed);
+        r.s = lcg_skip(r.s, 2u * (uint64_t)i0); /* two draws per normal */
+        for (size_t i = i0; i < i1; ++i) out[i] = orq_rng_next_normal(&r) * scale;
+    }
 }
 
 /* --------------------------------------------------------------- GEMV ---- */

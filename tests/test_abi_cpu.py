@@ -1,0 +1,98 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the
+header declares, and rejects invalid arguments before touching the device
+(the reference's hipErrorInvalidValue contract, matvec_q4k.hip:118,
+dequant_q4k.hip:152)."""
+import ctypes
+import subprocess
+
+import pytest
+
+from modgrad_amd import _lib
+
+INVALID = _lib.hipErrorInvalidValue
+FAKE = 0x10000  # never dereferenced: every call below fails validation first
+
+
+@pytest.fixture(scope="module")
+def L():
+    return _lib.load()
+
+
+def test_exports_every_declared_symbol(L):
+    declared = _lib.declared_symbols()
+    assert {"launch_matvec_q4k", "launch_dequant_q4k"} <= set(declared)
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = [s for s in declared if s not in exported]
+    assert not missing, missing
+    for s in declared:
+        getattr(L, s)
+
+
+def test_version(L):
+    assert L.mgq_version().startswith(b"modgrad_q4k")
+
+
+def test_matvec_rejects_nonpositive_dims(L):
+    assert L.launch_matvec_q4k(FAKE, FAKE, FAKE, 0, 14) == INVALID
+    assert L.launch_matvec_q4k(FAKE, FAKE, FAKE, 16, 0) == INVALID
+    assert L.launch_matvec_q4k(FAKE, FAKE, FAKE, -1, 14) == INVALID
+    assert L.launch_matvec_q4k(FAKE, FAKE, FAKE, 16, 1 << 24) == INVALID  # K overflows int
+
+
+def test_matvec_rejects_null_and_misaligned(L):
+    assert L.launch_matvec_q4k(None, FAKE, FAKE, 16, 1) == INVALID
+    assert L.launch_matvec_q4k(FAKE, None, FAKE, 16, 1) == INVALID
+    assert L.launch_matvec_q4k(FAKE + 2, FAKE, FAKE, 16, 1) == INVALID
+    assert L.launch_matvec_q4k(FAKE, FAKE + 1, FAKE, 16, 1) == INVALID
+
+
+def test_matvec_ex_layout_rules(L):
+    # row layout needs k % 256 == 0; flat layout needs n*k % 256 == 0
+    assert L.launch_matvec_q4k_ex(FAKE, FAKE, FAKE, 16, 300, _lib.LAYOUT_ROWS, None) == INVALID
+    assert L.launch_matvec_q4k_ex(FAKE, FAKE, FAKE, 3, 100, _lib.LAYOUT_FLAT, None) == INVALID
+    assert L.launch_matvec_q4k_ex(FAKE, FAKE, FAKE, 16, 256, 7, None) == INVALID
+
+
+def test_dequant_rejects_bad_args(L):
+    assert L.launch_dequant_q4k(FAKE, 0, FAKE) == INVALID
+    assert L.launch_dequant_q4k(FAKE, -3, FAKE) == INVALID
+    assert L.launch_dequant_q4k(None, 1, FAKE) == INVALID
+    assert L.launch_dequant_q4k(FAKE, 1, FAKE + 2) == INVALID
+
+
+def test_batched_and_gemm_reject_bad_args(L):
+    assert L.launch_matvec_q4k_batched(FAKE, FAKE, FAKE, 16, 1, 0, None) == INVALID
+    assert L.launch_matvec_q4k_batched(FAKE, FAKE, FAKE, 16, 1, 17, None) == INVALID
+    assert L.launch_gemm_q4k_f16(FAKE, FAKE, FAKE, 16, 1, 0, None) == INVALID
+    assert L.launch_gemm_q4k_f16(FAKE, FAKE, FAKE, 0, 1, 4, None) == INVALID
+
+
+def test_chain_rejects_bad_descs(L):
+    h = ctypes.c_void_p()
+    assert L.mgq_chain_create(None, 1, ctypes.byref(h)) == INVALID
+    arr = (_lib.GemvDesc * 1)(_lib.GemvDesc(FAKE, FAKE, FAKE, 0, 14))
+    assert L.mgq_chain_create(arr, 1, ctypes.byref(h)) == INVALID
+    assert L.mgq_chain_create(arr, 0, ctypes.byref(h)) == INVALID
+    assert L.mgq_chain_launch(None, None) == INVALID
+    assert L.mgq_chain_destroy(None) == INVALID
+
+
+def test_host_api_rejects_misshaped_weights():
+    import numpy as np
+    from modgrad_amd.q4k import BackendError, LinearResidentQuantized
+    with pytest.raises(BackendError):
+        LinearResidentQuantized.from_q4k(np.zeros(144, np.uint8), np.zeros(3), 100, 3)
+    with pytest.raises(BackendError):
+        LinearResidentQuantized.from_q4k(np.zeros(100, np.uint8), np.zeros(4), 64, 4)
+
+
+def test_host_size_savings():
+    # neuron.rs:2002-2028: a 1024->256 layer's Q4_K host footprint < 16% of f32
+    import numpy as np
+    from modgrad_amd.q4k import LinearResidentQuantized
+    lin = LinearResidentQuantized.from_q4k(np.zeros(1024 * 256 // 256 * 144, np.uint8),
+                                           np.zeros(256, np.float32), 1024, 256)
+    ratio = lin.host_size_bytes() / (1024 * 256 * 4 + 256 * 4)
+    assert ratio < 0.16 and abs(ratio - 0.1415) < 0.001

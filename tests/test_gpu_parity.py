@@ -1,0 +1,258 @@
+"""GPU parity: libmodgrad_q4k through its C ABI vs the CPU oracle.
+
+Gates (BASELINE): dequant bit-exact; GEMV per row
+|y - y_f64| <= 1e-4 * sum_k |w_rk||x_k|. Inputs follow the seeded convention
+(oracle.oracle docstring); each case prints its name before touching the GPU.
+"""
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+
+from modgrad_amd import _lib
+from tests.gpu_util import assert_gemv_close, dev, empty_f32, host, ptr, random_q4k_bytes
+
+pytestmark = pytest.mark.gpu
+
+
+def note(msg: str) -> None:
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def L():
+    return _lib.load()
+
+
+def run_gemv(L, w: np.ndarray, x: np.ndarray, n: int, bpr: int, w_offset: int = 0) -> np.ndarray:
+    import torch
+    wt = torch.zeros(w.size + 64, dtype=torch.uint8, device="cuda")
+    wt[w_offset: w_offset + w.size].copy_(torch.from_numpy(w))
+    xt = dev(x)
+    yt = empty_f32(n)
+    _lib.check("launch_matvec_q4k", L.launch_matvec_q4k(ptr(wt) + w_offset, ptr(xt), ptr(yt), n, bpr))
+    return host(yt)
+
+
+# ------------------------------------------------------------------ dequant --
+@pytest.mark.parametrize("n_blocks", [1, 8])
+def test_dequant_matches_host_reference_signal(L, orc, n_blocks):
+    # tests/dequant_q4k.rs:48-129 (there max|diff| < 1e-5; here bit-exact)
+    note(f"dequant smooth n_blocks={n_blocks}")
+    q = orc.quantize(orc.smooth(n_blocks * 256))
+    qt, out = dev(q), empty_f32(n_blocks * 256)
+    _lib.check("launch_dequant_q4k", L.launch_dequant_q4k(ptr(qt), n_blocks, ptr(out)))
+    got = host(out)
+    assert got.view(np.uint32).tolist() == orc.dequantize(q).view(np.uint32).tolist()
+
+
+def test_dequant_every_half_scale_value(L, orc):
+    # d takes all 65536 half bit patterns (subnormals, Inf, NaN included)
+    note("dequant exhaustive d/dmin")
+    rng = np.random.default_rng(100)
+    b = rng.integers(0, 256, size=(65536, 144), dtype=np.uint8)
+    h = np.arange(65536, dtype=np.uint16)
+    b[:, 0:2] = h.view(np.uint8).reshape(-1, 2)
+    b[:, 2:4] = ((h.astype(np.uint32) * 7919) & 0xFFFF).astype(np.uint16).view(np.uint8).reshape(-1, 2)
+    q = b.ravel()
+    qt, out = dev(q), empty_f32(65536 * 256)
+    _lib.check("launch_dequant_q4k", L.launch_dequant_q4k(ptr(qt), 65536, ptr(out)))
+    got = host(out)
+    want = orc.dequantize(q)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_dequant_seeded_layer_tensor_and_unaligned_output(L, orc):
+    note("dequant seeded 512x3584, out offset 4 B")
+    import torch
+    q = orc.seeded_weight(orc.layer_seed(0, 1), 512, 3584)
+    nb = q.size // 144
+    qt = dev(q)
+    out = torch.zeros(nb * 256 + 4, dtype=torch.float32, device="cuda")
+    _lib.check("launch_dequant_q4k", L.launch_dequant_q4k(ptr(qt), nb, ptr(out) + 4))
+    got = host(out)[1:]
+    assert np.array_equal(got.view(np.uint32), orc.dequantize(q).view(np.uint32))
+
+
+# --------------------------------------------------------------------- GEMV --
+SMALL = [(1, 1), (15, 1), (16, 2), (17, 3), (31, 13), (33, 14), (64, 74), (100, 5), (47, 148)]
+
+
+@pytest.mark.parametrize("n,bpr", SMALL)
+def test_matvec_small_shapes_seeded(L, orc, n, bpr):
+    note(f"matvec seeded n={n} bpr={bpr}")
+    w = orc.seeded_weight(1000 + n * 7 + bpr, n, bpr * 256)
+    x = orc.normal(2000 + n + bpr, bpr * 256)
+    y = run_gemv(L, w, x, n, bpr)
+    y_ref, a = orc.gemv(w, x, n, bpr)
+    assert_gemv_close(y, y_ref, a)
+
+
+def test_matvec_random_bytes_wide_dynamic_range(L, orc):
+    note("matvec random bytes, x over 1e-20..1e20")
+    rng = np.random.default_rng(7)
+    n, bpr = 96, 14
+    w = random_q4k_bytes(rng, n * bpr, finite_scales=False)
+    w.reshape(-1, 144)[::5, 0:2] = 0x00  # some zero d
+    mag = 10.0 ** rng.uniform(-20, 20, size=bpr * 256)
+    x = (mag * rng.choice([-1.0, 1.0], size=mag.size)).astype(np.float32)
+    y = run_gemv(L, w, x, n, bpr)
+    y_ref, a = orc.gemv(w, x, n, bpr)
+    ok = np.isfinite(y_ref)
+    assert np.array_equal(np.isfinite(y), ok)
+    assert_gemv_close(y[ok], y_ref[ok], a[ok])
+
+
+def test_matvec_unit_vectors_extract_columns(L, orc):
+    note("matvec x = e_k")
+    n, bpr = 48, 3
+    w = orc.seeded_weight(31, n, bpr * 256)
+    wd = orc.dequantize(w).reshape(n, -1)
+    for k in (0, 5, 32, 63, 64, 255, 256, 511, 767):
+        x = np.zeros(bpr * 256, np.float32)
+        x[k] = 1.0
+        y = run_gemv(L, w, x, n, bpr)
+        # d*sc*q - dmin*m may cancel; the kernel rounds its two terms in a
+        # different order than the oracle, so compare at that terms' scale.
+        assert np.all(np.abs(y - wd[:, k]) <= 1e-6 * np.abs(wd).max())
+
+
+def test_matvec_all_zero_rows_give_zero(L, orc):
+    note("matvec zero weights")
+    n, bpr = 40, 4
+    w = np.zeros(n * bpr * 144, np.uint8)
+    x = orc.normal(5, bpr * 256)
+    y = run_gemv(L, w, x, n, bpr)
+    assert np.all(y == 0.0)
+
+
+@pytest.mark.parametrize("name,n,k,t", [("q", 3584, 3584, 0), ("k", 512, 3584, 1),
+                                        ("gate", 18944, 3584, 4), ("down", 3584, 18944, 6)])
+def test_matvec_baseline_layer_shapes(L, orc, name, n, k, t):
+    note(f"matvec layer-0 {name} {n}x{k}")
+    seed = orc.layer_seed(0, t)
+    w = orc.seeded_weight(seed, n, k)
+    x = orc.normal(seed ^ 0xA5A5, k)
+    y = run_gemv(L, w, x, n, k // 256)
+    y_ref, a = orc.gemv(w, x, n, k // 256)
+    worst = assert_gemv_close(y, y_ref, a)
+    print(f"{name}: worst err/absdot = {worst:.3e}")
+
+
+def test_matvec_generic_kernel_on_misaligned_weights(L, orc):
+    # a 4-byte-aligned (not 16) weight pointer takes the vector-ALU kernel
+    note("matvec generic path (w offset 4 B)")
+    n, bpr = 70, 14
+    w = orc.seeded_weight(41, n, bpr * 256)
+    x = orc.normal(42, bpr * 256)
+    y = run_gemv(L, w, x, n, bpr, w_offset=4)
+    y_ref, a = orc.gemv(w, x, n, bpr)
+    assert_gemv_close(y, y_ref, a)
+
+
+@pytest.mark.parametrize("n,k", [(4864, 896), (8, 96), (128, 258), (3, 256 * 3)])
+def test_matvec_flat_layout(L, orc, n, k):
+    note(f"matvec flat {n}x{k}")
+    w = orc.seeded_weight(0xC0F1 + k, n, k)
+    x = orc.normal(0xC0F1 ^ 0xA5A5, k)
+    wt, xt, yt = dev(w), dev(x), empty_f32(n)
+    _lib.check("launch_matvec_q4k_ex",
+               L.launch_matvec_q4k_ex(ptr(wt), ptr(xt), ptr(yt), n, k, _lib.LAYOUT_FLAT, None))
+    y = host(yt)
+    y_ref, a = orc.gemv_flat(w, x, n, k)
+    assert_gemv_close(y, y_ref, a)
+
+
+# ------------------------------------------------------------------ batched --
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 8, 16])
+def test_matvec_batched(L, orc, batch):
+    note(f"batched B={batch}")
+    n, bpr = 1000, 14
+    w = orc.seeded_weight(51, n, bpr * 256)
+    X = orc.normal(52 + batch, batch * bpr * 256).reshape(batch, -1)
+    wt, Xt, Yt = dev(w), dev(X), empty_f32(batch * n)
+    _lib.check("batched", L.launch_matvec_q4k_batched(ptr(wt), ptr(Xt), ptr(Yt), n, bpr, batch, None))
+    Y = host(Yt).reshape(batch, n)
+    Y_ref, A = orc.gemv_batched(w, X, n, bpr)
+    for b in range(batch):
+        assert_gemv_close(Y[b], Y_ref[b], A[b])
+
+
+# --------------------------------------------------------------------- GEMM --
+@pytest.mark.parametrize("n,bpr,m", [(64, 2, 8), (100, 14, 33)])
+def test_gemm_f16_small(L, orc, n, bpr, m):
+    note(f"gemm n={n} bpr={bpr} m={m}")
+    w = orc.seeded_weight(61, n, bpr * 256)
+    a = orc.normal(0xF16, m * bpr * 256).astype(np.float16).reshape(m, -1)
+    wt, at, ct = dev(w), dev(a.view(np.uint16)), empty_f32(m * n)
+    _lib.check("gemm", L.launch_gemm_q4k_f16(ptr(wt), ptr(at), ptr(ct), n, bpr, m, None))
+    C = host(ct).reshape(m, n)
+    C_ref, A = orc.gemm_f16(w, a.view(np.uint16), n, bpr)
+    k = bpr * 256
+    assert np.all(np.abs(C - C_ref) <= 1e-2 * A / np.sqrt(k))
+    assert np.linalg.norm(C - C_ref) <= 1e-3 * np.linalg.norm(C_ref)
+
+
+# -------------------------------------------------------------------- chain --
+def test_chain_replays_the_recorded_matvecs(L, orc):
+    note("chain of 3 matvecs")
+    from modgrad_amd.q4k import Chain
+    shapes = [(256, 14), (64, 74), (512, 14)]
+    bufs, descs, refs = [], [], []
+    for i, (n, bpr) in enumerate(shapes):
+        w = orc.seeded_weight(70 + i, n, bpr * 256)
+        x = orc.normal(80 + i, bpr * 256)
+        wt, xt, yt = dev(w), dev(x), empty_f32(n)
+        bufs += [wt, xt, yt]
+        descs.append((ptr(wt), ptr(xt), ptr(yt), n, bpr))
+        refs.append(orc.gemv(w, x, n, bpr))
+    ch = Chain(descs)
+    for rep in range(3):
+        for t in bufs[2::3]:
+            t.fill_(float("nan"))
+        ch.launch()
+        for (y_ref, a), yt in zip(refs, bufs[2::3]):
+            assert_gemv_close(host(yt), y_ref, a)
+    ch.close()
+
+
+# ---------------------------------------------- LinearResidentQuantized ------
+def test_linear_resident_quantized_forward_and_evict(L, orc):
+    # neuron.rs:1944-1994 (evict_then_redequant: bit-identical re-dequant)
+    note("LinearResidentQuantized 896->4864 flat")
+    from modgrad_amd.q4k import HipBuffer, LinearResidentQuantized
+    in_dim, out_dim = 896, 4864
+    w = orc.seeded_weight(0xCAFEBABE, out_dim, in_dim)
+    bias = orc.normal(0xC0FFEEFE, out_dim, 0.1)
+    lin = LinearResidentQuantized.from_q4k(w, bias, in_dim, out_dim)
+    x = orc.normal(3, in_dim)
+    xb, yb = HipBuffer(in_dim * 4), HipBuffer(out_dim * 4)
+    xb.copy_from_host(x)
+    lin.forward(xb, yb)
+    y = yb.copy_to_host(out_dim)
+    y_ref, a = orc.gemv_flat(w, x, out_dim, in_dim)
+    assert_gemv_close(y - bias, y_ref, a + 1e-30)
+    first = lin.weight_dev.copy_to_host()
+    assert np.array_equal(first.view(np.uint32), orc.dequantize(w).view(np.uint32))
+    lin.evict()
+    assert not lin.is_resident()
+    lin.ensure_resident()
+    assert np.array_equal(lin.weight_dev.copy_to_host().view(np.uint32), first.view(np.uint32))
+
+
+def test_hipbuffer_matvec_q4k_host_roundtrip(L, orc):
+    # rocm.rs:681-709 path (host x in, host y out)
+    note("HipBuffer.matvec_q4k")
+    from modgrad_amd.q4k import HipBuffer
+    n, bpr = 300, 15
+    w = orc.seeded_weight(90, n, bpr * 256)
+    wb = HipBuffer(w.size)
+    wb.copy_from_host_bytes(w)
+    x = (np.sin(np.arange(bpr * 256, dtype=np.float32) * np.float32(0.37)) * np.float32(180.0)
+         + (np.arange(bpr * 256) * 7 % 13).astype(np.float32)).astype(np.float32)
+    y = wb.matvec_q4k(x, n, bpr)
+    y_ref, a = orc.gemv(w, x, n, bpr)
+    assert_gemv_close(y, y_ref, a)
+    assert np.max(np.abs(y - y_ref)) < 0.02  # rocm_matvec_check.rs:49-54 gate

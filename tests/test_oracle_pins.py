@@ -275,6 +275,15 @@ def test_rng_normal_box_muller(orc):
     assert abs(float(v.mean())) < 0.01 and abs(float(v.std()) - 1.0) < 0.01
 
 
+def test_rng_parallel_fill_is_the_sequential_stream(orc):
+    # orq_fill_normal splits the stream across threads with an LCG skip-ahead.
+    n = 3 * (1 << 16) + 123
+    bulk = orc.normal(0x51B00, n, 0.02)
+    r = orc.SimpleRng(0x51B00)
+    seq = np.array([r.next_normal() for _ in range(n)], np.float32) * np.float32(0.02)
+    assert np.array_equal(bulk, seq.astype(np.float32))
+
+
 # ------------------------------------------------------------ GEMV ---------
 def test_gemv_unit_vector_returns_column(orc):
     n, bpr = 24, 3
