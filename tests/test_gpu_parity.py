@@ -72,8 +72,9 @@ def test_dequant_seeded_layer_tensor_and_unaligned_output(L, orc):
     qt = dev(q)
     out = torch.zeros(nb * 256 + 4, dtype=torch.float32, device="cuda")
     _lib.check("launch_dequant_q4k", L.launch_dequant_q4k(ptr(qt), nb, ptr(out) + 4))
-    got = host(out)[1:]
-    assert np.array_equal(got.view(np.uint32), orc.dequantize(q).view(np.uint32))
+    got = host(out)
+    assert np.all(got[0] == 0) and np.all(got[1 + nb * 256:] == 0)  # nothing outside
+    assert np.array_equal(got[1:1 + nb * 256].view(np.uint32), orc.dequantize(q).view(np.uint32))
 
 
 # --------------------------------------------------------------------- GEMV --
