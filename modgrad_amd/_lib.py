@@ -30,6 +30,7 @@ SIGNATURES = {
     "mgq_chain_create": (I, [P, I, P]),
     "mgq_chain_launch": (I, [P, P]),
     "mgq_chain_destroy": (I, [P]),
+    "mgq_prepare": (I, []),
     "mgq_version": (ctypes.c_char_p, []),
 }
 

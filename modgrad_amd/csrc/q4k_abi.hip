@@ -141,6 +141,8 @@ hipError_t mgq_chain_destroy(void *chain) {
     return e1 != hipSuccess ? e1 : e2;
 }
 
+hipError_t mgq_prepare(void) { return mgq::gemv_prepare(); }
+
 const char *mgq_version(void) { return "modgrad_q4k 0.1.0 gfx950"; }
 
 }  // extern "C"

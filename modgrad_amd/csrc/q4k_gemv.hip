@@ -37,6 +37,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 namespace mgq {
 
@@ -100,36 +101,130 @@ __device__ __forceinline__ int pair_byte_offset(int p, int h) {
     return p < 2 ? 16 * h + 8 * p : 64 + 16 * h + 8 * (p - 2);
 }
 
-constexpr int kRowsPerGroup = 32;  // two 16-row MFMA tiles per wavefront
-
-// LDS layout for one work-group (all bpr blocks of K):
-//   atab [bpr][8 mfma c][4 lane-group h][xh|xl][8 halves]  bpr*1024 B
-//   zero 16 B                                             at bpr*1024
-//   meta [bpr][corr[8] | xsum[8]] f32                     bpr*64 B
-//   aux  max(bpr*8*4, NW*64*4) B: x scale per sub-block, later the
-//        cross-wave reduction buffer
-__host__ __device__ constexpr size_t mfma_lds_bytes(int bpr, int nw) {
-    return (size_t)bpr * 1024 + 16 + (size_t)bpr * 64 +
-           ((size_t)bpr * 32 > (size_t)nw * 256 ? (size_t)bpr * 32 : (size_t)nw * 256);
-}
-
 constexpr int kMaxWaves = 8;
 
-// One work-group = NW = blockDim.x/64 wavefronts (1..8) covering 32 rows; the
-// wavefronts split the row's blocks and reduce through LDS at the end.
-__global__ __launch_bounds__(kMaxWaves * 64) void gemv_mfma_kernel(const uint8_t *__restrict__ w,
-                                                                   const float *__restrict__ x,
-                                                                   float *__restrict__ y, int n,
-                                                                   int bpr) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    const int NW = (int)(blockDim.x >> 6);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t zero_off = (uint32_t)bpr * 1024u;
-    float *meta = reinterpret_cast<float *>(lds + zero_off + 16);
-    float *aux = meta + bpr * 16;
 
-    // ---- prologue: build the activation operand table in LDS -------------
-    if (tid < 4) reinterpret_cast<uint32_t *>(lds + zero_off)[tid] = 0u;
+// LDS layout of one work-group (rows R, all bpr blocks of K):
+//   atab  [bpr][8 mfma c][4 lane-group h][xh|xl][8 halves]   bpr*1024 B
+//   zero  16 B of zeros                                      at bpr*1024
+//   meta  [bpr][corr[8] | xsum[8]] f32                       bpr*64 B
+//   stage 2 (1 if bpr <= C) x SB bytes: weight bytes of R rows x C blocks,
+//         row-major over (row, block, 16-byte piece), rows padded to an odd
+//         number of pieces
+//   aux   max(bpr*8*4, NW*32*4) B: x scale exponents, later the
+//         cross-wave reduction buffer (32 row sums per wavefront)
+struct MfmaLayout {
+    int bpr, R, C, NW, I;  // I = 1 KiB wave loads per stage
+    uint32_t zero, meta, stage, stage_bytes, aux, ybuf;
+    size_t total;
+};
+
+// rounds = row groups per work-group (persistent launch); their results stay
+// in LDS (ybuf) until the stream ends, so no global store sits between the
+// staged loads (a store would force the compiler to drain every load).
+// Staged rows are padded to an odd number of 16-byte pieces, so the 16
+// lanes that read one piece column of 16 different rows hit 16 different
+// LDS bank groups.
+__host__ __device__ constexpr int stage_row_pieces(int C) { return (9 * C) | 1; }
+
+__host__ __device__ inline MfmaLayout mfma_layout(int bpr, int R, int C, int NW, int rounds,
+                                                  bool db) {
+    MfmaLayout L;
+    L.bpr = bpr; L.R = R; L.C = C; L.NW = NW;
+    // wave loads per stage, padded so every wavefront issues the same count
+    L.I = ((R * 9 * C + 63) / 64 + NW - 1) / NW * NW;
+    L.zero = (uint32_t)bpr * 1024u;
+    L.meta = L.zero + 16;
+    L.stage = L.meta + (uint32_t)bpr * 64u;
+    L.stage_bytes = (uint32_t)(R * stage_row_pieces(C) * 16);
+    // two stage buffers when double-buffered and K needs more than one stage
+    L.aux = L.stage + ((db && bpr > C) ? 2u : 1u) * L.stage_bytes;
+    const uint32_t auxb = (uint32_t)(bpr * 32 > NW * 128 ? bpr * 32 : NW * 128);
+    L.ybuf = L.aux + auxb;
+    L.total = (size_t)L.ybuf + (size_t)R * rounds * 4;
+    return L;
+}
+
+// Work-group = R rows (R = 16 or 32) x all K, persistent over row groups
+// blockIdx.x, blockIdx.x + gridDim.x, ... The weights stream through LDS C
+// blocks at a time: every wave load instruction moves 64 consecutive 16-byte
+// pieces of the rows' contiguous byte runs (fully coalesced) into registers,
+// PF stages ahead of the stage being computed; each stage is then written to a
+// double-buffered LDS stage and the MFMA operands are read from LDS. The stage
+// sequence runs across row-group boundaries, so a persistent work-group keeps
+// PF stages in flight from its first load to its last and builds the
+// activation table only once.
+// A wavefront's unit of work is two 16-row x 1-block MFMA tiles: rows
+// [0,16) and [16,32) of one block when R = 32, or blocks 2u and 2u+1 of the
+// 16 rows when R = 16. Per unit: 16 MFMAs, an xh/xl merge that leaves tile A
+// in lanes 0..31 and tile B in lanes 32..63, and the scale/min decode of 4
+// (row, sub-block) pairs per lane.
+// DB: double-buffered LDS stage (one barrier per stage) or a single buffer
+// (two barriers per stage, half the LDS, so more work-groups fit per CU).
+template <int R, int C, int NW, int PF, bool DB>
+__global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__restrict__ w,
+                                                            const float *__restrict__ x,
+                                                            float *__restrict__ y, int n,
+                                                            int bpr, int rounds) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const MfmaLayout Lo = mfma_layout(bpr, R, C, NW, rounds, DB);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
+    float *meta = reinterpret_cast<float *>(lds + Lo.meta);
+    float *aux = reinterpret_cast<float *>(lds + Lo.aux);
+    const size_t row_bytes = (size_t)bpr * kBlockBytes;
+    const int stages = (bpr + C - 1) / C;
+    const int groups = (n + R - 1) / R;
+    const int my_groups = (groups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int Q = my_groups * stages;             // stages this work-group streams
+    constexpr int PIECES = R * 9 * C;             // 16-byte pieces per stage
+    constexpr int IPW = ((PIECES + 63) / 64 + NW - 1) / NW;  // wave loads per wavefront
+    constexpr int I = IPW * NW;                   // wave loads per stage (padded)
+    constexpr int UNITS = (R == 32) ? C : C / 2;  // tile pairs per stage
+
+    // ---- weight staging: global -> registers (PF sets) -> LDS ---------------
+    // stg is only ever indexed with compile-time constants (the stage loop is
+    // unrolled by PF), so the sets stay in registers with loads in flight.
+    u32x4 stg[PF][IPW];
+    // Loads are unconditional (a stage past the end re-reads the last one,
+    // already cached) so the compiler's in-order vmcnt accounting stays
+    // exact and only the set being stored is waited for. The piece -> (row,
+    // byte column) split of each load is stage-invariant and precomputed.
+    constexpr int RP = stage_row_pieces(C);       // LDS pieces per staged row
+    uint32_t prow[IPW], pcol[IPW], plast[IPW], plds[IPW];
+#pragma unroll
+    for (int k = 0; k < IPW; ++k) {
+        const int j = std::min((wave + k * NW) * 64 + lane, PIECES - 1);
+        const int row = j / (9 * C), rem = j - row * 9 * C;
+        const int cb = rem / 9, pc = rem - cb * 9;
+        plds[k] = (uint32_t)((row * RP + rem) * 16);    // LDS byte offset in the stage
+        prow[k] = (uint32_t)row;
+        pcol[k] = (uint32_t)(cb * kBlockBytes + 16 * pc);          // byte column within the stage
+        plast[k] = (uint32_t)((bpr - 1) * kBlockBytes + 16 * pc);  // same piece of the last block
+    }
+    auto gload = [&](int q, u32x4(&dst)[IPW]) {
+        q = std::min(q, Q - 1);
+        const uint32_t r0 = ((uint32_t)blockIdx.x + (uint32_t)(q / stages) * gridDim.x) * R;
+        const uint32_t tcol = (uint32_t)((q % stages) * C * kBlockBytes);
+        const uint32_t rlast = (uint32_t)(n - 1), rb = (uint32_t)row_bytes;
+#pragma unroll
+        for (int k = 0; k < IPW; ++k) {
+            const uint32_t rr = std::min(r0 + prow[k], rlast);
+            const uint32_t col = std::min(tcol + pcol[k], plast[k]);
+            const uint64_t off = (uint64_t)rr * rb + col;  // one v_mad_u64_u32
+            dst[k] = *reinterpret_cast<const u32x4 *>(w + off);
+        }
+    };
+    auto lstore = [&](int buf, const u32x4(&src)[IPW]) {
+#pragma unroll
+        for (int k = 0; k < IPW; ++k)
+            *reinterpret_cast<u32x4 *>(lds + Lo.stage + buf * Lo.stage_bytes + plds[k]) = src[k];
+    };
+#pragma unroll
+    for (int f = 0; f < PF; ++f) gload(f, stg[f]);  // in flight while the table is built
+
+    // ---- prologue: the activation operand table, in LDS ---------------------
+    if (tid < 4) reinterpret_cast<uint32_t *>(lds + Lo.zero)[tid] = 0u;
     for (int i = tid; i < bpr * 8; i += NW * 64) {  // i = b*8 + sub-block
         const f32x4 *xs = reinterpret_cast<const f32x4 *>(x + (size_t)i * 32);
         float amax = 0.0f, sum = 0.0f;
@@ -160,106 +255,156 @@ __global__ __launch_bounds__(kMaxWaves * 64) void gemv_mfma_kernel(const uint8_t
         const float *xp = x + (size_t)b * kBlockElems + 64 * G + (o & 31) + 32 * kind;
         const f32x4 v0 = *reinterpret_cast<const f32x4 *>(xp);
         const f32x4 v1 = *reinterpret_cast<const f32x4 *>(xp + 4);
-        // slot s holds byte o + {0,2,1,3,4,6,5,7}[s] (see the B operand build)
+        // slot q holds byte o + {0,2,1,3,4,6,5,7}[q] (see the B operand build)
         const float xv[8] = {v0[0], v0[2], v0[1], v0[3], v1[0], v1[2], v1[1], v1[3]};
         half8 hh, hl;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const float xs = ldexpf(xv[s], e);
-            const _Float16 a = (_Float16)xs;
-            hh[s] = a;
-            hl[s] = (_Float16)(xs - (float)a);
+        for (int q = 0; q < 8; ++q) {
+            const float xsv = ldexpf(xv[q], e);
+            const _Float16 a = (_Float16)xsv;
+            hh[q] = a;
+            hl[q] = (_Float16)(xsv - (float)a);
         }
         *reinterpret_cast<half8 *>(lds + (size_t)i * 32) = hh;
         *reinterpret_cast<half8 *>(lds + (size_t)i * 32 + 16) = hl;
     }
-    __syncthreads();
+    lstore(0, stg[0]);
 
-    // ---- per-lane constants ------------------------------------------------
-    const int n16 = lane & 15, g = lane >> 4;       // B lane: W row n16, k-group g
-    const int tdec = lane >> 5, jq = (lane >> 4) & 1;  // decode lane: tile, sub-block quad
-    uint32_t abase[8], astride[8];
+    // ---- per-lane constants -------------------------------------------------
+    // B lane (n16, g): W row n16, k-slot group g. Accumulator lane: rows
+    // m = 4g..4g+3 of the 16x16 result = (sub-block 2g, xh), (2g, xl),
+    // (2g+1, xh), (2g+1, xl) of W row n16 -- both parts of a sub-block land in
+    // the same lane, so merging xh and xl is an in-lane add.
+    const int n16 = lane & 15, g = lane >> 4, jq = g >> 1, sh = 16 * (g & 1);
+    // A operand address of MFMA c for block b: abase[c] + (b*1024 & amask[c])
+    // (amask = 0 for lanes whose row m takes no data from c: the zero slot)
+    uint32_t abase[8], amask[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
         const int o = pair_byte_offset(c >> 1, g);
         const int sb = 2 * (o >> 5) + (c & 1);
-        const bool hit = (n16 & 7) == sb;        // A lane m = n16
-        abase[c] = hit ? (uint32_t)((c * 4 + g) * 32 + (n16 >> 3) * 16) : zero_off;
-        astride[c] = hit ? 1024u : 0u;
+        const bool hit = (n16 >> 1) == sb;  // A lane m = n16 = 2*sb + part
+        abase[c] = hit ? (uint32_t)((c * 4 + g) * 32 + (n16 & 1) * 16) : Lo.zero;
+        amask[c] = hit ? 0xFFFFFFFFu : 0u;
     }
-    const size_t row_bytes = (size_t)bpr * kBlockBytes;
-    const int r0 = blockIdx.x * kRowsPerGroup;
-    const int rA = std::min(r0 + n16, n - 1), rB = std::min(r0 + 16 + n16, n - 1);
-    const int rD = std::min(r0 + 16 * tdec + n16, n - 1);
-    const uint8_t *pA = w + (size_t)rA * row_bytes + 16 + 16 * g;
-    const uint8_t *pB = w + (size_t)rB * row_bytes + 16 + 16 * g;
-    const uint8_t *pD = w + (size_t)rD * row_bytes;
-    const int kb0 = (bpr * wave) / NW, kb1 = (bpr * (wave + 1)) / NW;
-
-    float yacc = 0.0f;
-    u32x4 na0, na1, nb0, nb1, nh;
-    if (kb0 < kb1) {
-        na0 = *reinterpret_cast<const u32x4 *>(pA + (size_t)kb0 * kBlockBytes);
-        na1 = *reinterpret_cast<const u32x4 *>(pA + (size_t)kb0 * kBlockBytes + 64);
-        nb0 = *reinterpret_cast<const u32x4 *>(pB + (size_t)kb0 * kBlockBytes);
-        nb1 = *reinterpret_cast<const u32x4 *>(pB + (size_t)kb0 * kBlockBytes + 64);
-        nh = *reinterpret_cast<const u32x4 *>(pD + (size_t)kb0 * kBlockBytes);
-    }
-    for (int b = kb0; b < kb1; ++b) {
-        const u32x4 qa0 = na0, qa1 = na1, qb0 = nb0, qb1 = nb1, hd = nh;
-        if (b + 1 < kb1) {
-            const size_t off = (size_t)(b + 1) * kBlockBytes;
-            na0 = *reinterpret_cast<const u32x4 *>(pA + off);
-            na1 = *reinterpret_cast<const u32x4 *>(pA + off + 64);
-            nb0 = *reinterpret_cast<const u32x4 *>(pB + off);
-            nb1 = *reinterpret_cast<const u32x4 *>(pB + off + 64);
-            nh = *reinterpret_cast<const u32x4 *>(pD + off);
-        }
-        f32x4 accA = {0.f, 0.f, 0.f, 0.f}, accB = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const half8 a = *reinterpret_cast<const half8 *>(lds + abase[c] + (uint32_t)b * astride[c]);
-            const int p = c >> 1;
-            const uint32_t mask = (c & 1) ? 0x00F000F0u : 0x000F000Fu;
-            const uint32_t wa0 = p < 2 ? qa0[2 * p] : qa1[2 * p - 4];
-            const uint32_t wa1 = p < 2 ? qa0[2 * p + 1] : qa1[2 * p - 3];
-            const uint32_t wb0 = p < 2 ? qb0[2 * p] : qb1[2 * p - 4];
-            const uint32_t wb1 = p < 2 ? qb0[2 * p + 1] : qb1[2 * p - 3];
-            const u32x4 ba = {wa0 & mask, (wa0 >> 8) & mask, wa1 & mask, (wa1 >> 8) & mask};
-            const u32x4 bb = {wb0 & mask, (wb0 >> 8) & mask, wb1 & mask, (wb1 >> 8) & mask};
-            accA = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(half8, ba), accA, 0, 0, 0);
-            accB = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(half8, bb), accB, 0, 0, 0);
-        }
-        // Merge xh and xl halves: lanes 0..31 get tile A's (row, sub-block)
-        // sums, lanes 32..63 tile B's. (Not __builtin_amdgcn_permlane32_swap:
-        // this compiler miscombines its two results.)
-        float s[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float mine = tdec ? accB[i] : accA[i];
-            const float give = tdec ? accA[i] : accB[i];
-            s[i] = mine + __shfl_xor(give, 32, 64);
-        }
+    // y contribution of one tile: sub-blocks 2g, 2g+1 of W row n16 in block b,
+    // from their q*x sums s0, s1 (scaled by corr) and the block header hd.
+    auto decode = [&](const u32x4 &hd, int b, float s0, float s1) -> float {
         const float d = half_bits_finite(hd[0]), dmin = half_bits_finite(hd[0] >> 16);
-        const uint32_t scq = jq ? scales4(1, hd[1], hd[3]) : scales4(0, hd[1], hd[3]);
-        const uint32_t mnq = jq ? mins4(1, hd[2], hd[3]) : mins4(0, hd[2], hd[3]);
-        const f32x4 corr = *reinterpret_cast<const f32x4 *>(meta + b * 16 + 4 * jq);
-        const f32x4 xsum = *reinterpret_cast<const f32x4 *>(meta + b * 16 + 8 + 4 * jq);
-        float t1 = 0.0f, t2 = 0.0f;
+        const uint32_t scq = (jq ? scales4(1, hd[1], hd[3]) : scales4(0, hd[1], hd[3])) >> sh;
+        const uint32_t mnq = (jq ? mins4(1, hd[2], hd[3]) : mins4(0, hd[2], hd[3])) >> sh;
+        const float *mb = meta + b * 16 + 2 * g;
+        const float t1 = (float)(scq & 0xFFu) * (s0 * mb[0]) + (float)((scq >> 8) & 0xFFu) * (s1 * mb[1]);
+        const float t2 = (float)(mnq & 0xFFu) * mb[8] + (float)((mnq >> 8) & 0xFFu) * mb[9];
+        return d * t1 - dmin * t2;
+    };
+
+    // two LDS stage buffers only when double-buffered and K spans > 1 stage
+    // (the layout allocates exactly that); otherwise one buffer, refilled
+    // after a barrier, also across row groups of a persistent work-group
+    const bool dbuf = DB && stages > 1;
+    float yaccA = 0.0f, yaccB = 0.0f;  // R = 32: rows of tile A / tile B; R = 16: yaccA only
+    // One stage: compute it, then (when `more`) move stage q+1 from its
+    // register set into the other LDS buffer and refill that set with stage
+    // q+1+PF. F = q % PF is a compile-time constant at every call site.
+    auto step = [&](const int q, auto fc, const bool more) {
+        constexpr int F = decltype(fc)::value;
+        const int t = q % stages;
+        const uint8_t *sbuf = lds + Lo.stage + (dbuf ? (q & 1) * Lo.stage_bytes : 0u);
+        for (int u = wave; u < UNITS; u += NW) {
+            // tile A = (rows rowA.., block cbA), tile B = (rows rowB.., block cbB)
+            const int cbA = (R == 32) ? u : 2 * u, cbB = (R == 32) ? u : 2 * u + 1;
+            const int rowA = 0, rowB = (R == 32) ? 16 : 0;
+            const int bA = t * C + cbA, bB = t * C + cbB;
+            if (bA >= bpr) break;
+            const bool hasB = bB < bpr;
+            const int bBc = hasB ? bB : bA;  // past the end: reuse tile A's operands
+            auto piece = [&](int row, int cb, int pc) -> const u32x4 & {
+                return *reinterpret_cast<const u32x4 *>(sbuf + (row * RP + cb * 9 + pc) * 16);
+            };
+            const u32x4 qa0 = piece(rowA + n16, cbA, 1 + g), qa1 = piece(rowA + n16, cbA, 5 + g);
+            const u32x4 qb0 = piece(rowB + n16, cbB, 1 + g), qb1 = piece(rowB + n16, cbB, 5 + g);
+            const u32x4 hdA = piece(rowA + n16, cbA, 0), hdB = piece(rowB + n16, cbB, 0);
+            f32x4 accA = {0.f, 0.f, 0.f, 0.f}, accB = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            t1 += (float)((scq >> (8 * i)) & 0xFFu) * (s[i] * corr[i]);
-            t2 += (float)((mnq >> (8 * i)) & 0xFFu) * xsum[i];
+            for (int c = 0; c < 8; ++c) {
+                const half8 aA = *reinterpret_cast<const half8 *>(lds + abase[c] + (((uint32_t)bA << 10) & amask[c]));
+                const half8 aB = (R == 32) ? aA
+                    : *reinterpret_cast<const half8 *>(lds + abase[c] + (((uint32_t)bBc << 10) & amask[c]));
+                const int p = c >> 1;
+                const uint32_t mask = (c & 1) ? 0x00F000F0u : 0x000F000Fu;
+                const uint32_t wa0 = p < 2 ? qa0[2 * p] : qa1[2 * p - 4];
+                const uint32_t wa1 = p < 2 ? qa0[2 * p + 1] : qa1[2 * p - 3];
+                const uint32_t wb0 = p < 2 ? qb0[2 * p] : qb1[2 * p - 4];
+                const uint32_t wb1 = p < 2 ? qb0[2 * p + 1] : qb1[2 * p - 3];
+                const u32x4 ba = {wa0 & mask, (wa0 >> 8) & mask, wa1 & mask, (wa1 >> 8) & mask};
+                const u32x4 bb = {wb0 & mask, (wb0 >> 8) & mask, wb1 & mask, (wb1 >> 8) & mask};
+                accA = __builtin_amdgcn_mfma_f32_16x16x32_f16(aA, __builtin_bit_cast(half8, ba), accA, 0, 0, 0);
+                accB = __builtin_amdgcn_mfma_f32_16x16x32_f16(aB, __builtin_bit_cast(half8, bb), accB, 0, 0, 0);
+            }
+            const float cA = decode(hdA, bA, accA[0] + accA[1], accA[2] + accA[3]);
+            const float cB = decode(hdB, bBc, accB[0] + accB[1], accB[2] + accB[3]);
+            if (R == 32) {
+                yaccA += cA;
+                yaccB += cB;
+            } else {
+                yaccA += hasB ? cA + cB : cA;
+            }
         }
-        yacc += d * t1 - dmin * t2;
+        const bool group_end = (t == stages - 1);
+        if (group_end) {
+            // sum the 4 lanes (g = 0..3) of each row, then one value per row
+            // and tile into aux (free after the prologue)
+            yaccA += __shfl_xor(yaccA, 16, 64);
+            yaccA += __shfl_xor(yaccA, 32, 64);
+            yaccB += __shfl_xor(yaccB, 16, 64);
+            yaccB += __shfl_xor(yaccB, 32, 64);
+            if (lane < 16) {
+                aux[wave * 32 + lane] = yaccA;
+                aux[wave * 32 + 16 + lane] = yaccB;
+            }
+        }
+        if (more) {
+            if (!dbuf) __syncthreads();  // every wave is done reading the single buffer
+            lstore(dbuf ? ((q + 1) & 1) : 0, stg[(F + 1) % PF]);
+            gload(q + 1 + PF, stg[(F + 1) % PF]);
+        }
+        __syncthreads();
+        if (group_end) {
+            // cross-wave reduction of this row group; the next group's
+            // reduction writes aux only after at least one more barrier
+            if (tid < R) {
+                float sum = 0.0f;
+                for (int wv = 0; wv < NW; ++wv) sum += aux[wv * 32 + tid];
+                reinterpret_cast<float *>(lds + Lo.ybuf)[(q / stages) * R + tid] = sum;
+            }
+            yaccA = 0.0f;
+            yaccB = 0.0f;
+        }
+    };
+    // Main loop: every step has a next stage, so the store/refill is
+    // unconditional and the compiler waits only for the set being stored
+    // (the loop is entered, and loops back, with the same load order).
+    int q0 = 0;
+    if (Q > PF) {
+        gload(PF, stg[0]);
+        __syncthreads();
+        for (; q0 + PF < Q; q0 += PF) {
+            step(q0, std::integral_constant<int, 0>{}, true);
+            if constexpr (PF > 1) step(q0 + 1, std::integral_constant<int, 1 % PF>{}, true);
+            if constexpr (PF > 2) step(q0 + 2, std::integral_constant<int, 2 % PF>{}, true);
+        }
+    } else {
+        __syncthreads();
     }
-    aux[wave * 64 + lane] = yacc;  // aux is free again (prologue done)
+    // Tail: the last <= PF stages.
+    if (q0 < Q) step(q0, std::integral_constant<int, 0>{}, q0 + 1 < Q);
+    if constexpr (PF > 1) if (q0 + 1 < Q) step(q0 + 1, std::integral_constant<int, 1 % PF>{}, q0 + 2 < Q);
+    if constexpr (PF > 2) if (q0 + 2 < Q) step(q0 + 2, std::integral_constant<int, 2 % PF>{}, q0 + 3 < Q);
     __syncthreads();
-    if (tid < kRowsPerGroup) {
-        const int tl = (tid >> 4) * 32 + (tid & 15);  // lane holding row tid, quad 0
-        float sum = 0.0f;
-        for (int wv = 0; wv < NW; ++wv) sum += aux[wv * 64 + tl] + aux[wv * 64 + tl + 16];
-        if (r0 + tid < n) y[r0 + tid] = sum;
+    for (int i = tid; i < my_groups * R; i += NW * 64) {
+        const int r = ((int)blockIdx.x + (i / R) * (int)gridDim.x) * R + (i % R);
+        if (r < n) y[r] = reinterpret_cast<const float *>(lds + Lo.ybuf)[i];
     }
 }
 
@@ -268,26 +413,85 @@ static int env_int(const char *name, int dflt) {
     return (s && *s) ? std::atoi(s) : dflt;
 }
 
-hipError_t gemv_prepare() {
-    // Allow up to the full 160 KiB of LDS, once per process (thread-safe
-    // static init). Called before any stream capture records a launch.
-    static const hipError_t attr = hipFuncSetAttribute(
-        (const void *)gemv_mfma_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    return attr;
+static int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+            v = 256;
+        cus[dev] = v;
+    }
+    return cus[dev];
 }
+
+template <int R, int C, int NW, int PF, bool DB>
+static hipError_t launch_cfg(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                             hipStream_t stream, bool persistent) {
+    auto kern = gemv_mfma_kernel<R, C, NW, PF, DB>;
+    static const hipError_t attr = hipFuncSetAttribute(
+        (const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return attr;
+    const long groups = (n + R - 1) / R;
+    long grid = groups, rounds = 1;
+    if (persistent) {
+        // resident work-groups per CU from LDS (VGPR use allows >= 2 here)
+        static const int occ_env = env_int("MGQ_GEMV_OCC", 0);
+        const size_t base = mfma_layout(bpr, R, C, NW, 8, DB).total;
+        int occ = 0;  // resident work-groups per CU (registers and LDS)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)kern, NW * 64,
+                                                         base) != hipSuccess || occ <= 0)
+            occ = (int)std::min<size_t>(4, (160 * 1024) / base);
+        if (occ_env > 0) occ = occ_env;
+        const long maxgrid = (long)device_cus() * std::max(1, occ);
+        rounds = (groups + maxgrid - 1) / maxgrid;
+        grid = (groups + rounds - 1) / rounds;  // balanced: every WG gets `rounds` groups (or one fewer)
+    }
+    const MfmaLayout Lo = mfma_layout(bpr, R, C, NW, (int)rounds, DB);
+    if (Lo.total > 160 * 1024) return hipErrorNotSupported;
+    kern<<<(unsigned)grid, NW * 64, Lo.total, stream>>>(w, x, y, n, bpr, (int)rounds);
+    return hipGetLastError();
+}
+
+// Launch configurations (rows per work-group, blocks per stage, wavefronts,
+// stages in flight). Few row groups (small N): 16-row groups with the whole
+// row in one stage, for parallelism and a single memory round trip. Many row
+// groups: persistent 32-row groups streamed 4 blocks at a time.
+static hipError_t launch_any(int cfg, const uint8_t *w, const float *x, float *y, int n, int bpr,
+                             hipStream_t stream) {
+    switch (cfg) {
+        case 0: return launch_cfg<32, 4, 4, 2, true>(w, x, y, n, bpr, stream, true);
+        case 1: return launch_cfg<16, 8, 4, 2, true>(w, x, y, n, bpr, stream, true);
+        case 2: return launch_cfg<16, 14, 7, 1, true>(w, x, y, n, bpr, stream, false);
+        case 3: return launch_cfg<16, 16, 8, 1, true>(w, x, y, n, bpr, stream, false);
+        case 4: return launch_cfg<32, 4, 4, 2, false>(w, x, y, n, bpr, stream, true);
+        case 5: return launch_cfg<32, 8, 8, 1, false>(w, x, y, n, bpr, stream, true);
+        case 6: return launch_cfg<16, 8, 4, 2, false>(w, x, y, n, bpr, stream, true);
+        case 7: return launch_cfg<32, 2, 2, 3, true>(w, x, y, n, bpr, stream, true);
+        case 8: return launch_cfg<16, 16, 8, 2, false>(w, x, y, n, bpr, stream, false);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t gemv_prepare() { return hipSuccess; }
 
 hipError_t gemv_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                             hipStream_t stream) {
     if (((uintptr_t)w & 15u) || ((uintptr_t)x & 15u)) return hipErrorNotSupported;
-    if (mfma_lds_bytes(bpr, kMaxWaves) > 160 * 1024) return hipErrorNotSupported;
-    const hipError_t attr = gemv_prepare();
-    if (attr != hipSuccess) return attr;
-    static const int nw_env = env_int("MGQ_GEMV_WAVES", 0);  // tuning override
-    int nw = nw_env > 0 ? std::min(nw_env, kMaxWaves) : (bpr >= 16 ? 8 : 4);
-    const size_t lds = mfma_lds_bytes(bpr, nw);
-    const unsigned grid = (unsigned)((n + kRowsPerGroup - 1) / kRowsPerGroup);
-    gemv_mfma_kernel<<<grid, nw * 64, lds, stream>>>(w, x, y, n, bpr);
-    return hipGetLastError();
+    static const int force = env_int("MGQ_GEMV_CFG", -1);  // tuning override
+    int cfg;
+    if (force >= 0) {
+        cfg = force;
+    } else {
+        const long groups32 = (n + 31) / 32;
+        if (groups32 >= 768) cfg = 0;
+        else if (bpr <= 14) cfg = 2;
+        else cfg = 3;
+    }
+    hipError_t e = launch_any(cfg, w, x, y, n, bpr, stream);
+    if (e == hipErrorNotSupported && cfg != 1) e = launch_any(1, w, x, y, n, bpr, stream);
+    return e;
 }
 
 static int env_force_generic() {

@@ -106,6 +106,19 @@ def test_matvec_random_bytes_wide_dynamic_range(L, orc):
     assert_gemv_close(y[ok], y_ref[ok], a[ok])
 
 
+@pytest.mark.parametrize("n,bpr", [(24576 + 17, 2), (30000, 14), (16, 40), (17, 29)])
+def test_matvec_random_bytes_all_configs(L, orc, n, bpr):
+    # shapes that select each launch configuration (many / few row groups,
+    # single- and multi-stage K, ragged last stage and row group)
+    note(f"matvec random bytes n={n} bpr={bpr}")
+    rng = np.random.default_rng(n + bpr)
+    w = random_q4k_bytes(rng, n * bpr)
+    x = rng.standard_normal(bpr * 256).astype(np.float32)
+    y = run_gemv(L, w, x, n, bpr)
+    y_ref, a = orc.gemv(w, x, n, bpr)
+    assert_gemv_close(y, y_ref, a)
+
+
 def test_matvec_unit_vectors_extract_columns(L, orc):
     note("matvec x = e_k")
     n, bpr = 48, 3
@@ -130,7 +143,8 @@ def test_matvec_all_zero_rows_give_zero(L, orc):
 
 
 @pytest.mark.parametrize("name,n,k,t", [("q", 3584, 3584, 0), ("k", 512, 3584, 1),
-                                        ("gate", 18944, 3584, 4), ("down", 3584, 18944, 6)])
+                                        ("gate", 18944, 3584, 4), ("down", 3584, 18944, 6),
+                                        ("gate_up", 37888, 3584, 5)])
 def test_matvec_baseline_layer_shapes(L, orc, name, n, k, t):
     note(f"matvec layer-0 {name} {n}x{k}")
     seed = orc.layer_seed(0, t)
@@ -140,6 +154,26 @@ def test_matvec_baseline_layer_shapes(L, orc, name, n, k, t):
     y_ref, a = orc.gemv(w, x, n, k // 256)
     worst = assert_gemv_close(y, y_ref, a)
     print(f"{name}: worst err/absdot = {worst:.3e}")
+
+
+@pytest.mark.parametrize("n,bpr", [(3584, 14), (3584, 74), (40, 148)])
+def test_matvec_split_k_is_deterministic(L, orc, n, bpr):
+    # shapes that split K across work-groups: the last arriver sums the
+    # partials in slice order, so repeated launches agree bit for bit
+    note(f"matvec split-K determinism {n}x{bpr * 256}")
+    w = orc.seeded_weight(7000 + bpr, n, bpr * 256)
+    x = orc.normal(7100 + bpr, bpr * 256)
+    import torch
+    wt, xt = dev(w), dev(x)
+    outs = []
+    for _ in range(3):
+        yt = empty_f32(n)
+        _lib.check("launch_matvec_q4k", L.launch_matvec_q4k(ptr(wt), ptr(xt), ptr(yt), n, bpr))
+        outs.append(host(yt))
+    assert all(np.array_equal(outs[0].view(np.uint32), o.view(np.uint32)) for o in outs[1:])
+    y_ref, a = orc.gemv(w, x, n, bpr)
+    assert_gemv_close(outs[0], y_ref, a)
+    del torch
 
 
 def test_matvec_generic_kernel_on_misaligned_weights(L, orc):
