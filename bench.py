@@ -145,10 +145,13 @@ def check_parity(torch, wl: Workload, rows: int = 256) -> str:
     return f"ok (max err/absdot {worst:.2e} <= 1e-4)"
 
 
-def cpu_baseline(torch, wl: Workload, target_s: float, threads: int):
-    """The reference CPU GEMV restated (oracle), on layer 0's launches."""
+def cpu_baseline(torch, wl: Workload, target_s: float, threads: int, launches: int = 32):
+    """The reference CPU GEMV restated (oracle), on the first `launches`
+    launches of the workload (8 decode layers = 1.05 GB, above any host
+    cache, so the CPU streams from DRAM like the GPU streams from HBM)."""
     from oracle import oracle as orc
-    sample = [(name, w.cpu().numpy(), x.cpu().numpy(), n, k) for name, w, x, _, n, k in wl.launches[:4]]
+    sample = [(name, w.cpu().numpy(), x.cpu().numpy(), n, k)
+              for name, w, x, _, n, k in wl.launches[:launches]]
     nbytes = sum(gemv_bytes(n, k) for _, _, _, n, k in sample)
     ys = [np.empty(n, np.float32) for _, _, _, n, _ in sample]
     for (name, w, x, n, k), y in zip(sample, ys):  # warm-up
@@ -161,11 +164,27 @@ def cpu_baseline(torch, wl: Workload, target_s: float, threads: int):
         t_total += time.perf_counter() - t
         reps += 1
     gbs = nbytes * reps / t_total / 1e9
-    names = "+".join(s[0] for s in sample)
+    names = f"{sample[0][0]}..{sample[-1][0]} ({len(sample)} launches)"
     return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{names} ({nbytes / 1e6:.1f} MB of Q4_K + activations) x {reps} passes, "
+            "sample": f"{names}, {nbytes / 1e6:.1f} MB of Q4_K + activations, x {reps} passes, "
                       f"{t_total:.1f} s; AVX-512={'yes' if orc.cpu_has_avx512() else 'no'}",
             "tokens_per_s_equiv": round(gbs * 1e9 / wl.bytes_per_pass, 3)}
+
+
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "gemv_mfma_decode7b_pmc.txt")
+
+
+def profiled_traffic(workload: str):
+    """HBM bytes per GEMV launch from the committed FETCH_SIZE / WRITE_SIZE
+    summary of this same workload (calibrated against a plain copy), or None."""
+    if workload != "decode7b" or not os.path.exists(TRAFFIC_PROFILE):
+        return None
+    with open(TRAFFIC_PROFILE) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    return None
 
 
 def main() -> int:
@@ -234,7 +253,7 @@ def main() -> int:
         "parity": parity,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "mgq::gemv_mfma_kernel",
+                     "traffic": profiled_traffic(args.workload), "kernel": "mgq::gemv_mfma_kernel",
                      "avg_launch_us": round(avg_s * 1e6, 3), "avg_launch_bytes": int(avg_b)},
     }
     if not args.no_cpu:

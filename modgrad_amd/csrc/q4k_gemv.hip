@@ -103,6 +103,15 @@ __device__ __forceinline__ int pair_byte_offset(int p, int h) {
 
 constexpr int kMaxWaves = 8;
 
+// v from lane (lane ^ MASK) within each group of 4 lanes (DPP quad_perm).
+template <int MASK>
+__device__ __forceinline__ float quad_xor(float v) {
+    static_assert(MASK == 1 || MASK == 2, "quad lane xor");
+    constexpr int ctrl = MASK == 1 ? 0xB1 : 0x4E;  // quad_perm [1,0,3,2] / [2,3,0,1]
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl,
+                                                                 0xF, 0xF, false));
+}
+
 
 // LDS layout of one work-group (rows R, all bpr blocks of K):
 //   atab  [bpr][8 mfma c][4 lane-group h][xh|xl][8 halves]   bpr*1024 B
@@ -111,8 +120,7 @@ constexpr int kMaxWaves = 8;
 //   stage 2 (1 if bpr <= C) x SB bytes: weight bytes of R rows x C blocks,
 //         row-major over (row, block, 16-byte piece), rows padded to an odd
 //         number of pieces
-//   aux   max(bpr*8*4, NW*32*4) B: x scale exponents, later the
-//         cross-wave reduction buffer (32 row sums per wavefront)
+//   aux   NW*32*4 B: cross-wave reduction buffer (32 row sums per wavefront)
 struct MfmaLayout {
     int bpr, R, C, NW, I;  // I = 1 KiB wave loads per stage
     uint32_t zero, meta, stage, stage_bytes, aux, ybuf;
@@ -139,8 +147,7 @@ __host__ __device__ inline MfmaLayout mfma_layout(int bpr, int R, int C, int NW,
     L.stage_bytes = (uint32_t)(R * stage_row_pieces(C) * 16);
     // two stage buffers when double-buffered and K needs more than one stage
     L.aux = L.stage + ((db && bpr > C) ? 2u : 1u) * L.stage_bytes;
-    const uint32_t auxb = (uint32_t)(bpr * 32 > NW * 128 ? bpr * 32 : NW * 128);
-    L.ybuf = L.aux + auxb;
+    L.ybuf = L.aux + (uint32_t)NW * 128u;
     L.total = (size_t)L.ybuf + (size_t)R * rounds * 4;
     return L;
 }
@@ -161,7 +168,7 @@ __host__ __device__ inline MfmaLayout mfma_layout(int bpr, int R, int C, int NW,
 // (row, sub-block) pairs per lane.
 // DB: double-buffered LDS stage (one barrier per stage) or a single buffer
 // (two barriers per stage, half the LDS, so more work-groups fit per CU).
-template <int R, int C, int NW, int PF, bool DB>
+template <int R, int C, int NW, int PF, bool DB, int XIT>
 __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__restrict__ w,
                                                             const float *__restrict__ x,
                                                             float *__restrict__ y, int n,
@@ -220,54 +227,66 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         for (int k = 0; k < IPW; ++k)
             *reinterpret_cast<u32x4 *>(lds + Lo.stage + buf * Lo.stage_bytes + plds[k]) = src[k];
     };
-#pragma unroll
-    for (int f = 0; f < PF; ++f) gload(f, stg[f]);  // in flight while the table is built
-
     // ---- prologue: the activation operand table, in LDS ---------------------
-    if (tid < 4) reinterpret_cast<uint32_t *>(lds + Lo.zero)[tid] = 0u;
-    for (int i = tid; i < bpr * 8; i += NW * 64) {  // i = b*8 + sub-block
-        const f32x4 *xs = reinterpret_cast<const f32x4 *>(x + (size_t)i * 32);
-        float amax = 0.0f, sum = 0.0f;
+    // Item i = one 8-float chunk of x: block i/32, sub-block (i/4)%8, chunk
+    // i%4, so the 4 chunks of a sub-block sit in 4 adjacent lanes. Every
+    // lane loads its XIT chunks before any weight load is issued: the loads
+    // complete in issue order, so waiting for x leaves the weight stream in
+    // flight while the table is built.
+    const int nitems = bpr * 32;
+    f32x4 xv0[XIT], xv1[XIT];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const f32x4 v = xs[t];
-            sum += (v[0] + v[1]) + (v[2] + v[3]);
-            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])),
-                                     fmaxf(fabsf(v[2]), fabsf(v[3]))));
-        }
-        int e = 0;
+    for (int it = 0; it < XIT; ++it) {
+        const int i = std::min(tid + it * NW * 64, nitems - 1);
+        xv0[it] = *reinterpret_cast<const f32x4 *>(x + (size_t)i * 8);
+        xv1[it] = *reinterpret_cast<const f32x4 *>(x + (size_t)i * 8 + 4);
+    }
+#pragma unroll
+    for (int f = 0; f < PF; ++f) gload(f, stg[f]);
+
+    if (tid < 4) reinterpret_cast<uint32_t *>(lds + Lo.zero)[tid] = 0u;
+#pragma unroll
+    for (int it = 0; it < XIT; ++it) {
+        const int i = tid + it * NW * 64;  // lanes of one sub-block share i/4
+        const f32x4 v0 = xv0[it], v1 = xv1[it];
+        float amax = fmaxf(fmaxf(fmaxf(fabsf(v0[0]), fabsf(v0[1])), fmaxf(fabsf(v0[2]), fabsf(v0[3]))),
+                           fmaxf(fmaxf(fabsf(v1[0]), fabsf(v1[1])), fmaxf(fabsf(v1[2]), fabsf(v1[3]))));
+        float sum = ((v0[0] + v0[1]) + (v0[2] + v0[3])) + ((v1[0] + v1[1]) + (v1[2] + v1[3]));
+        amax = fmaxf(amax, quad_xor<1>(amax));
+        amax = fmaxf(amax, quad_xor<2>(amax));
+        sum += quad_xor<1>(sum);
+        sum += quad_xor<2>(sum);
+        if (i >= nitems) continue;
+        int e = 0;  // x*2^e puts the sub-block's largest |x| in [2^13, 2^14)
         if (amax > 0.0f && amax <= 3.402823466e38f) {
             int ex;
             frexpf(amax, &ex);  // amax in [2^(ex-1), 2^ex)
             e = std::min(std::max(14 - ex, -90), 140);
         }
-        reinterpret_cast<int *>(aux)[i] = e;  // 2^e may exceed f32: keep the exponent
-        const int sb = i & 7;
-        meta[(i >> 3) * 16 + sb] = ldexpf(1.0f, ((sb & 1) ? 20 : 24) - e);
-        meta[(i >> 3) * 16 + 8 + sb] = sum;
-    }
-    __syncthreads();
-    for (int i = tid; i < bpr * 32; i += NW * 64) {  // i = (b*8 + c)*4 + h
-        const int b = i >> 5, c = (i >> 2) & 7, h = i & 3;
-        const int o = pair_byte_offset(c >> 1, h), kind = c & 1;
-        const int G = o >> 5;
-        const int e = reinterpret_cast<const int *>(aux)[b * 8 + 2 * G + kind];
-        const float *xp = x + (size_t)b * kBlockElems + 64 * G + (o & 31) + 32 * kind;
-        const f32x4 v0 = *reinterpret_cast<const f32x4 *>(xp);
-        const f32x4 v1 = *reinterpret_cast<const f32x4 *>(xp + 4);
+        const int b = i >> 5, sb = (i >> 2) & 7, j = i & 3;
+        if (j == 0) {
+            meta[b * 16 + sb] = ldexpf(1.0f, ((sb & 1) ? 20 : 24) - e);
+            meta[b * 16 + 8 + sb] = sum;
+        }
+        // table entry (c, h) of this chunk: byte offset pair_byte_offset(c/2, h)
+        // = 32*(sb/2) + 8*j within the qs run, nibble parity c%2 = sb%2
+        const int G = sb >> 1;
+        const int c = 2 * (2 * (G >> 1) + (j & 1)) + (sb & 1), h = 2 * (G & 1) + (j >> 1);
         // slot q holds byte o + {0,2,1,3,4,6,5,7}[q] (see the B operand build)
-        const float xv[8] = {v0[0], v0[2], v0[1], v0[3], v1[0], v1[2], v1[1], v1[3]};
+        const float xs[8] = {v0[0], v0[2], v0[1], v0[3], v1[0], v1[2], v1[1], v1[3]};
         half8 hh, hl;
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            const float xsv = ldexpf(xv[q], e);
+            const float xsv = ldexpf(xs[q], e);
             const _Float16 a = (_Float16)xsv;
             hh[q] = a;
             hl[q] = (_Float16)(xsv - (float)a);
         }
-        *reinterpret_cast<half8 *>(lds + (size_t)i * 32) = hh;
-        *reinterpret_cast<half8 *>(lds + (size_t)i * 32 + 16) = hl;
+        uint8_t *ent = lds + (size_t)(((b * 8 + c) * 4 + h) * 32);
+        *reinterpret_cast<half8 *>(ent) = hh;
+        *reinterpret_cast<half8 *>(ent + 16) = hl;
     }
+    // (the barrier before the first stage is computed also orders the table)
     lstore(0, stg[0]);
 
     // ---- per-lane constants -------------------------------------------------
@@ -426,17 +445,16 @@ static int device_cus() {
     return cus[dev];
 }
 
-template <int R, int C, int NW, int PF, bool DB>
-static hipError_t launch_cfg(const uint8_t *w, const float *x, float *y, int n, int bpr,
+template <int R, int C, int NW, int PF, bool DB, int XIT>
+static hipError_t launch_xit(const uint8_t *w, const float *x, float *y, int n, int bpr,
                              hipStream_t stream, bool persistent) {
-    auto kern = gemv_mfma_kernel<R, C, NW, PF, DB>;
+    auto kern = gemv_mfma_kernel<R, C, NW, PF, DB, XIT>;
     static const hipError_t attr = hipFuncSetAttribute(
         (const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (attr != hipSuccess) return attr;
     const long groups = (n + R - 1) / R;
     long grid = groups, rounds = 1;
     if (persistent) {
-        // resident work-groups per CU from LDS (VGPR use allows >= 2 here)
         static const int occ_env = env_int("MGQ_GEMV_OCC", 0);
         const size_t base = mfma_layout(bpr, R, C, NW, 8, DB).total;
         int occ = 0;  // resident work-groups per CU (registers and LDS)
@@ -454,22 +472,29 @@ static hipError_t launch_cfg(const uint8_t *w, const float *x, float *y, int n, 
     return hipGetLastError();
 }
 
+// The activation chunks per lane (XIT) are a compile-time count so they stay
+// in registers: 1, 2, 4 or 8 (covering bpr <= 8*NW*64/32 blocks).
+template <int R, int C, int NW, int PF, bool DB>
+static hipError_t launch_cfg(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                             hipStream_t stream, bool persistent) {
+    const int need = (bpr * 32 + NW * 64 - 1) / (NW * 64);
+    if (need <= 1) return launch_xit<R, C, NW, PF, DB, 1>(w, x, y, n, bpr, stream, persistent);
+    if (need <= 2) return launch_xit<R, C, NW, PF, DB, 2>(w, x, y, n, bpr, stream, persistent);
+    if (need <= 4) return launch_xit<R, C, NW, PF, DB, 4>(w, x, y, n, bpr, stream, persistent);
+    if (need <= 8) return launch_xit<R, C, NW, PF, DB, 8>(w, x, y, n, bpr, stream, persistent);
+    return hipErrorNotSupported;
+}
+
 // Launch configurations (rows per work-group, blocks per stage, wavefronts,
-// stages in flight). Few row groups (small N): 16-row groups with the whole
-// row in one stage, for parallelism and a single memory round trip. Many row
-// groups: persistent 32-row groups streamed 4 blocks at a time.
+// stages in flight, LDS double buffer). Few row groups (small N): one 16-row
+// work-group per CU, with the whole row in one stage when K <= 3584. Many row
+// groups: persistent 32-row work-groups streamed 8 blocks at a time.
 static hipError_t launch_any(int cfg, const uint8_t *w, const float *x, float *y, int n, int bpr,
                              hipStream_t stream) {
     switch (cfg) {
-        case 0: return launch_cfg<32, 4, 4, 2, true>(w, x, y, n, bpr, stream, true);
-        case 1: return launch_cfg<16, 8, 4, 2, true>(w, x, y, n, bpr, stream, true);
-        case 2: return launch_cfg<16, 14, 7, 1, true>(w, x, y, n, bpr, stream, false);
-        case 3: return launch_cfg<16, 16, 8, 1, true>(w, x, y, n, bpr, stream, false);
-        case 4: return launch_cfg<32, 4, 4, 2, false>(w, x, y, n, bpr, stream, true);
-        case 5: return launch_cfg<32, 8, 8, 1, false>(w, x, y, n, bpr, stream, true);
-        case 6: return launch_cfg<16, 8, 4, 2, false>(w, x, y, n, bpr, stream, true);
-        case 7: return launch_cfg<32, 2, 2, 3, true>(w, x, y, n, bpr, stream, true);
-        case 8: return launch_cfg<16, 16, 8, 2, false>(w, x, y, n, bpr, stream, false);
+        case 0: return launch_cfg<32, 8, 8, 1, false>(w, x, y, n, bpr, stream, true);
+        case 1: return launch_cfg<16, 14, 7, 1, true>(w, x, y, n, bpr, stream, false);
+        case 2: return launch_cfg<16, 16, 8, 1, true>(w, x, y, n, bpr, stream, false);
         default: return hipErrorInvalidValue;
     }
 }
@@ -484,13 +509,16 @@ hipError_t gemv_mfma_launch(const uint8_t *w, const float *x, float *y, int n, i
     if (force >= 0) {
         cfg = force;
     } else {
-        const long groups32 = (n + 31) / 32;
-        if (groups32 >= 768) cfg = 0;
-        else if (bpr <= 14) cfg = 2;
-        else cfg = 3;
+        // one 16-row work-group per CU when that covers N (latency-bound
+        // shapes), else persistent 32-row work-groups
+        const long groups16 = (n + 15) / 16;
+        if (groups16 > device_cus()) cfg = 0;
+        else if (bpr <= 14) cfg = 1;
+        else cfg = 2;
     }
     hipError_t e = launch_any(cfg, w, x, y, n, bpr, stream);
-    if (e == hipErrorNotSupported && cfg != 1) e = launch_any(1, w, x, y, n, bpr, stream);
+    // LDS too small for the double-buffered stages: single-buffered persistent
+    if (e == hipErrorNotSupported && cfg != 0) e = launch_any(0, w, x, y, n, bpr, stream);
     return e;
 }
 

@@ -106,10 +106,13 @@ def test_matvec_random_bytes_wide_dynamic_range(L, orc):
     assert_gemv_close(y[ok], y_ref[ok], a[ok])
 
 
-@pytest.mark.parametrize("n,bpr", [(24576 + 17, 2), (30000, 14), (16, 40), (17, 29)])
+@pytest.mark.parametrize("n,bpr", [(24576 + 17, 2), (30000, 14), (16, 40), (17, 29),
+                                   (4100, 17), (4200, 74), (5000, 112), (300, 100)])
 def test_matvec_random_bytes_all_configs(L, orc, n, bpr):
     # shapes that select each launch configuration (many / few row groups,
-    # single- and multi-stage K, ragged last stage and row group)
+    # single- and multi-stage K, ragged last stage and row group) and each
+    # count of activation chunks per lane (1, 2, 4, 8), including the
+    # single-buffered fallback when the double-buffered stages do not fit
     note(f"matvec random bytes n={n} bpr={bpr}")
     rng = np.random.default_rng(n + bpr)
     w = random_q4k_bytes(rng, n * bpr)
