@@ -109,12 +109,10 @@ hipError_t mgq_chain_create(const mgq_gemv_desc *descs, int n, void **chain_out)
 hipError_t mgq_chain_launch(void *chain, hipStream_t stream);
 hipError_t mgq_chain_destroy(void *chain);
 
-/* Prepares the current device: sets kernel attributes and allocates the
- * library's split-K workspace (4 MiB partial sums + arrival counters, zeroed).
- * Every launcher does this on first use; call it explicitly before capturing
- * launches into a graph, since it allocates and synchronizes. Launches that use
- * the workspace must be ordered on one stream per device (concurrent launches
- * on different streams of the same device would share it). */
+/* Prepares the current device: sets the GEMV kernels' LDS attributes (every
+ * launcher also does this on first use). Allocates nothing; the library keeps
+ * no device memory and no mutable device state, so launches on different
+ * streams may run concurrently. Safe to call more than once. */
 hipError_t mgq_prepare(void);
 
 /* Library version string, e.g. "modgrad_q4k 0.1.0 gfx950". */

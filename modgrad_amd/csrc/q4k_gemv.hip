@@ -5,33 +5,36 @@
 // rocm_matvec_check.rs:38-47: y[r] = sum_k dequant(W)[r][k] * x[k], canonical
 // element order (gguf.rs:364-404).
 //
-// Two kernels:
+// Kernels:
 //
 // 1. gemv_generic_kernel -- vector-ALU, one wavefront per row, flat-stream
 //    addressing (element (r,c) at flat index r*k+c), so it serves both the
 //    row-aligned GGUF layout and LinearResidentQuantized's flattened layout
-//    (neuron.rs:931-951) where rows start mid-block.
+//    (neuron.rs:931-951) where rows start mid-block, and weights that are
+//    only 4-byte aligned.
 //
 // 2. gemv_mfma_kernel -- the fast path for the row-aligned layout. The
 //    dequantize-multiply runs on the matrix cores (v_mfma_f32_16x16x32_f16):
-//      * B operand = weights: lane (n = l%16, h = l/16) holds qs bytes of row n.
+//      * B operand = weights: lane (n = l%16, g = l/16) holds qs bytes of row n.
 //        A nibble masked in place, (dword & 0x000F000F) or (dword & 0x00F000F0),
 //        is already an f16 *subnormal* equal to q*2^-24 (or 16q*2^-24), so one
 //        AND turns two nibbles into two exact f16 operands.
-//      * A operand = activations, laid out per k-slot in LDS by a prologue: the
-//        slot's x value goes to MFMA row m = its sub-block (xh part) and
-//        m = 8 + sub-block (xl part), zero elsewhere. x is split as
+//      * A operand = activations, from a table the work-group builds in LDS
+//        once: the k-slot's x value sits in MFMA row m = 2*sub-block (xh part)
+//        and m = 2*sub-block + 1 (xl part), zero elsewhere. x is split as
 //        x*2^e = xh + xl (two f16, ~22 bits) with a per-sub-block power of two
 //        e, so the f32 accumulators receive sum q*x per (sub-block, row) to
 //        within ~2^-22 relative -- f32-grade, far inside the 1e-4 bound.
-//      * The 16x16 accumulator then holds, per W row, the 8 sub-block partial
-//        sums (xh and xl halves); one permlane32 swap merges the halves of two
-//        16-row tiles at once, and each lane applies d*sc and dmin*m*sum(x)
-//        for 4 (row, sub-block) pairs.
-//    Per 32 rows x 1 block a wave issues 5 16-byte loads per lane, 16 MFMAs and
-//    about 130 VALU ops, i.e. ~1 VALU op per weight -- low enough to stay
-//    HBM-bound on MI355X, where FP32 VALU rate / HBM rate leaves ~2.8 ops per
-//    Q4_K weight at 100% of 8 TB/s.
+//      * Accumulator lane (n, g) holds rows 4g..4g+3 = both parts of
+//        sub-blocks 2g and 2g+1 of W row n, so merging xh and xl is an in-lane
+//        add, and each lane applies d*sc*2^-e and dmin*m*sum(x) for its two
+//        (row, sub-block) pairs.
+//      * Weights stream HBM -> registers -> LDS with fully coalesced 16-byte
+//        loads (64 consecutive pieces per wave instruction), PF stages ahead
+//        of the one being computed.
+//    Per 32 rows x 1 block a wave issues 16 MFMAs and about 220 VALU ops.
+//
+// 3. gemv_batched_kernel -- vector-ALU batched GEMV (up to 16 activation rows).
 #include "q4k_device.hpp"
 #include "q4k_launch.hpp"
 
@@ -445,12 +448,29 @@ static int device_cus() {
     return cus[dev];
 }
 
+// Allows the kernel the whole 160 KiB of gfx950 LDS (once per process).
+template <int R, int C, int NW, int PF, bool DB, int XIT>
+static hipError_t lds_attr() {
+    static const hipError_t attr = hipFuncSetAttribute(
+        (const void *)gemv_mfma_kernel<R, C, NW, PF, DB, XIT>,
+        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    return attr;
+}
+
+template <int R, int C, int NW, int PF, bool DB>
+static hipError_t lds_attr_all() {
+    hipError_t e = lds_attr<R, C, NW, PF, DB, 1>();
+    if (e == hipSuccess) e = lds_attr<R, C, NW, PF, DB, 2>();
+    if (e == hipSuccess) e = lds_attr<R, C, NW, PF, DB, 4>();
+    if (e == hipSuccess) e = lds_attr<R, C, NW, PF, DB, 8>();
+    return e;
+}
+
 template <int R, int C, int NW, int PF, bool DB, int XIT>
 static hipError_t launch_xit(const uint8_t *w, const float *x, float *y, int n, int bpr,
                              hipStream_t stream, bool persistent) {
     auto kern = gemv_mfma_kernel<R, C, NW, PF, DB, XIT>;
-    static const hipError_t attr = hipFuncSetAttribute(
-        (const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    const hipError_t attr = lds_attr<R, C, NW, PF, DB, XIT>();
     if (attr != hipSuccess) return attr;
     const long groups = (n + R - 1) / R;
     long grid = groups, rounds = 1;
@@ -499,7 +519,12 @@ static hipError_t launch_any(int cfg, const uint8_t *w, const float *x, float *y
     }
 }
 
-hipError_t gemv_prepare() { return hipSuccess; }
+hipError_t gemv_prepare() {
+    hipError_t e = lds_attr_all<32, 8, 8, 1, false>();
+    if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, true>();
+    if (e == hipSuccess) e = lds_attr_all<16, 16, 8, 1, true>();
+    return e;
+}
 
 hipError_t gemv_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                             hipStream_t stream) {

@@ -160,10 +160,10 @@ def test_matvec_baseline_layer_shapes(L, orc, name, n, k, t):
 
 
 @pytest.mark.parametrize("n,bpr", [(3584, 14), (3584, 74), (40, 148)])
-def test_matvec_split_k_is_deterministic(L, orc, n, bpr):
+def test_matvec_is_deterministic(L, orc, n, bpr):
     # shapes that split K across work-groups: the last arriver sums the
     # partials in slice order, so repeated launches agree bit for bit
-    note(f"matvec split-K determinism {n}x{bpr * 256}")
+    note(f"matvec determinism {n}x{bpr * 256}")
     w = orc.seeded_weight(7000 + bpr, n, bpr * 256)
     x = orc.normal(7100 + bpr, bpr * 256)
     import torch
