@@ -25,6 +25,7 @@
 #define MODGRAD_Q4K_H
 
 #include <hip/hip_runtime_api.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -79,9 +80,17 @@ hipError_t launch_dequant_q4k_ex(const unsigned char *q4k, int n_blocks, float *
 /* Batched matvec for multi-sequence decode: Y[b][r] = dequant(W)[r] . X[b] for
  * b < batch (1..16). X is [batch][blocks_per_row*256] f32 row-major, Y is
  * [batch][out_dim] f32. Each super-block is decoded once and reused across
- * the batch. Same per-(b,r) tolerance as launch_matvec_q4k. */
+ * the batch (on the matrix cores, batch rows on the MFMA M dimension). Same
+ * per-(b,r) tolerance as launch_matvec_q4k.
+ * `workspace` is caller-owned device memory of at least
+ * mgq_batched_workspace_bytes(blocks_per_row, batch) bytes, 16-byte aligned;
+ * it holds X converted to matrix-core operands for the duration of the call,
+ * so calls that may overlap need distinct workspaces. A smaller or null
+ * workspace -> hipErrorInvalidValue. */
+size_t mgq_batched_workspace_bytes(int blocks_per_row, int batch);
 hipError_t launch_matvec_q4k_batched(const unsigned char *w_q4, const float *X, float *Y,
                                      int out_dim, int blocks_per_row, int batch,
+                                     void *workspace, size_t workspace_bytes,
                                      hipStream_t stream);
 
 /* Prefill dequant-GEMM: C[m][r] = sum_k dequant(W)[r][k] * A[m][k] for

@@ -19,13 +19,15 @@ hipErrorNotSupported = 801
 
 P = ctypes.c_void_p
 I = ctypes.c_int
+S = ctypes.c_size_t
 
 SIGNATURES = {
     "launch_dequant_q4k": (I, [P, I, P]),
     "launch_matvec_q4k": (I, [P, P, P, I, I]),
     "launch_matvec_q4k_ex": (I, [P, P, P, I, I, I, P]),
     "launch_dequant_q4k_ex": (I, [P, I, P, P]),
-    "launch_matvec_q4k_batched": (I, [P, P, P, I, I, I, P]),
+    "mgq_batched_workspace_bytes": (S, [I, I]),
+    "launch_matvec_q4k_batched": (I, [P, P, P, I, I, I, P, S, P]),
     "launch_gemm_q4k_f16": (I, [P, P, P, I, I, I, P]),
     "mgq_chain_create": (I, [P, I, P]),
     "mgq_chain_launch": (I, [P, P]),

@@ -57,13 +57,24 @@ hipError_t launch_matvec_q4k(const unsigned char *w_q4, const float *x, float *y
                                 nullptr);
 }
 
+size_t mgq_batched_workspace_bytes(int blocks_per_row, int batch) {
+    if (blocks_per_row <= 0 || batch <= 0 || batch > 16) return 0;
+    return mgq::batched_workspace_bytes(blocks_per_row, batch);
+}
+
 hipError_t launch_matvec_q4k_batched(const unsigned char *w_q4, const float *X, float *Y,
                                      int out_dim, int blocks_per_row, int batch,
+                                     void *workspace, size_t workspace_bytes,
                                      hipStream_t stream) {
     if (out_dim <= 0 || blocks_per_row <= 0 || batch <= 0 || batch > 16) return hipErrorInvalidValue;
     if (!w_q4 || !X || !Y || misaligned4(w_q4) || misaligned4(X) || misaligned4(Y))
         return hipErrorInvalidValue;
     if ((int64_t)blocks_per_row * 256 > kMaxI32) return hipErrorInvalidValue;
+    if (!workspace || workspace_bytes < mgq::batched_workspace_bytes(blocks_per_row, batch))
+        return hipErrorInvalidValue;
+    const hipError_t e = mgq::gemv_batched_mfma_launch(w_q4, X, Y, out_dim, blocks_per_row, batch,
+                                                       workspace, workspace_bytes, stream);
+    if (e != hipErrorNotSupported) return e;
     return mgq::gemv_batched_launch(w_q4, X, Y, out_dim, blocks_per_row, batch, stream);
 }
 

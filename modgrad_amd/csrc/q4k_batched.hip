@@ -1,0 +1,432 @@
+// Batched Q4_K GEMV on the gfx950 matrix cores: Y[b][r] = dequant(W)[r] . X[b]
+// for b < batch <= 16 (multi-sequence decode). No counterpart in the
+// reference; the oracle is its f64 dequant-dot (rocm_matvec_check.rs:38-47)
+// applied row by row.
+//
+// Two kernels:
+//
+// 1. batched_table_kernel turns X into matrix-core A operands, once per call,
+//    in a caller-provided workspace. Batch b of a set of 8 occupies MFMA rows
+//    m = 2*(b%8) + part, where x*2^e = xh + xl (part 0 = xh, 1 = xl, both f16)
+//    with one power of two e per (batch, block). The k-slot order of every
+//    16-byte entry matches the weight operand built from qs (below). A ninth
+//    operand per (block, set) carries the 8 sub-block sums of x (same split)
+//    for the dmin*m term.
+//
+// 2. gemv_batched_mfma_kernel streams the weights exactly as the GEMV does
+//    (fully coalesced 16-byte loads -> registers -> LDS stage of 32 rows x 8
+//    blocks) and keeps the batch on the MFMA M dimension, so one weight
+//    operand serves 8 batch rows per v_mfma_f32_16x16x32_f16:
+//      * B operand = sc*q: the nibble masked in place is the f16 subnormal
+//        q*2^-24 (low) or 16q*2^-24 (high); one packed f16 multiply by 16*sc
+//        (low) or sc (high) makes it q*sc*2^-20 exactly (q*sc <= 945 fits the
+//        f16 significand), so all 8 sub-blocks of a block accumulate into one
+//        accumulator and only d is applied afterwards.
+//      * min term: one more MFMA per block with the sub-block sums of x
+//        (A) against m[0..7] of each row (B).
+//      * Stages run K-slice-major (all of a work-group's row groups for
+//        blocks 8s..8s+7, then s+1), so wave w keeps the A operands of block
+//        8s+w in registers for the whole slice; per-stage partial sums are
+//        reduced across waves into an LDS row buffer.
+#include "q4k_device.hpp"
+#include "q4k_launch.hpp"
+
+#include <algorithm>
+#include <cstdlib>
+#include <type_traits>
+
+namespace mgq {
+
+constexpr int kBatchOps = 9;  // A operands per (block, set): 8 k-slot groups + sub-block sums
+
+// Workspace layout (bytes): atab [bpr][sets][9][64 lanes][16 B], then meta
+// [bpr][sets][8 batches][corr, corr_min] f32.
+struct BatchedWs {
+    size_t meta, total;
+};
+__host__ __device__ inline BatchedWs batched_ws(int bpr, int sets) {
+    BatchedWs L;
+    L.meta = (size_t)bpr * sets * kBatchOps * 1024;
+    L.total = L.meta + (size_t)bpr * sets * 8 * 8;
+    return L;
+}
+
+size_t batched_workspace_bytes(int bpr, int batch) {
+    return batched_ws(bpr, (batch + 7) / 8).total;
+}
+
+// Byte offset inside qs[128] of the 8 bytes that lane group g reads for
+// pair p (the same map the GEMV uses): pairs 0,1 from qs[16g..16g+15],
+// pairs 2,3 from qs[64+16g..64+16g+15].
+__device__ __forceinline__ int bt_pair_offset(int p, int g) {
+    return p < 2 ? 16 * g + 8 * p : 64 + 16 * g + 8 * (p - 2);
+}
+
+// exponent e with max|v|*2^e in [2^13, 2^14); 0 for 0 or non-finite
+__device__ __forceinline__ int split_exponent(float amax) {
+    int e = 0;
+    if (amax > 0.0f && amax <= 3.402823466e38f) {
+        int ex;
+        frexpf(amax, &ex);
+        e = std::min(std::max(14 - ex, -90), 120);
+    }
+    return e;
+}
+
+// grid (bpr, sets), 256 threads: thread = (batch b' = tid/32, 8-float chunk)
+__global__ __launch_bounds__(256) void batched_table_kernel(const float *__restrict__ X, int batch,
+                                                            int bpr, int sets, bool x_aligned16,
+                                                            uint8_t *__restrict__ ws) {
+    __shared__ float xs[8][256];
+    __shared__ float xsum[8][8];
+    const int j = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
+    const int bl = tid >> 5, ch = tid & 31, b = s * 8 + bl;
+    const size_t K = (size_t)bpr * kBlockElems;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    if (b < batch) {
+        const float *xp = X + (size_t)b * K + (size_t)j * kBlockElems + ch * 8;
+        if (x_aligned16) {
+            const f32x4 a = *reinterpret_cast<const f32x4 *>(xp);
+            const f32x4 c = *reinterpret_cast<const f32x4 *>(xp + 4);
+            v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
+            v[4] = c[0]; v[5] = c[1]; v[6] = c[2]; v[7] = c[3];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = xp[i];
+        }
+    }
+    float amax = 0.0f, sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        amax = fmaxf(amax, fabsf(v[i]));
+        sum += v[i];
+    }
+    // sub-block sums: the 4 chunks of sub-block ch/4 are lanes ch^1, ch^2
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    // block max over the 32 chunks of batch b'
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    const int e = split_exponent(amax);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xs[bl][ch * 8 + i] = ldexpf(v[i], e);
+    if ((ch & 3) == 0) xsum[bl][ch >> 2] = sum;
+    float *meta = reinterpret_cast<float *>(ws + batched_ws(bpr, sets).meta);
+    const size_t js = (size_t)j * sets + s;
+    if (ch == 0) meta[(js * 8 + bl) * 2] = ldexpf(1.0f, 20 - e);
+    __syncthreads();
+
+    // k-slot groups: entry (c, lane), lane = (m = 2b' + part, g); slot q
+    // holds qs byte o + {0,2,1,3,4,6,5,7}[q] with o = bt_pair_offset(c/2, g),
+    // i.e. block position 64*(o/32) + 32*(c%2) + o%32 + ...
+    uint8_t *atab = ws + js * kBatchOps * 1024;
+    for (int E = tid; E < 8 * 64; E += 256) {
+        const int c = E >> 6, lane = E & 63, m = lane & 15, g = lane >> 4;
+        const int bb = m >> 1, part = m & 1;
+        const int o = bt_pair_offset(c >> 1, g);
+        const int pos0 = 64 * (o >> 5) + 32 * (c & 1) + (o & 31);
+        constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+        half8 out;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float xv = xs[bb][pos0 + perm[q]];
+            const _Float16 h = (_Float16)xv;
+            out[q] = part ? (_Float16)(xv - (float)h) : h;
+        }
+        *reinterpret_cast<half8 *>(atab + (size_t)c * 1024 + lane * 16) = out;
+    }
+    // sub-block sums: lanes (m, g = 0) hold xsum[b'][0..7], other lanes zero
+    if (tid < 64) {
+        const int lane = tid, m = lane & 15, g = lane >> 4, bb = m >> 1, part = m & 1;
+        float smax = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) smax = fmaxf(smax, fabsf(xsum[bb][q]));
+        const int es = split_exponent(smax);
+        half8 out;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float xv = ldexpf(xsum[bb][q], es);
+            const _Float16 h = (_Float16)xv;
+            out[q] = g != 0 ? (_Float16)0.0f : (part ? (_Float16)(xv - (float)h) : h);
+        }
+        *reinterpret_cast<half8 *>(atab + (size_t)8 * 1024 + lane * 16) = out;
+        if (g == 0 && part == 0) meta[(js * 8 + bb) * 2 + 1] = ldexpf(1.0f, -es);
+    }
+}
+
+// Two f16 values from the bytes of src that sel picks for result bytes 0 and
+// 2 (v_perm_b32 selectors 0..3; 4 picks 0x64): 1024 + byte via the
+// exponent field, minus 1024 (both exact).
+__device__ __forceinline__ uint32_t byte_to_h2(uint32_t src, uint32_t sel) {
+    const uint32_t biased = __builtin_amdgcn_perm(0x64646464u, src, sel);
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 r = __builtin_bit_cast(h2, biased) - (h2){(_Float16)1024.0f, (_Float16)1024.0f};
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// Work-group = 8 waves; stage = R (16 or 32) rows x 8 blocks (single LDS
+// buffer), PF stages in flight; persistent over row groups. SETS = batch sets
+// of 8.
+template <int R, int SETS, int PF>
+__global__ __launch_bounds__(512) void gemv_batched_mfma_kernel(const uint8_t *__restrict__ w,
+                                                                const uint8_t *__restrict__ ws,
+                                                                float *__restrict__ Y, int n,
+                                                                int bpr, int batch, int rounds) {
+    constexpr int C = 8, NW = 8, BP = 8 * SETS, TILES = R / 16;
+    constexpr int RP = (9 * C) | 1;               // LDS pieces per staged row (odd: no bank conflicts)
+    constexpr int STAGE_BYTES = R * RP * 16;
+    constexpr int AUX_BYTES = NW * R * BP * 4;    // per buffer
+    constexpr int PIECES = R * 9 * C;
+    constexpr int IPW = ((PIECES + 63) / 64 + NW - 1) / NW;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    float *aux0 = reinterpret_cast<float *>(lds + STAGE_BYTES);
+    float *ybuf = reinterpret_cast<float *>(lds + STAGE_BYTES + 2 * AUX_BYTES);
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const size_t row_bytes = (size_t)bpr * kBlockBytes;
+    const int slices = (bpr + C - 1) / C;
+    const int groups = (n + R - 1) / R;
+    const int my_groups = (groups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int Q = my_groups * slices;  // stage q = (slice q / my_groups, group q % my_groups)
+
+    u32x4 stg[PF][IPW];
+    uint32_t prow[IPW], pcol[IPW], plast[IPW], plds[IPW];
+#pragma unroll
+    for (int k = 0; k < IPW; ++k) {
+        const int jp = std::min((wave + k * NW) * 64 + lane, PIECES - 1);
+        const int row = jp / (9 * C), rem = jp - row * 9 * C;
+        const int cb = rem / 9, pc = rem - cb * 9;
+        plds[k] = (uint32_t)((row * RP + rem) * 16);
+        prow[k] = (uint32_t)row;
+        pcol[k] = (uint32_t)(cb * kBlockBytes + 16 * pc);
+        plast[k] = (uint32_t)((bpr - 1) * kBlockBytes + 16 * pc);
+    }
+    auto gload = [&](int q, u32x4(&dst)[IPW]) {
+        q = std::min(q, Q - 1);
+        const int sl = q / my_groups, t = q - sl * my_groups;
+        const uint32_t r0 = ((uint32_t)blockIdx.x + (uint32_t)t * gridDim.x) * R;
+        const uint32_t tcol = (uint32_t)(sl * C * kBlockBytes);
+        const uint32_t rlast = (uint32_t)(n - 1), rb = (uint32_t)row_bytes;
+#pragma unroll
+        for (int k = 0; k < IPW; ++k) {
+            const uint32_t rr = std::min(r0 + prow[k], rlast);
+            const uint32_t col = std::min(tcol + pcol[k], plast[k]);
+            dst[k] = *reinterpret_cast<const u32x4 *>(w + (uint64_t)rr * rb + col);
+        }
+    };
+    auto lstore = [&](const u32x4(&src)[IPW]) {
+#pragma unroll
+        for (int k = 0; k < IPW; ++k) *reinterpret_cast<u32x4 *>(lds + plds[k]) = src[k];
+    };
+    const int n16 = lane & 15, g = lane >> 4, hsel = g >> 1;
+    // byte selectors for this lane's scales: sub-blocks 2h, 2h+1 of a
+    // scales4 word (bytes 2h, 2h+1)
+    const uint32_t sel0 = 0x04000400u | (uint32_t)(2 * hsel) | ((uint32_t)(2 * hsel) << 16);
+    const uint32_t sel1 = sel0 + 0x00010001u;
+    const BatchedWs Lw = batched_ws(bpr, SETS);
+
+    // A operands of this wave's block of the current slice, and of the next
+    // slice: the next slice's are loaded during the current slice's last
+    // stage, ahead of that stage's weight refill, so waiting for them never
+    // drains the weight stream.
+    u32x4 areg[SETS][kBatchOps], anext[SETS][kBatchOps];
+    f32x4 mreg[SETS], mnext[SETS];  // (corr, corr_min) of batches 2g, 2g+1 of each set
+    auto load_a = [&](int sl, u32x4(&a)[SETS][kBatchOps], f32x4(&mr)[SETS]) {
+        const int jb = std::min(sl * C + wave, bpr - 1);
+#pragma unroll
+        for (int s = 0; s < SETS; ++s) {
+            const uint8_t *base = ws + ((size_t)jb * SETS + s) * kBatchOps * 1024 + lane * 16;
+#pragma unroll
+            for (int c = 0; c < kBatchOps; ++c) a[s][c] = *reinterpret_cast<const u32x4 *>(base + c * 1024);
+            mr[s] = *reinterpret_cast<const f32x4 *>(ws + Lw.meta + (((size_t)jb * SETS + s) * 8 + 2 * g) * 8);
+        }
+    };
+    load_a(0, anext, mnext);
+#pragma unroll
+    for (int f = 0; f < PF; ++f) gload(f, stg[f]);
+
+    auto step = [&](const int q, auto fc, const bool more) {
+        constexpr int F = decltype(fc)::value;
+        const int sl = q / my_groups, t = q - sl * my_groups;
+        if (t == 0) {
+#pragma unroll
+            for (int s = 0; s < SETS; ++s) {
+                mreg[s] = mnext[s];
+#pragma unroll
+                for (int c = 0; c < kBatchOps; ++c) areg[s][c] = anext[s][c];
+            }
+        }
+        const int jb = sl * C + wave;  // this wave's block of the slice
+        float *aux = aux0 + (q & 1) * (AUX_BYTES / 4);
+        if (jb < bpr) {
+#pragma unroll
+            for (int T = 0; T < TILES; ++T) {
+                const int row = T * 16 + n16;
+                auto piece = [&](int pc) -> const u32x4 & {
+                    return *reinterpret_cast<const u32x4 *>(lds + (row * RP + wave * 9 + pc) * 16);
+                };
+                const u32x4 hd = piece(0), qa0 = piece(1 + g), qa1 = piece(5 + g);
+                const float d = half_bits_finite(hd[0]), dmin = half_bits_finite(hd[0] >> 16);
+                // 16*sc (low nibbles) and sc (high nibbles) as f16 pairs, for
+                // sub-block pairs G = h (k-slot pairs 0,1) and G = 2+h (2,3)
+                const uint32_t sc_lo = scales4(0, hd[1], hd[3]), sc_hi = scales4(1, hd[1], hd[3]);
+                typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+                const h2 sixteen = {(_Float16)16.0f, (_Float16)16.0f};
+                uint32_t sf[2][2];
+                sf[0][0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, byte_to_h2(sc_lo, sel0)) * sixteen);
+                sf[0][1] = byte_to_h2(sc_lo, sel1);
+                sf[1][0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, byte_to_h2(sc_hi, sel0)) * sixteen);
+                sf[1][1] = byte_to_h2(sc_hi, sel1);
+                // mins m0..m7 as f16 (k-slots of lane group 0; other groups
+                // multiply zero A entries)
+                const uint32_t mn_lo = mins4(0, hd[2], hd[3]), mn_hi = mins4(1, hd[2], hd[3]);
+                const u32x4 bm = {byte_to_h2(mn_lo, 0x04010400u), byte_to_h2(mn_lo, 0x04030402u),
+                                  byte_to_h2(mn_hi, 0x04010400u), byte_to_h2(mn_hi, 0x04030402u)};
+                f32x4 acc[SETS], accm[SETS];
+#pragma unroll
+                for (int s = 0; s < SETS; ++s) {
+                    acc[s] = (f32x4){0.f, 0.f, 0.f, 0.f};
+                    accm[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        __builtin_bit_cast(half8, areg[s][8]), __builtin_bit_cast(half8, bm),
+                        (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                }
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const int p = c >> 1, kind = c & 1;
+                    const uint32_t mask = kind ? 0x00F000F0u : 0x000F000Fu;
+                    const uint32_t w0 = p < 2 ? qa0[2 * p] : qa1[2 * p - 4];
+                    const uint32_t w1 = p < 2 ? qa0[2 * p + 1] : qa1[2 * p - 3];
+                    const h2 f = __builtin_bit_cast(h2, sf[p >> 1][kind]);
+                    const u32x4 bq = {
+                        __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, w0 & mask) * f),
+                        __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, (w0 >> 8) & mask) * f),
+                        __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, w1 & mask) * f),
+                        __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, (w1 >> 8) & mask) * f)};
+#pragma unroll
+                    for (int s = 0; s < SETS; ++s)
+                        acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(half8, areg[s][c]), __builtin_bit_cast(half8, bq), acc[s],
+                            0, 0, 0);
+                }
+#pragma unroll
+                for (int s = 0; s < SETS; ++s) {
+                    const f32x4 mr = mreg[s];
+                    const float y0 = d * ((acc[s][0] + acc[s][1]) * mr[0]) -
+                                     dmin * ((accm[s][0] + accm[s][1]) * mr[1]);
+                    const float y1 = d * ((acc[s][2] + acc[s][3]) * mr[2]) -
+                                     dmin * ((accm[s][2] + accm[s][3]) * mr[3]);
+                    // aux[wave][row][batch]
+                    float *ap = aux + (wave * R + row) * BP + s * 8 + 2 * g;
+                    ap[0] = y0;
+                    ap[1] = y1;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int T = 0; T < TILES; ++T)
+#pragma unroll
+                for (int s = 0; s < SETS; ++s) {
+                    float *ap = aux + (wave * R + T * 16 + n16) * BP + s * 8 + 2 * g;
+                    ap[0] = 0.0f;
+                    ap[1] = 0.0f;
+                }
+        }
+        if (more) {
+            if (t == my_groups - 1) load_a(sl + 1, anext, mnext);
+            __syncthreads();  // every wave is done reading the stage buffer
+            lstore(stg[(F + 1) % PF]);
+            gload(q + 1 + PF, stg[(F + 1) % PF]);
+        }
+        __syncthreads();
+        // cross-wave (block) reduction of this stage into the row buffer
+        if (tid < R * BP) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int wv = 0; wv < NW; ++wv) sum += aux[wv * R * BP + tid];
+            float *yb = ybuf + t * R * BP + tid;
+            *yb = (sl == 0) ? sum : *yb + sum;
+        }
+    };
+    lstore(stg[0]);
+    int q0 = 0;
+    if (Q > PF) {
+        gload(PF, stg[0]);
+        __syncthreads();
+        for (; q0 + PF < Q; q0 += PF) {
+            step(q0, std::integral_constant<int, 0>{}, true);
+            if constexpr (PF > 1) step(q0 + 1, std::integral_constant<int, 1 % PF>{}, true);
+        }
+    } else {
+        __syncthreads();
+    }
+    if (q0 < Q) step(q0, std::integral_constant<int, 0>{}, q0 + 1 < Q);
+    if constexpr (PF > 1) if (q0 + 1 < Q) step(q0 + 1, std::integral_constant<int, 1 % PF>{}, q0 + 2 < Q);
+    __syncthreads();
+    // Y[b][r], rows fastest
+    for (int i = tid; i < my_groups * R * BP; i += NW * 64) {
+        const int t = i / (R * BP), rem = i - t * R * BP, b = rem / R, r = rem - b * R;
+        const int row = ((int)blockIdx.x + t * (int)gridDim.x) * R + r;
+        if (row < n && b < batch) Y[(size_t)b * n + row] = ybuf[(t * R + r) * BP + b];
+    }
+}
+
+static int cu_count() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+            v = 256;
+        cus[dev] = v;
+    }
+    return cus[dev];
+}
+
+template <int R, int SETS, int PF>
+static hipError_t batched_main_launch(const uint8_t *w, const uint8_t *ws, float *Y, int n, int bpr,
+                                      int batch, hipStream_t stream) {
+    auto kern = gemv_batched_mfma_kernel<R, SETS, PF>;
+    static const hipError_t attr = hipFuncSetAttribute(
+        (const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return attr;
+    constexpr int BP = 8 * SETS;
+    constexpr size_t base = (size_t)R * ((9 * 8) | 1) * 16 + 2 * (size_t)8 * R * BP * 4;
+    const long groups = (n + R - 1) / R;
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)kern, 512,
+                                                     base + 8 * R * BP * 4) != hipSuccess || occ <= 0)
+        occ = 1;
+    const long maxgrid = (long)cu_count() * occ;
+    const long rounds = (groups + maxgrid - 1) / maxgrid;
+    const long grid = (groups + rounds - 1) / rounds;
+    const size_t lds = base + (size_t)rounds * R * BP * 4;
+    if (lds > 160 * 1024) return hipErrorNotSupported;
+    kern<<<(unsigned)grid, 512, lds, stream>>>(w, ws, Y, n, bpr, batch, (int)rounds);
+    return hipGetLastError();
+}
+
+hipError_t gemv_batched_mfma_launch(const uint8_t *w, const float *X, float *Y, int n, int bpr,
+                                    int batch, void *workspace, size_t workspace_bytes,
+                                    hipStream_t stream) {
+    const int sets = (batch + 7) / 8;
+    if (workspace_bytes < batched_ws(bpr, sets).total) return hipErrorInvalidValue;
+    if (((uintptr_t)w & 15u) || ((uintptr_t)workspace & 15u)) return hipErrorNotSupported;
+    uint8_t *ws = static_cast<uint8_t *>(workspace);
+    batched_table_kernel<<<dim3((unsigned)bpr, (unsigned)sets), 256, 0, stream>>>(
+        X, batch, bpr, sets, ((uintptr_t)X & 15u) == 0, ws);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    // 16-row groups when 32-row groups would leave CUs idle
+    const bool small = (n + 31) / 32 < cu_count();
+    if (sets == 1)
+        return small ? batched_main_launch<16, 1, 2>(w, ws, Y, n, bpr, batch, stream)
+                     : batched_main_launch<32, 1, 2>(w, ws, Y, n, bpr, batch, stream);
+    return small ? batched_main_launch<16, 2, 1>(w, ws, Y, n, bpr, batch, stream)
+                 : batched_main_launch<32, 2, 1>(w, ws, Y, n, bpr, batch, stream);
+}
+
+}  // namespace mgq

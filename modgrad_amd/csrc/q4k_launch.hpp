@@ -27,8 +27,17 @@ hipError_t gemv_prepare();
 hipError_t gemv_rows_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                             hipStream_t stream);
 
+// Vector-ALU batched GEMV (any 4-byte alignment, no workspace).
 hipError_t gemv_batched_launch(const uint8_t *w, const float *X, float *Y, int n, int bpr,
                                int batch, hipStream_t stream);
+
+// Matrix-core batched GEMV: an operand-table pass into `workspace`, then the
+// main kernel. hipErrorNotSupported when w or the workspace is not 16-byte
+// aligned (the caller then uses the vector-ALU kernel).
+size_t batched_workspace_bytes(int bpr, int batch);
+hipError_t gemv_batched_mfma_launch(const uint8_t *w, const float *X, float *Y, int n, int bpr,
+                                    int batch, void *workspace, size_t workspace_bytes,
+                                    hipStream_t stream);
 
 hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n, int bpr,
                            int m_tokens, hipStream_t stream);

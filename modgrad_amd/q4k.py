@@ -141,10 +141,28 @@ class kern:
                                               _stream_ptr(stream)), "matvec_q4k_ex")
 
     @staticmethod
+    def batched_workspace_bytes(bpr: int, batch: int) -> int:
+        return int(_lib.load().mgq_batched_workspace_bytes(bpr, batch))
+
+    @staticmethod
     def matvec_q4k_batched(w: int, X: int, Y: int, out_dim: int, bpr: int, batch: int,
-                           stream=None) -> None:
-        _chk(_lib.load().launch_matvec_q4k_batched(w, X, Y, out_dim, bpr, batch,
-                                                   _stream_ptr(stream)), "matvec_q4k_batched")
+                           stream=None, workspace=None) -> None:
+        """Y[b] = dequant(W) X[b] for b < batch. `workspace` is a device
+        tensor of at least batched_workspace_bytes(bpr, batch) bytes; without
+        one, a fresh one comes from torch's caching allocator, tied to the
+        launch stream."""
+        torch = _torch()
+        nbytes = kern.batched_workspace_bytes(bpr, batch)
+        if workspace is None:
+            workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda")
+            if isinstance(stream, torch.cuda.Stream):
+                workspace.record_stream(stream)
+        if workspace.numel() * workspace.element_size() < nbytes:
+            raise BackendError("Runtime", "matvec_q4k_batched: workspace too small")
+        _chk(_lib.load().launch_matvec_q4k_batched(
+            w, X, Y, out_dim, bpr, batch, workspace.data_ptr(),
+            workspace.numel() * workspace.element_size(), _stream_ptr(stream)),
+            "matvec_q4k_batched")
 
     @staticmethod
     def gemm_q4k_f16(w: int, a: int, c: int, out_dim: int, bpr: int, m_tokens: int,

@@ -26,6 +26,12 @@ def empty_f32(n: int):
     return torch.full((n,), float("nan"), dtype=torch.float32, device="cuda")
 
 
+def filled_u8(n: int, value: int):
+    """Device byte buffer of n bytes, every byte = value (stale-workspace stand-in)."""
+    import torch
+    return torch.full((max(n, 1),), value, dtype=torch.uint8, device="cuda")
+
+
 def assert_gemv_close(y: np.ndarray, y_ref: np.ndarray, absdot: np.ndarray, tol: float = 1e-4):
     """BASELINE gate: per row |y - y_ref| <= tol * sum_k |w_rk||x_k|."""
     err = np.abs(y.astype(np.float64) - y_ref.astype(np.float64))

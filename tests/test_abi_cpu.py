@@ -62,9 +62,22 @@ def test_dequant_rejects_bad_args(L):
     assert L.launch_dequant_q4k(FAKE, 1, FAKE + 2) == INVALID
 
 
+def test_batched_workspace_size(L):
+    # 9 operand tables of 1 KiB plus 8 (corr, corr_min) pairs per (block, set of 8)
+    for bpr, batch in [(1, 1), (14, 8), (14, 9), (74, 16)]:
+        sets = (batch + 7) // 8
+        assert L.mgq_batched_workspace_bytes(bpr, batch) == bpr * sets * (9 * 1024 + 64)
+    assert L.mgq_batched_workspace_bytes(0, 4) == 0
+    assert L.mgq_batched_workspace_bytes(4, 17) == 0
+
+
 def test_batched_and_gemm_reject_bad_args(L):
-    assert L.launch_matvec_q4k_batched(FAKE, FAKE, FAKE, 16, 1, 0, None) == INVALID
-    assert L.launch_matvec_q4k_batched(FAKE, FAKE, FAKE, 16, 1, 17, None) == INVALID
+    ws = L.mgq_batched_workspace_bytes(1, 16)
+    assert L.launch_matvec_q4k_batched(FAKE, FAKE, FAKE, 16, 1, 0, FAKE, ws, None) == INVALID
+    assert L.launch_matvec_q4k_batched(FAKE, FAKE, FAKE, 16, 1, 17, FAKE, ws, None) == INVALID
+    # missing or undersized workspace
+    assert L.launch_matvec_q4k_batched(FAKE, FAKE, FAKE, 16, 1, 4, None, ws, None) == INVALID
+    assert L.launch_matvec_q4k_batched(FAKE, FAKE, FAKE, 16, 1, 16, FAKE, ws - 1, None) == INVALID
     assert L.launch_gemm_q4k_f16(FAKE, FAKE, FAKE, 16, 1, 0, None) == INVALID
     assert L.launch_gemm_q4k_f16(FAKE, FAKE, FAKE, 0, 1, 4, None) == INVALID
 

@@ -11,7 +11,8 @@ import numpy as np
 import pytest
 
 from modgrad_amd import _lib
-from tests.gpu_util import assert_gemv_close, dev, empty_f32, host, ptr, random_q4k_bytes
+from tests.gpu_util import (assert_gemv_close, dev, empty_f32, filled_u8, host, ptr,
+                            random_q4k_bytes)
 
 pytestmark = pytest.mark.gpu
 
@@ -204,15 +205,66 @@ def test_matvec_flat_layout(L, orc, n, k):
 
 
 # ------------------------------------------------------------------ batched --
-@pytest.mark.parametrize("batch", [1, 2, 3, 4, 8, 16])
+def run_batched(L, w, X, n, bpr, batch, w_offset=0):
+    wt = dev(np.concatenate([np.zeros(w_offset, np.uint8), w]))
+    Xt, Yt = dev(X), empty_f32(batch * n)
+    nws = L.mgq_batched_workspace_bytes(bpr, batch)
+    ws = filled_u8(nws, 0xAB)  # stale bytes from an earlier user
+    _lib.check("batched", L.launch_matvec_q4k_batched(ptr(wt) + w_offset, ptr(Xt), ptr(Yt), n, bpr,
+                                                      batch, ptr(ws), nws, None))
+    return host(Yt).reshape(batch, n)
+
+
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 8, 9, 16])
 def test_matvec_batched(L, orc, batch):
     note(f"batched B={batch}")
     n, bpr = 1000, 14
     w = orc.seeded_weight(51, n, bpr * 256)
     X = orc.normal(52 + batch, batch * bpr * 256).reshape(batch, -1)
-    wt, Xt, Yt = dev(w), dev(X), empty_f32(batch * n)
-    _lib.check("batched", L.launch_matvec_q4k_batched(ptr(wt), ptr(Xt), ptr(Yt), n, bpr, batch, None))
-    Y = host(Yt).reshape(batch, n)
+    Y = run_batched(L, w, X, n, bpr, batch)
+    Y_ref, A = orc.gemv_batched(w, X, n, bpr)
+    for b in range(batch):
+        assert_gemv_close(Y[b], Y_ref[b], A[b])
+
+
+@pytest.mark.parametrize("n,bpr,batch", [(17, 1, 5), (33, 3, 16), (700, 74, 4), (300, 9, 12),
+                                         (9000, 16, 2)])
+def test_matvec_batched_shapes_random_bytes(L, orc, n, bpr, batch):
+    # ragged row groups, partial K slices (idle waves), several K slices,
+    # two batch sets, many row groups per work-group
+    note(f"batched random bytes n={n} bpr={bpr} B={batch}")
+    rng = np.random.default_rng(n * 31 + bpr + batch)
+    w = random_q4k_bytes(rng, n * bpr)
+    X = rng.standard_normal((batch, bpr * 256)).astype(np.float32)
+    X[:, ::7] *= 1e-3  # mixed magnitudes within a block
+    Y = run_batched(L, w, X, n, bpr, batch)
+    Y_ref, A = orc.gemv_batched(w, X, n, bpr)
+    for b in range(batch):
+        assert_gemv_close(Y[b], Y_ref[b], A[b])
+
+
+def test_matvec_batched_matches_gemv_and_is_deterministic(L, orc):
+    note("batched vs gemv, determinism")
+    n, bpr, batch = 512, 14, 16
+    w = orc.seeded_weight(61, n, bpr * 256)
+    X = orc.normal(62, batch * bpr * 256).reshape(batch, -1)
+    Y1 = run_batched(L, w, X, n, bpr, batch)
+    Y2 = run_batched(L, w, X, n, bpr, batch)
+    assert np.array_equal(Y1, Y2)
+    for b in (0, 7, 8, 15):
+        y = run_gemv(L, w, X[b], n, bpr)
+        y_ref, a = orc.gemv(w, X[b], n, bpr)
+        assert_gemv_close(Y1[b], y_ref, a)
+        assert_gemv_close(y, y_ref, a)
+
+
+def test_matvec_batched_vector_alu_fallback(L, orc):
+    # weights only 4-byte aligned: the vector-ALU batched kernel runs
+    note("batched misaligned weights")
+    n, bpr, batch = 70, 3, 6
+    w = orc.seeded_weight(71, n, bpr * 256)
+    X = orc.normal(72, batch * bpr * 256).reshape(batch, -1)
+    Y = run_batched(L, w, X, n, bpr, batch, w_offset=4)
     Y_ref, A = orc.gemv_batched(w, X, n, bpr)
     for b in range(batch):
         assert_gemv_close(Y[b], Y_ref[b], A[b])
