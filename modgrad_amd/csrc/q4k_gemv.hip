@@ -298,6 +298,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     // (2g+1, xh), (2g+1, xl) of W row n16 -- both parts of a sub-block land in
     // the same lane, so merging xh and xl is an in-lane add.
     const int n16 = lane & 15, g = lane >> 4, jq = g >> 1, sh = 16 * (g & 1);
+    // scales4/mins4 of quad jq without a divergent branch: the low bits come
+    // from scale dword 0 (jq = 0) or 2 (jq = 1), the top two bits of quad 1
+    // from dword 0 (scales) or 1 (mins)
+    const uint32_t lmask = jq ? 0x0F0F0F0Fu : 0x3F3F3F3Fu, hmask = jq ? 0x30303030u : 0u;
     // A operand address of MFMA c for block b: abase[c] + (b*1024 & amask[c])
     // (amask = 0 for lanes whose row m takes no data from c: the zero slot)
     uint32_t abase[8], amask[8];
@@ -313,8 +317,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     // from their q*x sums s0, s1 (scaled by corr) and the block header hd.
     auto decode = [&](const u32x4 &hd, int b, float s0, float s1) -> float {
         const float d = half_bits_finite(hd[0]), dmin = half_bits_finite(hd[0] >> 16);
-        const uint32_t scq = (jq ? scales4(1, hd[1], hd[3]) : scales4(0, hd[1], hd[3])) >> sh;
-        const uint32_t mnq = (jq ? mins4(1, hd[2], hd[3]) : mins4(0, hd[2], hd[3])) >> sh;
+        const uint32_t scs = jq ? hd[3] : hd[1], mns = jq ? (hd[3] >> 4) : hd[2];
+        const uint32_t scq = ((scs & lmask) | ((hd[1] >> 2) & hmask)) >> sh;
+        const uint32_t mnq = ((mns & lmask) | ((hd[2] >> 2) & hmask)) >> sh;
         const float *mb = meta + b * 16 + 2 * g;
         const float t1 = (float)(scq & 0xFFu) * (s0 * mb[0]) + (float)((scq >> 8) & 0xFFu) * (s1 * mb[1]);
         const float t2 = (float)(mnq & 0xFFu) * mb[8] + (float)((mnq >> 8) & 0xFFu) * mb[9];
@@ -515,6 +520,10 @@ static hipError_t launch_any(int cfg, const uint8_t *w, const float *x, float *y
         case 0: return launch_cfg<32, 8, 8, 1, false>(w, x, y, n, bpr, stream, true);
         case 1: return launch_cfg<16, 14, 7, 1, true>(w, x, y, n, bpr, stream, false);
         case 2: return launch_cfg<16, 16, 8, 1, true>(w, x, y, n, bpr, stream, false);
+        case 3: return launch_cfg<16, 16, 8, 2, true>(w, x, y, n, bpr, stream, false);
+        case 4: return launch_cfg<16, 16, 8, 3, true>(w, x, y, n, bpr, stream, false);
+        case 5: return launch_cfg<16, 8, 8, 4, true>(w, x, y, n, bpr, stream, false);
+        case 6: return launch_cfg<16, 8, 4, 4, true>(w, x, y, n, bpr, stream, false);
         default: return hipErrorInvalidValue;
     }
 }
