@@ -14,6 +14,11 @@ the reference CPU GEMV, llm.rs:468-806, on a bounded sample). Progress goes to
 stderr.
 
   python bench.py [--steps K] [--warmup W] [--workload decode7b|layer|gateup]
+
+The other BASELINE configs have their own workloads (one JSON line each,
+measured the same way, not the headline): --workload config1 (4864x896
+flattened layout), --workload batched --batch B (config 4) and --workload
+prefill (config 5, TFLOP/s against the f16 matrix-core peak).
 """
 from __future__ import annotations
 
@@ -26,6 +31,7 @@ import time
 import numpy as np
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16 matrix-core peak
 METRIC = "Q4_K GEMV achieved HBM GB/s (% of peak); 7B-class decode tokens/sec"
 BLOCK_BYTES, BLOCK_ELEMS = 144, 256
 
@@ -147,6 +153,140 @@ def cpu_baseline(torch, wl: Workload, target_s: float, threads: int, launches: i
             "tokens_per_s_equiv": round(gbs * 1e9 / wl.bytes_per_pass, 3)}
 
 
+def time_captured(torch, launch, steps: int, warmup: int) -> float:
+    """ms per replay of a HIP graph captured (through torch) from `launch`,
+    a callable that enqueues one pass on the stream it is given."""
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        launch(stream)  # eager warm-up: first-use kernel attributes
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        launch(torch.cuda.current_stream())
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(cur)
+    for _ in range(steps):
+        g.replay()
+    t1.record(cur)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
+
+
+def run_config1(torch, q4k, args):
+    """Qwen2.5-0.5B up-projection 4864x896 (896 % 256 != 0,
+    so the flattened-tensor layout of LinearResidentQuantized), rotating
+    copies past 1 GiB so no cache holds the weights."""
+    from oracle import oracle as orc
+    n, k = 4864, 896
+    nblk = n * k // BLOCK_ELEMS
+    wbytes = nblk * BLOCK_BYTES
+    copies = -(-(1 << 30) // wbytes)
+    # weights from the reference quantizer on seeded N(0, 0.02) (neuron.rs:931-951)
+    w_host = orc.seeded_weight(0x514B00 + 5, n, k)
+    x_host = orc.normal(0x514B05 ^ 0xA5A5, k)
+    w = torch.from_numpy(w_host).cuda().repeat(copies).view(copies, wbytes)
+    x = torch.from_numpy(x_host).cuda()
+    y = torch.empty((copies, n), device="cuda")
+
+    def launch(st):
+        for c in range(copies):
+            q4k.kern.matvec_q4k_ex(w[c].data_ptr(), x.data_ptr(), y[c].data_ptr(), n, k,
+                                   1, st)  # MGQ_LAYOUT_FLAT
+    ms = time_captured(torch, launch, args.steps, args.warmup)
+    nbytes = copies * (wbytes + 4 * (n + k))
+    y_ref, a = orc.gemv_flat(w_host, x_host, n, k)
+    r = np.abs(y[copies - 1].cpu().numpy().astype(np.float64) - y_ref) / np.maximum(a, 1e-300)
+    parity = f"ok (max err/absdot {r.max():.2e} <= 1e-4)" if np.all(r <= 1e-4) else \
+        f"FAIL: max err/absdot {r.max():.3e}"
+    us = ms * 1e3 / copies
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": "config1: 4864x896 flattened Q4_K (LinearResidentQuantized layout), "
+                        f"{copies} rotating copies, one graph", "us_per_launch": round(us, 3),
+            "gbs": gbs, "bytes_per_launch": nbytes // copies, "parity": parity,
+            "kernel": "mgq::gemv_generic_kernel<false>"}
+
+
+def run_batched(torch, q4k, args):
+    """gate/up 18944x3584 and down 3584x18944 at batch B."""
+    from oracle import oracle as orc
+    B = args.batch
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x514B40 + B)
+    shapes = [("gate", INTER, HIDDEN), ("down", HIDDEN, INTER)]
+    copies = 16  # 16 x 76 MB: past the 256 MiB MALL
+    items = []
+    for c in range(copies):
+        for name, n, k in shapes:
+            bpr = k // BLOCK_ELEMS
+            w = make_q4k(torch, n, k, gen)
+            X = torch.randn((B, k), device="cuda", generator=gen)
+            Y = torch.empty((B, n), device="cuda")
+            ws = torch.empty(q4k.kern.batched_workspace_bytes(bpr, B), dtype=torch.uint8, device="cuda")
+            items.append((name, w, X, Y, ws, n, bpr))
+
+    def launch(st):
+        for name, w, X, Y, ws, n, bpr in items:
+            q4k.kern.matvec_q4k_batched(w.data_ptr(), X.data_ptr(), Y.data_ptr(), n, bpr, B, st,
+                                        workspace=ws)
+    ms = time_captured(torch, launch, args.steps, args.warmup)
+    nbytes = sum(n * bpr * BLOCK_BYTES + 4 * B * (bpr * BLOCK_ELEMS + n) for _, _, _, _, _, n, bpr in items)
+    worst = 0.0
+    parity = None
+    for name, w, X, Y, ws, n, bpr in items[-2:]:
+        idx = np.sort(np.random.default_rng(n).choice(n, size=128, replace=False))
+        wr = w.view(n, bpr * BLOCK_BYTES)[torch.from_numpy(idx).cuda()].cpu().numpy().ravel()
+        Xh, Yh = X.cpu().numpy(), Y.cpu().numpy()[:, idx]
+        for b in range(B):
+            y_ref, a = orc.gemv(wr, Xh[b], idx.size, bpr)
+            r = np.abs(Yh[b].astype(np.float64) - y_ref) / np.maximum(a, 1e-300)
+            worst = max(worst, float(r.max()))
+            if not np.all(r <= 1e-4):
+                parity = f"FAIL {name} b={b}: max err/absdot {r.max():.3e}"
+    parity = parity or f"ok (max err/absdot {worst:.2e} <= 1e-4)"
+    return {"workload": f"config4: batched B={B}, gate 18944x3584 + down 3584x18944, "
+                        f"{copies} rotating copies, one graph",
+            "us_per_launch": round(ms * 1e3 / len(items), 3), "gbs": nbytes / (ms * 1e-3) / 1e9,
+            "bytes_per_launch": nbytes // len(items), "parity": parity,
+            "kernel": "mgq::gemv_batched_mfma_kernel (+ batched_table_kernel)"}
+
+
+def run_prefill(torch, q4k, args):
+    """Q4_K W 18944x3584 times f16 A [512 x 3584]."""
+    from oracle import oracle as orc
+    n, k, m = INTER, HIDDEN, 512
+    bpr = k // BLOCK_ELEMS
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0xF16)
+    copies = 4
+    ws = [make_q4k(torch, n, k, gen) for _ in range(copies)]
+    A = torch.randn((m, k), device="cuda", generator=gen).to(torch.float16)
+    Cs = [torch.empty((m, n), device="cuda") for _ in range(copies)]
+
+    def launch(st):
+        for w, C in zip(ws, Cs):
+            q4k.kern.gemm_q4k_f16(w.data_ptr(), A.data_ptr(), C.data_ptr(), n, bpr, m, st)
+    ms = time_captured(torch, launch, args.steps, args.warmup)
+    s = ms * 1e-3 / copies
+    tflops = 2.0 * n * k * m / s / 1e12
+    idx = np.sort(np.random.default_rng(5).choice(n, size=64, replace=False))
+    wr = ws[-1].view(n, bpr * BLOCK_BYTES)[torch.from_numpy(idx).cuda()].cpu().numpy().ravel()
+    a16 = A.cpu().numpy().view(np.uint16).reshape(m, k)
+    C_ref, absd = orc.gemm_f16(wr, a16, idx.size, bpr)   # [m][sampled rows]
+    C_ref = C_ref.astype(np.float64)
+    Cg = Cs[-1].cpu().numpy()[:, idx].astype(np.float64)
+    elem_ok = np.all(np.abs(Cg - C_ref) <= 1e-2 * absd / np.sqrt(k))
+    frob = float(np.linalg.norm(Cg - C_ref) / max(np.linalg.norm(C_ref), 1e-300))
+    parity = (f"ok (frobenius rel {frob:.2e} <= 1e-3, per-element <= 1e-2*sum|w||a|/sqrt(K))"
+              if elem_ok and frob <= 1e-3 else f"FAIL: frobenius rel {frob:.3e}, elementwise {elem_ok}")
+    return {"workload": f"config5: prefill 18944x3584 Q4_K x f16 [512x3584], {copies} weight copies",
+            "us_per_launch": round(s * 1e6, 3), "tflops": tflops, "parity": parity,
+            "kernel": "mgq::gemm_q4k_f16_kernel"}
+
+
 TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                "gemv_mfma_decode7b_pmc.txt")
 
@@ -163,12 +303,40 @@ def profiled_traffic(workload: str):
     return None
 
 
+def run_side_workload(torch, q4k, args) -> int:
+    """BASELINE configs 1, 4 and 5: one JSON line each, same field layout."""
+    fn = {"config1": run_config1, "batched": run_batched, "prefill": run_prefill}[args.workload]
+    r = fn(torch, q4k, args)
+    out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": "synthetic",
+           "config": {"workload": r["workload"]}, "parity": r["parity"]}
+    if "tflops" in r:
+        out.update({"value": round(r["tflops"], 2), "unit": "TFLOP/s", "dtype": "f16 x q4_k -> f32",
+                    "us_per_launch": r["us_per_launch"],
+                    "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 2),
+                                 "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                 "frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
+                                 "traffic": None, "kernel": r["kernel"]}})
+    else:
+        out.update({"value": round(r["gbs"], 2), "unit": "GB/s", "dtype": "f32",
+                    "us_per_launch": r["us_per_launch"],
+                    "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 2), "peak": HBM_PEAK_GBS,
+                                 "unit": "GB/s", "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                                 "traffic": None, "kernel": r["kernel"],
+                                 "avg_launch_bytes": r["bytes_per_launch"]}})
+    log(f"{r['workload']}: {r['us_per_launch']} us per launch; parity {r['parity']}")
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="decode7b", choices=["decode7b", "layer", "gateup"])
+    ap.add_argument("--workload", default="decode7b",
+                    choices=["decode7b", "layer", "gateup", "config1", "batched", "prefill"])
+    ap.add_argument("--batch", type=int, default=8, help="batch for --workload batched (1..16)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
@@ -185,6 +353,8 @@ def main() -> int:
     _lib.load()
     log(f"device {torch.cuda.get_device_name(0)}; workload {args.workload}")
 
+    if args.workload in ("config1", "batched", "prefill"):
+        return run_side_workload(torch, q4k, args)
     if args.workload == "decode7b":
         wl = Workload(torch, decode_step_shapes())
         desc = ("decode7b: 28 x (qkv 4608x3584, o 3584x3584, gate|up 37888x3584, down 3584x18944) "
