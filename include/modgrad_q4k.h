@@ -54,6 +54,26 @@ hipError_t launch_dequant_q4k(const unsigned char *q4k, int n_blocks, float *fp3
 hipError_t launch_matvec_q4k(const unsigned char *w_q4, const float *x, float *y,
                              int out_dim, int blocks_per_row);
 
+/* Replaces launch_quantize_q8_1 (decl rocm.rs:477, def
+ * kernels/matvec_q4k_dp4a.hip:29-55): the int8 activations of the dp4a path.
+ * For each of the n/32 sub-blocks s (trailing n%32 values are ignored, as in
+ * the reference): xd[s] = amax/127, xq = clamp(rint(x*127/amax), -127, 127)
+ * (round half to even), xsum[s] = sum of the 32 xq; amax = 0, or a scale whose
+ * inverse is not finite, gives an all-zero sub-block. Bit-identical to the
+ * reference. n < 32 -> hipErrorInvalidValue. */
+hipError_t launch_quantize_q8_1(const float *x, signed char *xq, float *xd, float *xsum, int n);
+
+/* Replaces launch_matvec_q4k_dp4a (decl rocm.rs:478-479, def
+ * kernels/matvec_q4k_dp4a.hip:52-116): y[r] = sum over sub-blocks s of
+ * xd[s]*(d*sc_s*isum_s - dmin*m_s*xsum[s]), isum_s = sum of nibble*xq over the
+ * sub-block (exact integer dot, canonical order); a non-finite row result is
+ * written as 0, as the reference does. xq/xd/xsum as produced by
+ * launch_quantize_q8_1 for x of blocks_per_row*256 values. Its accuracy
+ * against the f32 matvec is the int8 quantization's (the reference accepts
+ * RMS-relative error < 0.02, examples/rocm_dp4a_check.rs:63). */
+hipError_t launch_matvec_q4k_dp4a(const unsigned char *w, const signed char *xq, const float *xd,
+                                  const float *xsum, float *y, int out_dim, int bpr);
+
 /* ---------------------------------------------------------------------------
  * Additive entry points (no counterpart in the reference unless noted)
  * ------------------------------------------------------------------------ */
@@ -72,6 +92,13 @@ hipError_t launch_matvec_q4k(const unsigned char *w_q4, const float *x, float *y
 hipError_t launch_matvec_q4k_ex(const unsigned char *w_q4, const float *x, float *y,
                                 int out_dim, int k_elems, int layout,
                                 hipStream_t stream);
+
+/* launch_quantize_q8_1 / launch_matvec_q4k_dp4a with an explicit stream. */
+hipError_t launch_quantize_q8_1_ex(const float *x, signed char *xq, float *xd, float *xsum, int n,
+                                   hipStream_t stream);
+hipError_t launch_matvec_q4k_dp4a_ex(const unsigned char *w, const signed char *xq,
+                                     const float *xd, const float *xsum, float *y, int out_dim,
+                                     int bpr, hipStream_t stream);
 
 /* launch_dequant_q4k with an explicit stream. */
 hipError_t launch_dequant_q4k_ex(const unsigned char *q4k, int n_blocks, float *fp32_out,

@@ -25,6 +25,10 @@ SIGNATURES = {
     "launch_dequant_q4k": (I, [P, I, P]),
     "launch_matvec_q4k": (I, [P, P, P, I, I]),
     "launch_matvec_q4k_ex": (I, [P, P, P, I, I, I, P]),
+    "launch_quantize_q8_1": (I, [P, P, P, P, I]),
+    "launch_matvec_q4k_dp4a": (I, [P, P, P, P, P, I, I]),
+    "launch_quantize_q8_1_ex": (I, [P, P, P, P, I, P]),
+    "launch_matvec_q4k_dp4a_ex": (I, [P, P, P, P, P, I, I, P]),
     "launch_dequant_q4k_ex": (I, [P, I, P, P]),
     "mgq_batched_workspace_bytes": (S, [I, I]),
     "launch_matvec_q4k_batched": (I, [P, P, P, I, I, I, P, S, P]),

@@ -78,6 +78,36 @@ hipError_t launch_matvec_q4k_batched(const unsigned char *w_q4, const float *X, 
     return mgq::gemv_batched_launch(w_q4, X, Y, out_dim, blocks_per_row, batch, stream);
 }
 
+hipError_t launch_quantize_q8_1_ex(const float *x, signed char *xq, float *xd, float *xsum, int n,
+                                   hipStream_t stream) {
+    if (n < 32) return hipErrorInvalidValue;
+    if (!x || !xq || !xd || !xsum || misaligned4(x) || misaligned4(xq) || misaligned4(xd) ||
+        misaligned4(xsum))
+        return hipErrorInvalidValue;
+    return mgq::quantize_q8_1_launch(x, reinterpret_cast<int8_t *>(xq), xd, xsum, n, stream);
+}
+
+hipError_t launch_quantize_q8_1(const float *x, signed char *xq, float *xd, float *xsum, int n) {
+    return launch_quantize_q8_1_ex(x, xq, xd, xsum, n, nullptr);
+}
+
+hipError_t launch_matvec_q4k_dp4a_ex(const unsigned char *w, const signed char *xq,
+                                     const float *xd, const float *xsum, float *y, int out_dim,
+                                     int bpr, hipStream_t stream) {
+    if (out_dim <= 0 || bpr <= 0) return hipErrorInvalidValue;
+    if (!w || !xq || !xd || !xsum || !y || misaligned4(w) || misaligned4(xq) || misaligned4(xd) ||
+        misaligned4(xsum) || misaligned4(y))
+        return hipErrorInvalidValue;
+    if ((int64_t)bpr * 256 > kMaxI32) return hipErrorInvalidValue;
+    return mgq::gemv_q8_launch(w, reinterpret_cast<const int8_t *>(xq), xd, xsum, y, out_dim, bpr,
+                               stream);
+}
+
+hipError_t launch_matvec_q4k_dp4a(const unsigned char *w, const signed char *xq, const float *xd,
+                                  const float *xsum, float *y, int out_dim, int bpr) {
+    return launch_matvec_q4k_dp4a_ex(w, xq, xd, xsum, y, out_dim, bpr, nullptr);
+}
+
 hipError_t launch_gemm_q4k_f16(const unsigned char *w_q4, const uint16_t *a_f16, float *c,
                                int out_dim, int blocks_per_row, int m_tokens,
                                hipStream_t stream) {

@@ -118,8 +118,9 @@ __device__ __forceinline__ float quad_xor(float v) {
 
 // LDS layout of one work-group (rows R, all bpr blocks of K):
 //   atab  [bpr][8 mfma c][4 lane-group h][xh|xl][8 halves]   bpr*1024 B
-//   zero  16 B of zeros                                      at bpr*1024
-//   meta  [bpr][corr[8] | xsum[8]] f32                       bpr*64 B
+//         (Q8: the int8 activations xq, bpr*256 B)
+//   zero  16 B of zeros
+//   meta  [bpr][corr[8] | xsum[8]] f32 (Q8: [xd[8] | xsum[8]]) bpr*64 B
 //   stage 2 (1 if bpr <= C) x SB bytes: weight bytes of R rows x C blocks,
 //         row-major over (row, block, 16-byte piece), rows padded to an odd
 //         number of pieces
@@ -139,12 +140,14 @@ struct MfmaLayout {
 __host__ __device__ constexpr int stage_row_pieces(int C) { return (9 * C) | 1; }
 
 __host__ __device__ inline MfmaLayout mfma_layout(int bpr, int R, int C, int NW, int rounds,
-                                                  bool db) {
+                                                  bool db, bool q8 = false) {
     MfmaLayout L;
     L.bpr = bpr; L.R = R; L.C = C; L.NW = NW;
     // wave loads per stage, padded so every wavefront issues the same count
     L.I = ((R * 9 * C + 63) / 64 + NW - 1) / NW * NW;
-    L.zero = (uint32_t)bpr * 1024u;
+    // activation table: 1 KiB of f16 operands per block, or (Q8) the 256
+    // int8 activations of the block
+    L.zero = (uint32_t)bpr * (q8 ? 256u : 1024u);
     L.meta = L.zero + 16;
     L.stage = L.meta + (uint32_t)bpr * 64u;
     L.stage_bytes = (uint32_t)(R * stage_row_pieces(C) * 16);
@@ -171,13 +174,20 @@ __host__ __device__ inline MfmaLayout mfma_layout(int bpr, int R, int C, int NW,
 // (row, sub-block) pairs per lane.
 // DB: double-buffered LDS stage (one barrier per stage) or a single buffer
 // (two barriers per stage, half the LDS, so more work-groups fit per CU).
-template <int R, int C, int NW, int PF, bool DB, int XIT>
+// Q8: the dp4a matvec of kernels/matvec_q4k_dp4a.hip:52-106 on the same
+// weight stream: activations arrive as int8 xq with per-sub-block scale xd and
+// sum xsum; each lane dots its 32 qs bytes (4 sub-block halves) with
+// v_dot4_i32_i8 and applies xd*(d*sc*isum - dmin*m*xsum).
+template <int R, int C, int NW, int PF, bool DB, int XIT, bool Q8>
 __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__restrict__ w,
                                                             const float *__restrict__ x,
+                                                            const int8_t *__restrict__ xq,
+                                                            const float *__restrict__ xdv,
+                                                            const float *__restrict__ xsv,
                                                             float *__restrict__ y, int n,
                                                             int bpr, int rounds) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    const MfmaLayout Lo = mfma_layout(bpr, R, C, NW, rounds, DB);
+    const MfmaLayout Lo = mfma_layout(bpr, R, C, NW, rounds, DB, Q8);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
     float *meta = reinterpret_cast<float *>(lds + Lo.meta);
@@ -236,6 +246,35 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     // lane loads its XIT chunks before any weight load is issued: the loads
     // complete in issue order, so waiting for x leaves the weight stream in
     // flight while the table is built.
+  if constexpr (Q8) {
+    // Q8: copy xq (16 B items 0 .. 16*bpr), then xd and xsum (4 floats per
+    // item) to LDS, loads again issued ahead of the weight stream
+    const int nq = bpr * 16, nitems = bpr * 20;
+    u32x4 cv[XIT];
+#pragma unroll
+    for (int it = 0; it < XIT; ++it) {
+        const int i = std::min(tid + it * NW * 64, nitems - 1);
+        const uint8_t *src = i < nq ? reinterpret_cast<const uint8_t *>(xq) + (size_t)i * 16
+                           : i < nq + 2 * bpr ? reinterpret_cast<const uint8_t *>(xdv + (size_t)(i - nq) * 4)
+                                              : reinterpret_cast<const uint8_t *>(xsv + (size_t)(i - nq - 2 * bpr) * 4);
+        cv[it] = *reinterpret_cast<const u32x4 *>(src);
+    }
+#pragma unroll
+    for (int f = 0; f < PF; ++f) gload(f, stg[f]);
+#pragma unroll
+    for (int it = 0; it < XIT; ++it) {
+        const int i = tid + it * NW * 64;
+        if (i >= nitems) break;
+        uint32_t dst;
+        if (i < nq) {
+            dst = (uint32_t)i * 16u;
+        } else {
+            const int k = (i < nq + 2 * bpr) ? i - nq : i - nq - 2 * bpr;  // 4-float chunk
+            dst = Lo.meta + (uint32_t)(((k >> 1) * 16 + (i < nq + 2 * bpr ? 0 : 8) + 4 * (k & 1)) * 4);
+        }
+        *reinterpret_cast<u32x4 *>(lds + dst) = cv[it];
+    }
+  } else {
     const int nitems = bpr * 32;
     f32x4 xv0[XIT], xv1[XIT];
 #pragma unroll
@@ -289,6 +328,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         *reinterpret_cast<half8 *>(ent) = hh;
         *reinterpret_cast<half8 *>(ent + 16) = hl;
     }
+  }
     // (the barrier before the first stage is computed also orders the table)
     lstore(0, stg[0]);
 
@@ -325,6 +365,41 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         const float t2 = (float)(mnq & 0xFFu) * mb[8] + (float)((mnq >> 8) & 0xFFu) * mb[9];
         return d * t1 - dmin * t2;
     };
+    // Q8: this lane's 32 qs bytes of W row n16 in block b are elements
+    // 16*(g&1) .. +15 of sub-blocks s0 = 2*(g>>1) (low nibbles of q0), s0+1
+    // (high), s0+4 (low nibbles of q1) and s0+5 (high); the other halves of
+    // those sub-blocks sit in lane group g^1. The dmin*m*xsum term is added by
+    // the lanes with g even only.
+    auto decode_q8 = [&](const u32x4 &hd, int b, const u32x4 &q0, const u32x4 &q1) -> float {
+        const int s0 = 2 * (g >> 1), half = g & 1;
+        const uint8_t *xb = lds + (size_t)b * 256 + 16 * half;
+        const u32x4 x0 = *reinterpret_cast<const u32x4 *>(xb + s0 * 32);
+        const u32x4 x1 = *reinterpret_cast<const u32x4 *>(xb + (s0 + 1) * 32);
+        const u32x4 x4 = *reinterpret_cast<const u32x4 *>(xb + (s0 + 4) * 32);
+        const u32x4 x5 = *reinterpret_cast<const u32x4 *>(xb + (s0 + 5) * 32);
+        int i0 = 0, i1 = 0, i4 = 0, i5 = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            i0 = __builtin_amdgcn_sdot4((int)(q0[j] & 0x0F0F0F0Fu), (int)x0[j], i0, false);
+            i1 = __builtin_amdgcn_sdot4((int)((q0[j] >> 4) & 0x0F0F0F0Fu), (int)x1[j], i1, false);
+            i4 = __builtin_amdgcn_sdot4((int)(q1[j] & 0x0F0F0F0Fu), (int)x4[j], i4, false);
+            i5 = __builtin_amdgcn_sdot4((int)((q1[j] >> 4) & 0x0F0F0F0Fu), (int)x5[j], i5, false);
+        }
+        const float d = half_bits_finite(hd[0]), dmin = half_bits_finite(hd[0] >> 16);
+        // sub-blocks s0, s0+1 are bytes s0, s0+1 of quad 0; s0+4, s0+5 of quad 1
+        const uint32_t shq = 8 * s0;
+        const uint32_t sc0 = scales4(0, hd[1], hd[3]) >> shq, sc1 = scales4(1, hd[1], hd[3]) >> shq;
+        const uint32_t mn0 = mins4(0, hd[2], hd[3]) >> shq, mn1 = mins4(1, hd[2], hd[3]) >> shq;
+        const float *mb = meta + b * 16;  // xd[8] | xsum[8]
+        const float mk = half ? 0.0f : dmin;
+        float r = mb[s0] * (d * (float)(sc0 & 0xFFu) * (float)i0 - mk * (float)(mn0 & 0xFFu) * mb[8 + s0]);
+        r += mb[s0 + 1] * (d * (float)((sc0 >> 8) & 0xFFu) * (float)i1 -
+                           mk * (float)((mn0 >> 8) & 0xFFu) * mb[9 + s0]);
+        r += mb[s0 + 4] * (d * (float)(sc1 & 0xFFu) * (float)i4 - mk * (float)(mn1 & 0xFFu) * mb[12 + s0]);
+        r += mb[s0 + 5] * (d * (float)((sc1 >> 8) & 0xFFu) * (float)i5 -
+                           mk * (float)((mn1 >> 8) & 0xFFu) * mb[13 + s0]);
+        return r;
+    };
 
     // two LDS stage buffers only when double-buffered and K spans > 1 stage
     // (the layout allocates exactly that); otherwise one buffer, refilled
@@ -352,6 +427,16 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
             const u32x4 qa0 = piece(rowA + n16, cbA, 1 + g), qa1 = piece(rowA + n16, cbA, 5 + g);
             const u32x4 qb0 = piece(rowB + n16, cbB, 1 + g), qb1 = piece(rowB + n16, cbB, 5 + g);
             const u32x4 hdA = piece(rowA + n16, cbA, 0), hdB = piece(rowB + n16, cbB, 0);
+          if constexpr (Q8) {
+            const float cA = decode_q8(hdA, bA, qa0, qa1);
+            const float cB = decode_q8(hdB, bBc, qb0, qb1);
+            if (R == 32) {
+                yaccA += cA;
+                yaccB += cB;
+            } else {
+                yaccA += hasB ? cA + cB : cA;
+            }
+          } else {
             f32x4 accA = {0.f, 0.f, 0.f, 0.f}, accB = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
@@ -377,6 +462,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
             } else {
                 yaccA += hasB ? cA + cB : cA;
             }
+          }
         }
         const bool group_end = (t == stages - 1);
         if (group_end) {
@@ -431,7 +517,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     __syncthreads();
     for (int i = tid; i < my_groups * R; i += NW * 64) {
         const int r = ((int)blockIdx.x + (i / R) * (int)gridDim.x) * R + (i % R);
-        if (r < n) y[r] = reinterpret_cast<const float *>(lds + Lo.ybuf)[i];
+        if (r < n) {
+            const float v = reinterpret_cast<const float *>(lds + Lo.ybuf)[i];
+            y[r] = (Q8 && !isfinite(v)) ? 0.0f : v;  // Q8: the reference's clamp
+        }
     }
 }
 
@@ -453,35 +542,43 @@ static int device_cus() {
     return cus[dev];
 }
 
+// Activation operands of one launch: f32 x, or (Q8) int8 xq with its
+// per-sub-block scale xd and sum xsum.
+struct GemvAct {
+    const float *x;
+    const int8_t *xq;
+    const float *xd, *xsum;
+};
+
 // Allows the kernel the whole 160 KiB of gfx950 LDS (once per process).
-template <int R, int C, int NW, int PF, bool DB, int XIT>
+template <int R, int C, int NW, int PF, bool DB, int XIT, bool Q8>
 static hipError_t lds_attr() {
     static const hipError_t attr = hipFuncSetAttribute(
-        (const void *)gemv_mfma_kernel<R, C, NW, PF, DB, XIT>,
+        (const void *)gemv_mfma_kernel<R, C, NW, PF, DB, XIT, Q8>,
         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     return attr;
 }
 
-template <int R, int C, int NW, int PF, bool DB>
+template <int R, int C, int NW, int PF, bool DB, bool Q8>
 static hipError_t lds_attr_all() {
-    hipError_t e = lds_attr<R, C, NW, PF, DB, 1>();
-    if (e == hipSuccess) e = lds_attr<R, C, NW, PF, DB, 2>();
-    if (e == hipSuccess) e = lds_attr<R, C, NW, PF, DB, 4>();
-    if (e == hipSuccess) e = lds_attr<R, C, NW, PF, DB, 8>();
+    hipError_t e = lds_attr<R, C, NW, PF, DB, 1, Q8>();
+    if (e == hipSuccess) e = lds_attr<R, C, NW, PF, DB, 2, Q8>();
+    if (e == hipSuccess) e = lds_attr<R, C, NW, PF, DB, 4, Q8>();
+    if (e == hipSuccess) e = lds_attr<R, C, NW, PF, DB, 8, Q8>();
     return e;
 }
 
-template <int R, int C, int NW, int PF, bool DB, int XIT>
-static hipError_t launch_xit(const uint8_t *w, const float *x, float *y, int n, int bpr,
+template <int R, int C, int NW, int PF, bool DB, int XIT, bool Q8>
+static hipError_t launch_xit(const uint8_t *w, const GemvAct &a, float *y, int n, int bpr,
                              hipStream_t stream, bool persistent) {
-    auto kern = gemv_mfma_kernel<R, C, NW, PF, DB, XIT>;
-    const hipError_t attr = lds_attr<R, C, NW, PF, DB, XIT>();
+    auto kern = gemv_mfma_kernel<R, C, NW, PF, DB, XIT, Q8>;
+    const hipError_t attr = lds_attr<R, C, NW, PF, DB, XIT, Q8>();
     if (attr != hipSuccess) return attr;
     const long groups = (n + R - 1) / R;
     long grid = groups, rounds = 1;
     if (persistent) {
         static const int occ_env = env_int("MGQ_GEMV_OCC", 0);
-        const size_t base = mfma_layout(bpr, R, C, NW, 8, DB).total;
+        const size_t base = mfma_layout(bpr, R, C, NW, 8, DB, Q8).total;
         int occ = 0;  // resident work-groups per CU (registers and LDS)
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)kern, NW * 64,
                                                          base) != hipSuccess || occ <= 0)
@@ -491,22 +588,24 @@ static hipError_t launch_xit(const uint8_t *w, const float *x, float *y, int n, 
         rounds = (groups + maxgrid - 1) / maxgrid;
         grid = (groups + rounds - 1) / rounds;  // balanced: every WG gets `rounds` groups (or one fewer)
     }
-    const MfmaLayout Lo = mfma_layout(bpr, R, C, NW, (int)rounds, DB);
+    const MfmaLayout Lo = mfma_layout(bpr, R, C, NW, (int)rounds, DB, Q8);
     if (Lo.total > 160 * 1024) return hipErrorNotSupported;
-    kern<<<(unsigned)grid, NW * 64, Lo.total, stream>>>(w, x, y, n, bpr, (int)rounds);
+    kern<<<(unsigned)grid, NW * 64, Lo.total, stream>>>(w, a.x, a.xq, a.xd, a.xsum, y, n, bpr,
+                                                        (int)rounds);
     return hipGetLastError();
 }
 
-// The activation chunks per lane (XIT) are a compile-time count so they stay
-// in registers: 1, 2, 4 or 8 (covering bpr <= 8*NW*64/32 blocks).
-template <int R, int C, int NW, int PF, bool DB>
-static hipError_t launch_cfg(const uint8_t *w, const float *x, float *y, int n, int bpr,
+// The activation loads per lane (XIT) are a compile-time count so they stay
+// in registers: 1, 2, 4 or 8 (f32: 8-float chunks, bpr*32 of them; Q8:
+// 16-byte items, bpr*20 of them).
+template <int R, int C, int NW, int PF, bool DB, bool Q8>
+static hipError_t launch_cfg(const uint8_t *w, const GemvAct &a, float *y, int n, int bpr,
                              hipStream_t stream, bool persistent) {
-    const int need = (bpr * 32 + NW * 64 - 1) / (NW * 64);
-    if (need <= 1) return launch_xit<R, C, NW, PF, DB, 1>(w, x, y, n, bpr, stream, persistent);
-    if (need <= 2) return launch_xit<R, C, NW, PF, DB, 2>(w, x, y, n, bpr, stream, persistent);
-    if (need <= 4) return launch_xit<R, C, NW, PF, DB, 4>(w, x, y, n, bpr, stream, persistent);
-    if (need <= 8) return launch_xit<R, C, NW, PF, DB, 8>(w, x, y, n, bpr, stream, persistent);
+    const int need = (bpr * (Q8 ? 20 : 32) + NW * 64 - 1) / (NW * 64);
+    if (need <= 1) return launch_xit<R, C, NW, PF, DB, 1, Q8>(w, a, y, n, bpr, stream, persistent);
+    if (need <= 2) return launch_xit<R, C, NW, PF, DB, 2, Q8>(w, a, y, n, bpr, stream, persistent);
+    if (need <= 4) return launch_xit<R, C, NW, PF, DB, 4, Q8>(w, a, y, n, bpr, stream, persistent);
+    if (need <= 8) return launch_xit<R, C, NW, PF, DB, 8, Q8>(w, a, y, n, bpr, stream, persistent);
     return hipErrorNotSupported;
 }
 
@@ -514,30 +613,30 @@ static hipError_t launch_cfg(const uint8_t *w, const float *x, float *y, int n, 
 // stages in flight, LDS double buffer). Few row groups (small N): one 16-row
 // work-group per CU, with the whole row in one stage when K <= 3584. Many row
 // groups: persistent 32-row work-groups streamed 8 blocks at a time.
-static hipError_t launch_any(int cfg, const uint8_t *w, const float *x, float *y, int n, int bpr,
-                             hipStream_t stream) {
+template <bool Q8>
+static hipError_t launch_any(int cfg, const uint8_t *w, const GemvAct &a, float *y, int n,
+                             int bpr, hipStream_t stream) {
     switch (cfg) {
-        case 0: return launch_cfg<32, 8, 8, 1, false>(w, x, y, n, bpr, stream, true);
-        case 1: return launch_cfg<16, 14, 7, 1, true>(w, x, y, n, bpr, stream, false);
-        case 2: return launch_cfg<16, 16, 8, 1, true>(w, x, y, n, bpr, stream, false);
-        case 3: return launch_cfg<16, 16, 8, 2, true>(w, x, y, n, bpr, stream, false);
-        case 4: return launch_cfg<16, 16, 8, 3, true>(w, x, y, n, bpr, stream, false);
-        case 5: return launch_cfg<16, 8, 8, 4, true>(w, x, y, n, bpr, stream, false);
-        case 6: return launch_cfg<16, 8, 4, 4, true>(w, x, y, n, bpr, stream, false);
+        case 0: return launch_cfg<32, 8, 8, 1, false, Q8>(w, a, y, n, bpr, stream, true);
+        case 1: return launch_cfg<16, 14, 7, 1, true, Q8>(w, a, y, n, bpr, stream, false);
+        case 2: return launch_cfg<16, 16, 8, 1, true, Q8>(w, a, y, n, bpr, stream, false);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t gemv_prepare() {
-    hipError_t e = lds_attr_all<32, 8, 8, 1, false>();
-    if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, true>();
-    if (e == hipSuccess) e = lds_attr_all<16, 16, 8, 1, true>();
+    hipError_t e = lds_attr_all<32, 8, 8, 1, false, false>();
+    if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, true, false>();
+    if (e == hipSuccess) e = lds_attr_all<16, 16, 8, 1, true, false>();
+    if (e == hipSuccess) e = lds_attr_all<32, 8, 8, 1, false, true>();
+    if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, true, true>();
+    if (e == hipSuccess) e = lds_attr_all<16, 16, 8, 1, true, true>();
     return e;
 }
 
-hipError_t gemv_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
-                            hipStream_t stream) {
-    if (((uintptr_t)w & 15u) || ((uintptr_t)x & 15u)) return hipErrorNotSupported;
+template <bool Q8>
+static hipError_t mfma_dispatch(const uint8_t *w, const GemvAct &a, float *y, int n, int bpr,
+                                hipStream_t stream) {
     static const int force = env_int("MGQ_GEMV_CFG", -1);  // tuning override
     int cfg;
     if (force >= 0) {
@@ -550,10 +649,26 @@ hipError_t gemv_mfma_launch(const uint8_t *w, const float *x, float *y, int n, i
         else if (bpr <= 14) cfg = 1;
         else cfg = 2;
     }
-    hipError_t e = launch_any(cfg, w, x, y, n, bpr, stream);
+    hipError_t e = launch_any<Q8>(cfg, w, a, y, n, bpr, stream);
     // LDS too small for the double-buffered stages: single-buffered persistent
-    if (e == hipErrorNotSupported && cfg != 0) e = launch_any(0, w, x, y, n, bpr, stream);
+    if (e == hipErrorNotSupported && cfg != 0) e = launch_any<Q8>(0, w, a, y, n, bpr, stream);
     return e;
+}
+
+hipError_t gemv_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                            hipStream_t stream) {
+    if (((uintptr_t)w & 15u) || ((uintptr_t)x & 15u)) return hipErrorNotSupported;
+    return mfma_dispatch<false>(w, GemvAct{x, nullptr, nullptr, nullptr}, y, n, bpr, stream);
+}
+
+hipError_t gemv_q8_launch(const uint8_t *w, const int8_t *xq, const float *xd, const float *xsum,
+                          float *y, int n, int bpr, hipStream_t stream) {
+    const bool aligned = !(((uintptr_t)w | (uintptr_t)xq | (uintptr_t)xd | (uintptr_t)xsum) & 15u);
+    if (aligned) {
+        const hipError_t e = mfma_dispatch<true>(w, GemvAct{nullptr, xq, xd, xsum}, y, n, bpr, stream);
+        if (e != hipErrorNotSupported) return e;
+    }
+    return gemv_q8_generic_launch(w, xq, xd, xsum, y, n, bpr, stream);
 }
 
 static int env_force_generic() {

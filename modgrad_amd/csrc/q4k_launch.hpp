@@ -39,6 +39,17 @@ hipError_t gemv_batched_mfma_launch(const uint8_t *w, const float *X, float *Y, 
                                     int batch, void *workspace, size_t workspace_bytes,
                                     hipStream_t stream);
 
+// Q8_1 activation quantizer (bit-identical to the reference's) and the dp4a
+// matvec on the quantized activations: the matrix-core kernel's Q8 mode when
+// every pointer is 16-byte aligned and the shape fits LDS, else the
+// vector-ALU kernel.
+hipError_t quantize_q8_1_launch(const float *x, int8_t *xq, float *xd, float *xsum, int n,
+                                hipStream_t stream);
+hipError_t gemv_q8_launch(const uint8_t *w, const int8_t *xq, const float *xd, const float *xsum,
+                          float *y, int n, int bpr, hipStream_t stream);
+hipError_t gemv_q8_generic_launch(const uint8_t *w, const int8_t *xq, const float *xd,
+                                  const float *xsum, float *y, int n, int bpr, hipStream_t stream);
+
 hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n, int bpr,
                            int m_tokens, hipStream_t stream);
 

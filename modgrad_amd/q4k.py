@@ -133,6 +133,19 @@ class kern:
     def matvec_q4k(w: int, x: int, y: int, out_dim: int, bpr: int) -> None:
         _chk(_lib.load().launch_matvec_q4k(w, x, y, out_dim, bpr), "matvec_q4k")
 
+    @staticmethod
+    def quantize_q8_1(x: int, xq: int, xd: int, xsum: int, n: int, stream=None) -> None:
+        """rocm.rs:970-972: int8 activations + per-32 scale and sum."""
+        _chk(_lib.load().launch_quantize_q8_1_ex(x, xq, xd, xsum, n, _stream_ptr(stream)),
+             "quantize_q8_1")
+
+    @staticmethod
+    def matvec_q4k_dp4a(w: int, xq: int, xd: int, xsum: int, y: int, out_dim: int, bpr: int,
+                        stream=None) -> None:
+        """rocm.rs:973-976: the dp4a matvec on quantize_q8_1's output."""
+        _chk(_lib.load().launch_matvec_q4k_dp4a_ex(w, xq, xd, xsum, y, out_dim, bpr,
+                                                   _stream_ptr(stream)), "matvec_q4k_dp4a")
+
     # additive entry points -------------------------------------------------
     @staticmethod
     def matvec_q4k_ex(w: int, x: int, y: int, out_dim: int, k_elems: int,

@@ -61,6 +61,8 @@ def lib() -> ctypes.CDLL:
         "orq_cpu_matvec_q4k": (i, [P, P, P, i, i, i]),
         "orq_cpu_has_avx512": (i, []),
         "orq_fill_smooth": (None, [P, z]),
+        "orq_quantize_q8_1": (None, [P, i, P, P, P]),
+        "orq_gemv_q4k_dp4a_f64": (None, [P, P, P, P, i, i, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -181,6 +183,31 @@ def gemv_batched(w: np.ndarray, X: np.ndarray, out_dim: int, bpr: int):
     A = np.empty((batch, out_dim), dtype=np.float64)
     lib().orq_gemv_batched_f64_abs(_p(w), _p(X), _p(Y), _p(A), out_dim, bpr, batch)
     return Y, A
+
+
+def quantize_q8_1(x: np.ndarray):
+    """(xq int8[n/32*32], xd f32[n/32], xsum f32[n/32]) -- matvec_q4k_dp4a.hip:29-50."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    nsub = x.size // 32
+    xq = np.zeros(nsub * 32, dtype=np.int8)
+    xd = np.zeros(nsub, dtype=np.float32)
+    xs = np.zeros(nsub, dtype=np.float32)
+    lib().orq_quantize_q8_1(_p(x), x.size, _p(xq), _p(xd), _p(xs))
+    return xq, xd, xs
+
+
+def gemv_dp4a(w: np.ndarray, xq: np.ndarray, xd: np.ndarray, xsum: np.ndarray, out_dim: int,
+              bpr: int):
+    """(y f64, absterm f64) -- the dp4a matvec of matvec_q4k_dp4a.hip:52-106 in f64."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    xq = np.ascontiguousarray(xq, dtype=np.int8)
+    xd = np.ascontiguousarray(xd, dtype=np.float32)
+    xsum = np.ascontiguousarray(xsum, dtype=np.float32)
+    assert xq.size >= bpr * BLOCK_ELEMS and xd.size >= bpr * 8
+    y = np.empty(out_dim, dtype=np.float64)
+    a = np.empty(out_dim, dtype=np.float64)
+    lib().orq_gemv_q4k_dp4a_f64(_p(w), _p(xq), _p(xd), _p(xsum), out_dim, bpr, _p(y), _p(a))
+    return y, a
 
 
 def gemm_f16(w: np.ndarray, a_f16: np.ndarray, out_dim: int, bpr: int, rows=None):

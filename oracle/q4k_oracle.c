@@ -290,6 +290,65 @@ void orq_gemv_flat_f64_abs(const uint8_t *w, const float *x, float *y,
     }
 }
 
+/* kernels/matvec_q4k_dp4a.hip:29-50 (quantize_q8_1_kernel). */
+void orq_quantize_q8_1(const float *x, int n, int8_t *xq, float *xd, float *xsum) {
+    const int nsub = n / 32;
+    for (int s = 0; s < nsub; ++s) {
+        const float *xs = x + (size_t)s * 32;
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(xs[i]));
+        float d = amax / 127.0f;
+        float id = (amax > 0.0f) ? 127.0f / amax : 0.0f;
+        if (!isfinite(id)) { id = 0.0f; d = 0.0f; }
+        int sum = 0;
+        for (int i = 0; i < 32; ++i) {
+            const float p = xs[i] * id;
+            const float r = rintf(p);
+            /* float -> int as the GPU converts: NaN -> 0, saturating */
+            int q = isnan(r) ? 0 : (r >= 2147483647.0f ? 2147483647 : (r <= -2147483648.0f ? (-2147483647 - 1) : (int)r));
+            q = q < -127 ? -127 : (q > 127 ? 127 : q);
+            xq[(size_t)s * 32 + i] = (int8_t)q;
+            sum += q;
+        }
+        xd[s] = d;
+        xsum[s] = (float)sum;
+    }
+}
+
+/* kernels/matvec_q4k_dp4a.hip:52-106 (matvec_q4k_dp4a_kernel), in f64. */
+void orq_gemv_q4k_dp4a_f64(const uint8_t *w, const int8_t *xq, const float *xd,
+                           const float *xsum, int out_dim, int bpr, double *y,
+                           double *absterm) {
+    for (int r = 0; r < out_dim; ++r) {
+        const uint8_t *wrow = w + (size_t)r * bpr * ORQ_BLOCK_BYTES;
+        double acc = 0.0, aabs = 0.0;
+        for (int s = 0; s < bpr * 8; ++s) {
+            const int blk = s >> 3, sub = s & 7;
+            const uint8_t *b = wrow + (size_t)blk * ORQ_BLOCK_BYTES;
+            float dw = orq_f16_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+            float dmw = orq_f16_to_f32((uint16_t)(b[2] | (b[3] << 8)));
+            if (!isfinite(dw)) dw = 0.0f;
+            if (!isfinite(dmw)) dmw = 0.0f;
+            uint8_t sc, m;
+            orq_get_scale_min_k4(sub, b + 4, &sc, &m);
+            const int g = sub >> 1, hi = sub & 1;
+            const uint8_t *qs = b + 16 + g * 32;
+            const int8_t *xv = xq + (size_t)s * 32;
+            long isum = 0;
+            for (int l = 0; l < 32; ++l) {
+                const int nib = hi ? (qs[l] >> 4) : (qs[l] & 15);
+                isum += (long)nib * (long)xv[l];
+            }
+            const double t1 = (double)dw * (double)sc * (double)isum;
+            const double t2 = (double)dmw * (double)m * (double)xsum[s];
+            acc += (double)xd[s] * (t1 - t2);
+            aabs += fabs((double)xd[s]) * (fabs(t1) + fabs(t2));
+        }
+        y[r] = isfinite(acc) ? acc : 0.0;
+        if (absterm) absterm[r] = aabs;
+    }
+}
+
 void orq_gemv_batched_f64_abs(const uint8_t *w, const float *X, float *Y,
                               double *absdot, int out_dim, int bpr, int batch) {
     size_t k = (size_t)bpr * ORQ_BLOCK_ELEMS;

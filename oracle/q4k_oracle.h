@@ -73,6 +73,23 @@ void orq_gemm_f16_f64(const uint8_t *w, const uint16_t *a_f16, float *c,
                       double *absdot, int out_dim, int bpr, int m_tokens,
                       const int *rows, int n_rows);
 
+/* Q8_1 activation quantizer: kernels/matvec_q4k_dp4a.hip:29-50. Per 32-value
+ * sub-block s < n/32: amax = max|x|, d = amax/127, id = amax > 0 ? 127/amax : 0
+ * (non-finite id -> id = d = 0), q = clamp(rint(x*id), -127, 127) (round half
+ * to even; a NaN product converts to 0, as the GPU's float->int conversion
+ * does), xd[s] = d, xsum[s] = (float)sum q. */
+void orq_quantize_q8_1(const float *x, int n, int8_t *xq, float *xd, float *xsum);
+
+/* dp4a Q4_K matvec: kernels/matvec_q4k_dp4a.hip:52-106, evaluated in f64 with
+ * the integer dots exact: y[r] = sum_s xd[s]*(dw*sc_s*isum_s - dmw*m_s*xsum[s]),
+ * isum_s = sum of nibble*xq over the sub-block (canonical order); a
+ * non-finite row result becomes 0 (the reference clamps it). absterm[r] =
+ * sum_s |xd[s]|*(|dw*sc_s*isum_s| + |dmw*m_s*xsum[s]|), the scale of the
+ * rounding any f32 evaluation of the same formula can add. */
+void orq_gemv_q4k_dp4a_f64(const uint8_t *w, const int8_t *xq, const float *xd,
+                           const float *xsum, int out_dim, int bpr, double *y,
+                           double *absterm);
+
 /* CPU timing baseline: kfd::llm::matvec (llm.rs:468-534) with the fused
  * dequant-dot of llm.rs:684-806 (AVX-512 when the host has it, else scalar),
  * parallel over rows. threads <= 0 -> all cores. Returns 1 if AVX-512 used. */

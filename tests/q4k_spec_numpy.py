@@ -44,3 +44,31 @@ def dequantize(data: np.ndarray) -> np.ndarray:
     m1 = (dmin[:, None] * m.astype(np.float32))[:, sub]
     out = (d1 * q).astype(np.float32) - m1                      # two roundings
     return out.astype(np.float32).reshape(nb * 256)
+
+
+def nibbles(data: np.ndarray) -> np.ndarray:
+    """Canonical-order quants q[p] in 0..15 per block: int64 [nb, 256]."""
+    blocks = np.asarray(data, np.uint8).reshape(-1, 144)
+    qs = blocks[:, 16:144]
+    p = np.arange(256)
+    byte = qs[:, 32 * (p // 64) + p % 32].astype(np.int64)
+    return np.where((p // 32) % 2 == 0, byte & 15, byte >> 4)
+
+
+def quantize_q8_1(x: np.ndarray):
+    """Q8_1 activation quantizer in numpy float32 arithmetic (written from the
+    description: per 32 values, d = amax/127, id = 127/amax (0 when amax is
+    0 or 127/amax is not finite, which also zeroes d), q = clamp(rint(x*id)))."""
+    x = np.asarray(x, np.float32).reshape(-1, 32)
+    amax = np.max(np.abs(x), axis=1)
+    with np.errstate(divide="ignore", over="ignore", invalid="ignore"):
+        d = (amax / np.float32(127.0)).astype(np.float32)
+        idv = np.where(amax > 0, np.float32(127.0) / np.where(amax > 0, amax, 1), 0).astype(np.float32)
+        bad = ~np.isfinite(idv)
+        idv[bad] = 0
+        d[bad] = 0
+        prod = (x * idv[:, None]).astype(np.float32)
+        r = np.rint(prod)
+    r = np.where(np.isnan(r), 0, r)
+    q = np.clip(r, -127, 127).astype(np.int8)
+    return q.ravel(), d, q.astype(np.int64).sum(axis=1).astype(np.float32)

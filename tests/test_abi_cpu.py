@@ -41,6 +41,19 @@ def test_matvec_rejects_nonpositive_dims(L):
     assert L.launch_matvec_q4k(FAKE, FAKE, FAKE, 16, 1 << 24) == INVALID  # K overflows int
 
 
+def test_dp4a_path_rejects_bad_args(L):
+    # launch_quantize_q8_1: fewer than one 32-value sub-block, null, misaligned
+    assert L.launch_quantize_q8_1(FAKE, FAKE, FAKE, FAKE, 31) == INVALID
+    assert L.launch_quantize_q8_1(FAKE, FAKE, FAKE, FAKE, 0) == INVALID
+    assert L.launch_quantize_q8_1(None, FAKE, FAKE, FAKE, 64) == INVALID
+    assert L.launch_quantize_q8_1(FAKE, FAKE + 1, FAKE, FAKE, 64) == INVALID
+    # launch_matvec_q4k_dp4a: reference checks (matvec_q4k_dp4a.hip:111) + pointers
+    assert L.launch_matvec_q4k_dp4a(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 14) == INVALID
+    assert L.launch_matvec_q4k_dp4a(FAKE, FAKE, FAKE, FAKE, FAKE, 16, 0) == INVALID
+    assert L.launch_matvec_q4k_dp4a(FAKE, None, FAKE, FAKE, FAKE, 16, 1) == INVALID
+    assert L.launch_matvec_q4k_dp4a(FAKE, FAKE, FAKE, FAKE + 2, FAKE, 16, 1) == INVALID
+
+
 def test_matvec_rejects_null_and_misaligned(L):
     assert L.launch_matvec_q4k(None, FAKE, FAKE, 16, 1) == INVALID
     assert L.launch_matvec_q4k(FAKE, None, FAKE, 16, 1) == INVALID

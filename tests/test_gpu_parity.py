@@ -346,3 +346,107 @@ def test_hipbuffer_matvec_q4k_host_roundtrip(L, orc):
     y_ref, a = orc.gemv(w, x, n, bpr)
     assert_gemv_close(y, y_ref, a)
     assert np.max(np.abs(y - y_ref)) < 0.02  # rocm_matvec_check.rs:49-54 gate
+
+
+# ------------------------------------------------------- dp4a / Q8_1 path --
+def run_q8(L, x: np.ndarray, off: int = 0):
+    """launch_quantize_q8_1 on x (device copy at byte offset `off`)."""
+    n = x.size
+    xt = dev(np.concatenate([np.zeros(off // 4, np.float32), x]))
+    nsub = n // 32
+    xq, xd, xs = filled_u8(nsub * 32 + 64, 0x5A), empty_f32(nsub + 4), empty_f32(nsub + 4)
+    _lib.check("quantize_q8_1", L.launch_quantize_q8_1(ptr(xt) + off, ptr(xq), ptr(xd), ptr(xs), n))
+    return (xq, xd, xs), (host(xq)[:nsub * 32].view(np.int8), host(xd)[:nsub], host(xs)[:nsub])
+
+
+def test_quantize_q8_1_bit_exact(L, orc):
+    note("quantize_q8_1 bit-exact")
+    rng = np.random.default_rng(91)
+    x = (rng.standard_normal(32 * 600) * rng.choice([1e-6, 1e-2, 1.0, 300.0], size=32 * 600))
+    x = x.astype(np.float32)
+    x[0:32] = 0.0
+    x[32:64] = np.float32(1e-40)          # 127/amax overflows: zero sub-block
+    x[64:96] = np.float32(3.0e38)
+    x[96:128] = (np.arange(32, dtype=np.float32) - 16) * np.float32(0.5)
+    x[128:160] = np.float32(7.0)
+    x[160] = np.float32(127.0)
+    x[161:166] = [0.5, 1.5, 2.5, -0.5, -2.5]  # halves: round to even
+    for off in (0, 4):                    # 16-byte aligned and 4-byte aligned input
+        _, (q, d, s) = run_q8(L, x, off)
+        rq, rd, rs = orc.quantize_q8_1(x)
+        assert np.array_equal(q, rq)
+        assert np.array_equal(d.view(np.uint32), rd.view(np.uint32))
+        assert np.array_equal(s, rs)
+
+
+def assert_dp4a_close(y, y_ref, absterm, tol=1e-5):
+    """Same formula in f32 (kernel) and f64 (oracle): only rounding differs."""
+    err = np.abs(y.astype(np.float64) - y_ref)
+    bad = np.nonzero(~(err <= tol * absterm + 1e-30))[0]
+    assert bad.size == 0, (bad[:5].tolist(), err[bad[:5]].tolist(), absterm[bad[:5]].tolist())
+
+
+@pytest.mark.parametrize("n,bpr", [(1, 1), (17, 3), (64, 14), (3584, 14), (700, 74), (4100, 17),
+                                   (30000, 14), (300, 100)])
+def test_dp4a_matvec_matches_oracle(L, orc, n, bpr):
+    # shapes that take each launch configuration of the matrix-core kernel's
+    # Q8 mode (few/many row groups, one/several stages, fallback to
+    # single-buffered stages)
+    note(f"dp4a n={n} bpr={bpr}")
+    rng = np.random.default_rng(n * 7 + bpr)
+    w = random_q4k_bytes(rng, n * bpr)
+    x = rng.standard_normal(bpr * 256).astype(np.float32)
+    (xq, xd, xs), (q, d, s) = run_q8(L, x)
+    wt, yt = dev(w), empty_f32(n)
+    _lib.check("dp4a", L.launch_matvec_q4k_dp4a(ptr(wt), ptr(xq), ptr(xd), ptr(xs), ptr(yt), n, bpr))
+    y_ref, absterm = orc.gemv_dp4a(w, q, d, s, n, bpr)
+    assert_dp4a_close(host(yt), y_ref, absterm)
+
+
+def test_dp4a_vector_alu_fallback_matches_oracle(L, orc):
+    # xq only 4-byte aligned: the vector-ALU dp4a kernel runs
+    note("dp4a misaligned activations")
+    n, bpr = 45, 5
+    rng = np.random.default_rng(93)
+    w = random_q4k_bytes(rng, n * bpr)
+    x = rng.standard_normal(bpr * 256).astype(np.float32)
+    q, d, s = orc.quantize_q8_1(x)
+    xq = dev(np.concatenate([np.zeros(4, np.int8), q]))
+    xdt, xst, wt, yt = dev(d), dev(s), dev(w), empty_f32(n)
+    _lib.check("dp4a", L.launch_matvec_q4k_dp4a(ptr(wt), ptr(xq) + 4, ptr(xdt), ptr(xst), ptr(yt), n, bpr))
+    y_ref, absterm = orc.gemv_dp4a(w, q, d, s, n, bpr)
+    assert_dp4a_close(host(yt), y_ref, absterm)
+
+
+@pytest.mark.parametrize("bias", [0.0, 100.0])
+def test_dp4a_reference_acceptance_check(L, orc, bias):
+    # examples/rocm_dp4a_check.rs:31-63: x = sin(0.21 i)*30 + bias,
+    # RMS_rel(dp4a GPU - f64 dequant-dot) < 0.02, on a seeded 7B shape
+    note(f"dp4a acceptance bias={bias}")
+    n, bpr = 3584, 14
+    w = orc.seeded_weight(orc.layer_seed(0, 0), n, bpr * 256)
+    x = (np.sin(np.arange(bpr * 256, dtype=np.float32) * np.float32(0.21)) * np.float32(30.0)
+         + np.float32(bias)).astype(np.float32)
+    (xq, xd, xs), _ = run_q8(L, x)
+    wt, yt = dev(w), empty_f32(n)
+    _lib.check("dp4a", L.launch_matvec_q4k_dp4a(ptr(wt), ptr(xq), ptr(xd), ptr(xs), ptr(yt), n, bpr))
+    y_ref, _ = orc.gemv(w, x, n, bpr)
+    y = host(yt).astype(np.float64)
+    rms_rel = np.sqrt(np.sum((y - y_ref) ** 2) / np.sum(y_ref.astype(np.float64) ** 2))
+    assert rms_rel < 0.02
+
+
+def test_dp4a_nonfinite_rows_are_zero(L, orc):
+    # an Inf activation gives xd = Inf and a non-finite row sum: written as 0
+    note("dp4a non-finite clamp")
+    n, bpr = 40, 2
+    w = orc.seeded_weight(94, n, bpr * 256)
+    x = orc.normal(95, bpr * 256)
+    x[3] = np.inf
+    (xq, xd, xs), (q, d, s) = run_q8(L, x)
+    wt, yt = dev(w), empty_f32(n)
+    _lib.check("dp4a", L.launch_matvec_q4k_dp4a(ptr(wt), ptr(xq), ptr(xd), ptr(xs), ptr(yt), n, bpr))
+    y_ref, absterm = orc.gemv_dp4a(w, q, d, s, n, bpr)
+    y = host(yt)
+    assert np.all(np.isfinite(y))
+    assert np.array_equal(y == 0, y_ref == 0)

@@ -356,3 +356,87 @@ def test_cpu_baseline_matches_oracle(orc):
         y = np.empty(n, np.float32)
         orc.cpu_matvec(w, x, y, n, bpr, threads)
         assert np.all(np.abs(y - y_ref) <= 1e-5 * a)
+
+
+# --------------------------------------------------- dp4a / Q8_1 activations --
+def test_quantize_q8_1_matches_numpy_and_special_blocks(orc):
+    rng = np.random.default_rng(81)
+    x = (rng.standard_normal(32 * 64) * rng.choice([1e-3, 1.0, 50.0], size=32 * 64)).astype(np.float32)
+    x[0:32] = 0.0                                  # all-zero block
+    x[32:64] = np.float32(1e-40)                   # denormal max: 127/amax overflows -> zeroed
+    x[64:96] = np.float32(3.0e38) * np.sign(rng.standard_normal(32)).astype(np.float32)
+    x[96:128] = np.float32(2.5)                    # constant block: every q = 127
+    x[128:160] = (np.arange(32, dtype=np.float32) - 16) * np.float32(0.5)  # exact halves after scaling
+    xq, xd, xs = orc.quantize_q8_1(x)
+    rq, rd, rs = spec.quantize_q8_1(x)
+    assert np.array_equal(xq, rq)
+    assert np.array_equal(xd.view(np.uint32), rd.view(np.uint32))
+    assert np.array_equal(xs, rs)
+    assert np.all(xq[0:64] == 0) and xd[0] == 0 and xd[1] == 0
+    assert np.all(xq[96:128] == 127) and xs[3] == 32 * 127
+    assert np.all(np.abs(xq.astype(int)) <= 127)
+
+
+def test_quantize_q8_1_rounds_half_to_even(orc):
+    # amax = 127 -> id = 1 exactly, so q = rint(x): 0.5 -> 0, 1.5 -> 2, 2.5 -> 2
+    x = np.zeros(32, np.float32)
+    x[0] = 127.0
+    x[1:6] = [0.5, 1.5, 2.5, -0.5, -2.5]
+    xq, xd, xs = orc.quantize_q8_1(x)
+    assert xq[1:6].tolist() == [0, 2, 2, 0, -2]
+    assert xd[0] == np.float32(1.0) and xs[0] == 127 + 2 + 2 - 2
+
+
+def test_dp4a_gemv_extracts_nibbles_in_canonical_order(orc):
+    # one block, d = 1, dmin = 0, every scale 1: y = xd * q[p] for xq = e_p
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.array([0x3C00], np.uint16).view(np.uint8)
+    sc = np.ones(8, np.uint8)
+    blk[4:16] = np.frombuffer(orc.pack_scales_mins(sc, np.zeros(8, np.uint8)), np.uint8)
+    blk[16:144] = np.random.default_rng(3).integers(0, 256, 128, dtype=np.uint8)
+    q = spec.nibbles(blk)[0]
+    xd = np.ones(8, np.float32)
+    xs = np.zeros(8, np.float32)
+    for p in (0, 1, 31, 32, 63, 64, 100, 191, 255):
+        xq = np.zeros(256, np.int8)
+        xq[p] = 1
+        y, _ = orc.gemv_dp4a(blk, xq, xd, xs, 1, 1)
+        assert y[0] == q[p], p
+
+
+def test_dp4a_gemv_matches_numpy_formula(orc):
+    rng = np.random.default_rng(82)
+    n, bpr = 7, 3
+    from tests.gpu_util import random_q4k_bytes
+    w = random_q4k_bytes(rng, n * bpr)
+    x = rng.standard_normal(bpr * 256).astype(np.float32)
+    xq, xd, xs = orc.quantize_q8_1(x)
+    y, a = orc.gemv_dp4a(w, xq, xd, xs, n, bpr)
+    blocks = w.reshape(n, bpr, 144)
+    q = spec.nibbles(w).reshape(n, bpr, 8, 32)
+    d = spec.half_bits_to_f32(blocks[:, :, 0:2].copy().view(np.uint16)[..., 0]).astype(np.float64)
+    dm = spec.half_bits_to_f32(blocks[:, :, 2:4].copy().view(np.uint16)[..., 0]).astype(np.float64)
+    sc, m = spec.unpack_scales(blocks.reshape(-1, 144)[:, 4:16])
+    sc = sc.reshape(n, bpr, 8).astype(np.float64)
+    m = m.reshape(n, bpr, 8).astype(np.float64)
+    isum = (q * xq.reshape(bpr, 8, 32)[None].astype(np.int64)).sum(axis=3)
+    t = xd.reshape(bpr, 8)[None].astype(np.float64) * (
+        d[..., None] * sc * isum - dm[..., None] * m * xs.reshape(bpr, 8)[None].astype(np.float64))
+    assert np.allclose(y, t.sum(axis=(1, 2)), rtol=1e-12, atol=0)
+    assert np.all(a >= np.abs(y))
+
+
+@pytest.mark.parametrize("bias", [0.0, 100.0])
+def test_dp4a_close_to_f32_gemv_reference_check(orc, bias):
+    # the reference's own acceptance check (examples/rocm_dp4a_check.rs:31-63):
+    # x = sin(0.21 i) * 30 + bias, RMS_rel(dp4a - f32 dequant-dot) < 0.02
+    n, bpr = 64, 14
+    w = orc.seeded_weight(orc.layer_seed(0, 4), n, bpr * 256)
+    x = (np.sin(np.arange(bpr * 256, dtype=np.float32) * np.float32(0.21)) * np.float32(30.0)
+         + np.float32(bias)).astype(np.float32)
+    xq, xd, xs = orc.quantize_q8_1(x)
+    y8, _ = orc.gemv_dp4a(w, xq, xd, xs, n, bpr)
+    y32, _ = orc.gemv(w, x, n, bpr)
+    rms_rel = np.sqrt(np.sum((y8 - y32) ** 2) / np.sum(y32.astype(np.float64) ** 2))
+    assert rms_rel < 0.02
+    assert rms_rel > 1e-6  # int8 activations really are lossy
