@@ -287,6 +287,44 @@ def run_prefill(torch, q4k, args):
             "kernel": "mgq::gemm_q4k_f16_kernel"}
 
 
+def run_decode_dp4a(torch, q4k, args):
+    """The decode step of the default workload on the reference engine's
+    default arm (rocm_gemma.rs:298-306): per matvec, launch_quantize_q8_1 on
+    its x, then launch_matvec_q4k_dp4a. Accuracy is int8's: the check is the
+    reference's RMS-relative error < 0.02 against the f32 dequant-dot."""
+    from oracle import oracle as orc
+    wl = Workload(torch, decode_step_shapes())
+    q8 = []
+    for name, w, x, y, n, k in wl.launches:
+        nsub = k // 32
+        q8.append((torch.empty(k, dtype=torch.int8, device="cuda"),
+                   torch.empty(nsub, device="cuda"), torch.empty(nsub, device="cuda")))
+
+    def launch(st):
+        for (name, w, x, y, n, k), (xq, xd, xs) in zip(wl.launches, q8):
+            q4k.kern.quantize_q8_1(x.data_ptr(), xq.data_ptr(), xd.data_ptr(), xs.data_ptr(), k, st)
+            q4k.kern.matvec_q4k_dp4a(w.data_ptr(), xq.data_ptr(), xd.data_ptr(), xs.data_ptr(),
+                                     y.data_ptr(), n, k // BLOCK_ELEMS, st)
+    ms = time_captured(torch, launch, args.steps, args.warmup)
+    worst = 0.0
+    for name, w, x, y, n, k in (wl.launches[0], wl.launches[3], wl.launches[-1]):
+        bpr = k // BLOCK_ELEMS
+        idx = np.sort(np.random.default_rng(n).choice(n, size=min(512, n), replace=False))
+        wr = w.view(n, bpr * BLOCK_BYTES)[torch.from_numpy(idx).cuda()].cpu().numpy().ravel()
+        y_ref, _ = orc.gemv(wr, x.cpu().numpy(), idx.size, bpr)
+        yg = y.cpu().numpy()[idx].astype(np.float64)
+        worst = max(worst, float(np.sqrt(np.sum((yg - y_ref) ** 2) / np.sum(y_ref.astype(np.float64) ** 2))))
+    parity = (f"ok (RMS_rel vs f32 dequant-dot {worst:.2e} < 0.02)" if worst < 0.02
+              else f"FAIL: RMS_rel {worst:.3e}")
+    nbytes = wl.bytes_per_pass
+    return {"workload": "decode7b_dp4a: the decode7b step, each matvec as quantize_q8_1 + "
+                        "matvec_q4k_dp4a (226 launches), one graph",
+            "us_per_launch": round(ms * 1e3 / len(wl.launches), 3), "gbs": nbytes / (ms * 1e-3) / 1e9,
+            "bytes_per_launch": nbytes // len(wl.launches), "parity": parity,
+            "kernel": "mgq::gemv_mfma_kernel<..., Q8> (+ quantize_q8_1_kernel)",
+            "tokens_per_s": 1000.0 / ms, "ms_per_step": ms}
+
+
 TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                "gemv_mfma_decode7b_pmc.txt")
 
@@ -305,7 +343,8 @@ def profiled_traffic(workload: str):
 
 def run_side_workload(torch, q4k, args) -> int:
     """BASELINE configs 1, 4 and 5: one JSON line each, same field layout."""
-    fn = {"config1": run_config1, "batched": run_batched, "prefill": run_prefill}[args.workload]
+    fn = {"config1": run_config1, "batched": run_batched, "prefill": run_prefill,
+          "decode7b_dp4a": run_decode_dp4a}[args.workload]
     r = fn(torch, q4k, args)
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": "synthetic",
@@ -324,6 +363,9 @@ def run_side_workload(torch, q4k, args) -> int:
                                  "unit": "GB/s", "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
                                  "traffic": None, "kernel": r["kernel"],
                                  "avg_launch_bytes": r["bytes_per_launch"]}})
+    for key in ("tokens_per_s", "ms_per_step"):
+        if key in r:
+            out[key] = round(r[key], 4)
     log(f"{r['workload']}: {r['us_per_launch']} us per launch; parity {r['parity']}")
     print(json.dumps(out), flush=True)
     return 0
@@ -335,7 +377,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="decode7b",
-                    choices=["decode7b", "layer", "gateup", "config1", "batched", "prefill"])
+                    choices=["decode7b", "layer", "gateup", "config1", "batched", "prefill",
+                             "decode7b_dp4a"])
     ap.add_argument("--batch", type=int, default=8, help="batch for --workload batched (1..16)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -353,7 +396,7 @@ def main() -> int:
     _lib.load()
     log(f"device {torch.cuda.get_device_name(0)}; workload {args.workload}")
 
-    if args.workload in ("config1", "batched", "prefill"):
+    if args.workload in ("config1", "batched", "prefill", "decode7b_dp4a"):
         return run_side_workload(torch, q4k, args)
     if args.workload == "decode7b":
         wl = Workload(torch, decode_step_shapes())
