@@ -74,6 +74,24 @@ hipError_t launch_quantize_q8_1(const float *x, signed char *xq, float *xd, floa
 hipError_t launch_matvec_q4k_dp4a(const unsigned char *w, const signed char *xq, const float *xd,
                                   const float *xsum, float *y, int out_dim, int bpr);
 
+/* Replace launch_matvec_q5k (decl rocm.rs:467-472, def kernels/matvec_q5k.hip)
+ * and launch_matvec_q6k (decl rocm.rs:482-485, def kernels/matvec_q6k.hip):
+ * the same matvec for Q5_K (176 B per 256 weights) and Q6_K (210 B) rows,
+ * canonical order as dequantize_row_q5_k / dequantize_row_q6_k
+ * (gguf.rs:419-477); same per-row tolerance as launch_matvec_q4k. */
+hipError_t launch_matvec_q5k(const unsigned char *w_q5, const float *x, float *y, int out_dim,
+                             int blocks_per_row);
+hipError_t launch_matvec_q6k(const unsigned char *w_q6, const float *x, float *y, int out_dim,
+                             int blocks_per_row);
+
+/* Replaces launch_matvec_q6k_dp4a (decl rocm.rs:490-491, def
+ * kernels/matvec_q6k_dp4a.hip): Q6_K rows on launch_quantize_q8_1's output,
+ * y[r] = sum_s xd[s]*d*(sc_lo*isum_lo + sc_hi*isum_hi) over the two 16-value
+ * halves of each sub-block (exact integer dots; xsum is not used, as in the
+ * reference, and no non-finite clamp is applied). */
+hipError_t launch_matvec_q6k_dp4a(const unsigned char *w, const signed char *xq, const float *xd,
+                                  const float *xsum, float *y, int out_dim, int bpr);
+
 /* ---------------------------------------------------------------------------
  * Additive entry points (no counterpart in the reference unless noted)
  * ------------------------------------------------------------------------ */
@@ -97,6 +115,16 @@ hipError_t launch_matvec_q4k_ex(const unsigned char *w_q4, const float *x, float
 hipError_t launch_quantize_q8_1_ex(const float *x, signed char *xq, float *xd, float *xsum, int n,
                                    hipStream_t stream);
 hipError_t launch_matvec_q4k_dp4a_ex(const unsigned char *w, const signed char *xq,
+                                     const float *xd, const float *xsum, float *y, int out_dim,
+                                     int bpr, hipStream_t stream);
+
+/* launch_matvec_q5k / launch_matvec_q6k / launch_matvec_q6k_dp4a with an
+ * explicit stream. */
+hipError_t launch_matvec_q5k_ex(const unsigned char *w_q5, const float *x, float *y, int out_dim,
+                                int blocks_per_row, hipStream_t stream);
+hipError_t launch_matvec_q6k_ex(const unsigned char *w_q6, const float *x, float *y, int out_dim,
+                                int blocks_per_row, hipStream_t stream);
+hipError_t launch_matvec_q6k_dp4a_ex(const unsigned char *w, const signed char *xq,
                                      const float *xd, const float *xsum, float *y, int out_dim,
                                      int bpr, hipStream_t stream);
 

@@ -26,6 +26,12 @@ SIGNATURES = {
     "launch_matvec_q4k": (I, [P, P, P, I, I]),
     "launch_matvec_q4k_ex": (I, [P, P, P, I, I, I, P]),
     "launch_quantize_q8_1": (I, [P, P, P, P, I]),
+    "launch_matvec_q5k": (I, [P, P, P, I, I]),
+    "launch_matvec_q6k": (I, [P, P, P, I, I]),
+    "launch_matvec_q6k_dp4a": (I, [P, P, P, P, P, I, I]),
+    "launch_matvec_q5k_ex": (I, [P, P, P, I, I, P]),
+    "launch_matvec_q6k_ex": (I, [P, P, P, I, I, P]),
+    "launch_matvec_q6k_dp4a_ex": (I, [P, P, P, P, P, I, I, P]),
     "launch_matvec_q4k_dp4a": (I, [P, P, P, P, P, I, I]),
     "launch_quantize_q8_1_ex": (I, [P, P, P, P, I, P]),
     "launch_matvec_q4k_dp4a_ex": (I, [P, P, P, P, P, I, I, P]),

@@ -108,6 +108,52 @@ hipError_t launch_matvec_q4k_dp4a(const unsigned char *w, const signed char *xq,
     return launch_matvec_q4k_dp4a_ex(w, xq, xd, xsum, y, out_dim, bpr, nullptr);
 }
 
+static hipError_t check_kquant(const unsigned char *w, const float *x, const float *y,
+                               int out_dim, int bpr) {
+    if (out_dim <= 0 || bpr <= 0) return hipErrorInvalidValue;
+    if (!w || !x || !y || misaligned4(x) || misaligned4(y)) return hipErrorInvalidValue;
+    if ((int64_t)bpr * 256 > kMaxI32) return hipErrorInvalidValue;
+    return hipSuccess;
+}
+
+hipError_t launch_matvec_q5k_ex(const unsigned char *w_q5, const float *x, float *y, int out_dim,
+                                int blocks_per_row, hipStream_t stream) {
+    const hipError_t e = check_kquant(w_q5, x, y, out_dim, blocks_per_row);
+    return e != hipSuccess ? e : mgq::gemv_q5k_launch(w_q5, x, y, out_dim, blocks_per_row, stream);
+}
+
+hipError_t launch_matvec_q5k(const unsigned char *w_q5, const float *x, float *y, int out_dim,
+                             int blocks_per_row) {
+    return launch_matvec_q5k_ex(w_q5, x, y, out_dim, blocks_per_row, nullptr);
+}
+
+hipError_t launch_matvec_q6k_ex(const unsigned char *w_q6, const float *x, float *y, int out_dim,
+                                int blocks_per_row, hipStream_t stream) {
+    const hipError_t e = check_kquant(w_q6, x, y, out_dim, blocks_per_row);
+    return e != hipSuccess ? e : mgq::gemv_q6k_launch(w_q6, x, y, out_dim, blocks_per_row, stream);
+}
+
+hipError_t launch_matvec_q6k(const unsigned char *w_q6, const float *x, float *y, int out_dim,
+                             int blocks_per_row) {
+    return launch_matvec_q6k_ex(w_q6, x, y, out_dim, blocks_per_row, nullptr);
+}
+
+hipError_t launch_matvec_q6k_dp4a_ex(const unsigned char *w, const signed char *xq,
+                                     const float *xd, const float *xsum, float *y, int out_dim,
+                                     int bpr, hipStream_t stream) {
+    (void)xsum;  // part of the reference signature; the Q6_K formula has no min term
+    if (out_dim <= 0 || bpr <= 0) return hipErrorInvalidValue;
+    if (!w || !xq || !xd || !y || misaligned4(xd) || misaligned4(y)) return hipErrorInvalidValue;
+    if ((int64_t)bpr * 256 > kMaxI32) return hipErrorInvalidValue;
+    return mgq::gemv_q6k_q8_launch(w, reinterpret_cast<const int8_t *>(xq), xd, y, out_dim, bpr,
+                                   stream);
+}
+
+hipError_t launch_matvec_q6k_dp4a(const unsigned char *w, const signed char *xq, const float *xd,
+                                  const float *xsum, float *y, int out_dim, int bpr) {
+    return launch_matvec_q6k_dp4a_ex(w, xq, xd, xsum, y, out_dim, bpr, nullptr);
+}
+
 hipError_t launch_gemm_q4k_f16(const unsigned char *w_q4, const uint16_t *a_f16, float *c,
                                int out_dim, int blocks_per_row, int m_tokens,
                                hipStream_t stream) {

@@ -50,6 +50,14 @@ hipError_t gemv_q8_launch(const uint8_t *w, const int8_t *xq, const float *xd, c
 hipError_t gemv_q8_generic_launch(const uint8_t *w, const int8_t *xq, const float *xd,
                                   const float *xsum, float *y, int n, int bpr, hipStream_t stream);
 
+// Q5_K / Q6_K matvecs (f32 activations) and Q6_K on Q8_1 activations.
+hipError_t gemv_q5k_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                           hipStream_t stream);
+hipError_t gemv_q6k_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                           hipStream_t stream);
+hipError_t gemv_q6k_q8_launch(const uint8_t *w, const int8_t *xq, const float *xd, float *y,
+                              int n, int bpr, hipStream_t stream);
+
 hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n, int bpr,
                            int m_tokens, hipStream_t stream);
 

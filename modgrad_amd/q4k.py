@@ -134,6 +134,25 @@ class kern:
         _chk(_lib.load().launch_matvec_q4k(w, x, y, out_dim, bpr), "matvec_q4k")
 
     @staticmethod
+    def matvec_q5k(w: int, x: int, y: int, out_dim: int, bpr: int, stream=None) -> None:
+        """rocm.rs:964-966."""
+        _chk(_lib.load().launch_matvec_q5k_ex(w, x, y, out_dim, bpr, _stream_ptr(stream)),
+             "matvec_q5k")
+
+    @staticmethod
+    def matvec_q6k(w: int, x: int, y: int, out_dim: int, bpr: int, stream=None) -> None:
+        """rocm.rs:967-969."""
+        _chk(_lib.load().launch_matvec_q6k_ex(w, x, y, out_dim, bpr, _stream_ptr(stream)),
+             "matvec_q6k")
+
+    @staticmethod
+    def matvec_q6k_dp4a(w: int, xq: int, xd: int, xsum: int, y: int, out_dim: int, bpr: int,
+                        stream=None) -> None:
+        """rocm.rs:977-980."""
+        _chk(_lib.load().launch_matvec_q6k_dp4a_ex(w, xq, xd, xsum, y, out_dim, bpr,
+                                                   _stream_ptr(stream)), "matvec_q6k_dp4a")
+
+    @staticmethod
     def quantize_q8_1(x: int, xq: int, xd: int, xsum: int, n: int, stream=None) -> None:
         """rocm.rs:970-972: int8 activations + per-32 scale and sum."""
         _chk(_lib.load().launch_quantize_q8_1_ex(x, xq, xd, xsum, n, _stream_ptr(stream)),

@@ -62,6 +62,10 @@ def lib() -> ctypes.CDLL:
         "orq_cpu_has_avx512": (i, []),
         "orq_fill_smooth": (None, [P, z]),
         "orq_quantize_q8_1": (None, [P, i, P, P, P]),
+        "orq_dequantize_row_q5_k": (None, [P, P, z, z]),
+        "orq_dequantize_row_q6_k": (None, [P, P, z, z]),
+        "orq_gemv_kquant_f64_abs": (None, [i, P, P, P, P, i, i]),
+        "orq_gemv_q6k_dp4a_f64": (None, [P, P, P, i, i, P, P]),
         "orq_gemv_q4k_dp4a_f64": (None, [P, P, P, P, i, i, P, P]),
     }
     for name, (res, args) in sig.items():
@@ -183,6 +187,46 @@ def gemv_batched(w: np.ndarray, X: np.ndarray, out_dim: int, bpr: int):
     A = np.empty((batch, out_dim), dtype=np.float64)
     lib().orq_gemv_batched_f64_abs(_p(w), _p(X), _p(Y), _p(A), out_dim, bpr, batch)
     return Y, A
+
+
+Q5K_BYTES, Q6K_BYTES = 176, 210
+
+
+def dequantize_q5k(data: np.ndarray) -> np.ndarray:
+    data = np.ascontiguousarray(data, dtype=np.uint8)
+    nb = data.size // Q5K_BYTES
+    out = np.empty(nb * BLOCK_ELEMS, dtype=np.float32)
+    lib().orq_dequantize_row_q5_k(_p(data), _p(out), out.size, nb)
+    return out
+
+
+def dequantize_q6k(data: np.ndarray) -> np.ndarray:
+    data = np.ascontiguousarray(data, dtype=np.uint8)
+    nb = data.size // Q6K_BYTES
+    out = np.empty(nb * BLOCK_ELEMS, dtype=np.float32)
+    lib().orq_dequantize_row_q6_k(_p(data), _p(out), out.size, nb)
+    return out
+
+
+def gemv_kquant(block_bytes: int, w: np.ndarray, x: np.ndarray, out_dim: int, bpr: int):
+    """(y f32, absdot f64): f64 dequant-dot of a Q4_K/Q5_K/Q6_K row-aligned matrix."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert w.size >= out_dim * bpr * block_bytes and x.size >= bpr * BLOCK_ELEMS
+    y = np.empty(out_dim, dtype=np.float32)
+    a = np.empty(out_dim, dtype=np.float64)
+    lib().orq_gemv_kquant_f64_abs(block_bytes, _p(w), _p(x), _p(y), _p(a), out_dim, bpr)
+    return y, a
+
+
+def gemv_q6k_dp4a(w: np.ndarray, xq: np.ndarray, xd: np.ndarray, out_dim: int, bpr: int):
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    xq = np.ascontiguousarray(xq, dtype=np.int8)
+    xd = np.ascontiguousarray(xd, dtype=np.float32)
+    y = np.empty(out_dim, dtype=np.float64)
+    a = np.empty(out_dim, dtype=np.float64)
+    lib().orq_gemv_q6k_dp4a_f64(_p(w), _p(xq), _p(xd), out_dim, bpr, _p(y), _p(a))
+    return y, a
 
 
 def quantize_q8_1(x: np.ndarray):

@@ -290,6 +290,120 @@ void orq_gemv_flat_f64_abs(const uint8_t *w, const float *x, float *y,
     }
 }
 
+/* gguf.rs:419-447 (dequantize_row_q5_k). */
+void orq_dequantize_row_q5_k(const uint8_t *data, float *out, size_t out_len, size_t n_blocks) {
+    for (size_t blk = 0; blk < n_blocks; ++blk) {
+        const uint8_t *b = data + blk * ORQ_Q5K_BYTES;
+        float d = orq_f16_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+        float dmin = orq_f16_to_f32((uint16_t)(b[2] | (b[3] << 8)));
+        if (!isfinite(d)) d = 0.0f;
+        if (!isfinite(dmin)) dmin = 0.0f;
+        const uint8_t *scales = b + 4, *qh = b + 16, *ql = b + 48;
+        size_t out_idx = blk * ORQ_BLOCK_ELEMS;
+        for (int grp = 0; grp < 4; ++grp) {
+            uint8_t sc1, m1, sc2, m2;
+            orq_get_scale_min_k4(2 * grp, scales, &sc1, &m1);
+            orq_get_scale_min_k4(2 * grp + 1, scales, &sc2, &m2);
+            const float d1 = d * (float)sc1, dm1 = dmin * (float)m1;
+            const float d2 = d * (float)sc2, dm2 = dmin * (float)m2;
+            const uint8_t u1 = (uint8_t)(1u << (2 * grp)), u2 = (uint8_t)(2u << (2 * grp));
+            for (int l = 0; l < 32; ++l) {
+                const int hbit = (qh[l] & u1) ? 16 : 0;
+                const float q = (float)((ql[32 * grp + l] & 0xF) + hbit);
+                if (out_idx < out_len) out[out_idx] = d1 * q - dm1;
+                ++out_idx;
+            }
+            for (int l = 0; l < 32; ++l) {
+                const int hbit = (qh[l] & u2) ? 16 : 0;
+                const float q = (float)((ql[32 * grp + l] >> 4) + hbit);
+                if (out_idx < out_len) out[out_idx] = d2 * q - dm2;
+                ++out_idx;
+            }
+        }
+    }
+}
+
+/* gguf.rs:450-477 (dequantize_row_q6_k). */
+void orq_dequantize_row_q6_k(const uint8_t *data, float *out, size_t out_len, size_t n_blocks) {
+    for (size_t blk = 0; blk < n_blocks; ++blk) {
+        const uint8_t *b = data + blk * ORQ_Q6K_BYTES;
+        const uint8_t *ql = b, *qh = b + 128;
+        const int8_t *sc = (const int8_t *)(b + 192);
+        float d = orq_f16_to_f32((uint16_t)(b[208] | (b[209] << 8)));
+        if (!isfinite(d)) d = 0.0f;
+        const size_t base = blk * ORQ_BLOCK_ELEMS;
+        for (int grp = 0; grp < 2; ++grp) {
+            const int qlb = grp * 64, qhb = grp * 32, scb = grp * 8;
+            const size_t yb = base + (size_t)grp * 128;
+            for (int l = 0; l < 32; ++l) {
+                const int is = l / 16;
+                const int q1 = ((ql[qlb + l] & 0xF) | ((qh[qhb + l] & 3) << 4)) - 32;
+                const int q2 = ((ql[qlb + l + 32] & 0xF) | (((qh[qhb + l] >> 2) & 3) << 4)) - 32;
+                const int q3 = ((ql[qlb + l] >> 4) | (((qh[qhb + l] >> 4) & 3) << 4)) - 32;
+                const int q4 = ((ql[qlb + l + 32] >> 4) | (((qh[qhb + l] >> 6) & 3) << 4)) - 32;
+                if (yb + l + 96 < out_len) {
+                    out[yb + l] = d * (float)sc[scb + is] * (float)q1;
+                    out[yb + l + 32] = d * (float)sc[scb + is + 2] * (float)q2;
+                    out[yb + l + 64] = d * (float)sc[scb + is + 4] * (float)q3;
+                    out[yb + l + 96] = d * (float)sc[scb + is + 6] * (float)q4;
+                }
+            }
+        }
+    }
+}
+
+void orq_gemv_kquant_f64_abs(int block_bytes, const uint8_t *w, const float *x, float *y,
+                             double *absdot, int out_dim, int bpr) {
+    size_t k = (size_t)bpr * ORQ_BLOCK_ELEMS;
+    float *wr = (float *)malloc(k * sizeof(float));
+    for (int r = 0; r < out_dim; ++r) {
+        const uint8_t *row = w + (size_t)r * bpr * block_bytes;
+        if (block_bytes == ORQ_Q5K_BYTES) orq_dequantize_row_q5_k(row, wr, k, (size_t)bpr);
+        else if (block_bytes == ORQ_Q6K_BYTES) orq_dequantize_row_q6_k(row, wr, k, (size_t)bpr);
+        else orq_dequantize_row_q4_k(row, wr, k, (size_t)bpr);
+        double acc = 0.0, aabs = 0.0;
+        for (size_t i = 0; i < k; ++i) {
+            acc += (double)wr[i] * (double)x[i];
+            aabs += fabs((double)wr[i]) * fabs((double)x[i]);
+        }
+        y[r] = (float)acc;
+        if (absdot) absdot[r] = aabs;
+    }
+    free(wr);
+}
+
+/* kernels/matvec_q6k_dp4a.hip (matvec_q6k_dp4a_kernel), in f64. */
+void orq_gemv_q6k_dp4a_f64(const uint8_t *w, const int8_t *xq, const float *xd, int out_dim,
+                           int bpr, double *y, double *absterm) {
+    for (int r = 0; r < out_dim; ++r) {
+        const uint8_t *wrow = w + (size_t)r * bpr * ORQ_Q6K_BYTES;
+        double acc = 0.0, aabs = 0.0;
+        for (int s = 0; s < bpr * 8; ++s) {
+            const int blk = s >> 3, sub = s & 7, g = sub >> 2, quad = sub & 3;
+            const uint8_t *b = wrow + (size_t)blk * ORQ_Q6K_BYTES;
+            float d = orq_f16_to_f32((uint16_t)(b[208] | (b[209] << 8)));
+            if (!isfinite(d)) d = 0.0f;
+            const uint8_t *ql = b + g * 64, *qh = b + 128 + g * 32;
+            const int8_t *sc = (const int8_t *)(b + 192);
+            const int sc_lo = sc[g * 8 + quad * 2], sc_hi = sc[g * 8 + 1 + quad * 2];
+            const int8_t *xv = xq + (size_t)s * 32;
+            long ilo = 0, ihi = 0;
+            for (int l = 0; l < 32; ++l) {
+                const uint8_t qb = ql[l + ((quad & 1) ? 32 : 0)];
+                const int nib = (quad >> 1) ? (qb >> 4) : (qb & 0xF);
+                const int q6 = (nib | (((qh[l] >> (2 * quad)) & 3) << 4)) - 32;
+                if (l < 16) ilo += (long)q6 * xv[l]; else ihi += (long)q6 * xv[l];
+            }
+            const double t = (double)sc_lo * (double)ilo + (double)sc_hi * (double)ihi;
+            acc += (double)xd[s] * (double)d * t;
+            aabs += fabs((double)xd[s] * (double)d) *
+                    (fabs((double)sc_lo * (double)ilo) + fabs((double)sc_hi * (double)ihi));
+        }
+        y[r] = acc;
+        if (absterm) absterm[r] = aabs;
+    }
+}
+
 /* kernels/matvec_q4k_dp4a.hip:29-50 (quantize_q8_1_kernel). */
 void orq_quantize_q8_1(const float *x, int n, int8_t *xq, float *xd, float *xsum) {
     const int nsub = n / 32;

@@ -90,6 +90,28 @@ void orq_gemv_q4k_dp4a_f64(const uint8_t *w, const int8_t *xq, const float *xd,
                            const float *xsum, int out_dim, int bpr, double *y,
                            double *absterm);
 
+/* Q5_K (176 B / 256 values: d, dmin f16; scales[12]; qh[32]; ql[128]) and
+ * Q6_K (210 B: ql[128]; qh[64]; int8 scales[16]; d f16) dequantizers:
+ * gguf.rs:419-447 and :450-477. Canonical order. Same out_len bound as Q4_K. */
+#define ORQ_Q5K_BYTES 176
+#define ORQ_Q6K_BYTES 210
+void orq_dequantize_row_q5_k(const uint8_t *data, float *out, size_t out_len, size_t n_blocks);
+void orq_dequantize_row_q6_k(const uint8_t *data, float *out, size_t out_len, size_t n_blocks);
+
+/* f64 dequant-dot GEMV for a row-aligned K-quant matrix of block size
+ * block_bytes (144 = Q4_K, 176 = Q5_K, 210 = Q6_K): the reference's check
+ * method (rocm_matvec_check.rs:38-47) with that format's dequantizer. */
+void orq_gemv_kquant_f64_abs(int block_bytes, const uint8_t *w, const float *x, float *y,
+                             double *absdot, int out_dim, int bpr);
+
+/* Q6_K dp4a matvec: kernels/matvec_q6k_dp4a.hip (matvec_q6k_dp4a_kernel), in
+ * f64 with exact integer dots: y[r] = sum_s xd[s]*d*(sc_lo*isum_lo +
+ * sc_hi*isum_hi), the two 16-value halves of each 32-value sub-block s having
+ * their own int8 scale; no xsum term (the q6 values are signed) and no
+ * non-finite clamp. absterm as for orq_gemv_q4k_dp4a_f64. */
+void orq_gemv_q6k_dp4a_f64(const uint8_t *w, const int8_t *xq, const float *xd, int out_dim,
+                           int bpr, double *y, double *absterm);
+
 /* CPU timing baseline: kfd::llm::matvec (llm.rs:468-534) with the fused
  * dequant-dot of llm.rs:684-806 (AVX-512 when the host has it, else scalar),
  * parallel over rows. threads <= 0 -> all cores. Returns 1 if AVX-512 used. */

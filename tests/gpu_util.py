@@ -54,3 +54,16 @@ def random_q4k_bytes(rng: np.random.Generator, n_blocks: int, finite_scales: boo
 
 
 c_void_p = ctypes.c_void_p
+
+
+def random_kquant_bytes(rng: np.random.Generator, n_blocks: int, block_bytes: int,
+                        d_scale: float = 1e-3) -> np.ndarray:
+    """Random Q5_K (176 B) or Q6_K (210 B) blocks with finite f16 d (and dmin)."""
+    b = rng.integers(0, 256, size=(n_blocks, block_bytes), dtype=np.uint8)
+    if block_bytes == 176:
+        d = np.abs(rng.normal(0, d_scale, size=(n_blocks, 2))).astype(np.float16)
+        b[:, 0:4] = d.view(np.uint8).reshape(n_blocks, 4)
+    else:
+        d = np.abs(rng.normal(0, d_scale, size=(n_blocks, 1))).astype(np.float16)
+        b[:, 208:210] = d.view(np.uint8).reshape(n_blocks, 2)
+    return b.ravel()

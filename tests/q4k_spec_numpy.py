@@ -72,3 +72,51 @@ def quantize_q8_1(x: np.ndarray):
     r = np.where(np.isnan(r), 0, r)
     q = np.clip(r, -127, 127).astype(np.int8)
     return q.ravel(), d, q.astype(np.int64).sum(axis=1).astype(np.float32)
+
+
+def dequantize_q5k(data: np.ndarray) -> np.ndarray:
+    """Q5_K, 176 B: +0 d f16, +2 dmin f16, +4 scales[12] (Q4_K packing),
+    +16 qh[32], +48 ql[128]. Position p: sub-block j = p // 32, low nibble of
+    ql[32*(p // 64) + p % 32] for even j (high for odd), plus 16 when bit j of
+    qh[p % 32] is set; w = f32(f32(d*sc_j) * q) - f32(dmin*m_j)."""
+    blocks = np.asarray(data, np.uint8).reshape(-1, 176)
+    nb = blocks.shape[0]
+    d = half_bits_to_f32(blocks[:, 0:2].copy().view(np.uint16)[:, 0])
+    dmin = half_bits_to_f32(blocks[:, 2:4].copy().view(np.uint16)[:, 0])
+    sc, m = unpack_scales(blocks[:, 4:16])
+    qh, ql = blocks[:, 16:48], blocks[:, 48:176]
+    p = np.arange(256)
+    j = p // 32
+    byte = ql[:, 32 * (p // 64) + p % 32].astype(np.int64)
+    nib = np.where(j % 2 == 0, byte & 15, byte >> 4)
+    hb = (qh[:, p % 32].astype(np.int64) >> j) & 1
+    q = (nib + 16 * hb).astype(np.float32)
+    d1 = (d[:, None] * sc.astype(np.float32))[:, j]
+    m1 = (dmin[:, None] * m.astype(np.float32))[:, j]
+    return ((d1 * q).astype(np.float32) - m1).astype(np.float32).reshape(nb * 256)
+
+
+def q6k_values(data: np.ndarray):
+    """(q in -32..31, scale index) per canonical position of each Q6_K block."""
+    blocks = np.asarray(data, np.uint8).reshape(-1, 210)
+    ql, qh = blocks[:, 0:128].astype(np.int64), blocks[:, 128:192].astype(np.int64)
+    p = np.arange(256)
+    g, r = p // 128, p % 128
+    quad, l = r // 32, r % 32
+    byte = ql[:, 64 * g + l + 32 * (quad % 2)]
+    nib = np.where(quad < 2, byte & 15, byte >> 4)
+    hb = (qh[:, 32 * g + l] >> (2 * quad)) & 3
+    return (nib | (hb << 4)) - 32, 8 * g + l // 16 + 2 * quad
+
+
+def dequantize_q6k(data: np.ndarray) -> np.ndarray:
+    """Q6_K, 210 B: +0 ql[128], +128 qh[64], +192 int8 scales[16], +208 d f16.
+    Position p = 128g + 32quad + l: low (quad < 2) or high nibble of
+    ql[64g + l + 32*(quad % 2)], bits 2quad..2quad+1 of qh[32g + l] on top,
+    minus 32; scale scales[8g + l // 16 + 2quad]; w = f32(f32(d*s) * q)."""
+    blocks = np.asarray(data, np.uint8).reshape(-1, 210)
+    nb = blocks.shape[0]
+    q, si = q6k_values(blocks)
+    s = blocks[:, 192:208].view(np.int8).astype(np.float32)[:, si]
+    d = half_bits_to_f32(blocks[:, 208:210].copy().view(np.uint16)[:, 0])
+    return ((d[:, None] * s).astype(np.float32) * q.astype(np.float32)).astype(np.float32).reshape(nb * 256)

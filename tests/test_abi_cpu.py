@@ -54,6 +54,16 @@ def test_dp4a_path_rejects_bad_args(L):
     assert L.launch_matvec_q4k_dp4a(FAKE, FAKE, FAKE, FAKE + 2, FAKE, 16, 1) == INVALID
 
 
+def test_q5k_q6k_reject_bad_args(L):
+    for fn in (L.launch_matvec_q5k, L.launch_matvec_q6k):
+        assert fn(FAKE, FAKE, FAKE, 0, 14) == INVALID
+        assert fn(FAKE, FAKE, FAKE, 16, 0) == INVALID
+        assert fn(None, FAKE, FAKE, 16, 1) == INVALID
+        assert fn(FAKE, FAKE + 2, FAKE, 16, 1) == INVALID
+    assert L.launch_matvec_q6k_dp4a(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 1) == INVALID
+    assert L.launch_matvec_q6k_dp4a(FAKE, None, FAKE, FAKE, FAKE, 8, 1) == INVALID
+
+
 def test_matvec_rejects_null_and_misaligned(L):
     assert L.launch_matvec_q4k(None, FAKE, FAKE, 16, 1) == INVALID
     assert L.launch_matvec_q4k(FAKE, None, FAKE, 16, 1) == INVALID

@@ -450,3 +450,48 @@ def test_dp4a_nonfinite_rows_are_zero(L, orc):
     y = host(yt)
     assert np.all(np.isfinite(y))
     assert np.array_equal(y == 0, y_ref == 0)
+
+
+# ------------------------------------------------------------ Q5_K / Q6_K --
+@pytest.mark.parametrize("fmt", [176, 210])
+@pytest.mark.parametrize("n,bpr", [(1, 1), (5, 3), (64, 14), (3584, 14), (300, 74), (4099, 2)])
+def test_kquant_matvec_matches_oracle(L, orc, fmt, n, bpr):
+    from tests.gpu_util import random_kquant_bytes
+    note(f"{'q5k' if fmt == 176 else 'q6k'} n={n} bpr={bpr}")
+    rng = np.random.default_rng(fmt * 1000 + n + bpr)
+    w = random_kquant_bytes(rng, n * bpr, fmt)
+    x = rng.standard_normal(bpr * 256).astype(np.float32)
+    wt, xt, yt = dev(w), dev(x), empty_f32(n)
+    fn = L.launch_matvec_q5k if fmt == 176 else L.launch_matvec_q6k
+    _lib.check("kquant", fn(ptr(wt), ptr(xt), ptr(yt), n, bpr))
+    y_ref, a = orc.gemv_kquant(fmt, w, x, n, bpr)
+    assert_gemv_close(host(yt), y_ref, a)
+
+
+def test_kquant_matvec_odd_weight_offset(L, orc):
+    # the reference arena places tensors at arbitrary offsets: Q6_K weights
+    # starting 2 bytes past an allocation boundary
+    from tests.gpu_util import random_kquant_bytes
+    note("q6k weights at an odd offset")
+    n, bpr = 33, 5
+    w = random_kquant_bytes(np.random.default_rng(7), n * bpr, 210)
+    x = orc.normal(8, bpr * 256)
+    wt = dev(np.concatenate([np.zeros(2, np.uint8), w]))
+    xt, yt = dev(x), empty_f32(n)
+    _lib.check("q6k", L.launch_matvec_q6k(ptr(wt) + 2, ptr(xt), ptr(yt), n, bpr))
+    y_ref, a = orc.gemv_kquant(210, w, x, n, bpr)
+    assert_gemv_close(host(yt), y_ref, a)
+
+
+@pytest.mark.parametrize("n,bpr", [(1, 1), (40, 14), (3584, 14), (129, 74)])
+def test_q6k_dp4a_matches_oracle(L, orc, n, bpr):
+    from tests.gpu_util import random_kquant_bytes
+    note(f"q6k dp4a n={n} bpr={bpr}")
+    rng = np.random.default_rng(n + 17 * bpr)
+    w = random_kquant_bytes(rng, n * bpr, 210)
+    x = rng.standard_normal(bpr * 256).astype(np.float32)
+    (xq, xd, xs), (q, d, s) = run_q8(L, x)
+    wt, yt = dev(w), empty_f32(n)
+    _lib.check("q6k dp4a", L.launch_matvec_q6k_dp4a(ptr(wt), ptr(xq), ptr(xd), ptr(xs), ptr(yt), n, bpr))
+    y_ref, absterm = orc.gemv_q6k_dp4a(w, q, d, n, bpr)
+    assert_dp4a_close(host(yt), y_ref, absterm)

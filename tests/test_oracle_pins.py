@@ -440,3 +440,90 @@ def test_dp4a_close_to_f32_gemv_reference_check(orc, bias):
     rms_rel = np.sqrt(np.sum((y8 - y32) ** 2) / np.sum(y32.astype(np.float64) ** 2))
     assert rms_rel < 0.02
     assert rms_rel > 1e-6  # int8 activations really are lossy
+
+
+# ------------------------------------------------------------- Q5_K, Q6_K --
+def test_q5k_dequant_matches_numpy_spec(orc):
+    rng = np.random.default_rng(55)
+    data = rng.integers(0, 256, size=(40, 176), dtype=np.uint8)
+    data[:, 0:4] = np.abs(rng.normal(0, 1e-2, (40, 2))).astype(np.float16).view(np.uint8).reshape(40, 4)
+    data[3, 0:2] = np.array([0x7C00], np.uint16).view(np.uint8)  # d = Inf -> 0
+    got = orc.dequantize_q5k(data.ravel())
+    ref = spec.dequantize_q5k(data)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_q5k_high_bit_closed_form(orc):
+    # d = 1, dmin = 0, all scales 1: out[p] = nibble + 16*(bit j of qh[p%32])
+    blk = np.zeros(176, np.uint8)
+    blk[0:2] = np.array([0x3C00], np.uint16).view(np.uint8)
+    blk[4:16] = np.frombuffer(orc.pack_scales_mins(np.ones(8, np.uint8), np.zeros(8, np.uint8)), np.uint8)
+    blk[48:176] = (np.arange(128) % 16) | ((15 - np.arange(128) % 16) << 4)
+    blk[16 + 5] = 0b10100101  # position 5 of sub-blocks 0, 2, 5, 7 gets +16
+    out = orc.dequantize_q5k(blk)
+    for p in range(256):
+        j, byte_i = p // 32, 32 * (p // 64) + p % 32
+        nib = (byte_i % 16) if j % 2 == 0 else 15 - byte_i % 16
+        hb = 16 if (p % 32 == 5 and j in (0, 2, 5, 7)) else 0
+        assert out[p] == nib + hb, p
+
+
+def test_q6k_dequant_matches_numpy_spec_and_signed_scales(orc):
+    rng = np.random.default_rng(66)
+    data = rng.integers(0, 256, size=(40, 210), dtype=np.uint8)
+    data[:, 208:210] = np.abs(rng.normal(0, 1e-2, (40, 1))).astype(np.float16).view(np.uint8).reshape(40, 2)
+    got = orc.dequantize_q6k(data.ravel())
+    ref = spec.dequantize_q6k(data)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    # closed form: d = 1, scales[i] = i - 8, q = -32 everywhere except where set
+    blk = np.zeros(210, np.uint8)
+    blk[208:210] = np.array([0x3C00], np.uint16).view(np.uint8)
+    blk[192:208] = (np.arange(16) - 8).astype(np.int8).view(np.uint8)
+    out = orc.dequantize_q6k(blk)
+    _, si = spec.q6k_values(blk)
+    assert np.array_equal(out, (si - 8).astype(np.float32) * -32.0)
+
+
+@pytest.mark.parametrize("fmt", [176, 210])
+def test_kquant_gemv_unit_vectors_return_columns(orc, fmt):
+    rng = np.random.default_rng(fmt)
+    n, bpr = 9, 2
+    w = rng.integers(0, 256, size=n * bpr * fmt, dtype=np.uint8).reshape(n * bpr, fmt)
+    dpos = 0 if fmt == 176 else 208
+    w[:, dpos:dpos + 2] = np.abs(rng.normal(0, 1e-2, (n * bpr, 1))).astype(np.float16).view(np.uint8)
+    w = w.ravel()
+    deq = (orc.dequantize_q5k(w) if fmt == 176 else orc.dequantize_q6k(w)).reshape(n, -1)
+    for k in (0, 31, 32, 100, 255, 256, 511):
+        x = np.zeros(bpr * 256, np.float32)
+        x[k] = 1.0
+        y, _ = orc.gemv_kquant(fmt, w, x, n, bpr)
+        assert np.array_equal(y, deq[:, k])
+
+
+def test_q6k_dp4a_matches_numpy_and_reference_check(orc):
+    rng = np.random.default_rng(67)
+    n, bpr = 32, 14
+    w = rng.integers(0, 256, size=(n * bpr, 210), dtype=np.uint8)
+    w[:, 208:210] = np.abs(rng.normal(0, 1e-3, (n * bpr, 1))).astype(np.float16).view(np.uint8)
+    w = w.ravel()
+    x = (np.sin(np.arange(bpr * 256, dtype=np.float32) * np.float32(0.21)) * np.float32(30.0))
+    xq, xd, _ = orc.quantize_q8_1(x)
+    y, a = orc.gemv_q6k_dp4a(w, xq, xd, n, bpr)
+    q, si = spec.q6k_values(w)
+    blocks = w.reshape(n * bpr, 210)
+    s = blocks[:, 192:208].view(np.int8).astype(np.int64)
+    d = spec.half_bits_to_f32(blocks[:, 208:210].copy().view(np.uint16)[:, 0]).astype(np.float64)
+    xqb = xq.reshape(bpr, 256).astype(np.int64)
+    yr = np.zeros(n)
+    for r in range(n):
+        for b in range(bpr):
+            bi = r * bpr + b
+            prod = q[bi] * xqb[b]                       # per position
+            per16 = prod.reshape(16, 16).sum(axis=1)    # 16-value halves
+            sc16 = s[bi][si.reshape(16, 16)[:, 0]]
+            xd16 = np.repeat(xd.reshape(bpr, 8)[b].astype(np.float64), 2)
+            yr[r] += np.sum(xd16 * d[bi] * sc16 * per16)
+    assert np.allclose(y, yr, rtol=1e-12, atol=1e-300)
+    y32, _ = orc.gemv_kquant(210, w, x, n, bpr)
+    rms = np.sqrt(np.sum((y - y32) ** 2) / np.sum(y32.astype(np.float64) ** 2))
+    assert 1e-6 < rms < 0.02
