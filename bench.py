@@ -325,6 +325,57 @@ def run_decode_dp4a(torch, q4k, args):
             "tokens_per_s": 1000.0 / ms, "ms_per_step": ms}
 
 
+def run_kquant(torch, q4k, args):
+    """Q5_K (176 B / 256 weights) on the gate and down shapes, or Q6_K
+    (210 B / 256) on the lm_head shape -- the K-quants real GGUFs mix in."""
+    from oracle import oracle as orc
+    fmt = 176 if args.workload == "q5k" else 210
+    shapes = [("gate", INTER, HIDDEN), ("down", HIDDEN, INTER)] if fmt == 176 else \
+        [("lm_head", VOCAB, HIDDEN)]
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x5150 + fmt)
+    per = sum(n * (k // BLOCK_ELEMS) * fmt for _, n, k in shapes)
+    copies = max(2, -(-int(1.2e9) // per))
+    items = []
+    for c in range(copies):
+        for name, n, k in shapes:
+            nblk = n * (k // BLOCK_ELEMS)
+            w = torch.randint(0, 256, (nblk, fmt), dtype=torch.uint8, device="cuda", generator=gen)
+            dd = (torch.rand((nblk, 2 if fmt == 176 else 1), device="cuda", generator=gen) * 2e-3
+                  + 1e-4).to(torch.float16).view(torch.uint8)
+            if fmt == 176:
+                w[:, 0:4] = dd.view(nblk, 4)
+            else:
+                w[:, 208:210] = dd.view(nblk, 2)
+            x = torch.randn(k, device="cuda", generator=gen)
+            y = torch.empty(n, device="cuda")
+            items.append((name, w.view(-1), x, y, n, k))
+    fn = q4k.kern.matvec_q5k if fmt == 176 else q4k.kern.matvec_q6k
+
+    def launch(st):
+        for name, w, x, y, n, k in items:
+            fn(w.data_ptr(), x.data_ptr(), y.data_ptr(), n, k // BLOCK_ELEMS, st)
+    ms = time_captured(torch, launch, args.steps, args.warmup)
+    nbytes = sum(n * (k // BLOCK_ELEMS) * fmt + 4 * (n + k) for _, _, _, _, n, k in items)
+    worst, parity = 0.0, None
+    for name, w, x, y, n, k in items[-len(shapes):]:
+        bpr = k // BLOCK_ELEMS
+        idx = np.sort(np.random.default_rng(n).choice(n, size=min(256, n), replace=False))
+        wr = w.view(n, bpr * fmt)[torch.from_numpy(idx).cuda()].cpu().numpy().ravel()
+        y_ref, a = orc.gemv_kquant(fmt, wr, x.cpu().numpy(), idx.size, bpr)
+        r = np.abs(y.cpu().numpy()[idx].astype(np.float64) - y_ref) / np.maximum(a, 1e-300)
+        worst = max(worst, float(r.max()))
+        if not np.all(r <= 1e-4):
+            parity = f"FAIL {name}: max err/absdot {r.max():.3e}"
+    parity = parity or f"ok (max err/absdot {worst:.2e} <= 1e-4)"
+    label = "q5k: Q5_K gate 18944x3584 + down 3584x18944" if fmt == 176 else \
+        "q6k: Q6_K lm_head 152064x3584"
+    return {"workload": f"{label}, {copies} rotating copies, one graph",
+            "us_per_launch": round(ms * 1e3 / len(items), 3), "gbs": nbytes / (ms * 1e-3) / 1e9,
+            "bytes_per_launch": nbytes // len(items), "parity": parity,
+            "kernel": "mgq::gemv_q5k_kernel" if fmt == 176 else "mgq::gemv_q6k_kernel"}
+
+
 TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                "gemv_mfma_decode7b_pmc.txt")
 
@@ -344,7 +395,7 @@ def profiled_traffic(workload: str):
 def run_side_workload(torch, q4k, args) -> int:
     """BASELINE configs 1, 4 and 5: one JSON line each, same field layout."""
     fn = {"config1": run_config1, "batched": run_batched, "prefill": run_prefill,
-          "decode7b_dp4a": run_decode_dp4a}[args.workload]
+          "decode7b_dp4a": run_decode_dp4a, "q5k": run_kquant, "q6k": run_kquant}[args.workload]
     r = fn(torch, q4k, args)
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": "synthetic",
@@ -378,7 +429,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="decode7b",
                     choices=["decode7b", "layer", "gateup", "config1", "batched", "prefill",
-                             "decode7b_dp4a"])
+                             "decode7b_dp4a", "q5k", "q6k"])
     ap.add_argument("--batch", type=int, default=8, help="batch for --workload batched (1..16)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -396,7 +447,7 @@ def main() -> int:
     _lib.load()
     log(f"device {torch.cuda.get_device_name(0)}; workload {args.workload}")
 
-    if args.workload in ("config1", "batched", "prefill", "decode7b_dp4a"):
+    if args.workload in ("config1", "batched", "prefill", "decode7b_dp4a", "q5k", "q6k"):
         return run_side_workload(torch, q4k, args)
     if args.workload == "decode7b":
         wl = Workload(torch, decode_step_shapes())
