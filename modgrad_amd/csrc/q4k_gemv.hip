@@ -104,7 +104,6 @@ __device__ __forceinline__ int pair_byte_offset(int p, int h) {
     return p < 2 ? 16 * h + 8 * p : 64 + 16 * h + 8 * (p - 2);
 }
 
-constexpr int kMaxWaves = 8;
 
 // v from lane (lane ^ MASK) within each group of 4 lanes (DPP quad_perm).
 template <int MASK>
@@ -117,9 +116,8 @@ __device__ __forceinline__ float quad_xor(float v) {
 
 
 // LDS layout of one work-group (rows R, all bpr blocks of K):
-//   atab  [bpr][8 mfma c][4 lane-group h][xh|xl][8 halves]   bpr*1024 B
-//         (Q8: the int8 activations xq, bpr*256 B)
-//   zero  16 B of zeros
+//   atab  [bpr][8 mfma c][4 lane-group h][xh|xl][8 halves] + 16 B of zeros,
+//         bpr*1040 B (Q8: the int8 activations xq, bpr*256 B)
 //   meta  [bpr][corr[8] | xsum[8]] f32 (Q8: [xd[8] | xsum[8]]) bpr*64 B
 //   stage 2 (1 if bpr <= C) x SB bytes: weight bytes of R rows x C blocks,
 //         row-major over (row, block, 16-byte piece), rows padded to an odd
@@ -127,7 +125,7 @@ __device__ __forceinline__ float quad_xor(float v) {
 //   aux   NW*32*4 B: cross-wave reduction buffer (32 row sums per wavefront)
 struct MfmaLayout {
     int bpr, R, C, NW, I;  // I = 1 KiB wave loads per stage
-    uint32_t zero, meta, stage, stage_bytes, aux, ybuf;
+    uint32_t tab_stride, meta, stage, stage_bytes, aux, ybuf;
     size_t total;
 };
 
@@ -145,10 +143,11 @@ __host__ __device__ inline MfmaLayout mfma_layout(int bpr, int R, int C, int NW,
     L.bpr = bpr; L.R = R; L.C = C; L.NW = NW;
     // wave loads per stage, padded so every wavefront issues the same count
     L.I = ((R * 9 * C + 63) / 64 + NW - 1) / NW * NW;
-    // activation table: 1 KiB of f16 operands per block, or (Q8) the 256
-    // int8 activations of the block
-    L.zero = (uint32_t)bpr * (q8 ? 256u : 1024u);
-    L.meta = L.zero + 16;
+    // activation table: per block 1 KiB of f16 operands plus a 16-byte zero
+    // slot (so a lane's A address is the block base plus a fixed offset), or
+    // (Q8) the block's 256 int8 activations
+    L.tab_stride = q8 ? 256u : 1040u;
+    L.meta = (uint32_t)bpr * L.tab_stride;
     L.stage = L.meta + (uint32_t)bpr * 64u;
     L.stage_bytes = (uint32_t)(R * stage_row_pieces(C) * 16);
     // two stage buffers when double-buffered and K needs more than one stage
@@ -250,9 +249,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     // Q8: copy xq (16 B items 0 .. 16*bpr), then xd and xsum (4 floats per
     // item) to LDS, loads again issued ahead of the weight stream
     const int nq = bpr * 16, nitems = bpr * 20;
+    const int its = (nitems + NW * 64 - 1) / (NW * 64);  // <= XIT
     u32x4 cv[XIT];
 #pragma unroll
     for (int it = 0; it < XIT; ++it) {
+        if (it >= its) break;
         const int i = std::min(tid + it * NW * 64, nitems - 1);
         const uint8_t *src = i < nq ? reinterpret_cast<const uint8_t *>(xq) + (size_t)i * 16
                            : i < nq + 2 * bpr ? reinterpret_cast<const uint8_t *>(xdv + (size_t)(i - nq) * 4)
@@ -276,9 +277,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     }
   } else {
     const int nitems = bpr * 32;
+    const int its = (nitems + NW * 64 - 1) / (NW * 64);  // <= XIT
     f32x4 xv0[XIT], xv1[XIT];
 #pragma unroll
     for (int it = 0; it < XIT; ++it) {
+        if (it >= its) break;
         const int i = std::min(tid + it * NW * 64, nitems - 1);
         xv0[it] = *reinterpret_cast<const f32x4 *>(x + (size_t)i * 8);
         xv1[it] = *reinterpret_cast<const f32x4 *>(x + (size_t)i * 8 + 4);
@@ -286,9 +289,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
 #pragma unroll
     for (int f = 0; f < PF; ++f) gload(f, stg[f]);
 
-    if (tid < 4) reinterpret_cast<uint32_t *>(lds + Lo.zero)[tid] = 0u;
+    for (int b = tid; b < bpr; b += NW * 64)  // the blocks' zero slots
+        *reinterpret_cast<u32x4 *>(lds + (size_t)b * Lo.tab_stride + 1024) = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int it = 0; it < XIT; ++it) {
+        if (it >= its) break;
         const int i = tid + it * NW * 64;  // lanes of one sub-block share i/4
         const f32x4 v0 = xv0[it], v1 = xv1[it];
         float amax = fmaxf(fmaxf(fmaxf(fabsf(v0[0]), fabsf(v0[1])), fmaxf(fabsf(v0[2]), fabsf(v0[3]))),
@@ -314,19 +319,22 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         // = 32*(sb/2) + 8*j within the qs run, nibble parity c%2 = sb%2
         const int G = sb >> 1;
         const int c = 2 * (2 * (G >> 1) + (j & 1)) + (sb & 1), h = 2 * (G & 1) + (j >> 1);
-        // slot q holds byte o + {0,2,1,3,4,6,5,7}[q] (see the B operand build)
+        // slot q holds byte o + {0,2,1,3,4,6,5,7}[q] (see the B operand build).
+        // xh = x*2^e rounded toward zero to f16, xl = the (exact) f32
+        // remainder rounded toward zero: two packed conversions per pair.
         const float xs[8] = {v0[0], v0[2], v0[1], v0[3], v1[0], v1[2], v1[1], v1[3]};
-        half8 hh, hl;
+        u32x4 hh, hl;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const float xsv = ldexpf(xs[q], e);
-            const _Float16 a = (_Float16)xsv;
-            hh[q] = a;
-            hl[q] = (_Float16)(xsv - (float)a);
+        for (int q = 0; q < 4; ++q) {
+            const float a0 = ldexpf(xs[2 * q], e), a1 = ldexpf(xs[2 * q + 1], e);
+            const auto hp = __builtin_amdgcn_cvt_pkrtz(a0, a1);
+            const auto lp = __builtin_amdgcn_cvt_pkrtz(a0 - (float)hp[0], a1 - (float)hp[1]);
+            hh[q] = __builtin_bit_cast(uint32_t, hp);
+            hl[q] = __builtin_bit_cast(uint32_t, lp);
         }
-        uint8_t *ent = lds + (size_t)(((b * 8 + c) * 4 + h) * 32);
-        *reinterpret_cast<half8 *>(ent) = hh;
-        *reinterpret_cast<half8 *>(ent + 16) = hl;
+        uint8_t *ent = lds + (size_t)b * Lo.tab_stride + (size_t)((c * 4 + h) * 32);
+        *reinterpret_cast<u32x4 *>(ent) = hh;
+        *reinterpret_cast<u32x4 *>(ent + 16) = hl;
     }
   }
     // (the barrier before the first stage is computed also orders the table)
@@ -342,16 +350,15 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     // from scale dword 0 (jq = 0) or 2 (jq = 1), the top two bits of quad 1
     // from dword 0 (scales) or 1 (mins)
     const uint32_t lmask = jq ? 0x0F0F0F0Fu : 0x3F3F3F3Fu, hmask = jq ? 0x30303030u : 0u;
-    // A operand address of MFMA c for block b: abase[c] + (b*1024 & amask[c])
-    // (amask = 0 for lanes whose row m takes no data from c: the zero slot)
-    uint32_t abase[8], amask[8];
+    // A operand address of MFMA c for block b: b*1040 + aoff[c], where lanes
+    // whose row m takes no data from c point at the block's zero slot
+    uint32_t aoff[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
         const int o = pair_byte_offset(c >> 1, g);
         const int sb = 2 * (o >> 5) + (c & 1);
         const bool hit = (n16 >> 1) == sb;  // A lane m = n16 = 2*sb + part
-        abase[c] = hit ? (uint32_t)((c * 4 + g) * 32 + (n16 & 1) * 16) : Lo.zero;
-        amask[c] = hit ? 0xFFFFFFFFu : 0u;
+        aoff[c] = hit ? (uint32_t)((c * 4 + g) * 32 + (n16 & 1) * 16) : 1024u;
     }
     // y contribution of one tile: sub-blocks 2g, 2g+1 of W row n16 in block b,
     // from their q*x sums s0, s1 (scaled by corr) and the block header hd.
@@ -440,9 +447,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
             f32x4 accA = {0.f, 0.f, 0.f, 0.f}, accB = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-                const half8 aA = *reinterpret_cast<const half8 *>(lds + abase[c] + (((uint32_t)bA << 10) & amask[c]));
+                const half8 aA = *reinterpret_cast<const half8 *>(lds + (uint32_t)bA * 1040u + aoff[c]);
                 const half8 aB = (R == 32) ? aA
-                    : *reinterpret_cast<const half8 *>(lds + abase[c] + (((uint32_t)bBc << 10) & amask[c]));
+                    : *reinterpret_cast<const half8 *>(lds + (uint32_t)bBc * 1040u + aoff[c]);
                 const int p = c >> 1;
                 const uint32_t mask = (c & 1) ? 0x00F000F0u : 0x000F000Fu;
                 const uint32_t wa0 = p < 2 ? qa0[2 * p] : qa1[2 * p - 4];
