@@ -617,9 +617,8 @@ static hipError_t launch_cfg(const uint8_t *w, const GemvAct &a, float *y, int n
 }
 
 // Launch configurations (rows per work-group, blocks per stage, wavefronts,
-// stages in flight, LDS double buffer). Few row groups (small N): one 16-row
-// work-group per CU, with the whole row in one stage when K <= 3584. Many row
-// groups: persistent 32-row work-groups streamed 8 blocks at a time.
+// stages in flight, LDS double buffer, persistent). 4 and 5 are tuning
+// alternatives kept for the sweep (MGQ_GEMV_CFG).
 template <bool Q8>
 static hipError_t launch_any(int cfg, const uint8_t *w, const GemvAct &a, float *y, int n,
                              int bpr, hipStream_t stream) {
@@ -627,6 +626,9 @@ static hipError_t launch_any(int cfg, const uint8_t *w, const GemvAct &a, float 
         case 0: return launch_cfg<32, 8, 8, 1, false, Q8>(w, a, y, n, bpr, stream, true);
         case 1: return launch_cfg<16, 14, 7, 1, true, Q8>(w, a, y, n, bpr, stream, false);
         case 2: return launch_cfg<16, 16, 8, 1, true, Q8>(w, a, y, n, bpr, stream, false);
+        case 3: return launch_cfg<16, 14, 7, 1, true, Q8>(w, a, y, n, bpr, stream, true);
+        case 4: return launch_cfg<16, 14, 7, 2, true, Q8>(w, a, y, n, bpr, stream, true);
+        case 5: return launch_cfg<32, 14, 7, 1, true, Q8>(w, a, y, n, bpr, stream, true);
         default: return hipErrorInvalidValue;
     }
 }
@@ -649,12 +651,12 @@ static hipError_t mfma_dispatch(const uint8_t *w, const GemvAct &a, float *y, in
     if (force >= 0) {
         cfg = force;
     } else {
-        // one 16-row work-group per CU when that covers N (latency-bound
-        // shapes), else persistent 32-row work-groups
-        const long groups16 = (n + 15) / 16;
-        if (groups16 > device_cus()) cfg = 0;
-        else if (bpr <= 14) cfg = 1;
-        else cfg = 2;
+        // K <= 3584: whole rows per stage (each 16-row stage is one contiguous
+        // run of HBM), persistent when 16-row groups outnumber the CUs. Longer
+        // K: 16 blocks per stage, or persistent 32-row groups of 8 blocks.
+        const bool many = (n + 15) / 16 > device_cus();
+        if (bpr <= 14) cfg = many ? 3 : 1;
+        else cfg = many ? 0 : 2;
     }
     hipError_t e = launch_any<Q8>(cfg, w, a, y, n, bpr, stream);
     // LDS too small for the double-buffered stages: single-buffered persistent
