@@ -438,7 +438,7 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the Q4_K GEMV path is built and measured on a "
-              "single MI355X in this build (multi-GPU sharding is design-only; see DESIGN.md).",
+              "single MI355X in this build (multi-GPU sharding is not implemented).",
               file=sys.stderr)
         return 2
 

@@ -1,18 +1,35 @@
 // Prefill dequant-GEMM on the gfx950 matrix cores:
 //   C[m][r] = sum_k dequant(W)[r][k] * A[m][k],  A f16 [M][K], C f32 [M][N].
 // No counterpart in the reference (its prefill is a per-token GEMV loop,
-// crates/modgrad-gemma/examples/gemma4_rocm.rs:26-34); the dequantized value
-// of each weight is the canonical one (gguf.rs:364-404) rounded once to f16.
+// crates/modgrad-gemma/examples/gemma4_rocm.rs:26-34); each weight is the
+// canonical dequantized value (gguf.rs:364-404) with d*sc and dmin*m rounded
+// to f16 and the weight itself computed and rounded in f16.
 //
-// Work-group tile: 128 W rows x 128 tokens, K stepped by 64 (= one 32-byte qs
-// group: sub-blocks 2G and 2G+1 of a super-block). Per K step every thread
-// decodes 32 weights (16 qs bytes of one row) in f32, rounds them to f16 and
-// stores them to LDS next to the 128x64 f16 activation tile; LDS is double
-// buffered so the next step's global loads overlap this step's MFMAs.
-// 4 wavefronts, each a 64x64 output tile = 4x4 v_mfma_f32_16x16x32_f16 tiles,
-// W as the A operand (rows), activations as the B operand (tokens), so a
-// lane's 4 accumulators are 4 consecutive W rows of one token: one 16-byte
-// store into C's row-major [M][N].
+// Work-group tile: 128 W rows x 128 tokens, 4 wavefronts of 64x64 outputs
+// (4x4 v_mfma_f32_16x16x32_f16, W rows as the A operand, tokens as the B
+// operand, so a lane's 4 accumulators are 4 consecutive W rows of one token:
+// one 16-byte store into C's [M][N]).
+//
+// Memory path. Global loads are whole cache lines: the W tile of a
+// super-block (128 rows x 144 B) is copied raw into LDS as 1152 contiguous
+// 16-byte pieces (a wavefront's 64 pieces cover ~7 rows), once per 8 MFMA
+// k-steps; the activation tile of a 64-wide K step is 128 tokens x 128 B,
+// 8 lanes per token. Loads for the next super-block / K step are in flight
+// while the current one is computed.
+//
+// Dequantization happens where the MFMA operand is built, straight from the
+// raw bytes in LDS: a lane's 8 qs bytes B0..B7 give the operand of the low
+// nibbles (sub-block 2G) and of the high nibbles (2G+1). (w & 0x000F000F) |
+// 0x64006400 puts the low nibbles of bytes 0 and 2 into the mantissas of two
+// f16 1024.0s (exact), (w >> 8) does the same for bytes 1 and 3, and a mask of
+// 0x00F000F0 yields 1024 + 16*q for the high nibbles (scaled back by using
+// d*sc/16). v_pk_add_f16(-1024) and v_pk_fma_f16(d*sc, -dmin*m) finish two
+// weights per instruction. The operand's k order is therefore
+// 0,2,1,3,4,6,5,7 within each group of 8; the activation tile is stored in
+// the same order (two v_perm_b32 per 8 values), so every product pairs a
+// weight with its own activation. Per-row (d*sc, -dmin*m) pairs of the 8
+// sub-blocks are decoded once per super-block by the lane that loaded the
+// row's header piece.
 #include "q4k_device.hpp"
 #include "q4k_launch.hpp"
 
@@ -21,117 +38,235 @@ namespace mgq {
 namespace gemm {
 constexpr int BN = 128;        // W rows per work-group
 constexpr int BM = 128;        // tokens per work-group
-constexpr int BK = 64;         // k per step
-constexpr int LDS_ROW = 72;    // halves per LDS row (64 + 8 pad, 144 B)
-constexpr int TILE_HALVES = 128 * LDS_ROW;
+constexpr int BK = 64;         // k per step (one 32-byte qs group: 2 sub-blocks)
+constexpr int AROW = 72;       // halves per activation LDS row (64 + 8 pad, 144 B)
+constexpr int SROW = 10;       // dwords per scale row (8 + 2 pad: conflict-free b64 reads)
+constexpr int RAW_PIECES = BN * kBlockBytes / 16;  // 1152 16-byte pieces per super-block
+constexpr int NXCD = 8;        // XCDs the hardware deals work-groups across, round robin
 }  // namespace gemm
 
-__global__ __launch_bounds__(256) void gemm_q4k_f16_kernel(const uint8_t *__restrict__ w,
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// (v & mask) | magic in one instruction. gfx9 VOP3 encodings take no literal
+// constants, so the compiler would otherwise emit a v_and/v_or pair.
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t magic) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(mask), "v"(magic));
+    return r;
+}
+
+// Two f16 weights (bytes 0 and 2 of v, nibble selected by mask) as a pair:
+// (q * d1 + nm1) with q recovered exactly from the 1024.0 mantissa.
+__device__ __forceinline__ uint32_t dq2(uint32_t v, uint32_t mask, uint32_t magic, h2_t d1,
+                                        h2_t nm1) {
+    const h2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const h2_t q = __builtin_bit_cast(h2_t, and_or(v, mask, magic)) - k1024;
+    return __builtin_bit_cast(uint32_t, q * d1 + nm1);
+}
+
+// MFMA A operand of 8 weights from qs bytes B0..B7 (dwords w0, w1; s0, s1 =
+// w0 >> 8, w1 >> 8), k order 0,2,1,3,4,6,5,7; sp = (d1, nm1) of the
+// sub-block as an f16 pair. magic holds 0x64006400.
+__device__ __forceinline__ half8 dq8(uint32_t w0, uint32_t w1, uint32_t s0, uint32_t s1,
+                                     uint32_t mask, uint32_t magic, uint32_t sp) {
+    const h2_t s = __builtin_bit_cast(h2_t, sp);
+    const h2_t d1 = {s[0], s[0]}, nm1 = {s[1], s[1]};
+    u32x4 r;
+    r[0] = dq2(w0, mask, magic, d1, nm1);
+    r[1] = dq2(s0, mask, magic, d1, nm1);
+    r[2] = dq2(w1, mask, magic, d1, nm1);
+    r[3] = dq2(s1, mask, magic, d1, nm1);
+    return __builtin_bit_cast(half8, r);
+}
+
+// 8 consecutive f16 activations x0..x7 -> order x0,x2,x1,x3,x4,x6,x5,x7.
+__device__ __forceinline__ u32x4 act_order(u32x4 v) {
+    u32x4 r;
+    r[0] = __builtin_amdgcn_perm(v[1], v[0], 0x05040100u);
+    r[1] = __builtin_amdgcn_perm(v[1], v[0], 0x07060302u);
+    r[2] = __builtin_amdgcn_perm(v[3], v[2], 0x05040100u);
+    r[3] = __builtin_amdgcn_perm(v[3], v[2], 0x07060302u);
+    return r;
+}
+
+__global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__restrict__ w,
                                                            const uint16_t *__restrict__ a,
                                                            float *__restrict__ c, int n, int bpr,
-                                                           int m_tokens) {
+                                                           int m_tokens, int tiles_n, int tiles_m) {
     using namespace gemm;
-    __shared__ __attribute__((aligned(16))) _Float16 sW[2][TILE_HALVES];
-    __shared__ __attribute__((aligned(16))) _Float16 sA[2][TILE_HALVES];
+    __shared__ __attribute__((aligned(16))) uint8_t sRaw[BN * kBlockBytes];  // 18432 B
+    __shared__ __attribute__((aligned(16))) uint32_t sScl[BN * SROW];        // 5120 B
+    __shared__ __attribute__((aligned(16))) _Float16 sA[2][BM * AROW];      // 36864 B
+
+    // work-group -> tile: the hardware sends work-group i to XCD i % 8; give
+    // XCD x a contiguous range of tiles (token tiles of a W tile adjacent)
+    const int ntiles = tiles_n * tiles_m;
+    const int per_xcd = (ntiles + NXCD - 1) / NXCD;
+    const int tile = (int)(blockIdx.x % NXCD) * per_xcd + (int)(blockIdx.x / NXCD);
+    if (tile >= ntiles) return;  // uniform; only when ntiles % 8 != 0
+    const int n0 = (tile / tiles_m) * BN, m0 = (tile % tiles_m) * BM;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
     const int K = bpr * kBlockElems;
-    const int steps = K / BK;  // 4 per super-block
+    const int T = bpr * 4;  // K steps
     const size_t row_bytes = (size_t)bpr * kBlockBytes;
 
-    // loader roles: W -> (row wr, 16-byte half wh); A -> 4 x 16 B of one token row
-    const int wr = tid >> 1, wh = tid & 1;
-    const uint8_t *wrow = w + (size_t)min(n0 + wr, n - 1) * row_bytes;
-    const int ar = tid >> 1, ac = (tid & 1) * 32;  // token row, first half column
-    const uint16_t *arow = a + (size_t)min(m0 + ar, m_tokens - 1) * K;
-
-    u32x4 qreg, hreg;
-    u32x4 areg[4];
-    auto gload = [&](int s) {
-        const int b = s >> 2, G = s & 3;
-        const uint8_t *blk = wrow + (size_t)b * kBlockBytes;
-        hreg = *reinterpret_cast<const u32x4 *>(blk);
-        qreg = *reinterpret_cast<const u32x4 *>(blk + 16 + 32 * G + 16 * wh);
-        const uint16_t *ap = arow + (size_t)s * BK + ac;
+    // raw W loader: piece p = tid + 256*k (k < 4, and k = 4 for tid < 128)
+    // is bytes 16*(p%9) .. +15 of row p/9's super-block
+    const uint8_t *rsrc[5];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) areg[i] = *reinterpret_cast<const u32x4 *>(ap + 8 * i);
-    };
-    auto lstore = [&](int s, int buf) {
-        const int G = s & 3;
-        const float d = half_bits_finite(hreg[0]), dmin = half_bits_finite(hreg[0] >> 16);
-        uint32_t sc_lo, m_lo, sc_hi, m_hi;
-        scale_min(2 * G, hreg[1], hreg[2], hreg[3], sc_lo, m_lo);
-        scale_min(2 * G + 1, hreg[1], hreg[2], hreg[3], sc_hi, m_hi);
-        const float d1 = d * (float)sc_lo, m1 = dmin * (float)m_lo;
-        const float d2 = d * (float)sc_hi, m2 = dmin * (float)m_hi;
-        half8 lo[2], hi[2];
+    for (int k = 0; k < 5; ++k) {
+        const int p = min(tid + 256 * k, RAW_PIECES - 1);
+        rsrc[k] = w + (size_t)min(n0 + p / 9, n - 1) * row_bytes + 16 * (p % 9);
+    }
+    const bool has5 = tid < RAW_PIECES - 1024;
+    // the lane holding a row's header piece decodes that row's scales
+    int hk = -1, hrow = 0;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const uint32_t byte = (qreg[j >> 2] >> (8 * (j & 3))) & 0xFFu;
-            lo[j >> 3][j & 7] = (_Float16)(d1 * (float)(byte & 15u) - m1);
-            hi[j >> 3][j & 7] = (_Float16)(d2 * (float)(byte >> 4) - m2);
+    for (int k = 0; k < 5; ++k) {
+        const int p = tid + 256 * k;
+        if (p < RAW_PIECES && p % 9 == 0) {
+            hk = k;
+            hrow = p / 9;
         }
-        _Float16 *dst = &sW[buf][wr * LDS_ROW + 16 * wh];
-        *reinterpret_cast<half8 *>(dst) = lo[0];
-        *reinterpret_cast<half8 *>(dst + 8) = lo[1];
-        *reinterpret_cast<half8 *>(dst + 32) = hi[0];
-        *reinterpret_cast<half8 *>(dst + 40) = hi[1];
-        _Float16 *da = &sA[buf][ar * LDS_ROW + ac];
+    }
+    u32x4 R[5];
+    auto rload = [&](int b) {  // piece 4 is loaded by every lane (clamped address): no branch
 #pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4 *>(da + 8 * i) = areg[i];
+        for (int k = 0; k < 5; ++k)
+            R[k] = *reinterpret_cast<const u32x4 *>(rsrc[k] + (size_t)b * kBlockBytes);
+    };
+    auto rstore = [&]() {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) *reinterpret_cast<u32x4 *>(&sRaw[16 * (tid + 256 * k)]) = R[k];
+        if (has5) *reinterpret_cast<u32x4 *>(&sRaw[16 * (tid + 1024)]) = R[4];
+        if (hk >= 0) {
+            u32x4 h = R[0];
+#pragma unroll
+            for (int k = 1; k < 5; ++k)
+                if (hk == k) h = R[k];
+            const float d = half_bits_finite(h[0]), dmin = half_bits_finite(h[0] >> 16);
+            uint32_t pr[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                uint32_t sc, m;
+                scale_min(j, h[1], h[2], h[3], sc, m);
+                _Float16 d1 = (_Float16)(d * (float)sc);
+                if (j & 1) d1 = d1 * (_Float16)0.0625f;  // high nibbles arrive as 16*q
+                const _Float16 nm1 = (_Float16)(-(dmin * (float)m));
+                pr[j] = __builtin_bit_cast(uint32_t, (h2_t){d1, nm1});
+            }
+            u32x2 *dst = reinterpret_cast<u32x2 *>(&sScl[hrow * SROW]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dst[j] = (u32x2){pr[2 * j], pr[2 * j + 1]};
+        }
+    };
+
+    // activation loader: 8 lanes per token (128 B), tokens tid/8 + 32*k
+    const int ap = tid & 7;
+    const uint16_t *asrc[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        asrc[k] = a + (size_t)min(m0 + (tid >> 3) + 32 * k, m_tokens - 1) * K + 8 * ap;
+    u32x4 Areg[2][4];  // two register sets: step t+2's loads fly while t+1's are stored
+    auto aload = [&](int t, int set) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            Areg[set][k] = *reinterpret_cast<const u32x4 *>(asrc[k] + (size_t)t * BK);
+    };
+    auto astore = [&](int set, int buf) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            *reinterpret_cast<u32x4 *>(&sA[buf][((tid >> 3) + 32 * k) * AROW + 8 * ap]) =
+                act_order(Areg[set][k]);
     };
 
     // compute roles
     const int wn = (wave >> 1) * 64, wm = (wave & 1) * 64;  // wave's W-row / token offsets
-    const int l16 = lane & 15, kq = (lane >> 4) * 8;
+    const int l16 = lane & 15, q = lane >> 4;
     f32x4 acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int jj = 0; jj < 4; ++jj) acc[i][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    gload(0);
-    lstore(0, 0);
-    __syncthreads();
-    for (int s = 0; s < steps; ++s) {
-        const int buf = s & 1;
-        if (s + 1 < steps) gload(s + 1);
+    // magic 0x64006400 in a VGPR (the VOP3 constant bus takes one SGPR: the mask)
+    const uint32_t magic = __builtin_amdgcn_readfirstlane(0x64006400u) + (uint32_t)(tid >> 16);
+    auto compute = [&](int G, int buf) {
+        half8 wlo[4], whi[4];
 #pragma unroll
-        for (int kk = 0; kk < BK; kk += 32) {
-            half8 wa[4], tb[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                wa[i] = *reinterpret_cast<const half8 *>(&sW[buf][(wn + 16 * i + l16) * LDS_ROW + kk + kq]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                tb[j] = *reinterpret_cast<const half8 *>(&sA[buf][(wm + 16 * j + l16) * LDS_ROW + kk + kq]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[i], tb[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+            const int row = wn + 16 * i + l16;
+            const u32x2 wq = *reinterpret_cast<const u32x2 *>(&sRaw[row * kBlockBytes + 16 + 32 * G + 8 * q]);
+            const u32x2 sp = *reinterpret_cast<const u32x2 *>(&sScl[row * SROW + 2 * G]);
+            const uint32_t s0 = wq[0] >> 8, s1 = wq[1] >> 8;
+            wlo[i] = dq8(wq[0], wq[1], s0, s1, 0x000F000Fu, magic, sp[0]);
+            whi[i] = dq8(wq[0], wq[1], s0, s1, 0x00F000F0u, magic, sp[1]);
         }
-        if (s + 1 < steps) lstore(s + 1, buf ^ 1);
-        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            half8 tb[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+                tb[jj] = *reinterpret_cast<const half8 *>(
+                    &sA[buf][(wm + 16 * jj + l16) * AROW + 32 * h + 8 * q]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj)
+                    acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(h ? whi[i] : wlo[i], tb[jj],
+                                                                        acc[i][jj], 0, 0, 0);
+        }
+    };
+
+    // K step t = 4b + G computes activation buffer t&1 against super-block b
+    // in sRaw; it stores step t+1's activations (register set (t+1)&1) into
+    // the other buffer and refills that set with step t+3. After a
+    // super-block's last step and a barrier, the next super-block's raw
+    // bytes (loaded during this one) replace it. Every load is issued
+    // unconditionally (indices clamped to the last step / super-block), so
+    // the hardware load counter waits only for the data each store needs.
+    rload(0);
+    aload(0, 0);
+    aload(min(1, T - 1), 1);
+    rstore();
+    astore(0, 0);
+    rload(min(1, bpr - 1));
+    aload(min(2, T - 1), 0);
+    __syncthreads();
+    for (int b = 0; b < bpr; ++b) {
+#pragma unroll
+        for (int G = 0; G < 4; ++G) {
+            const int t = 4 * b + G;
+            compute(G, G & 1);
+            astore((G + 1) & 1, (G + 1) & 1);  // after the last step: an unused buffer
+            aload(min(t + 3, T - 1), (G + 1) & 1);
+            if (G == 3) {
+                __syncthreads();  // every wavefront is done with super-block b
+                rstore();         // after the last super-block: rewrites unused data
+                rload(min(b + 2, bpr - 1));
+            }
+            __syncthreads();
+        }
     }
 
-    // lane holds W rows wn+16i+4(l/16)+v (v=0..3) of token wm+16j+l%16
+    // lane holds W rows wn+16i+4q+v (v=0..3) of token wm+16jj+l16
     const bool vec = (n % 4) == 0 && (((uintptr_t)c & 15u) == 0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int m = m0 + wm + 16 * j + l16;
+    for (int jj = 0; jj < 4; ++jj) {
+        const int m = m0 + wm + 16 * jj + l16;
         if (m >= m_tokens) continue;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int r = n0 + wn + 16 * i + 4 * (lane >> 4);
+            const int r = n0 + wn + 16 * i + 4 * q;
             float *dst = c + (size_t)m * n + r;
             if (vec && r + 3 < n) {
-                *reinterpret_cast<f32x4 *>(dst) = acc[i][j];
+                *reinterpret_cast<f32x4 *>(dst) = acc[i][jj];
             } else {
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
-                    if (r + v < n) dst[v] = acc[i][j][v];
+                    if (r + v < n) dst[v] = acc[i][jj][v];
             }
         }
     }
@@ -140,10 +275,11 @@ __global__ __launch_bounds__(256) void gemm_q4k_f16_kernel(const uint8_t *__rest
 hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n, int bpr,
                            int m_tokens, hipStream_t stream) {
     if (((uintptr_t)w & 15u) || ((uintptr_t)a & 15u)) return hipErrorInvalidValue;
-    const unsigned gx = (unsigned)((n + gemm::BN - 1) / gemm::BN);
-    const unsigned gy = (unsigned)((m_tokens + gemm::BM - 1) / gemm::BM);
-    if (gy > 65535) return hipErrorInvalidValue;
-    gemm_q4k_f16_kernel<<<dim3(gx, gy), 256, 0, stream>>>(w, a, c, n, bpr, m_tokens);
+    const int tn = (n + gemm::BN - 1) / gemm::BN, tm = (m_tokens + gemm::BM - 1) / gemm::BM;
+    const long ntiles = (long)tn * tm;
+    const long grid = (ntiles + gemm::NXCD - 1) / gemm::NXCD * gemm::NXCD;
+    if (grid > 0x7FFFFFFFL) return hipErrorInvalidValue;
+    gemm_q4k_f16_kernel<<<(unsigned)grid, 256, 0, stream>>>(w, a, c, n, bpr, m_tokens, tn, tm);
     return hipGetLastError();
 }
 

@@ -4,7 +4,7 @@ TEST INFRASTRUCTURE ONLY: tests/, __graft_entry__.smoke() and bench.py's
 cpu_baseline leg import this module as the checker. The product package
 (modgrad_amd) never imports it.
 
-Seeded input generation follows one fixed convention (documented in DESIGN.md):
+Seeded input generation follows one fixed convention:
   W[n][k] = 0.02 * SimpleRng(seed_w).next_normal(), row-major, then quantized
   by the reference quantizer over the flattened tensor (neuron.rs:931-951);
   x[k] = SimpleRng(seed_x).next_normal().

@@ -271,7 +271,8 @@ def test_matvec_batched_vector_alu_fallback(L, orc):
 
 
 # --------------------------------------------------------------------- GEMM --
-@pytest.mark.parametrize("n,bpr,m", [(64, 2, 8), (100, 14, 33)])
+@pytest.mark.parametrize("n,bpr,m", [(64, 2, 8), (100, 14, 33), (256, 1, 1), (300, 5, 130),
+                                     (1030, 3, 257), (130, 9, 384)])
 def test_gemm_f16_small(L, orc, n, bpr, m):
     note(f"gemm n={n} bpr={bpr} m={m}")
     w = orc.seeded_weight(61, n, bpr * 256)
