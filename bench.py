@@ -376,16 +376,19 @@ def run_kquant(torch, q4k, args):
             "kernel": "mgq::gemv_q5k_kernel" if fmt == 176 else "mgq::gemv_q6k_kernel"}
 
 
-TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                               "gemv_mfma_decode7b_pmc.txt")
+TRAFFIC_PROFILES = {"decode7b": "gemv_mfma_decode7b_pmc.txt",
+                    "prefill": "gemm_q4k_f16_prefill_pmc.txt"}
 
 
 def profiled_traffic(workload: str):
-    """HBM bytes per GEMV launch from the committed FETCH_SIZE / WRITE_SIZE
-    summary of this same workload (calibrated against a plain copy), or None."""
-    if workload != "decode7b" or not os.path.exists(TRAFFIC_PROFILE):
+    """HBM bytes per launch of the workload's dominant kernel from the
+    committed FETCH_SIZE / WRITE_SIZE summary of this same workload
+    (calibrated against a plain copy), or None."""
+    name = TRAFFIC_PROFILES.get(workload)
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name or "")
+    if name is None or not os.path.exists(path):
         return None
-    with open(TRAFFIC_PROFILE) as f:
+    with open(path) as f:
         for line in f:
             if line.startswith("traffic_bytes_per_launch:"):
                 return int(float(line.split(":", 1)[1]))
@@ -406,7 +409,8 @@ def run_side_workload(torch, q4k, args) -> int:
                     "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 2),
                                  "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                  "frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
-                                 "traffic": None, "kernel": r["kernel"]}})
+                                 "traffic": profiled_traffic(args.workload),
+                                 "kernel": r["kernel"]}})
     else:
         out.update({"value": round(r["gbs"], 2), "unit": "GB/s", "dtype": "f32",
                     "us_per_launch": r["us_per_launch"],
