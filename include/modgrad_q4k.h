@@ -156,6 +156,57 @@ hipError_t launch_gemm_q4k_f16(const unsigned char *w_q4, const uint16_t *a_f16,
                                int out_dim, int blocks_per_row, int m_tokens,
                                hipStream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Decode glue (kernels/rms_norm.hip, kernels/transformer_ops.hip) and its
+ * fusion into the Q4_K matvec.
+ * ------------------------------------------------------------------------- */
+
+/* Replaces launch_rms_norm (decl rocm.rs:435-445, def kernels/rms_norm.hip:
+ * 79-95): y[r][c] = x[r][c] * rstd * weight[c] for r < n rows of `hidden`,
+ * rstd = 1/sqrt(mean(x[r]^2) + eps). The sum of squares follows the
+ * reference kernel's order; the result matches it to an ulp of rsqrt.
+ * hipErrorInvalidValue for n <= 0, hidden <= 0 or a null pointer. */
+hipError_t launch_rms_norm(const float *x, const float *weight, float *y, int n, int hidden,
+                           float eps);
+hipError_t launch_rms_norm_ex(const float *x, const float *weight, float *y, int n, int hidden,
+                              float eps, hipStream_t stream);
+
+/* Replaces launch_geglu (decl rocm.rs:505, def kernels/transformer_ops.hip:
+ * 32-46): out[i] = gelu_tanh(gate[i]) * up[i]. */
+hipError_t launch_geglu(const float *gate, const float *up, float *out, int n);
+
+/* GLU activations for launch_glu_ex / launch_matvec_q4k_glu_ex. */
+#define MGQ_ACT_GELU_TANH 0 /* the reference's geglu */
+#define MGQ_ACT_SILU 1      /* v * sigmoid(v) (SwiGLU); no counterpart in the reference */
+
+/* out[i] = act(gate[i]) * up[i] on `stream`. */
+hipError_t launch_glu_ex(const float *gate, const float *up, float *out, int n, int act,
+                         hipStream_t stream);
+
+/* Fused RMSNorm -> Q4_K matvec: y = W * rms_norm(x, norm_w, eps) for one
+ * activation row of K = blocks_per_row*256, replacing the reference decode's
+ * launch_rms_norm + launch_matvec_q4k pair (rocm_gemma.rs:439-440, 477-478).
+ * Computed as rstd * (W * (x .* norm_w)): the matvec's activation staging
+ * multiplies by norm_w and reduces sum(x^2) on the way, so the normalized
+ * vector never goes to memory. Same per-row bound as launch_matvec_q4k
+ * against the f64 matvec of the normalized vector. w, x and norm_w must be
+ * 16-byte aligned (hipErrorInvalidValue otherwise); hipErrorNotSupported when
+ * K exceeds the kernel's LDS staging (blocks_per_row > ~110). */
+hipError_t launch_matvec_q4k_rmsnorm_ex(const unsigned char *w_q4, const float *x,
+                                        const float *norm_w, float eps, float *y, int out_dim,
+                                        int blocks_per_row, hipStream_t stream);
+
+/* Fused gate/up matvec + GLU: y[i] = act(g[i]) * u[i] with g = W_gate * xn,
+ * u = W_up * xn, xn = rms_norm(x, norm_w, eps) when norm_w is not null (else
+ * xn = x). Replaces the reference FFN's launch_rms_norm + two
+ * launch_matvec_q4k + launch_geglu (rocm_gemma.rs:477-481): one launch, and
+ * gate/up never go to memory. W_gate and W_up are out_dim x blocks_per_row
+ * row-aligned Q4_K, both 16-byte aligned, as are x and norm_w. */
+hipError_t launch_matvec_q4k_glu_ex(const unsigned char *w_gate, const unsigned char *w_up,
+                                    const float *x, const float *norm_w, float eps, int act,
+                                    float *y, int out_dim, int blocks_per_row,
+                                    hipStream_t stream);
+
 /* One matvec of a decode-step chain. */
 typedef struct mgq_gemv_desc {
     const unsigned char *w_q4; /* row-aligned Q4_K bytes */

@@ -20,6 +20,7 @@ hipErrorNotSupported = 801
 P = ctypes.c_void_p
 I = ctypes.c_int
 S = ctypes.c_size_t
+F = ctypes.c_float
 
 SIGNATURES = {
     "launch_dequant_q4k": (I, [P, I, P]),
@@ -39,6 +40,12 @@ SIGNATURES = {
     "mgq_batched_workspace_bytes": (S, [I, I]),
     "launch_matvec_q4k_batched": (I, [P, P, P, I, I, I, P, S, P]),
     "launch_gemm_q4k_f16": (I, [P, P, P, I, I, I, P]),
+    "launch_rms_norm": (I, [P, P, P, I, I, F]),
+    "launch_rms_norm_ex": (I, [P, P, P, I, I, F, P]),
+    "launch_geglu": (I, [P, P, P, I]),
+    "launch_glu_ex": (I, [P, P, P, I, I, P]),
+    "launch_matvec_q4k_rmsnorm_ex": (I, [P, P, P, F, P, I, I, P]),
+    "launch_matvec_q4k_glu_ex": (I, [P, P, P, P, F, I, P, I, I, P]),
     "mgq_chain_create": (I, [P, I, P]),
     "mgq_chain_launch": (I, [P, P]),
     "mgq_chain_destroy": (I, [P]),
@@ -46,6 +53,8 @@ SIGNATURES = {
     "mgq_version": (ctypes.c_char_p, []),
 }
 
+ACT_GELU_TANH = 0
+ACT_SILU = 1
 LAYOUT_ROWS = 0
 LAYOUT_FLAT = 1
 

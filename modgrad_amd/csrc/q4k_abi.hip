@@ -228,6 +228,60 @@ hipError_t mgq_chain_destroy(void *chain) {
     return e1 != hipSuccess ? e1 : e2;
 }
 
+hipError_t launch_rms_norm_ex(const float *x, const float *weight, float *y, int n, int hidden,
+                              float eps, hipStream_t stream) {
+    if (n <= 0 || hidden <= 0 || !x || !weight || !y) return hipErrorInvalidValue;
+    if ((int64_t)n * hidden > kMaxI32 * 4LL) return hipErrorInvalidValue;
+    return mgq::rms_norm_launch(x, weight, y, n, hidden, eps, stream);
+}
+
+hipError_t launch_rms_norm(const float *x, const float *weight, float *y, int n, int hidden,
+                           float eps) {
+    return launch_rms_norm_ex(x, weight, y, n, hidden, eps, nullptr);
+}
+
+hipError_t launch_glu_ex(const float *gate, const float *up, float *out, int n, int act,
+                         hipStream_t stream) {
+    if (n <= 0 || !gate || !up || !out) return hipErrorInvalidValue;
+    if (act != MGQ_ACT_GELU_TANH && act != MGQ_ACT_SILU) return hipErrorInvalidValue;
+    return mgq::glu_launch(gate, up, out, n, act, stream);
+}
+
+hipError_t launch_geglu(const float *gate, const float *up, float *out, int n) {
+    return launch_glu_ex(gate, up, out, n, MGQ_ACT_GELU_TANH, nullptr);
+}
+
+namespace {
+bool misaligned16(const void *p) { return ((uintptr_t)p & 15u) != 0; }
+}  // namespace
+
+hipError_t launch_matvec_q4k_rmsnorm_ex(const unsigned char *w_q4, const float *x,
+                                        const float *norm_w, float eps, float *y, int out_dim,
+                                        int blocks_per_row, hipStream_t stream) {
+    if (out_dim <= 0 || blocks_per_row <= 0 || !w_q4 || !x || !norm_w || !y)
+        return hipErrorInvalidValue;
+    if ((int64_t)blocks_per_row * 256 > kMaxI32) return hipErrorInvalidValue;
+    if (misaligned16(w_q4) || misaligned16(x) || misaligned16(norm_w) || misaligned4(y))
+        return hipErrorInvalidValue;
+    return mgq::gemv_fused_launch(w_q4, nullptr, x, norm_w, eps, MGQ_ACT_GELU_TANH, y, out_dim,
+                                  blocks_per_row, stream);
+}
+
+hipError_t launch_matvec_q4k_glu_ex(const unsigned char *w_gate, const unsigned char *w_up,
+                                    const float *x, const float *norm_w, float eps, int act,
+                                    float *y, int out_dim, int blocks_per_row,
+                                    hipStream_t stream) {
+    if (out_dim <= 0 || blocks_per_row <= 0 || !w_gate || !w_up || !x || !y)
+        return hipErrorInvalidValue;
+    if (act != MGQ_ACT_GELU_TANH && act != MGQ_ACT_SILU) return hipErrorInvalidValue;
+    if ((int64_t)blocks_per_row * 256 > kMaxI32) return hipErrorInvalidValue;
+    if (misaligned16(w_gate) || misaligned16(w_up) || misaligned16(x) ||
+        (norm_w && misaligned16(norm_w)) || misaligned4(y))
+        return hipErrorInvalidValue;
+    return mgq::gemv_fused_launch(w_gate, w_up, x, norm_w, eps, act, y, out_dim, blocks_per_row,
+                                  stream);
+}
+
 hipError_t mgq_prepare(void) { return mgq::gemv_prepare(); }
 
 const char *mgq_version(void) { return "modgrad_q4k 0.1.0 gfx950"; }

@@ -58,4 +58,13 @@ __device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) {
     return *reinterpret_cast<const uint32_t *>(p);
 }
 
+// GLU activations: kActGeluTanh is gelu_tanh in the order
+// kernels/transformer_ops.hip:36-38 evaluates it; kActSilu is v*sigmoid(v).
+constexpr int kActGeluTanh = 0, kActSilu = 1;
+__device__ __forceinline__ float glu_act(float v, int act) {
+    if (act == kActSilu) return v / (1.0f + expf(-v));
+    const float c = 0.7978845608f * (v + 0.044715f * v * v * v);
+    return 0.5f * v * (1.0f + tanhf(c));
+}
+
 }  // namespace mgq

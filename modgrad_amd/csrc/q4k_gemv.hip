@@ -123,10 +123,26 @@ __device__ __forceinline__ float quad_xor(float v) {
 //         row-major over (row, block, 16-byte piece), rows padded to an odd
 //         number of pieces
 //   aux   NW*32*4 B: cross-wave reduction buffer (32 row sums per wavefront)
+//   ybuf  rounds x R row results (x2 with kFuseGlu: gate and up)
+//   normp 16 f32 sum(x^2) partials (kFuseNorm only)
 struct MfmaLayout {
     int bpr, R, C, NW, I;  // I = 1 KiB wave loads per stage
-    uint32_t tab_stride, meta, stage, stage_bytes, aux, ybuf;
+    uint32_t tab_stride, meta, stage, stage_bytes, aux, ybuf, normp;
     size_t total;
+};
+
+// Fused glue (f32 activations only). kFuseNorm: y = W * rms_norm(x, nw, eps),
+// computed as rstd * (W * (x .* nw)) -- the prologue multiplies x by nw and
+// accumulates sum(x^2), the row results are scaled once at the end.
+// kFuseGlu: two weight matrices (gate w, up w2) of one shape; each row group
+// streams through the same work-group twice (gate, then up) and the output is
+// act(gate_row . x) * (up_row . x).
+constexpr int kFuseNorm = 1, kFuseGlu = 2;
+struct GemvFuse {
+    const uint8_t *w2;  // kFuseGlu: the up matrix
+    const float *nw;    // kFuseNorm: RMSNorm weights [K]
+    float eps;
+    int act;            // kActGeluTanh or kActSilu
 };
 
 // rounds = row groups per work-group (persistent launch); their results stay
@@ -138,7 +154,7 @@ struct MfmaLayout {
 __host__ __device__ constexpr int stage_row_pieces(int C) { return (9 * C) | 1; }
 
 __host__ __device__ inline MfmaLayout mfma_layout(int bpr, int R, int C, int NW, int rounds,
-                                                  bool db, bool q8 = false) {
+                                                  bool db, bool q8 = false, int fuse = 0) {
     MfmaLayout L;
     L.bpr = bpr; L.R = R; L.C = C; L.NW = NW;
     // wave loads per stage, padded so every wavefront issues the same count
@@ -153,7 +169,11 @@ __host__ __device__ inline MfmaLayout mfma_layout(int bpr, int R, int C, int NW,
     // two stage buffers when double-buffered and K needs more than one stage
     L.aux = L.stage + ((db && bpr > C) ? 2u : 1u) * L.stage_bytes;
     L.ybuf = L.aux + (uint32_t)NW * 128u;
-    L.total = (size_t)L.ybuf + (size_t)R * rounds * 4;
+    // kFuseGlu: gate and up results of every row group (2x rounds);
+    // kFuseNorm: one sum(x^2) partial per wavefront
+    const int vm = (fuse & kFuseGlu) ? 2 : 1;
+    L.normp = L.ybuf + (uint32_t)(R * rounds * vm * 4);
+    L.total = (size_t)L.normp + ((fuse & kFuseNorm) ? 64 : 0);
     return L;
 }
 
@@ -177,16 +197,20 @@ __host__ __device__ inline MfmaLayout mfma_layout(int bpr, int R, int C, int NW,
 // weight stream: activations arrive as int8 xq with per-sub-block scale xd and
 // sum xsum; each lane dots its 32 qs bytes (4 sub-block halves) with
 // v_dot4_i32_i8 and applies xd*(d*sc*isum - dmin*m*xsum).
-template <int R, int C, int NW, int PF, bool DB, int XIT, bool Q8>
+// FUSE (f32 activations only): kFuseNorm and/or kFuseGlu, see GemvFuse.
+template <int R, int C, int NW, int PF, bool DB, int XIT, bool Q8, int FUSE>
 __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__restrict__ w,
                                                             const float *__restrict__ x,
                                                             const int8_t *__restrict__ xq,
                                                             const float *__restrict__ xdv,
                                                             const float *__restrict__ xsv,
                                                             float *__restrict__ y, int n,
-                                                            int bpr, int rounds) {
+                                                            int bpr, int rounds, GemvFuse fz) {
+    static_assert(!(Q8 && FUSE), "fused glue runs on f32 activations");
+    constexpr bool NORM = (FUSE & kFuseNorm) != 0;
+    constexpr int VM = (FUSE & kFuseGlu) ? 2 : 1;  // passes per row group (gate, up)
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    const MfmaLayout Lo = mfma_layout(bpr, R, C, NW, rounds, DB, Q8);
+    const MfmaLayout Lo = mfma_layout(bpr, R, C, NW, rounds, DB, Q8, FUSE);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
     float *meta = reinterpret_cast<float *>(lds + Lo.meta);
@@ -195,7 +219,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     const int stages = (bpr + C - 1) / C;
     const int groups = (n + R - 1) / R;
     const int my_groups = (groups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
-    const int Q = my_groups * stages;             // stages this work-group streams
+    const int Q = my_groups * VM * stages;        // stages this work-group streams
     constexpr int PIECES = R * 9 * C;             // 16-byte pieces per stage
     constexpr int IPW = ((PIECES + 63) / 64 + NW - 1) / NW;  // wave loads per wavefront
     constexpr int I = IPW * NW;                   // wave loads per stage (padded)
@@ -223,7 +247,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     }
     auto gload = [&](int q, u32x4(&dst)[IPW]) {
         q = std::min(q, Q - 1);
-        const uint32_t r0 = ((uint32_t)blockIdx.x + (uint32_t)(q / stages) * gridDim.x) * R;
+        const int vg = q / stages;  // pass index: row group vg / VM, matrix vg % VM
+        const uint32_t r0 = ((uint32_t)blockIdx.x + (uint32_t)(vg / VM) * gridDim.x) * R;
+        const uint8_t *wm = (VM == 2 && (vg & 1)) ? fz.w2 : w;
         const uint32_t tcol = (uint32_t)((q % stages) * C * kBlockBytes);
         const uint32_t rlast = (uint32_t)(n - 1), rb = (uint32_t)row_bytes;
 #pragma unroll
@@ -231,7 +257,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
             const uint32_t rr = std::min(r0 + prow[k], rlast);
             const uint32_t col = std::min(tcol + pcol[k], plast[k]);
             const uint64_t off = (uint64_t)rr * rb + col;  // one v_mad_u64_u32
-            dst[k] = *reinterpret_cast<const u32x4 *>(w + off);
+            dst[k] = *reinterpret_cast<const u32x4 *>(wm + off);
         }
     };
     auto lstore = [&](int buf, const u32x4(&src)[IPW]) {
@@ -278,14 +304,19 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
   } else {
     const int nitems = bpr * 32;
     const int its = (nitems + NW * 64 - 1) / (NW * 64);  // <= XIT
-    f32x4 xv0[XIT], xv1[XIT];
+    f32x4 xv0[XIT], xv1[XIT], nv0[XIT], nv1[XIT];
 #pragma unroll
     for (int it = 0; it < XIT; ++it) {
         if (it >= its) break;
         const int i = std::min(tid + it * NW * 64, nitems - 1);
         xv0[it] = *reinterpret_cast<const f32x4 *>(x + (size_t)i * 8);
         xv1[it] = *reinterpret_cast<const f32x4 *>(x + (size_t)i * 8 + 4);
+        if constexpr (NORM) {
+            nv0[it] = *reinterpret_cast<const f32x4 *>(fz.nw + (size_t)i * 8);
+            nv1[it] = *reinterpret_cast<const f32x4 *>(fz.nw + (size_t)i * 8 + 4);
+        }
     }
+    float ssq = 0.0f;  // kFuseNorm: this lane's sum of x^2
 #pragma unroll
     for (int f = 0; f < PF; ++f) gload(f, stg[f]);
 
@@ -295,7 +326,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     for (int it = 0; it < XIT; ++it) {
         if (it >= its) break;
         const int i = tid + it * NW * 64;  // lanes of one sub-block share i/4
-        const f32x4 v0 = xv0[it], v1 = xv1[it];
+        f32x4 v0 = xv0[it], v1 = xv1[it];
+        if constexpr (NORM) {
+            if (i < nitems)  // items past the end are clamped duplicates
+                ssq += ((v0[0] * v0[0] + v0[1] * v0[1]) + (v0[2] * v0[2] + v0[3] * v0[3])) +
+                       ((v1[0] * v1[0] + v1[1] * v1[1]) + (v1[2] * v1[2] + v1[3] * v1[3]));
+            v0 *= nv0[it];  // the table holds x .* nw; rstd scales the results
+            v1 *= nv1[it];
+        }
         float amax = fmaxf(fmaxf(fmaxf(fabsf(v0[0]), fabsf(v0[1])), fmaxf(fabsf(v0[2]), fabsf(v0[3]))),
                            fmaxf(fmaxf(fabsf(v1[0]), fabsf(v1[1])), fmaxf(fabsf(v1[2]), fabsf(v1[3]))));
         float sum = ((v0[0] + v0[1]) + (v0[2] + v0[3])) + ((v1[0] + v1[1]) + (v1[2] + v1[3]));
@@ -335,6 +373,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         uint8_t *ent = lds + (size_t)b * Lo.tab_stride + (size_t)((c * 4 + h) * 32);
         *reinterpret_cast<u32x4 *>(ent) = hh;
         *reinterpret_cast<u32x4 *>(ent + 16) = hl;
+    }
+    if constexpr (NORM) {
+        // one partial per wavefront; read after the stream's last barrier
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ssq += __shfl_xor(ssq, off, 64);
+        if (lane == 0) reinterpret_cast<float *>(lds + Lo.normp)[wave] = ssq;
     }
   }
     // (the barrier before the first stage is computed also orders the table)
@@ -522,11 +566,27 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     if constexpr (PF > 1) if (q0 + 1 < Q) step(q0 + 1, std::integral_constant<int, 1 % PF>{}, q0 + 2 < Q);
     if constexpr (PF > 2) if (q0 + 2 < Q) step(q0 + 2, std::integral_constant<int, 2 % PF>{}, q0 + 3 < Q);
     __syncthreads();
+    float rstd = 1.0f;
+    if constexpr (NORM) {
+        // rms_norm's 1/sqrt(mean(x^2) + eps) (kernels/rms_norm.hip:63-68)
+        const float *np = reinterpret_cast<const float *>(lds + Lo.normp);
+        float ss = 0.0f;
+        for (int wv = 0; wv < NW; ++wv) ss += np[wv];
+        rstd = rsqrtf(ss / (float)(bpr * kBlockElems) + fz.eps);
+    }
+    const float *yb = reinterpret_cast<const float *>(lds + Lo.ybuf);
     for (int i = tid; i < my_groups * R; i += NW * 64) {
         const int r = ((int)blockIdx.x + (i / R) * (int)gridDim.x) * R + (i % R);
         if (r < n) {
-            const float v = reinterpret_cast<const float *>(lds + Lo.ybuf)[i];
-            y[r] = (Q8 && !isfinite(v)) ? 0.0f : v;  // Q8: the reference's clamp
+            if constexpr (VM == 2) {
+                // pass 2j = gate rows of group j, 2j+1 = up rows
+                const int gi = (i / R) * 2 * R + (i % R);
+                const float gv = yb[gi] * rstd, uv = yb[gi + R] * rstd;
+                y[r] = glu_act(gv, fz.act) * uv;
+            } else {
+                const float v = NORM ? yb[i] * rstd : yb[i];
+                y[r] = (Q8 && !isfinite(v)) ? 0.0f : v;  // Q8: the reference's clamp
+            }
         }
     }
 }
@@ -558,34 +618,34 @@ struct GemvAct {
 };
 
 // Allows the kernel the whole 160 KiB of gfx950 LDS (once per process).
-template <int R, int C, int NW, int PF, bool DB, int XIT, bool Q8>
+template <int R, int C, int NW, int PF, bool DB, int XIT, bool Q8, int FUSE>
 static hipError_t lds_attr() {
     static const hipError_t attr = hipFuncSetAttribute(
-        (const void *)gemv_mfma_kernel<R, C, NW, PF, DB, XIT, Q8>,
+        (const void *)gemv_mfma_kernel<R, C, NW, PF, DB, XIT, Q8, FUSE>,
         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     return attr;
 }
 
-template <int R, int C, int NW, int PF, bool DB, bool Q8>
+template <int R, int C, int NW, int PF, bool DB, bool Q8, int FUSE = 0>
 static hipError_t lds_attr_all() {
-    hipError_t e = lds_attr<R, C, NW, PF, DB, 1, Q8>();
-    if (e == hipSuccess) e = lds_attr<R, C, NW, PF, DB, 2, Q8>();
-    if (e == hipSuccess) e = lds_attr<R, C, NW, PF, DB, 4, Q8>();
-    if (e == hipSuccess) e = lds_attr<R, C, NW, PF, DB, 8, Q8>();
+    hipError_t e = lds_attr<R, C, NW, PF, DB, 1, Q8, FUSE>();
+    if (e == hipSuccess) e = lds_attr<R, C, NW, PF, DB, 2, Q8, FUSE>();
+    if (e == hipSuccess) e = lds_attr<R, C, NW, PF, DB, 4, Q8, FUSE>();
+    if (e == hipSuccess) e = lds_attr<R, C, NW, PF, DB, 8, Q8, FUSE>();
     return e;
 }
 
-template <int R, int C, int NW, int PF, bool DB, int XIT, bool Q8>
-static hipError_t launch_xit(const uint8_t *w, const GemvAct &a, float *y, int n, int bpr,
-                             hipStream_t stream, bool persistent) {
-    auto kern = gemv_mfma_kernel<R, C, NW, PF, DB, XIT, Q8>;
-    const hipError_t attr = lds_attr<R, C, NW, PF, DB, XIT, Q8>();
+template <int R, int C, int NW, int PF, bool DB, int XIT, bool Q8, int FUSE>
+static hipError_t launch_xit(const uint8_t *w, const GemvAct &a, const GemvFuse &fz, float *y,
+                             int n, int bpr, hipStream_t stream, bool persistent) {
+    auto kern = gemv_mfma_kernel<R, C, NW, PF, DB, XIT, Q8, FUSE>;
+    const hipError_t attr = lds_attr<R, C, NW, PF, DB, XIT, Q8, FUSE>();
     if (attr != hipSuccess) return attr;
     const long groups = (n + R - 1) / R;
     long grid = groups, rounds = 1;
     if (persistent) {
         static const int occ_env = env_int("MGQ_GEMV_OCC", 0);
-        const size_t base = mfma_layout(bpr, R, C, NW, 8, DB, Q8).total;
+        const size_t base = mfma_layout(bpr, R, C, NW, 8, DB, Q8, FUSE).total;
         int occ = 0;  // resident work-groups per CU (registers and LDS)
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)kern, NW * 64,
                                                          base) != hipSuccess || occ <= 0)
@@ -595,57 +655,76 @@ static hipError_t launch_xit(const uint8_t *w, const GemvAct &a, float *y, int n
         rounds = (groups + maxgrid - 1) / maxgrid;
         grid = (groups + rounds - 1) / rounds;  // balanced: every WG gets `rounds` groups (or one fewer)
     }
-    const MfmaLayout Lo = mfma_layout(bpr, R, C, NW, (int)rounds, DB, Q8);
+    const MfmaLayout Lo = mfma_layout(bpr, R, C, NW, (int)rounds, DB, Q8, FUSE);
     if (Lo.total > 160 * 1024) return hipErrorNotSupported;
     kern<<<(unsigned)grid, NW * 64, Lo.total, stream>>>(w, a.x, a.xq, a.xd, a.xsum, y, n, bpr,
-                                                        (int)rounds);
+                                                        (int)rounds, fz);
     return hipGetLastError();
 }
 
 // The activation loads per lane (XIT) are a compile-time count so they stay
 // in registers: 1, 2, 4 or 8 (f32: 8-float chunks, bpr*32 of them; Q8:
 // 16-byte items, bpr*20 of them).
-template <int R, int C, int NW, int PF, bool DB, bool Q8>
-static hipError_t launch_cfg(const uint8_t *w, const GemvAct &a, float *y, int n, int bpr,
-                             hipStream_t stream, bool persistent) {
+template <int R, int C, int NW, int PF, bool DB, bool Q8, int FUSE>
+static hipError_t launch_cfg(const uint8_t *w, const GemvAct &a, const GemvFuse &fz, float *y,
+                             int n, int bpr, hipStream_t stream, bool persistent) {
     const int need = (bpr * (Q8 ? 20 : 32) + NW * 64 - 1) / (NW * 64);
-    if (need <= 1) return launch_xit<R, C, NW, PF, DB, 1, Q8>(w, a, y, n, bpr, stream, persistent);
-    if (need <= 2) return launch_xit<R, C, NW, PF, DB, 2, Q8>(w, a, y, n, bpr, stream, persistent);
-    if (need <= 4) return launch_xit<R, C, NW, PF, DB, 4, Q8>(w, a, y, n, bpr, stream, persistent);
-    if (need <= 8) return launch_xit<R, C, NW, PF, DB, 8, Q8>(w, a, y, n, bpr, stream, persistent);
+#define MGQ_XIT(X) launch_xit<R, C, NW, PF, DB, X, Q8, FUSE>(w, a, fz, y, n, bpr, stream, persistent)
+    if (need <= 1) return MGQ_XIT(1);
+    if (need <= 2) return MGQ_XIT(2);
+    if (need <= 4) return MGQ_XIT(4);
+    if (need <= 8) return MGQ_XIT(8);
+#undef MGQ_XIT
     return hipErrorNotSupported;
 }
 
 // Launch configurations (rows per work-group, blocks per stage, wavefronts,
 // stages in flight, LDS double buffer, persistent). 4 and 5 are tuning
 // alternatives kept for the sweep (MGQ_GEMV_CFG).
-template <bool Q8>
-static hipError_t launch_any(int cfg, const uint8_t *w, const GemvAct &a, float *y, int n,
-                             int bpr, hipStream_t stream) {
+// (The fused variants instantiate only the dispatched configurations 0-3.)
+template <bool Q8, int FUSE>
+static hipError_t launch_any(int cfg, const uint8_t *w, const GemvAct &a, const GemvFuse &fz,
+                             float *y, int n, int bpr, hipStream_t stream) {
     switch (cfg) {
-        case 0: return launch_cfg<32, 8, 8, 1, false, Q8>(w, a, y, n, bpr, stream, true);
-        case 1: return launch_cfg<16, 14, 7, 1, true, Q8>(w, a, y, n, bpr, stream, false);
-        case 2: return launch_cfg<16, 16, 8, 1, true, Q8>(w, a, y, n, bpr, stream, false);
-        case 3: return launch_cfg<16, 14, 7, 1, true, Q8>(w, a, y, n, bpr, stream, true);
-        case 4: return launch_cfg<16, 14, 7, 2, true, Q8>(w, a, y, n, bpr, stream, true);
-        case 5: return launch_cfg<32, 14, 7, 1, true, Q8>(w, a, y, n, bpr, stream, true);
-        default: return hipErrorInvalidValue;
+        case 0: return launch_cfg<32, 8, 8, 1, false, Q8, FUSE>(w, a, fz, y, n, bpr, stream, true);
+        case 1: return launch_cfg<16, 14, 7, 1, true, Q8, FUSE>(w, a, fz, y, n, bpr, stream, false);
+        case 2: return launch_cfg<16, 16, 8, 1, true, Q8, FUSE>(w, a, fz, y, n, bpr, stream, false);
+        case 3: return launch_cfg<16, 14, 7, 1, true, Q8, FUSE>(w, a, fz, y, n, bpr, stream, true);
+        default:
+            if constexpr (FUSE == 0) {
+                if (cfg == 4)
+                    return launch_cfg<16, 14, 7, 2, true, Q8, 0>(w, a, fz, y, n, bpr, stream, true);
+                if (cfg == 5)
+                    return launch_cfg<32, 14, 7, 1, true, Q8, 0>(w, a, fz, y, n, bpr, stream, true);
+            }
+            return hipErrorInvalidValue;
     }
 }
 
-hipError_t gemv_prepare() {
-    hipError_t e = lds_attr_all<32, 8, 8, 1, false, false>();
-    if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, true, false>();
-    if (e == hipSuccess) e = lds_attr_all<16, 16, 8, 1, true, false>();
-    if (e == hipSuccess) e = lds_attr_all<32, 8, 8, 1, false, true>();
-    if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, true, true>();
-    if (e == hipSuccess) e = lds_attr_all<16, 16, 8, 1, true, true>();
+template <int FUSE>
+static hipError_t prepare_fuse() {
+    hipError_t e = lds_attr_all<32, 8, 8, 1, false, false, FUSE>();
+    if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, true, false, FUSE>();
+    if (e == hipSuccess) e = lds_attr_all<16, 16, 8, 1, true, false, FUSE>();
     return e;
 }
 
-template <bool Q8>
+hipError_t gemv_prepare() {
+    hipError_t e = prepare_fuse<0>();
+    if (e == hipSuccess) e = lds_attr_all<32, 8, 8, 1, false, true>();
+    if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, true, true>();
+    if (e == hipSuccess) e = lds_attr_all<16, 16, 8, 1, true, true>();
+    if (e == hipSuccess) e = prepare_fuse<kFuseNorm>();
+    if (e == hipSuccess) e = prepare_fuse<kFuseGlu>();
+    if (e == hipSuccess) e = prepare_fuse<kFuseNorm | kFuseGlu>();
+    return e;
+}
+
+// work_rows: rows of work (2n for the gate/up pair) for the persistence choice
+template <bool Q8, int FUSE = 0>
 static hipError_t mfma_dispatch(const uint8_t *w, const GemvAct &a, float *y, int n, int bpr,
-                                hipStream_t stream) {
+                                hipStream_t stream, const GemvFuse &fz = GemvFuse{},
+                                int work_rows = 0) {
     static const int force = env_int("MGQ_GEMV_CFG", -1);  // tuning override
     int cfg;
     if (force >= 0) {
@@ -654,14 +733,30 @@ static hipError_t mfma_dispatch(const uint8_t *w, const GemvAct &a, float *y, in
         // K <= 3584: whole rows per stage (each 16-row stage is one contiguous
         // run of HBM), persistent when 16-row groups outnumber the CUs. Longer
         // K: 16 blocks per stage, or persistent 32-row groups of 8 blocks.
-        const bool many = (n + 15) / 16 > device_cus();
+        const bool many = ((work_rows > 0 ? work_rows : n) + 15) / 16 > device_cus();
         if (bpr <= 14) cfg = many ? 3 : 1;
         else cfg = many ? 0 : 2;
     }
-    hipError_t e = launch_any<Q8>(cfg, w, a, y, n, bpr, stream);
+    hipError_t e = launch_any<Q8, FUSE>(cfg, w, a, fz, y, n, bpr, stream);
     // LDS too small for the double-buffered stages: single-buffered persistent
-    if (e == hipErrorNotSupported && cfg != 0) e = launch_any<Q8>(0, w, a, y, n, bpr, stream);
+    if (e == hipErrorNotSupported && cfg != 0) e = launch_any<Q8, FUSE>(0, w, a, fz, y, n, bpr, stream);
     return e;
+}
+
+hipError_t gemv_fused_launch(const uint8_t *w_gate, const uint8_t *w_up, const float *x,
+                             const float *norm_w, float eps, int act, float *y, int n, int bpr,
+                             hipStream_t stream) {
+    if (((uintptr_t)w_gate | (uintptr_t)w_up | (uintptr_t)x | (uintptr_t)norm_w) & 15u)
+        return hipErrorNotSupported;
+    const GemvAct a{x, nullptr, nullptr, nullptr};
+    const GemvFuse fz{w_up, norm_w, eps, act};
+    if (w_up == nullptr) {
+        if (norm_w == nullptr) return mfma_dispatch<false, 0>(w_gate, a, y, n, bpr, stream, fz);
+        return mfma_dispatch<false, kFuseNorm>(w_gate, a, y, n, bpr, stream, fz);
+    }
+    if (norm_w == nullptr)
+        return mfma_dispatch<false, kFuseGlu>(w_gate, a, y, n, bpr, stream, fz, 2 * n);
+    return mfma_dispatch<false, kFuseNorm | kFuseGlu>(w_gate, a, y, n, bpr, stream, fz, 2 * n);
 }
 
 hipError_t gemv_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,

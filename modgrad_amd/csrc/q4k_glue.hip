@@ -1,0 +1,61 @@
+// Decode glue around the matvecs (kernels/rms_norm.hip, kernels/
+// transformer_ops.hip:32-46): RMSNorm and the gated-linear-unit product.
+// Standalone versions under the reference's names; the matvec also runs them
+// fused (q4k_gemv.hip: RMSNorm in the activation staging, the GLU on the
+// gate/up results).
+#include "q4k_device.hpp"
+#include "q4k_launch.hpp"
+
+namespace mgq {
+
+// y[r][c] = (x[r][c] * rstd) * w[c], rstd = 1/sqrt(mean(x[r]^2) + eps), one
+// 256-thread work-group per row. The sum of squares follows the reference's
+// order (thread t sums c = t, t+256, ...; then a pairwise tree t += t+128,
+// t+64, ..., 1), so it matches the reference bit for bit; the tree's last six
+// levels run inside one wavefront (DPP row shifts via shfl_down).
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float *__restrict__ x,
+                                                       const float *__restrict__ w,
+                                                       float *__restrict__ y, int hidden,
+                                                       float eps) {
+    __shared__ float part[256];
+    const int tid = threadIdx.x;
+    const float *xr = x + (size_t)blockIdx.x * hidden;
+    float *yr = y + (size_t)blockIdx.x * hidden;
+    float s = 0.0f;
+    for (int c = tid; c < hidden; c += 256) s += xr[c] * xr[c];
+    part[tid] = s;
+    __syncthreads();
+    if (tid < 128) part[tid] += part[tid + 128];
+    __syncthreads();
+    if (tid < 64) {
+        float v = part[tid] + part[tid + 64];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off, 64);
+        if (tid == 0) part[0] = v;
+    }
+    __syncthreads();
+    const float rstd = rsqrtf(part[0] / (float)hidden + eps);
+    for (int c = tid; c < hidden; c += 256) yr[c] = xr[c] * rstd * w[c];
+}
+
+hipError_t rms_norm_launch(const float *x, const float *w, float *y, int rows, int hidden,
+                           float eps, hipStream_t stream) {
+    rms_norm_kernel<<<(unsigned)rows, 256, 0, stream>>>(x, w, y, hidden, eps);
+    return hipGetLastError();
+}
+
+// out[i] = act(gate[i]) * up[i]
+__global__ __launch_bounds__(256) void glu_kernel(const float *__restrict__ gate,
+                                                  const float *__restrict__ up,
+                                                  float *__restrict__ out, int n, int act) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = glu_act(gate[i], act) * up[i];
+}
+
+hipError_t glu_launch(const float *gate, const float *up, float *out, int n, int act,
+                      hipStream_t stream) {
+    glu_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(gate, up, out, n, act);
+    return hipGetLastError();
+}
+
+}  // namespace mgq

@@ -1,5 +1,5 @@
-// Q5_K and Q6_K matvecs (SURVEY "next" row: real GGUFs mix K-quants per
-// layer; the lm_head is often Q6_K). Same C ABI shape as the Q4_K matvec:
+// Q5_K and Q6_K matvecs (real GGUFs mix K-quants per layer; the lm_head is
+// often Q6_K). Same C ABI shape as the Q4_K matvec:
 // launch_matvec_q5k / launch_matvec_q6k (rocm.rs:467-486; kernels
 // matvec_q5k.hip, matvec_q6k.hip) and launch_matvec_q6k_dp4a (rocm.rs:490-491,
 // kernels/matvec_q6k_dp4a.hip) on the Q8_1 activations of

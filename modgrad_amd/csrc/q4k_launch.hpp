@@ -58,6 +58,20 @@ hipError_t gemv_q6k_launch(const uint8_t *w, const float *x, float *y, int n, in
 hipError_t gemv_q6k_q8_launch(const uint8_t *w, const int8_t *xq, const float *xd, float *y,
                               int n, int bpr, hipStream_t stream);
 
+// Fused glue matvec: w_up == nullptr -> y = W * rms_norm(x) (norm_w not
+// null) or W * x; w_up != nullptr -> y = act(W_gate*xn) .* (W_up*xn). All
+// pointers 16-byte aligned (hipErrorNotSupported otherwise, as when the LDS
+// staging does not fit).
+hipError_t gemv_fused_launch(const uint8_t *w_gate, const uint8_t *w_up, const float *x,
+                             const float *norm_w, float eps, int act, float *y, int n, int bpr,
+                             hipStream_t stream);
+
+// Standalone glue: RMSNorm over rows of `hidden`, and act(gate) * up.
+hipError_t rms_norm_launch(const float *x, const float *w, float *y, int rows, int hidden,
+                           float eps, hipStream_t stream);
+hipError_t glu_launch(const float *gate, const float *up, float *out, int n, int act,
+                      hipStream_t stream);
+
 hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n, int bpr,
                            int m_tokens, hipStream_t stream);
 

@@ -165,7 +165,43 @@ class kern:
         _chk(_lib.load().launch_matvec_q4k_dp4a_ex(w, xq, xd, xsum, y, out_dim, bpr,
                                                    _stream_ptr(stream)), "matvec_q4k_dp4a")
 
+    @staticmethod
+    def rms_norm(x: int, w: int, y: int, n: int, hidden: int, eps: float, stream=None) -> None:
+        """rocm.rs:981-983: y = x * rstd * w over n rows of `hidden`."""
+        _chk(_lib.load().launch_rms_norm_ex(x, w, y, n, hidden, eps, _stream_ptr(stream)),
+             "rms_norm")
+
+    @staticmethod
+    def geglu(gate: int, up: int, out: int, n: int, stream=None) -> None:
+        """rocm.rs:990-992: out = gelu_tanh(gate) * up."""
+        _chk(_lib.load().launch_glu_ex(gate, up, out, n, _lib.ACT_GELU_TANH, _stream_ptr(stream)),
+             "geglu")
+
     # additive entry points -------------------------------------------------
+    @staticmethod
+    def glu(gate: int, up: int, out: int, n: int, act: int = _lib.ACT_GELU_TANH,
+            stream=None) -> None:
+        """out = act(gate) * up, act = ACT_GELU_TANH or ACT_SILU."""
+        _chk(_lib.load().launch_glu_ex(gate, up, out, n, act, _stream_ptr(stream)), "glu")
+
+    @staticmethod
+    def matvec_q4k_rmsnorm(w: int, x: int, norm_w: int, eps: float, y: int, out_dim: int,
+                           bpr: int, stream=None) -> None:
+        """y = W * rms_norm(x, norm_w, eps) in one launch (the reference's
+        rms_norm + matvec_q4k pair, rocm_gemma.rs:439-440)."""
+        _chk(_lib.load().launch_matvec_q4k_rmsnorm_ex(w, x, norm_w, eps, y, out_dim, bpr,
+                                                      _stream_ptr(stream)), "matvec_q4k_rmsnorm")
+
+    @staticmethod
+    def matvec_q4k_glu(w_gate: int, w_up: int, x: int, y: int, out_dim: int, bpr: int,
+                       norm_w: int | None = None, eps: float = 0.0,
+                       act: int = _lib.ACT_GELU_TANH, stream=None) -> None:
+        """y = act(W_gate xn) * (W_up xn), xn = rms_norm(x) when norm_w is
+        given: the reference FFN's rms_norm + gate + up + geglu
+        (rocm_gemma.rs:477-481) in one launch."""
+        _chk(_lib.load().launch_matvec_q4k_glu_ex(w_gate, w_up, x, norm_w, eps, act, y, out_dim,
+                                                  bpr, _stream_ptr(stream)), "matvec_q4k_glu")
+
     @staticmethod
     def matvec_q4k_ex(w: int, x: int, y: int, out_dim: int, k_elems: int,
                       layout: int = _lib.LAYOUT_ROWS, stream=None) -> None:

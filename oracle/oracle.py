@@ -67,6 +67,8 @@ def lib() -> ctypes.CDLL:
         "orq_gemv_kquant_f64_abs": (None, [i, P, P, P, P, i, i]),
         "orq_gemv_q6k_dp4a_f64": (None, [P, P, P, i, i, P, P]),
         "orq_gemv_q4k_dp4a_f64": (None, [P, P, P, P, i, i, P, P]),
+        "orq_rms_norm": (None, [P, P, P, i, i, f]),
+        "orq_glu": (None, [P, P, P, i, i]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -291,3 +293,21 @@ def layer_seed(layer: int, tensor: int) -> int:
     """seed_W for tensor t of layer l (q=0,k=1,v=2,o=3,gate=4,up=5,down=6;
     lm_head is layer 28, t=7); seed_x = seed_W ^ 0xA5A5."""
     return 0x514B00 + 16 * layer + tensor
+
+
+def rms_norm(x: np.ndarray, w: np.ndarray, rows: int, hidden: int, eps: float) -> np.ndarray:
+    """f32 [rows][hidden] -- kernels/rms_norm.hip:28-75 in the reference's order."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    y = np.empty(rows * hidden, dtype=np.float32)
+    lib().orq_rms_norm(_p(x), _p(w), _p(y), rows, hidden, eps)
+    return y
+
+
+def glu(gate: np.ndarray, up: np.ndarray, act: int = 0) -> np.ndarray:
+    """act(gate) * up -- act 0: gelu_tanh (transformer_ops.hip:32-40), 1: silu."""
+    gate = np.ascontiguousarray(gate, dtype=np.float32)
+    up = np.ascontiguousarray(up, dtype=np.float32)
+    out = np.empty(gate.size, dtype=np.float32)
+    lib().orq_glu(_p(gate), _p(up), _p(out), gate.size, act)
+    return out

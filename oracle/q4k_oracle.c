@@ -610,3 +610,39 @@ void orq_fill_smooth(float *out, size_t n) {
         out[i] = sinf(t * 7.3f) * 0.5f + cosf(t * 17.1f) * 0.2f;
     }
 }
+
+/* ------------------------------------------------------------- glue ---- */
+
+/* kernels/rms_norm.hip:28-75 (one 256-thread block per row). */
+void orq_rms_norm(const float *x, const float *w, float *y, int rows, int hidden, float eps) {
+    float part[256];
+    for (int r = 0; r < rows; ++r) {
+        const float *xr = x + (size_t)r * hidden;
+        float *yr = y + (size_t)r * hidden;
+        for (int t = 0; t < 256; ++t) {
+            float s = 0.0f;
+            for (int c = t; c < hidden; c += 256) s = fmaf(xr[c], xr[c], s);
+            part[t] = s;
+        }
+        for (int off = 128; off > 0; off >>= 1)
+            for (int t = 0; t < off; ++t) part[t] += part[t + off];
+        const float mean_sq = part[0] / (float)hidden;
+        const float rstd = 1.0f / sqrtf(mean_sq + eps);
+        for (int c = 0; c < hidden; ++c) yr[c] = xr[c] * rstd * w[c];
+    }
+}
+
+/* kernels/transformer_ops.hip:32-40 (act 0); act 1 = silu. */
+void orq_glu(const float *gate, const float *up, float *out, int n, int act) {
+    for (int i = 0; i < n; ++i) {
+        const float v = gate[i];
+        float g;
+        if (act == 1) {
+            g = v / (1.0f + expf(-v));
+        } else {
+            const float c = 0.7978845608f * fmaf(0.044715f * v * v, v, v);
+            g = 0.5f * v * (1.0f + tanhf(c));
+        }
+        out[i] = g * up[i];
+    }
+}

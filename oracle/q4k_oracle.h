@@ -112,6 +112,18 @@ void orq_gemv_kquant_f64_abs(int block_bytes, const uint8_t *w, const float *x, 
 void orq_gemv_q6k_dp4a_f64(const uint8_t *w, const int8_t *xq, const float *xd, int out_dim,
                            int bpr, double *y, double *absterm);
 
+/* Decode glue (kernels/rms_norm.hip:28-75, kernels/transformer_ops.hip:32-46).
+ * orq_rms_norm: y[r][c] = (x[r][c] * rstd) * w[c], rstd = 1/sqrt(mean + eps);
+ * the sum of squares in the reference kernel's order: thread t of 256 sums
+ * fmaf(x, x, s) over c = t, t+256, ... (hipcc -O3 contracts `partial += v*v`),
+ * then the pairwise tree t += t+128, t+64, ..., 1. The GPU's rsqrtf may
+ * differ from 1/sqrtf by an ulp, so tests use a few-ulp bound.
+ * orq_glu: out[i] = act(gate[i]) * up[i]; act 0 = gelu_tanh as the reference
+ * writes it (the inner v + 0.044715*v*v*v contracted to one fma, as hipcc
+ * does), act 1 = silu, v / (1 + exp(-v)). */
+void orq_rms_norm(const float *x, const float *w, float *y, int rows, int hidden, float eps);
+void orq_glu(const float *gate, const float *up, float *out, int n, int act);
+
 /* CPU timing baseline: kfd::llm::matvec (llm.rs:468-534) with the fused
  * dequant-dot of llm.rs:684-806 (AVX-512 when the host has it, else scalar),
  * parallel over rows. threads <= 0 -> all cores. Returns 1 if AVX-512 used. */

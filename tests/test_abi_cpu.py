@@ -132,3 +132,28 @@ def test_host_size_savings():
                                            np.zeros(256, np.float32), 1024, 256)
     ratio = lin.host_size_bytes() / (1024 * 256 * 4 + 256 * 4)
     assert ratio < 0.16 and abs(ratio - 0.1415) < 0.001
+
+
+def test_glue_rejects_bad_args(L):
+    # launch_rms_norm: the reference's n/hidden checks (rms_norm.hip:87-89) + pointers
+    assert L.launch_rms_norm(FAKE, FAKE, FAKE, 0, 3584, 1e-6) == INVALID
+    assert L.launch_rms_norm(FAKE, FAKE, FAKE, 1, 0, 1e-6) == INVALID
+    assert L.launch_rms_norm(None, FAKE, FAKE, 1, 3584, 1e-6) == INVALID
+    assert L.launch_geglu(FAKE, FAKE, FAKE, 0) == INVALID
+    assert L.launch_geglu(FAKE, None, FAKE, 16) == INVALID
+    assert L.launch_glu_ex(FAKE, FAKE, FAKE, 16, 2, None) == INVALID  # unknown activation
+
+
+def test_fused_matvecs_reject_bad_args(L):
+    rms = L.launch_matvec_q4k_rmsnorm_ex
+    assert rms(FAKE, FAKE, FAKE, 1e-6, FAKE, 0, 14, None) == INVALID
+    assert rms(FAKE, FAKE, FAKE, 1e-6, FAKE, 16, 0, None) == INVALID
+    assert rms(FAKE, FAKE, None, 1e-6, FAKE, 16, 14, None) == INVALID   # norm weights required
+    assert rms(FAKE + 4, FAKE, FAKE, 1e-6, FAKE, 16, 14, None) == INVALID  # w not 16-B aligned
+    assert rms(FAKE, FAKE, FAKE + 8, 1e-6, FAKE, 16, 14, None) == INVALID  # norm_w not 16-B aligned
+    glu = L.launch_matvec_q4k_glu_ex
+    assert glu(FAKE, None, FAKE, None, 0.0, 0, FAKE, 16, 14, None) == INVALID  # up matrix required
+    assert glu(FAKE, FAKE, FAKE, None, 0.0, 7, FAKE, 16, 14, None) == INVALID  # unknown activation
+    assert glu(FAKE, FAKE + 4, FAKE, None, 0.0, 0, FAKE, 16, 14, None) == INVALID
+    assert glu(FAKE, FAKE, FAKE, FAKE + 4, 0.0, 0, FAKE, 16, 14, None) == INVALID
+    assert glu(FAKE, FAKE, FAKE, None, 0.0, 1, FAKE, -1, 14, None) == INVALID

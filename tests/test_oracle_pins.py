@@ -527,3 +527,72 @@ def test_q6k_dp4a_matches_numpy_and_reference_check(orc):
     y32, _ = orc.gemv_kquant(210, w, x, n, bpr)
     rms = np.sqrt(np.sum((y - y32) ** 2) / np.sum(y32.astype(np.float64) ** 2))
     assert 1e-6 < rms < 0.02
+
+
+# ------------------------------------------------------------------ glue --
+# orq_rms_norm restates kernels/rms_norm.hip:28-75 and orq_glu
+# kernels/transformer_ops.hip:32-40 (+ silu). Pinned against f64 closed forms;
+# the f32 reduction order itself only shows at the ulp level (bounded below).
+
+@pytest.mark.parametrize("hidden", [1, 100, 256, 3584, 5000])
+def test_rms_norm_matches_f64_formula(orc, hidden):
+    rng = np.random.default_rng(hidden)
+    rows = 3
+    x = rng.standard_normal(rows * hidden).astype(np.float32) * 3.0
+    w = rng.standard_normal(hidden).astype(np.float32)
+    eps = 1e-6
+    y = orc.rms_norm(x, w, rows, hidden, eps).reshape(rows, hidden)
+    x64 = x.astype(np.float64).reshape(rows, hidden)
+    ref = x64 / np.sqrt(np.mean(x64 * x64, axis=1, keepdims=True) + eps) * w.astype(np.float64)
+    # f32 sums of non-negative terms: a few dozen ulps at most
+    assert np.all(np.abs(y - ref) <= 4e-6 * np.abs(ref) + 1e-30)
+
+
+def test_rms_norm_eps_is_added_to_the_mean(orc):
+    # c^2 == eps: y = c / sqrt(c^2 + eps); eps added to the sum (or outside
+    # the sqrt) would give a different value
+    hidden, c, eps = 512, np.float32(1e-3), 1e-6
+    x = np.full(hidden, c, np.float32)
+    y = orc.rms_norm(x, np.ones(hidden, np.float32), 1, hidden, eps)
+    assert np.allclose(y, 1e-3 / math.sqrt(2e-6), rtol=2e-6)
+    assert np.all(orc.rms_norm(np.zeros(hidden, np.float32), np.ones(hidden, np.float32), 1,
+                               hidden, eps) == 0.0)
+
+
+def test_rms_norm_rows_are_independent(orc):
+    rng = np.random.default_rng(7)
+    rows, hidden = 4, 300
+    x = rng.standard_normal(rows * hidden).astype(np.float32)
+    w = rng.standard_normal(hidden).astype(np.float32)
+    y = orc.rms_norm(x, w, rows, hidden, 1e-5)
+    for r in range(rows):
+        one = orc.rms_norm(x[r * hidden:(r + 1) * hidden], w, 1, hidden, 1e-5)
+        assert np.array_equal(y[r * hidden:(r + 1) * hidden], one)
+
+
+@pytest.mark.parametrize("act", [0, 1])
+def test_glu_matches_f64_formula(orc, act):
+    rng = np.random.default_rng(11 + act)
+    g = np.concatenate([rng.standard_normal(4000) * 4, [0.0, 1.0, -1.0, 30.0, -30.0]]).astype(np.float32)
+    u = rng.standard_normal(g.size).astype(np.float32)
+    out = orc.glu(g, u, act)
+    v = g.astype(np.float64)
+    if act == 0:
+        a = 0.5 * v * (1.0 + np.tanh(math.sqrt(2.0 / math.pi) * (v + 0.044715 * v ** 3)))
+    else:
+        a = v / (1.0 + np.exp(-v))
+    ref = a * u.astype(np.float64)
+    assert np.all(np.abs(out - ref) <= 2e-6 * np.abs(v * u) + 1e-30)
+
+
+@pytest.mark.parametrize("act", [0, 1])
+def test_glu_identities(orc, act):
+    # act(v) - act(-v) == v for both activations; up scales the product
+    v = np.linspace(-8, 8, 1601).astype(np.float32)
+    one = np.ones_like(v)
+    d = orc.glu(v, one, act).astype(np.float64) - orc.glu(-v, one, act).astype(np.float64)
+    assert np.all(np.abs(d - v) <= 2e-6 * np.abs(v) + 1e-7)
+    u = np.random.default_rng(3).standard_normal(v.size).astype(np.float32)
+    assert np.array_equal(orc.glu(v, 2 * u, act), 2 * orc.glu(v, u, act))
+    known = {0: (1.0, 0.8411919906082768), 1: (2.0, 1.7615941559557649)}[act]
+    assert abs(float(orc.glu(np.float32([known[0]]), np.float32([1.0]), act)[0]) - known[1]) < 1e-6
