@@ -18,7 +18,9 @@ stderr.
 The other BASELINE configs have their own workloads (one JSON line each,
 measured the same way, not the headline): --workload config1 (4864x896
 flattened layout), --workload batched --batch B (config 4) and --workload
-prefill (config 5, TFLOP/s against the f16 matrix-core peak).
+prefill (config 5, TFLOP/s against the f16 matrix-core peak). Further rows:
+--workload decode7b_dp4a (Q8_1 activations), q5k / q6k (the other K-quants)
+and decode7b_glue (the step with its RMSNorm/GeGLU glue, fused vs unfused).
 """
 from __future__ import annotations
 
@@ -325,6 +327,99 @@ def run_decode_dp4a(torch, q4k, args):
             "tokens_per_s": 1000.0 / ms, "ms_per_step": ms}
 
 
+def run_decode_glue(torch, q4k, args):
+    """The decode step with its glue, as the reference engine runs it
+    (rocm_gemma.rs:439-483, attention itself left out): per layer
+    rms_norm -> qkv, o, rms_norm -> gate|up -> geglu -> down, and the final
+    rms_norm -> lm_head. Timed twice, each as one captured graph:
+      unfused: launch_rms_norm / launch_geglu between the matvecs (198 launches);
+      fused:   launch_matvec_q4k_rmsnorm_ex (qkv, lm_head) and
+               launch_matvec_q4k_glu_ex (gate, up, geglu) (113 launches).
+    value = the fused step's algorithmic GB/s over the same bytes as decode7b."""
+    from oracle import oracle as orc
+    wl = Workload(torch, decode_step_shapes())
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x6E0)
+    eps = 1e-6
+    L = wl.launches
+    layers = []
+    for l in range(LAYERS):
+        qkv, o, gu, dn = L[4 * l: 4 * l + 4]
+        nw_a = torch.rand(HIDDEN, device="cuda", generator=gen) + 0.5
+        nw_f = torch.rand(HIDDEN, device="cuda", generator=gen) + 0.5
+        layers.append((qkv, o, gu, dn, nw_a, nw_f, torch.empty(HIDDEN, device="cuda"),
+                       torch.empty(HIDDEN, device="cuda"), torch.empty(INTER, device="cuda")))
+    lm = L[-1]
+    nw_lm = torch.rand(HIDDEN, device="cuda", generator=gen) + 0.5
+    xn_lm = torch.empty(HIDDEN, device="cuda")
+    bpr_h = HIDDEN // BLOCK_ELEMS
+    gu_rows_bytes = INTER * bpr_h * BLOCK_BYTES  # gate rows, then up rows
+
+    def unfused(st):
+        k = q4k.kern
+        for (qkv, o, gu, dn, nw_a, nw_f, xa, xf, glu) in layers:
+            k.rms_norm(qkv[2].data_ptr(), nw_a.data_ptr(), xa.data_ptr(), 1, HIDDEN, eps, st)
+            k.matvec_q4k_ex(qkv[1].data_ptr(), xa.data_ptr(), qkv[3].data_ptr(), qkv[4], HIDDEN, stream=st)
+            k.matvec_q4k_ex(o[1].data_ptr(), o[2].data_ptr(), o[3].data_ptr(), o[4], o[5], stream=st)
+            k.rms_norm(gu[2].data_ptr(), nw_f.data_ptr(), xf.data_ptr(), 1, HIDDEN, eps, st)
+            k.matvec_q4k_ex(gu[1].data_ptr(), xf.data_ptr(), gu[3].data_ptr(), gu[4], HIDDEN, stream=st)
+            k.glu(gu[3].data_ptr(), gu[3].data_ptr() + 4 * INTER, glu.data_ptr(), INTER, stream=st)
+            k.matvec_q4k_ex(dn[1].data_ptr(), glu.data_ptr(), dn[3].data_ptr(), dn[4], dn[5], stream=st)
+        k.rms_norm(lm[2].data_ptr(), nw_lm.data_ptr(), xn_lm.data_ptr(), 1, HIDDEN, eps, st)
+        k.matvec_q4k_ex(lm[1].data_ptr(), xn_lm.data_ptr(), lm[3].data_ptr(), lm[4], HIDDEN, stream=st)
+
+    def fused(st):
+        k = q4k.kern
+        for (qkv, o, gu, dn, nw_a, nw_f, xa, xf, glu) in layers:
+            k.matvec_q4k_rmsnorm(qkv[1].data_ptr(), qkv[2].data_ptr(), nw_a.data_ptr(), eps,
+                                 qkv[3].data_ptr(), qkv[4], bpr_h, st)
+            k.matvec_q4k_ex(o[1].data_ptr(), o[2].data_ptr(), o[3].data_ptr(), o[4], o[5], stream=st)
+            k.matvec_q4k_glu(gu[1].data_ptr(), gu[1].data_ptr() + gu_rows_bytes, gu[2].data_ptr(),
+                             glu.data_ptr(), INTER, bpr_h, nw_f.data_ptr(), eps, stream=st)
+            k.matvec_q4k_ex(dn[1].data_ptr(), glu.data_ptr(), dn[3].data_ptr(), dn[4], dn[5], stream=st)
+        k.matvec_q4k_rmsnorm(lm[1].data_ptr(), lm[2].data_ptr(), nw_lm.data_ptr(), eps,
+                             lm[3].data_ptr(), lm[4], bpr_h, st)
+
+    ms_unfused = time_captured(torch, unfused, args.steps, args.warmup)
+    ms = time_captured(torch, fused, args.steps, args.warmup)
+    # parity: layer 0's fused qkv and GLU outputs (sampled rows) against the
+    # oracle's rms_norm -> f64 matvec (-> gelu_tanh * up)
+    qkv, o, gu, dn, nw_a, nw_f, xa, xf, glu = layers[0]
+    worst, fail = 0.0, None
+    rng = np.random.default_rng(5)
+    xn = orc.rms_norm(qkv[2].cpu().numpy(), nw_a.cpu().numpy(), 1, HIDDEN, eps)
+    idx = np.sort(rng.choice(qkv[4], size=256, replace=False))
+    wr = qkv[1].view(qkv[4], -1)[torch.from_numpy(idx).cuda()].cpu().numpy().ravel()
+    y_ref, a = orc.gemv(wr, xn, idx.size, bpr_h)
+    r = np.abs(qkv[3].cpu().numpy()[idx].astype(np.float64) - y_ref) / a
+    worst = max(worst, float(r.max()))
+    if not np.all(r <= 1e-4):
+        fail = f"FAIL rmsnorm+qkv: {r.max():.3e}"
+    xn = orc.rms_norm(gu[2].cpu().numpy(), nw_f.cpu().numpy(), 1, HIDDEN, eps)
+    idx = np.sort(rng.choice(INTER, size=256, replace=False))
+    wv = gu[1].view(2 * INTER, -1)
+    g, ag = orc.gemv(wv[torch.from_numpy(idx).cuda()].cpu().numpy().ravel(), xn, idx.size, bpr_h)
+    u, au = orc.gemv(wv[torch.from_numpy(idx + INTER).cuda()].cpu().numpy().ravel(), xn, idx.size, bpr_h)
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    act = 0.5 * g64 * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (g64 + 0.044715 * g64 ** 3)))
+    ref = act * u64
+    bound = 1e-4 * (1.13 * ag * np.abs(u64) + np.abs(act) * au) + 1e-5 * np.abs(ref)
+    err = np.abs(glu.cpu().numpy()[idx].astype(np.float64) - ref)
+    if not np.all(err <= bound):
+        fail = fail or f"FAIL gate/up glu: max err/bound {float((err / bound).max()):.3e}"
+    parity = fail or (f"ok (rmsnorm+qkv max err/absdot {worst:.2e} <= 1e-4; gate/up glu within "
+                      f"the propagated 1e-4 bound, max err/bound {float((err / bound).max()):.2e})")
+    nbytes = wl.bytes_per_pass
+    return {"workload": "decode7b_glue: decode7b with its RMSNorm/GeGLU glue; fused "
+                        "(rmsnorm+qkv, o, rmsnorm+gate/up+geglu, down; 113 launches) vs unfused "
+                        "(198 launches), one graph each",
+            "us_per_launch": round(ms * 1e3 / 113, 3), "gbs": nbytes / (ms * 1e-3) / 1e9,
+            "bytes_per_launch": nbytes // len(wl.launches), "parity": parity,
+            "kernel": "mgq::gemv_mfma_kernel<..., FUSE>", "tokens_per_s": 1000.0 / ms,
+            "ms_per_step": ms, "unfused_ms_per_step": ms_unfused,
+            "unfused_tokens_per_s": 1000.0 / ms_unfused}
+
+
 def run_kquant(torch, q4k, args):
     """Q5_K (176 B / 256 weights) on the gate and down shapes, or Q6_K
     (210 B / 256) on the lm_head shape -- the K-quants real GGUFs mix in."""
@@ -398,7 +493,8 @@ def profiled_traffic(workload: str):
 def run_side_workload(torch, q4k, args) -> int:
     """BASELINE configs 1, 4 and 5: one JSON line each, same field layout."""
     fn = {"config1": run_config1, "batched": run_batched, "prefill": run_prefill,
-          "decode7b_dp4a": run_decode_dp4a, "q5k": run_kquant, "q6k": run_kquant}[args.workload]
+          "decode7b_dp4a": run_decode_dp4a, "q5k": run_kquant, "q6k": run_kquant,
+          "decode7b_glue": run_decode_glue}[args.workload]
     r = fn(torch, q4k, args)
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": "synthetic",
@@ -418,7 +514,7 @@ def run_side_workload(torch, q4k, args) -> int:
                                  "unit": "GB/s", "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
                                  "traffic": None, "kernel": r["kernel"],
                                  "avg_launch_bytes": r["bytes_per_launch"]}})
-    for key in ("tokens_per_s", "ms_per_step"):
+    for key in ("tokens_per_s", "ms_per_step", "unfused_ms_per_step", "unfused_tokens_per_s"):
         if key in r:
             out[key] = round(r[key], 4)
     log(f"{r['workload']}: {r['us_per_launch']} us per launch; parity {r['parity']}")
@@ -433,7 +529,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="decode7b",
                     choices=["decode7b", "layer", "gateup", "config1", "batched", "prefill",
-                             "decode7b_dp4a", "q5k", "q6k"])
+                             "decode7b_dp4a", "q5k", "q6k", "decode7b_glue"])
     ap.add_argument("--batch", type=int, default=8, help="batch for --workload batched (1..16)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -451,7 +547,8 @@ def main() -> int:
     _lib.load()
     log(f"device {torch.cuda.get_device_name(0)}; workload {args.workload}")
 
-    if args.workload in ("config1", "batched", "prefill", "decode7b_dp4a", "q5k", "q6k"):
+    if args.workload in ("config1", "batched", "prefill", "decode7b_dp4a", "q5k", "q6k",
+                         "decode7b_glue"):
         return run_side_workload(torch, q4k, args)
     if args.workload == "decode7b":
         wl = Workload(torch, decode_step_shapes())
