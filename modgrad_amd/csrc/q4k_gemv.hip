@@ -679,8 +679,8 @@ static hipError_t launch_cfg(const uint8_t *w, const GemvAct &a, const GemvFuse 
 }
 
 // Launch configurations (rows per work-group, blocks per stage, wavefronts,
-// stages in flight, LDS double buffer, persistent). 4 and 5 are tuning
-// alternatives kept for the sweep (MGQ_GEMV_CFG).
+// stages in flight, LDS double buffer, persistent). 1, 3, 4, 5 and 7 are
+// tuning alternatives kept for the sweep (MGQ_GEMV_CFG).
 // (The fused variants instantiate only the dispatched configurations 0-3.)
 template <bool Q8, int FUSE>
 static hipError_t launch_any(int cfg, const uint8_t *w, const GemvAct &a, const GemvFuse &fz,
@@ -690,12 +690,15 @@ static hipError_t launch_any(int cfg, const uint8_t *w, const GemvAct &a, const 
         case 1: return launch_cfg<16, 14, 7, 1, true, Q8, FUSE>(w, a, fz, y, n, bpr, stream, false);
         case 2: return launch_cfg<16, 16, 8, 1, true, Q8, FUSE>(w, a, fz, y, n, bpr, stream, false);
         case 3: return launch_cfg<16, 14, 7, 1, true, Q8, FUSE>(w, a, fz, y, n, bpr, stream, true);
+        case 6: return launch_cfg<16, 14, 7, 1, false, Q8, FUSE>(w, a, fz, y, n, bpr, stream, true);
         default:
             if constexpr (FUSE == 0) {
                 if (cfg == 4)
                     return launch_cfg<16, 14, 7, 2, true, Q8, 0>(w, a, fz, y, n, bpr, stream, true);
                 if (cfg == 5)
                     return launch_cfg<32, 14, 7, 1, true, Q8, 0>(w, a, fz, y, n, bpr, stream, true);
+                if (cfg == 7)
+                    return launch_cfg<16, 7, 7, 1, true, Q8, 0>(w, a, fz, y, n, bpr, stream, true);
             }
             return hipErrorInvalidValue;
     }
@@ -704,6 +707,7 @@ static hipError_t launch_any(int cfg, const uint8_t *w, const GemvAct &a, const 
 template <int FUSE>
 static hipError_t prepare_fuse() {
     hipError_t e = lds_attr_all<32, 8, 8, 1, false, false, FUSE>();
+    if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, false, false, FUSE>();
     if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, true, false, FUSE>();
     if (e == hipSuccess) e = lds_attr_all<16, 16, 8, 1, true, false, FUSE>();
     return e;
@@ -714,6 +718,7 @@ hipError_t gemv_prepare() {
     if (e == hipSuccess) e = lds_attr_all<32, 8, 8, 1, false, true>();
     if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, true, true>();
     if (e == hipSuccess) e = lds_attr_all<16, 16, 8, 1, true, true>();
+    if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, false, true>();
     if (e == hipSuccess) e = prepare_fuse<kFuseNorm>();
     if (e == hipSuccess) e = prepare_fuse<kFuseGlu>();
     if (e == hipSuccess) e = prepare_fuse<kFuseNorm | kFuseGlu>();
@@ -731,10 +736,11 @@ static hipError_t mfma_dispatch(const uint8_t *w, const GemvAct &a, float *y, in
         cfg = force;
     } else {
         // K <= 3584: whole rows per stage (each 16-row stage is one contiguous
-        // run of HBM), persistent when 16-row groups outnumber the CUs. Longer
-        // K: 16 blocks per stage, or persistent 32-row groups of 8 blocks.
+        // run of HBM), single-buffered so three work-groups share a CU,
+        // persistent. Longer K: 16 blocks per stage, or persistent 32-row
+        // groups of 8 blocks when the groups outnumber the CUs.
         const bool many = ((work_rows > 0 ? work_rows : n) + 15) / 16 > device_cus();
-        if (bpr <= 14) cfg = many ? 3 : 1;
+        if (bpr <= 14) cfg = 6;
         else cfg = many ? 0 : 2;
     }
     hipError_t e = launch_any<Q8, FUSE>(cfg, w, a, fz, y, n, bpr, stream);
