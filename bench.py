@@ -20,7 +20,8 @@ measured the same way, not the headline): --workload config1 (4864x896
 flattened layout), --workload batched --batch B (config 4) and --workload
 prefill (config 5, TFLOP/s against the f16 matrix-core peak). Further rows:
 --workload decode7b_dp4a (Q8_1 activations), q5k / q6k (the other K-quants)
-and decode7b_glue (the step with its RMSNorm/GeGLU glue, fused vs unfused).
+decode7b_glue (the step with its RMSNorm/GeGLU glue, fused vs unfused) and
+decode7b_q4km (a Q4_K_M-mixed step from one weight arena).
 """
 from __future__ import annotations
 
@@ -420,6 +421,116 @@ def run_decode_glue(torch, q4k, args):
             "unfused_tokens_per_s": 1000.0 / ms_unfused}
 
 
+def q4km_more_bits(i: int, n: int) -> bool:
+    """llama.cpp's Q4_K_M rule for attn_v / ffn_down: Q6_K on the first and
+    last eighth of the layers and every third layer between."""
+    return i < n // 8 or i >= 7 * n // 8 or (i - n // 8) % 3 == 2
+
+
+def run_decode_q4km(torch, q4k, args):
+    """A Q4_K_M 7B-class decode step from one weight arena (the GGUF loader's
+    layout): Q4_K everywhere except attn_v and ffn_down on the Q4_K_M
+    'more bits' layers (Q6_K) and the Q6_K output matrix, as llama.cpp's
+    Q4_K_M recipe assigns them. Per layer: RMSNorm fused into q|k (and v when
+    v is Q4_K; otherwise one rms_norm launch feeds q|k and the Q6_K v), o,
+    RMSNorm + gate/up + GeGLU fused, down (Q4_K or Q6_K); then rms_norm +
+    the Q6_K lm_head. Seeded random weights, one captured graph."""
+    from oracle import oracle as orc
+    from modgrad_amd.arena import WeightArena
+    from modgrad_amd.gguf import GgmlType
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x4B4D)
+    Q4, Q6 = GgmlType.Q4_K, GgmlType.Q6_K
+    kv = NKV * HEAD
+    entries = []
+    for l in range(LAYERS):
+        more = q4km_more_bits(l, LAYERS)
+        entries += [(f"blk.{l}.attn_qk.weight", [HIDDEN, HIDDEN + kv], Q4),
+                    (f"blk.{l}.attn_v.weight", [HIDDEN, kv], Q6 if more else Q4),
+                    (f"blk.{l}.attn_output.weight", [NQ * HEAD, HIDDEN], Q4),
+                    (f"blk.{l}.ffn_gate.weight", [HIDDEN, INTER], Q4),
+                    (f"blk.{l}.ffn_up.weight", [HIDDEN, INTER], Q4),
+                    (f"blk.{l}.ffn_down.weight", [INTER, HIDDEN], Q6 if more else Q4),
+                    (f"blk.{l}.attn_norm.weight", [HIDDEN], GgmlType.F32),
+                    (f"blk.{l}.ffn_norm.weight", [HIDDEN], GgmlType.F32)]
+    entries += [("output_norm.weight", [HIDDEN], GgmlType.F32), ("output.weight", [HIDDEN, VOCAB], Q6)]
+    arena = WeightArena(entries)
+    for name, dims, t in entries:
+        v = arena.tensor(name)
+        if t == GgmlType.F32:
+            v.view(torch.float32).copy_(torch.rand(dims[0], device="cuda", generator=gen) + 0.5)
+            continue
+        v.copy_(torch.randint(0, 256, (v.numel(),), dtype=torch.uint8, device="cuda", generator=gen))
+        bb = 144 if t == Q4 else 210
+        blk = v.view(-1, bb)
+        nd = 2 if t == Q4 else 1
+        dd = (torch.rand((blk.shape[0], nd), device="cuda", generator=gen) * 2e-3 + 1e-4).to(torch.float16)
+        if t == Q4:
+            blk[:, 0:4] = dd.view(torch.uint8).view(-1, 4)
+        else:
+            blk[:, 208:210] = dd.view(torch.uint8).view(-1, 2)
+    eps = 1e-6
+    f = lambda n: torch.empty(n, device="cuda")
+    hs = [torch.randn(HIDDEN, device="cuda", generator=gen) for _ in range(2 * LAYERS + 1)]
+    att = [torch.randn(NQ * HEAD, device="cuda", generator=gen) for _ in range(LAYERS)]
+    xn, qk, vv, o, glu, dn, logits = f(HIDDEN), f(HIDDEN + kv), f(kv), f(HIDDEN), f(INTER), f(HIDDEN), f(VOCAB)
+    launches = [0]
+
+    def step(st):
+        k, A, n = q4k.kern, arena, 0
+        for l in range(LAYERS):
+            p = f"blk.{l}."
+            h0, h1 = hs[2 * l].data_ptr(), hs[2 * l + 1].data_ptr()
+            if A.dtype[p + "attn_v.weight"] == Q4:
+                A.qmatvec_rmsnorm(p + "attn_qk.weight", h0, p + "attn_norm.weight", eps, qk.data_ptr(), st)
+                A.qmatvec_rmsnorm(p + "attn_v.weight", h0, p + "attn_norm.weight", eps, vv.data_ptr(), st)
+                n += 2
+            else:
+                k.rms_norm(h0, A.ptr(p + "attn_norm.weight"), xn.data_ptr(), 1, HIDDEN, eps, st)
+                A.qmatvec(p + "attn_qk.weight", xn.data_ptr(), qk.data_ptr(), st)
+                A.qmatvec(p + "attn_v.weight", xn.data_ptr(), vv.data_ptr(), st)
+                n += 3
+            A.qmatvec(p + "attn_output.weight", att[l].data_ptr(), o.data_ptr(), st)
+            A.qmatvec_glu(p + "ffn_gate.weight", p + "ffn_up.weight", h1, glu.data_ptr(),
+                          norm=p + "ffn_norm.weight", eps=eps, stream=st)
+            A.qmatvec(p + "ffn_down.weight", glu.data_ptr(), dn.data_ptr(), st)
+            n += 3
+        k.rms_norm(hs[-1].data_ptr(), A.ptr("output_norm.weight"), xn.data_ptr(), 1, HIDDEN, eps, st)
+        A.qmatvec("output.weight", xn.data_ptr(), logits.data_ptr(), st)
+        launches[0] = n + 2
+
+    ms = time_captured(torch, step, args.steps, args.warmup)
+    # parity: the last layer's Q6_K or Q4_K down (its GLU input as produced)
+    # and the Q6_K lm_head, sampled rows against the oracle
+    worst, fail = 0.0, None
+    checks = [(f"blk.{LAYERS - 1}.ffn_down.weight", glu, dn), ("output.weight", xn, logits)]
+    rng = np.random.default_rng(9)
+    for name, xin, yout in checks:
+        nrow, kin = arena.shape(name)
+        t = arena.dtype[name]
+        bb = 144 if t == Q4 else 210
+        idx = np.sort(rng.choice(nrow, size=256, replace=False))
+        wv = arena.tensor(name).view(nrow, -1)[torch.from_numpy(idx).cuda()].cpu().numpy().ravel()
+        if t == Q4:
+            y_ref, a = orc.gemv(wv, xin.cpu().numpy(), idx.size, kin // 256)
+        else:
+            y_ref, a = orc.gemv_kquant(bb, wv, xin.cpu().numpy(), idx.size, kin // 256)
+        r = np.abs(yout.cpu().numpy()[idx].astype(np.float64) - y_ref) / a
+        worst = max(worst, float(r.max()))
+        if not np.all(r <= 1e-4):
+            fail = f"FAIL {name}: max err/absdot {r.max():.3e}"
+    parity = fail or f"ok (Q6_K down + Q6_K lm_head sampled rows, max err/absdot {worst:.2e} <= 1e-4)"
+    qbytes = sum(arena.nbytes[nm] for nm, _, t in entries if t != GgmlType.F32)
+    n6 = sum(1 for nm, _, t in entries if t == Q6)
+    return {"workload": f"decode7b_q4km: Q4_K_M 7B-class decode step from one weight arena "
+                        f"({n6} Q6_K tensors incl. lm_head, the rest Q4_K; fused RMSNorm/GeGLU; "
+                        f"{launches[0]} launches), one graph",
+            "us_per_launch": round(ms * 1e3 / launches[0], 3), "gbs": qbytes / (ms * 1e-3) / 1e9,
+            "bytes_per_launch": qbytes // launches[0], "parity": parity,
+            "kernel": "mgq::gemv_mfma_kernel + mgq::gemv_q6k_staged_kernel",
+            "tokens_per_s": 1000.0 / ms, "ms_per_step": ms}
+
+
 def run_kquant(torch, q4k, args):
     """Q5_K (176 B / 256 weights) on the gate and down shapes, or Q6_K
     (210 B / 256) on the lm_head shape -- the K-quants real GGUFs mix in."""
@@ -494,7 +605,7 @@ def run_side_workload(torch, q4k, args) -> int:
     """BASELINE configs 1, 4 and 5: one JSON line each, same field layout."""
     fn = {"config1": run_config1, "batched": run_batched, "prefill": run_prefill,
           "decode7b_dp4a": run_decode_dp4a, "q5k": run_kquant, "q6k": run_kquant,
-          "decode7b_glue": run_decode_glue}[args.workload]
+          "decode7b_glue": run_decode_glue, "decode7b_q4km": run_decode_q4km}[args.workload]
     r = fn(torch, q4k, args)
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": "synthetic",
@@ -529,7 +640,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="decode7b",
                     choices=["decode7b", "layer", "gateup", "config1", "batched", "prefill",
-                             "decode7b_dp4a", "q5k", "q6k", "decode7b_glue"])
+                             "decode7b_dp4a", "q5k", "q6k", "decode7b_glue", "decode7b_q4km"])
     ap.add_argument("--batch", type=int, default=8, help="batch for --workload batched (1..16)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -548,7 +659,7 @@ def main() -> int:
     log(f"device {torch.cuda.get_device_name(0)}; workload {args.workload}")
 
     if args.workload in ("config1", "batched", "prefill", "decode7b_dp4a", "q5k", "q6k",
-                         "decode7b_glue"):
+                         "decode7b_glue", "decode7b_q4km"):
         return run_side_workload(torch, q4k, args)
     if args.workload == "decode7b":
         wl = Workload(torch, decode_step_shapes())
