@@ -11,11 +11,13 @@
 //   Q6_K, 210 B / 256 values: ql[128] | qh[64] | int8 scales[16] | d f16;
 //     q = (nibble | 2 qh bits << 4) - 32, one scale per 16 values.
 //
-// Vector-ALU kernels: one wavefront per row, lane l owns positions l, l+64,
-// l+128, l+192 of every block, so each byte array of a block is read by the
-// wavefront as consecutive bytes (coalesced), and the activations as
-// consecutive floats. Q6_K blocks are only 2-byte aligned (210 B), which is
-// why these kernels read bytes rather than staging 16-byte pieces.
+// Vector-ALU kernels, one wavefront per row. gemv_q5k_kernel,
+// gemv_q6k_kernel and gemv_q6k_q8_kernel read bytes: lane l owns positions
+// l, l+64, l+128, l+192 of every block, so each byte array of a block is read
+// by the wavefront as consecutive bytes and the activations as consecutive
+// floats; they serve any 2-byte alignment. For 16-byte aligned Q6_K weights
+// and x, gemv_q6k_staged_kernel streams whole 16-byte chunks through LDS
+// instead.
 #include "q4k_device.hpp"
 #include "q4k_launch.hpp"
 

@@ -456,7 +456,7 @@ def test_dp4a_nonfinite_rows_are_zero(L, orc):
 # ------------------------------------------------------------ Q5_K / Q6_K --
 @pytest.mark.parametrize("fmt", [176, 210])
 @pytest.mark.parametrize("n,bpr", [(1, 1), (5, 3), (64, 14), (3584, 14), (300, 74), (4099, 2),
-                                   (7, 15), (33, 29)])
+                                   (7, 15), (33, 29), (20000, 14), (9001, 3)])
 def test_kquant_matvec_matches_oracle(L, orc, fmt, n, bpr):
     from tests.gpu_util import random_kquant_bytes
     note(f"{'q5k' if fmt == 176 else 'q6k'} n={n} bpr={bpr}")
