@@ -293,7 +293,9 @@ def run_prefill(torch, q4k, args):
 def run_decode_dp4a(torch, q4k, args):
     """The decode step of the default workload on the reference engine's
     default arm (rocm_gemma.rs:298-306): per matvec, launch_quantize_q8_1 on
-    its x, then launch_matvec_q4k_dp4a. Accuracy is int8's: the check is the
+    its x, then launch_matvec_q4k_dp4a (226 launches); and the same with
+    launch_quantize_matvec_q4k_dp4a_ex, which quantizes inside the matvec
+    (113 launches, bit-identical y). Accuracy is int8's: the check is the
     reference's RMS-relative error < 0.02 against the f32 dequant-dot."""
     from oracle import oracle as orc
     wl = Workload(torch, decode_step_shapes())
@@ -303,12 +305,19 @@ def run_decode_dp4a(torch, q4k, args):
         q8.append((torch.empty(k, dtype=torch.int8, device="cuda"),
                    torch.empty(nsub, device="cuda"), torch.empty(nsub, device="cuda")))
 
-    def launch(st):
+    def two_launch(st):
         for (name, w, x, y, n, k), (xq, xd, xs) in zip(wl.launches, q8):
             q4k.kern.quantize_q8_1(x.data_ptr(), xq.data_ptr(), xd.data_ptr(), xs.data_ptr(), k, st)
             q4k.kern.matvec_q4k_dp4a(w.data_ptr(), xq.data_ptr(), xd.data_ptr(), xs.data_ptr(),
                                      y.data_ptr(), n, k // BLOCK_ELEMS, st)
-    ms = time_captured(torch, launch, args.steps, args.warmup)
+
+    def fused(st):
+        for name, w, x, y, n, k in wl.launches:
+            q4k.kern.quantize_matvec_q4k_dp4a(w.data_ptr(), x.data_ptr(), y.data_ptr(), n,
+                                              k // BLOCK_ELEMS, st)
+
+    ms_two = time_captured(torch, two_launch, args.steps, args.warmup)
+    ms = time_captured(torch, fused, args.steps, args.warmup)
     worst = 0.0
     for name, w, x, y, n, k in (wl.launches[0], wl.launches[3], wl.launches[-1]):
         bpr = k // BLOCK_ELEMS
@@ -320,12 +329,15 @@ def run_decode_dp4a(torch, q4k, args):
     parity = (f"ok (RMS_rel vs f32 dequant-dot {worst:.2e} < 0.02)" if worst < 0.02
               else f"FAIL: RMS_rel {worst:.3e}")
     nbytes = wl.bytes_per_pass
-    return {"workload": "decode7b_dp4a: the decode7b step, each matvec as quantize_q8_1 + "
-                        "matvec_q4k_dp4a (226 launches), one graph",
+    return {"workload": "decode7b_dp4a: the decode7b step on Q8_1 activations, each matvec as "
+                        "launch_quantize_matvec_q4k_dp4a_ex (113 launches; the reference's "
+                        "quantize_q8_1 + matvec_q4k_dp4a pair, 226 launches, timed beside it), "
+                        "one graph each",
             "us_per_launch": round(ms * 1e3 / len(wl.launches), 3), "gbs": nbytes / (ms * 1e-3) / 1e9,
             "bytes_per_launch": nbytes // len(wl.launches), "parity": parity,
-            "kernel": "mgq::gemv_mfma_kernel<..., Q8> (+ quantize_q8_1_kernel)",
-            "tokens_per_s": 1000.0 / ms, "ms_per_step": ms}
+            "kernel": "mgq::gemv_mfma_kernel<..., Q8, kFuseQuant>",
+            "tokens_per_s": 1000.0 / ms, "ms_per_step": ms,
+            "unfused_ms_per_step": ms_two, "unfused_tokens_per_s": 1000.0 / ms_two}
 
 
 def run_decode_glue(torch, q4k, args):

@@ -118,6 +118,15 @@ hipError_t launch_matvec_q4k_dp4a_ex(const unsigned char *w, const signed char *
                                      const float *xd, const float *xsum, float *y, int out_dim,
                                      int bpr, hipStream_t stream);
 
+/* launch_quantize_q8_1 followed by launch_matvec_q4k_dp4a, in one launch: the
+ * matvec quantizes x (blocks_per_row*256 f32) to Q8_1 itself, with the same
+ * steps as launch_quantize_q8_1, so y is bit-identical to the two-launch
+ * sequence (rocm_gemma.rs:298-306) while x, xq, xd and xsum never go to
+ * memory. w and x must be 16-byte aligned (hipErrorInvalidValue otherwise);
+ * hipErrorNotSupported when K exceeds the kernel's LDS staging. */
+hipError_t launch_quantize_matvec_q4k_dp4a_ex(const unsigned char *w, const float *x, float *y,
+                                              int out_dim, int bpr, hipStream_t stream);
+
 /* launch_matvec_q5k / launch_matvec_q6k / launch_matvec_q6k_dp4a with an
  * explicit stream. */
 hipError_t launch_matvec_q5k_ex(const unsigned char *w_q5, const float *x, float *y, int out_dim,

@@ -40,6 +40,7 @@ SIGNATURES = {
     "mgq_batched_workspace_bytes": (S, [I, I]),
     "launch_matvec_q4k_batched": (I, [P, P, P, I, I, I, P, S, P]),
     "launch_gemm_q4k_f16": (I, [P, P, P, I, I, I, P]),
+    "launch_quantize_matvec_q4k_dp4a_ex": (I, [P, P, P, I, I, P]),
     "launch_rms_norm": (I, [P, P, P, I, I, F]),
     "launch_rms_norm_ex": (I, [P, P, P, I, I, F, P]),
     "launch_geglu": (I, [P, P, P, I]),

@@ -116,6 +116,14 @@ static hipError_t check_kquant(const unsigned char *w, const float *x, const flo
     return hipSuccess;
 }
 
+hipError_t launch_quantize_matvec_q4k_dp4a_ex(const unsigned char *w, const float *x, float *y,
+                                              int out_dim, int bpr, hipStream_t stream) {
+    if (out_dim <= 0 || bpr <= 0 || !w || !x || !y) return hipErrorInvalidValue;
+    if ((int64_t)bpr * 256 > kMaxI32) return hipErrorInvalidValue;
+    if ((((uintptr_t)w | (uintptr_t)x) & 15u) || misaligned4(y)) return hipErrorInvalidValue;
+    return mgq::gemv_q8x_launch(w, x, y, out_dim, bpr, stream);
+}
+
 hipError_t launch_matvec_q5k_ex(const unsigned char *w_q5, const float *x, float *y, int out_dim,
                                 int blocks_per_row, hipStream_t stream) {
     const hipError_t e = check_kquant(w_q5, x, y, out_dim, blocks_per_row);

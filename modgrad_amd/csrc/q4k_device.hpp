@@ -16,6 +16,7 @@ constexpr int kBlockElems = 256;
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // IEEE half bits -> f32, with exponent 31 (Inf and NaN) mapped to 0, the
 // reference's treatment of d/dmin (gguf.rs:371-372, matvec_q4k.hip:78-79).

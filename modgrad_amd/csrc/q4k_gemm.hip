@@ -46,7 +46,6 @@ constexpr int NXCD = 8;        // XCDs the hardware deals work-groups across, ro
 }  // namespace gemm
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // (v & mask) | magic in one instruction. gfx9 VOP3 encodings take no literal
 // constants, so the compiler would otherwise emit a v_and/v_or pair.

@@ -137,7 +137,10 @@ struct MfmaLayout {
 // kFuseGlu: two weight matrices (gate w, up w2) of one shape; each row group
 // streams through the same work-group twice (gate, then up) and the output is
 // act(gate_row . x) * (up_row . x).
-constexpr int kFuseNorm = 1, kFuseGlu = 2;
+// kFuseQuant (Q8 mode only): the prologue quantizes f32 x to Q8_1 itself,
+// bit-identically to quantize_q8_1_kernel (launch_quantize_q8_1 followed by
+// the dp4a matvec, in one launch).
+constexpr int kFuseNorm = 1, kFuseGlu = 2, kFuseQuant = 4;
 struct GemvFuse {
     const uint8_t *w2;  // kFuseGlu: the up matrix
     const float *nw;    // kFuseNorm: RMSNorm weights [K]
@@ -206,7 +209,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
                                                             const float *__restrict__ xsv,
                                                             float *__restrict__ y, int n,
                                                             int bpr, int rounds, GemvFuse fz) {
-    static_assert(!(Q8 && FUSE), "fused glue runs on f32 activations");
+    static_assert(Q8 ? (FUSE == 0 || FUSE == kFuseQuant) : (FUSE & kFuseQuant) == 0,
+                  "fused glue runs on f32 activations; quantization only in Q8 mode");
     constexpr bool NORM = (FUSE & kFuseNorm) != 0;
     constexpr int VM = (FUSE & kFuseGlu) ? 2 : 1;  // passes per row group (gate, up)
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -271,7 +275,61 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     // lane loads its XIT chunks before any weight load is issued: the loads
     // complete in issue order, so waiting for x leaves the weight stream in
     // flight while the table is built.
-  if constexpr (Q8) {
+  if constexpr (Q8 && (FUSE & kFuseQuant)) {
+    // Q8 from f32 x: item i = 8 floats of sub-block (i/4)%8 of block i/32, the
+    // sub-block's 4 items in 4 adjacent lanes (amax and the integer sum reduce
+    // with two DPP quad permutes); the quantization steps are those of
+    // quantize_q8_1_kernel, so xq/xd/xsum are bit-identical to it.
+    const int nitems = bpr * 32;
+    const int its = (nitems + NW * 64 - 1) / (NW * 64);  // <= XIT
+    f32x4 xv0[XIT], xv1[XIT];
+#pragma unroll
+    for (int it = 0; it < XIT; ++it) {
+        if (it >= its) break;
+        const int i = std::min(tid + it * NW * 64, nitems - 1);
+        xv0[it] = *reinterpret_cast<const f32x4 *>(x + (size_t)i * 8);
+        xv1[it] = *reinterpret_cast<const f32x4 *>(x + (size_t)i * 8 + 4);
+    }
+#pragma unroll
+    for (int f = 0; f < PF; ++f) gload(f, stg[f]);
+#pragma unroll
+    for (int it = 0; it < XIT; ++it) {
+        if (it >= its) break;
+        const int i = tid + it * NW * 64;
+        const float v[8] = {xv0[it][0], xv0[it][1], xv0[it][2], xv0[it][3],
+                            xv1[it][0], xv1[it][1], xv1[it][2], xv1[it][3]};
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+        amax = fmaxf(amax, quad_xor<1>(amax));
+        amax = fmaxf(amax, quad_xor<2>(amax));
+        float d = __fdiv_rn(amax, 127.0f);
+        float id = (amax > 0.0f) ? __fdiv_rn(127.0f, amax) : 0.0f;
+        if (!isfinite(id)) {
+            id = 0.0f;
+            d = 0.0f;
+        }
+        int sum = 0;
+        uint32_t p0 = 0, p1 = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            int q = (int)__builtin_rintf(__fmul_rn(v[e], id));  // NaN converts to 0
+            q = std::max(-127, std::min(127, q));
+            sum += q;
+            if (e < 4) p0 |= (uint32_t)(q & 0xFF) << (8 * e);
+            else p1 |= (uint32_t)(q & 0xFF) << (8 * (e - 4));
+        }
+        sum += __builtin_bit_cast(int, quad_xor<1>(__builtin_bit_cast(float, sum)));
+        sum += __builtin_bit_cast(int, quad_xor<2>(__builtin_bit_cast(float, sum)));
+        if (i >= nitems) continue;
+        const int b = i >> 5, sb = (i >> 2) & 7, j = i & 3;
+        *reinterpret_cast<u32x2 *>(lds + (size_t)b * 256 + sb * 32 + j * 8) = u32x2{p0, p1};
+        if (j == 0) {
+            meta[b * 16 + sb] = d;
+            meta[b * 16 + 8 + sb] = (float)sum;
+        }
+    }
+  } else if constexpr (Q8) {
     // Q8: copy xq (16 B items 0 .. 16*bpr), then xd and xsum (4 floats per
     // item) to LDS, loads again issued ahead of the weight stream
     const int nq = bpr * 16, nitems = bpr * 20;
@@ -668,7 +726,8 @@ static hipError_t launch_xit(const uint8_t *w, const GemvAct &a, const GemvFuse 
 template <int R, int C, int NW, int PF, bool DB, bool Q8, int FUSE>
 static hipError_t launch_cfg(const uint8_t *w, const GemvAct &a, const GemvFuse &fz, float *y,
                              int n, int bpr, hipStream_t stream, bool persistent) {
-    const int need = (bpr * (Q8 ? 20 : 32) + NW * 64 - 1) / (NW * 64);
+    const int items = (Q8 && !(FUSE & kFuseQuant)) ? bpr * 20 : bpr * 32;
+    const int need = (items + NW * 64 - 1) / (NW * 64);
 #define MGQ_XIT(X) launch_xit<R, C, NW, PF, DB, X, Q8, FUSE>(w, a, fz, y, n, bpr, stream, persistent)
     if (need <= 1) return MGQ_XIT(1);
     if (need <= 2) return MGQ_XIT(2);
@@ -719,6 +778,10 @@ hipError_t gemv_prepare() {
     if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, true, true>();
     if (e == hipSuccess) e = lds_attr_all<16, 16, 8, 1, true, true>();
     if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, false, true>();
+    if (e == hipSuccess) e = lds_attr_all<32, 8, 8, 1, false, true, kFuseQuant>();
+    if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, true, true, kFuseQuant>();
+    if (e == hipSuccess) e = lds_attr_all<16, 16, 8, 1, true, true, kFuseQuant>();
+    if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, false, true, kFuseQuant>();
     if (e == hipSuccess) e = prepare_fuse<kFuseNorm>();
     if (e == hipSuccess) e = prepare_fuse<kFuseGlu>();
     if (e == hipSuccess) e = prepare_fuse<kFuseNorm | kFuseGlu>();
@@ -769,6 +832,13 @@ hipError_t gemv_mfma_launch(const uint8_t *w, const float *x, float *y, int n, i
                             hipStream_t stream) {
     if (((uintptr_t)w & 15u) || ((uintptr_t)x & 15u)) return hipErrorNotSupported;
     return mfma_dispatch<false>(w, GemvAct{x, nullptr, nullptr, nullptr}, y, n, bpr, stream);
+}
+
+hipError_t gemv_q8x_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                           hipStream_t stream) {
+    if (((uintptr_t)w | (uintptr_t)x) & 15u) return hipErrorNotSupported;
+    return mfma_dispatch<true, kFuseQuant>(w, GemvAct{x, nullptr, nullptr, nullptr}, y, n, bpr,
+                                           stream);
 }
 
 hipError_t gemv_q8_launch(const uint8_t *w, const int8_t *xq, const float *xd, const float *xsum,

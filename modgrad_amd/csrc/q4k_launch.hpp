@@ -47,6 +47,11 @@ hipError_t quantize_q8_1_launch(const float *x, int8_t *xq, float *xd, float *xs
                                 hipStream_t stream);
 hipError_t gemv_q8_launch(const uint8_t *w, const int8_t *xq, const float *xd, const float *xsum,
                           float *y, int n, int bpr, hipStream_t stream);
+// launch_quantize_q8_1 + the dp4a matvec in one launch (the matrix-core
+// kernel's Q8 mode quantizing f32 x in its prologue); w and x 16-byte aligned
+// (hipErrorNotSupported otherwise).
+hipError_t gemv_q8x_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                           hipStream_t stream);
 hipError_t gemv_q8_generic_launch(const uint8_t *w, const int8_t *xq, const float *xd,
                                   const float *xsum, float *y, int n, int bpr, hipStream_t stream);
 

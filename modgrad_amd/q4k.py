@@ -179,6 +179,14 @@ class kern:
 
     # additive entry points -------------------------------------------------
     @staticmethod
+    def quantize_matvec_q4k_dp4a(w: int, x: int, y: int, out_dim: int, bpr: int,
+                                 stream=None) -> None:
+        """quantize_q8_1 + matvec_q4k_dp4a in one launch (bit-identical y)."""
+        _chk(_lib.load().launch_quantize_matvec_q4k_dp4a_ex(w, x, y, out_dim, bpr,
+                                                            _stream_ptr(stream)),
+             "quantize_matvec_q4k_dp4a")
+
+    @staticmethod
     def glu(gate: int, up: int, out: int, n: int, act: int = _lib.ACT_GELU_TANH,
             stream=None) -> None:
         """out = act(gate) * up, act = ACT_GELU_TANH or ACT_SILU."""

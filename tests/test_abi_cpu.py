@@ -157,3 +157,12 @@ def test_fused_matvecs_reject_bad_args(L):
     assert glu(FAKE, FAKE + 4, FAKE, None, 0.0, 0, FAKE, 16, 14, None) == INVALID
     assert glu(FAKE, FAKE, FAKE, FAKE + 4, 0.0, 0, FAKE, 16, 14, None) == INVALID
     assert glu(FAKE, FAKE, FAKE, None, 0.0, 1, FAKE, -1, 14, None) == INVALID
+
+
+def test_fused_quantize_dp4a_rejects_bad_args(L):
+    fn = L.launch_quantize_matvec_q4k_dp4a_ex
+    assert fn(FAKE, FAKE, FAKE, 0, 14, None) == INVALID
+    assert fn(FAKE, FAKE, FAKE, 16, 0, None) == INVALID
+    assert fn(FAKE, None, FAKE, 16, 14, None) == INVALID
+    assert fn(FAKE + 4, FAKE, FAKE, 16, 14, None) == INVALID   # w not 16-B aligned
+    assert fn(FAKE, FAKE + 8, FAKE, 16, 14, None) == INVALID   # x not 16-B aligned

@@ -437,6 +437,34 @@ def test_dp4a_reference_acceptance_check(L, orc, bias):
     assert rms_rel < 0.02
 
 
+@pytest.mark.parametrize("n,bpr", [(1, 1), (64, 2), (300, 3), (3584, 14), (4608, 14),
+                                   (600, 74), (5000, 74)])
+def test_fused_quantize_dp4a_is_the_two_launch_sequence(L, orc, n, bpr):
+    # launch_quantize_matvec_q4k_dp4a_ex == launch_quantize_q8_1 followed by
+    # launch_matvec_q4k_dp4a, bit for bit, including the quantizer's special
+    # sub-blocks (zero, denormal max, huge, NaN / Inf, exact halves)
+    note(f"fused quantize+dp4a n={n} bpr={bpr}")
+    k = bpr * 256
+    rng = np.random.default_rng(n * 7 + bpr)
+    w = random_q4k_bytes(rng, n * bpr)
+    x = (rng.standard_normal(k) * rng.choice([1e-6, 1e-2, 1.0, 300.0], size=k)).astype(np.float32)
+    x[0:32] = 0.0
+    if k >= 256:
+        x[32:64] = np.float32(1e-40)
+        x[64:96] = np.float32(3.0e38)
+        x[96:128] = (np.arange(32, dtype=np.float32) - 16) * np.float32(0.5)
+        x[130] = np.float32("nan")
+        x[200] = np.float32("inf")
+    wt, xt = dev(w), dev(x)
+    (xq, xd, xs), _ = run_q8(L, x)
+    y_two = empty_f32(n)
+    _lib.check("dp4a", L.launch_matvec_q4k_dp4a(ptr(wt), ptr(xq), ptr(xd), ptr(xs), ptr(y_two), n, bpr))
+    y_one = empty_f32(n)
+    _lib.check("fused", L.launch_quantize_matvec_q4k_dp4a_ex(ptr(wt), ptr(xt), ptr(y_one), n, bpr, None))
+    a, b = host(y_two), host(y_one)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 def test_dp4a_nonfinite_rows_are_zero(L, orc):
     # an Inf activation gives xd = Inf and a non-finite row sum: written as 0
     note("dp4a non-finite clamp")
