@@ -140,7 +140,11 @@ struct MfmaLayout {
 // kFuseQuant (Q8 mode only): the prologue quantizes f32 x to Q8_1 itself,
 // bit-identically to quantize_q8_1_kernel (launch_quantize_q8_1 followed by
 // the dp4a matvec, in one launch).
-constexpr int kFuseNorm = 1, kFuseGlu = 2, kFuseQuant = 4;
+// kFmtQ5K (f32 mode, no other bit): the weights are Q5_K, 176-byte blocks
+// of 11 16-byte pieces (header | qh[32] | qs[128]); the header and its scale
+// packing are Q4_K's, and the fifth bit of every weight comes from qh.
+constexpr int kFuseNorm = 1, kFuseGlu = 2, kFuseQuant = 4, kFmtQ5K = 8;
+__host__ __device__ constexpr int block_pieces(int fuse) { return (fuse & kFmtQ5K) ? 11 : 9; }
 struct GemvFuse {
     const uint8_t *w2;  // kFuseGlu: the up matrix
     const float *nw;    // kFuseNorm: RMSNorm weights [K]
@@ -154,21 +158,22 @@ struct GemvFuse {
 // Staged rows are padded to an odd number of 16-byte pieces, so the 16
 // lanes that read one piece column of 16 different rows hit 16 different
 // LDS bank groups.
-__host__ __device__ constexpr int stage_row_pieces(int C) { return (9 * C) | 1; }
+__host__ __device__ constexpr int stage_row_pieces(int C, int bp = 9) { return (bp * C) | 1; }
 
 __host__ __device__ inline MfmaLayout mfma_layout(int bpr, int R, int C, int NW, int rounds,
                                                   bool db, bool q8 = false, int fuse = 0) {
     MfmaLayout L;
     L.bpr = bpr; L.R = R; L.C = C; L.NW = NW;
     // wave loads per stage, padded so every wavefront issues the same count
-    L.I = ((R * 9 * C + 63) / 64 + NW - 1) / NW * NW;
+    const int bp = block_pieces(fuse);
+    L.I = ((R * bp * C + 63) / 64 + NW - 1) / NW * NW;
     // activation table: per block 1 KiB of f16 operands plus a 16-byte zero
     // slot (so a lane's A address is the block base plus a fixed offset), or
     // (Q8) the block's 256 int8 activations
     L.tab_stride = q8 ? 256u : 1040u;
     L.meta = (uint32_t)bpr * L.tab_stride;
     L.stage = L.meta + (uint32_t)bpr * 64u;
-    L.stage_bytes = (uint32_t)(R * stage_row_pieces(C) * 16);
+    L.stage_bytes = (uint32_t)(R * stage_row_pieces(C, bp) * 16);
     // two stage buffers when double-buffered and K needs more than one stage
     L.aux = L.stage + ((db && bpr > C) ? 2u : 1u) * L.stage_bytes;
     L.ybuf = L.aux + (uint32_t)NW * 128u;
@@ -211,6 +216,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
                                                             int bpr, int rounds, GemvFuse fz) {
     static_assert(Q8 ? (FUSE == 0 || FUSE == kFuseQuant) : (FUSE & kFuseQuant) == 0,
                   "fused glue runs on f32 activations; quantization only in Q8 mode");
+    static_assert(!(FUSE & kFmtQ5K) || FUSE == kFmtQ5K, "Q5_K weights: plain f32 matvec only");
+    constexpr bool Q5 = (FUSE & kFmtQ5K) != 0;
+    constexpr int BP = block_pieces(FUSE);  // 16-byte pieces per block
+    constexpr int BB = BP * 16;              // block bytes
     constexpr bool NORM = (FUSE & kFuseNorm) != 0;
     constexpr int VM = (FUSE & kFuseGlu) ? 2 : 1;  // passes per row group (gate, up)
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -219,12 +228,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
     float *meta = reinterpret_cast<float *>(lds + Lo.meta);
     float *aux = reinterpret_cast<float *>(lds + Lo.aux);
-    const size_t row_bytes = (size_t)bpr * kBlockBytes;
+    const size_t row_bytes = (size_t)bpr * BB;
     const int stages = (bpr + C - 1) / C;
     const int groups = (n + R - 1) / R;
     const int my_groups = (groups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
     const int Q = my_groups * VM * stages;        // stages this work-group streams
-    constexpr int PIECES = R * 9 * C;             // 16-byte pieces per stage
+    constexpr int PIECES = R * BP * C;            // 16-byte pieces per stage
     constexpr int IPW = ((PIECES + 63) / 64 + NW - 1) / NW;  // wave loads per wavefront
     constexpr int I = IPW * NW;                   // wave loads per stage (padded)
     constexpr int UNITS = (R == 32) ? C : C / 2;  // tile pairs per stage
@@ -237,24 +246,24 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     // already cached) so the compiler's in-order vmcnt accounting stays
     // exact and only the set being stored is waited for. The piece -> (row,
     // byte column) split of each load is stage-invariant and precomputed.
-    constexpr int RP = stage_row_pieces(C);       // LDS pieces per staged row
+    constexpr int RP = stage_row_pieces(C, BP);   // LDS pieces per staged row
     uint32_t prow[IPW], pcol[IPW], plast[IPW], plds[IPW];
 #pragma unroll
     for (int k = 0; k < IPW; ++k) {
         const int j = std::min((wave + k * NW) * 64 + lane, PIECES - 1);
-        const int row = j / (9 * C), rem = j - row * 9 * C;
-        const int cb = rem / 9, pc = rem - cb * 9;
+        const int row = j / (BP * C), rem = j - row * BP * C;
+        const int cb = rem / BP, pc = rem - cb * BP;
         plds[k] = (uint32_t)((row * RP + rem) * 16);    // LDS byte offset in the stage
         prow[k] = (uint32_t)row;
-        pcol[k] = (uint32_t)(cb * kBlockBytes + 16 * pc);          // byte column within the stage
-        plast[k] = (uint32_t)((bpr - 1) * kBlockBytes + 16 * pc);  // same piece of the last block
+        pcol[k] = (uint32_t)(cb * BB + 16 * pc);          // byte column within the stage
+        plast[k] = (uint32_t)((bpr - 1) * BB + 16 * pc);  // same piece of the last block
     }
     auto gload = [&](int q, u32x4(&dst)[IPW]) {
         q = std::min(q, Q - 1);
         const int vg = q / stages;  // pass index: row group vg / VM, matrix vg % VM
         const uint32_t r0 = ((uint32_t)blockIdx.x + (uint32_t)(vg / VM) * gridDim.x) * R;
         const uint8_t *wm = (VM == 2 && (vg & 1)) ? fz.w2 : w;
-        const uint32_t tcol = (uint32_t)((q % stages) * C * kBlockBytes);
+        const uint32_t tcol = (uint32_t)((q % stages) * C * BB);
         const uint32_t rlast = (uint32_t)(n - 1), rb = (uint32_t)row_bytes;
 #pragma unroll
         for (int k = 0; k < IPW; ++k) {
@@ -408,7 +417,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         }
         const int b = i >> 5, sb = (i >> 2) & 7, j = i & 3;
         if (j == 0) {
-            meta[b * 16 + sb] = ldexpf(1.0f, ((sb & 1) ? 20 : 24) - e);
+            // Q4_K high-nibble operands are 16q*2^-24 (masked in place); Q5_K's are q*2^-24
+            meta[b * 16 + sb] = ldexpf(1.0f, ((sb & 1) && !Q5 ? 20 : 24) - e);
             meta[b * 16 + 8 + sb] = sum;
         }
         // table entry (c, h) of this chunk: byte offset pair_byte_offset(c/2, h)
@@ -531,10 +541,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
             const bool hasB = bB < bpr;
             const int bBc = hasB ? bB : bA;  // past the end: reuse tile A's operands
             auto piece = [&](int row, int cb, int pc) -> const u32x4 & {
-                return *reinterpret_cast<const u32x4 *>(sbuf + (row * RP + cb * 9 + pc) * 16);
+                return *reinterpret_cast<const u32x4 *>(sbuf + (row * RP + cb * BP + pc) * 16);
             };
-            const u32x4 qa0 = piece(rowA + n16, cbA, 1 + g), qa1 = piece(rowA + n16, cbA, 5 + g);
-            const u32x4 qb0 = piece(rowB + n16, cbB, 1 + g), qb1 = piece(rowB + n16, cbB, 5 + g);
+            // qs pieces 1+g, 5+g (Q5_K: 3+g, 7+g: qh takes pieces 1 and 2)
+            constexpr int QS = Q5 ? 3 : 1;
+            const u32x4 qa0 = piece(rowA + n16, cbA, QS + g), qa1 = piece(rowA + n16, cbA, QS + 4 + g);
+            const u32x4 qb0 = piece(rowB + n16, cbB, QS + g), qb1 = piece(rowB + n16, cbB, QS + 4 + g);
             const u32x4 hdA = piece(rowA + n16, cbA, 0), hdB = piece(rowB + n16, cbB, 0);
           if constexpr (Q8) {
             const float cA = decode_q8(hdA, bA, qa0, qa1);
@@ -546,6 +558,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
                 yaccA += hasB ? cA + cB : cA;
             }
           } else {
+            // Q5_K: the qh bytes of this lane's qs bytes t are qh[t % 32], the
+            // same byte offsets within qh piece 1 + (g & 1)
+            u32x4 hqa = {0u, 0u, 0u, 0u}, hqb = {0u, 0u, 0u, 0u};
+            if constexpr (Q5) {
+                hqa = piece(rowA + n16, cbA, 1 + (g & 1));
+                hqb = piece(rowB + n16, cbB, 1 + (g & 1));
+            }
             f32x4 accA = {0.f, 0.f, 0.f, 0.f}, accB = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
@@ -558,8 +577,26 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
                 const uint32_t wa1 = p < 2 ? qa0[2 * p + 1] : qa1[2 * p - 3];
                 const uint32_t wb0 = p < 2 ? qb0[2 * p] : qb1[2 * p - 4];
                 const uint32_t wb1 = p < 2 ? qb0[2 * p + 1] : qb1[2 * p - 3];
-                const u32x4 ba = {wa0 & mask, (wa0 >> 8) & mask, wa1 & mask, (wa1 >> 8) & mask};
-                const u32x4 bb = {wb0 & mask, (wb0 >> 8) & mask, wb1 & mask, (wb1 >> 8) & mask};
+                u32x4 ba, bb;
+                if constexpr (Q5) {
+                    // 5-bit q bytes: the nibble plus bit j (this MFMA's
+                    // sub-block) of the matching qh byte at bit 4, then two
+                    // bytes per dword into f16 subnormals, as for Q4_K
+                    const int d = p < 2 ? 2 * p : 2 * p - 4;
+                    const int j = 2 * ((p < 2 ? 0 : 2) + (g >> 1)) + (c & 1);
+                    auto q5 = [&](uint32_t wq, uint32_t hq) -> uint32_t {
+                        const uint32_t nib = (c & 1) ? ((wq >> 4) & 0x0F0F0F0Fu) : (wq & 0x0F0F0F0Fu);
+                        return nib | (((hq >> j) & 0x01010101u) << 4);
+                    };
+                    const uint32_t a0 = q5(wa0, hqa[d]), a1 = q5(wa1, hqa[d + 1]);
+                    const uint32_t b0 = q5(wb0, hqb[d]), b1 = q5(wb1, hqb[d + 1]);
+                    constexpr uint32_t m5 = 0x001F001Fu;
+                    ba = u32x4{a0 & m5, (a0 >> 8) & m5, a1 & m5, (a1 >> 8) & m5};
+                    bb = u32x4{b0 & m5, (b0 >> 8) & m5, b1 & m5, (b1 >> 8) & m5};
+                } else {
+                    ba = u32x4{wa0 & mask, (wa0 >> 8) & mask, wa1 & mask, (wa1 >> 8) & mask};
+                    bb = u32x4{wb0 & mask, (wb0 >> 8) & mask, wb1 & mask, (wb1 >> 8) & mask};
+                }
                 accA = __builtin_amdgcn_mfma_f32_16x16x32_f16(aA, __builtin_bit_cast(half8, ba), accA, 0, 0, 0);
                 accB = __builtin_amdgcn_mfma_f32_16x16x32_f16(aB, __builtin_bit_cast(half8, bb), accB, 0, 0, 0);
             }
@@ -782,6 +819,7 @@ hipError_t gemv_prepare() {
     if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, true, true, kFuseQuant>();
     if (e == hipSuccess) e = lds_attr_all<16, 16, 8, 1, true, true, kFuseQuant>();
     if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, false, true, kFuseQuant>();
+    if (e == hipSuccess) e = prepare_fuse<kFmtQ5K>();
     if (e == hipSuccess) e = prepare_fuse<kFuseNorm>();
     if (e == hipSuccess) e = prepare_fuse<kFuseGlu>();
     if (e == hipSuccess) e = prepare_fuse<kFuseNorm | kFuseGlu>();
@@ -832,6 +870,12 @@ hipError_t gemv_mfma_launch(const uint8_t *w, const float *x, float *y, int n, i
                             hipStream_t stream) {
     if (((uintptr_t)w & 15u) || ((uintptr_t)x & 15u)) return hipErrorNotSupported;
     return mfma_dispatch<false>(w, GemvAct{x, nullptr, nullptr, nullptr}, y, n, bpr, stream);
+}
+
+hipError_t gemv_q5k_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                                hipStream_t stream) {
+    if (((uintptr_t)w | (uintptr_t)x) & 15u) return hipErrorNotSupported;
+    return mfma_dispatch<false, kFmtQ5K>(w, GemvAct{x, nullptr, nullptr, nullptr}, y, n, bpr, stream);
 }
 
 hipError_t gemv_q8x_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,

@@ -275,6 +275,8 @@ __global__ __launch_bounds__(256) void gemv_q6k_staged_kernel(const uint8_t *__r
 
 hipError_t gemv_q5k_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                            hipStream_t stream) {
+    const hipError_t e = gemv_q5k_mfma_launch(w, x, y, n, bpr, stream);
+    if (e != hipErrorNotSupported) return e;
     gemv_q5k_kernel<<<(unsigned)((n + 3) / 4), 256, 0, stream>>>(w, x, y, n, bpr);
     return hipGetLastError();
 }

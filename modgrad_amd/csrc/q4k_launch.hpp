@@ -55,6 +55,11 @@ hipError_t gemv_q8x_launch(const uint8_t *w, const float *x, float *y, int n, in
 hipError_t gemv_q8_generic_launch(const uint8_t *w, const int8_t *xq, const float *xd,
                                   const float *xsum, float *y, int n, int bpr, hipStream_t stream);
 
+// Matrix-core Q5_K matvec (the Q4_K kernel's Q5_K format mode); w and x
+// 16-byte aligned, else hipErrorNotSupported (as when LDS does not fit).
+hipError_t gemv_q5k_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                                hipStream_t stream);
+
 // Q5_K / Q6_K matvecs (f32 activations) and Q6_K on Q8_1 activations.
 hipError_t gemv_q5k_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                            hipStream_t stream);

@@ -498,6 +498,21 @@ def test_kquant_matvec_matches_oracle(L, orc, fmt, n, bpr):
     assert_gemv_close(host(yt), y_ref, a)
 
 
+def test_q5k_matvec_misaligned_weights_use_the_vector_alu_kernel(L, orc):
+    from tests.gpu_util import random_kquant_bytes
+    note("q5k weights 4-byte aligned")
+    n, bpr = 70, 3
+    w = random_kquant_bytes(np.random.default_rng(8), n * bpr, 176)
+    x = np.random.default_rng(9).standard_normal(bpr * 256).astype(np.float32)
+    import torch
+    wt = torch.zeros(w.size + 64, dtype=torch.uint8, device="cuda")
+    wt[4:4 + w.size].copy_(torch.from_numpy(w))
+    xt, yt = dev(x), empty_f32(n)
+    _lib.check("q5k", L.launch_matvec_q5k(ptr(wt) + 4, ptr(xt), ptr(yt), n, bpr))
+    y_ref, a = orc.gemv_kquant(176, w, x, n, bpr)
+    assert_gemv_close(host(yt), y_ref, a)
+
+
 def test_kquant_matvec_odd_weight_offset(L, orc):
     # the reference arena places tensors at arbitrary offsets: Q6_K weights
     # starting 2 bytes past an allocation boundary
