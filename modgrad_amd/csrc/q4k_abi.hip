@@ -72,6 +72,8 @@ hipError_t launch_matvec_q4k_batched(const unsigned char *w_q4, const float *X, 
     if ((int64_t)blocks_per_row * 256 > kMaxI32) return hipErrorInvalidValue;
     if (!workspace || workspace_bytes < mgq::batched_workspace_bytes(blocks_per_row, batch))
         return hipErrorInvalidValue;
+    if (batch == 1)  // one activation row is a plain matvec: no operand-table pass
+        return mgq::gemv_rows_launch(w_q4, X, Y, out_dim, blocks_per_row, stream);
     const hipError_t e = mgq::gemv_batched_mfma_launch(w_q4, X, Y, out_dim, blocks_per_row, batch,
                                                        workspace, workspace_bytes, stream);
     if (e != hipErrorNotSupported) return e;

@@ -258,6 +258,16 @@ def test_matvec_batched_matches_gemv_and_is_deterministic(L, orc):
         assert_gemv_close(y, y_ref, a)
 
 
+def test_matvec_batched_single_row_is_the_matvec(L, orc):
+    # batch 1 runs the matvec itself (no operand-table pass): bit-identical
+    note("batched B=1 == gemv")
+    n, bpr = 3000, 14
+    w = orc.seeded_weight(63, n, bpr * 256)
+    x = orc.normal(64, bpr * 256)
+    Y = run_batched(L, w, x.reshape(1, -1), n, bpr, 1)
+    assert np.array_equal(Y[0], run_gemv(L, w, x, n, bpr))
+
+
 def test_matvec_batched_vector_alu_fallback(L, orc):
     # weights only 4-byte aligned: the vector-ALU batched kernel runs
     note("batched misaligned weights")
