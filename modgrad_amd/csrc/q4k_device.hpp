@@ -59,6 +59,15 @@ __device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) {
     return *reinterpret_cast<const uint32_t *>(p);
 }
 
+// v from lane (lane ^ MASK) within each group of 4 lanes (DPP quad_perm).
+template <int MASK>
+__device__ __forceinline__ float quad_xor(float v) {
+    static_assert(MASK == 1 || MASK == 2, "quad lane xor");
+    constexpr int ctrl = MASK == 1 ? 0xB1 : 0x4E;  // quad_perm [1,0,3,2] / [2,3,0,1]
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl,
+                                                                 0xF, 0xF, false));
+}
+
 // GLU activations: kActGeluTanh is gelu_tanh in the order
 // kernels/transformer_ops.hip:36-38 evaluates it; kActSilu is v*sigmoid(v).
 constexpr int kActGeluTanh = 0, kActSilu = 1;

@@ -105,15 +105,6 @@ __device__ __forceinline__ int pair_byte_offset(int p, int h) {
 }
 
 
-// v from lane (lane ^ MASK) within each group of 4 lanes (DPP quad_perm).
-template <int MASK>
-__device__ __forceinline__ float quad_xor(float v) {
-    static_assert(MASK == 1 || MASK == 2, "quad lane xor");
-    constexpr int ctrl = MASK == 1 ? 0xB1 : 0x4E;  // quad_perm [1,0,3,2] / [2,3,0,1]
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl,
-                                                                 0xF, 0xF, false));
-}
-
 
 // LDS layout of one work-group (rows R, all bpr blocks of K):
 //   atab  [bpr][8 mfma c][4 lane-group h][xh|xl][8 halves] + 16 B of zeros,

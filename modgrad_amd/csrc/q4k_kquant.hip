@@ -283,6 +283,8 @@ hipError_t gemv_q5k_launch(const uint8_t *w, const float *x, float *y, int n, in
 
 hipError_t gemv_q6k_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                            hipStream_t stream) {
+    const hipError_t e = gemv_q6k_mfma_launch(w, x, y, n, bpr, stream);
+    if (e != hipErrorNotSupported) return e;
     if ((((uintptr_t)w | (uintptr_t)x) & 15u) == 0)
         gemv_q6k_staged_kernel<<<(unsigned)((n + 3) / 4), 256, 0, stream>>>(w, x, y, n, bpr);
     else

@@ -60,6 +60,11 @@ hipError_t gemv_q8_generic_launch(const uint8_t *w, const int8_t *xq, const floa
 hipError_t gemv_q5k_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                                 hipStream_t stream);
 
+// Matrix-core Q6_K matvec for K <= 3584; hipErrorNotSupported for longer K,
+// misaligned w or x, or a tensor that does not end on a 16-byte boundary.
+hipError_t gemv_q6k_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                                hipStream_t stream);
+
 // Q5_K / Q6_K matvecs (f32 activations) and Q6_K on Q8_1 activations.
 hipError_t gemv_q5k_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                            hipStream_t stream);

@@ -1,0 +1,257 @@
+// Q6_K matvec on the gfx950 matrix cores (launch_matvec_q6k, rocm.rs:482-485;
+// canonical order of dequantize_row_q6_k, gguf.rs:441-477), for 16-byte
+// aligned weights and x with K <= kQ6mMaxBpr * 256 (the attention and lm_head
+// shapes of 7B-class models).
+//
+// Q6_K block, 210 B / 256 weights: ql[128] | qh[64] | int8 sc[16] | d f16.
+// Position p = 128g' + 32quad + l (l < 32) is sub-block j = 4g' + quad:
+// q = (nibble (quad >> 1) of ql[64g' + 32(quad & 1) + l]) | (2 bits (2quad) of
+// qh[32g' + l]) << 4, and w = d * sc[2j + l/16] * (q - 32).
+//
+// Work-group = 16 rows x all K, persistent over row groups; 7 wavefronts.
+//   * Stage: a row group's 16 rows are one contiguous byte range (16 x RB,
+//     RB = 210 bpr, a multiple of 16 bytes), copied flat into LDS as whole
+//     16-byte chunks; the next group's chunks wait in registers.
+//   * One v_mfma_f32_16x16x32_f16 per sub-block: B = weights (lane (n, g):
+//     row n, positions 8g..8g+7 of the sub-block; the 6-bit q are f16
+//     subnormals q*2^-24, exact), A = the activation table built once per
+//     work-group: x*2^e = xh + xl (f16) with one exponent per sub-block, in
+//     A row m = 4(j % 4) + 2 half + part, so sub-blocks 0-3 and 4-7 of a block
+//     land in two accumulators and lane (n, g) holds both halves (xh, xl) of
+//     sub-blocks g and 4 + g of row n.
+//   * A lane reads its 8 ql bytes (for two sub-blocks: low and high nibbles)
+//     and its 8 qh bytes (for four) once per 128-position half; blocks are
+//     only 2-byte aligned in LDS, so a 2-dword read is the 3 aligned dwords
+//     around it shifted into place (v_alignbyte_b32).
+//   * y_r = sum_j d * (corr_j * (sc_2j s_0 + sc_2j+1 s_1) - 32 (sc_2j X_0 +
+//     sc_2j+1 X_1)), s_h the scaled sums of q*x over half h, X_h the sums of x.
+// Bytes per unit: 210 per 256 weights of one row (plus x once per
+// work-group): HBM-bound.
+#include "q4k_device.hpp"
+#include "q4k_launch.hpp"
+
+#include <algorithm>
+
+namespace mgq {
+
+namespace q6m {
+constexpr int R = 16, NW = 7, NT = NW * 64;
+constexpr int BB = 210;                   // Q6_K block bytes
+constexpr int MAX_BPR = 14;               // whole-row stages
+constexpr int CPL = (R * MAX_BPR * BB / 16 + NT - 1) / NT;  // 16-byte chunks per lane (7)
+constexpr int TAB = 1040;                 // per block: 1 KiB of A operands + a zero slot
+constexpr int META = 24;                  // floats per block: corr[8] | X[16]
+}  // namespace q6m
+
+constexpr int kQ6mMaxBpr = q6m::MAX_BPR;
+
+struct Q6mLayout {
+    uint32_t meta, stage, aux, ybuf;
+    size_t total;
+};
+
+__host__ __device__ inline Q6mLayout q6m_layout(int bpr, int rounds) {
+    using namespace q6m;
+    Q6mLayout L;
+    L.meta = (uint32_t)bpr * TAB;
+    L.stage = L.meta + (uint32_t)bpr * META * 4;
+    // + 16: the 3-dword window around the last bytes of row 15 may end past them
+    L.aux = L.stage + (uint32_t)(R * bpr * BB) + 16;
+    L.ybuf = L.aux + (uint32_t)NW * R * 4;
+    L.total = (size_t)L.ybuf + (size_t)R * rounds * 4;
+    return L;
+}
+
+__global__ __launch_bounds__(q6m::NT) void gemv_q6k_mfma_kernel(const uint8_t *__restrict__ w,
+                                                                const float *__restrict__ x,
+                                                                float *__restrict__ y, int n,
+                                                                int bpr, int rounds) {
+    using namespace q6m;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const Q6mLayout Lo = q6m_layout(bpr, rounds);
+    float *meta = reinterpret_cast<float *>(lds + Lo.meta);
+    float *aux = reinterpret_cast<float *>(lds + Lo.aux);
+    float *ybuf = reinterpret_cast<float *>(lds + Lo.ybuf);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int RB = bpr * BB;            // row bytes; a group is RB 16-byte chunks
+    const int groups = (n + R - 1) / R;
+    const int my_groups = (groups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const u32x4 *wc = reinterpret_cast<const u32x4 *>(w);
+    const long last_chunk = (long)n * RB / 16 - 1;
+
+    // ---- stage loads: group q of this work-group, clamped (unconditional) ---
+    u32x4 reg[CPL];
+    auto gload = [&](int q) {
+        q = min(q, my_groups - 1);
+        const long base = (long)((int)blockIdx.x + q * (int)gridDim.x) * RB;
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) {
+            const int c = min(tid + k * NT, RB - 1);
+            reg[k] = wc[min(base + c, last_chunk)];
+        }
+    };
+    auto lstore = [&]() {
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) {
+            const int c = tid + k * NT;
+            if (c < RB) *reinterpret_cast<u32x4 *>(lds + Lo.stage + 16 * c) = reg[k];
+        }
+    };
+
+    // ---- prologue: the activation table (x loads first, then the weights) --
+    // item i = 8 floats: block i/32, sub-block (i/4)%8, lane group kg = i%4;
+    // bpr <= 14 makes it at most one item per thread
+    const int nitems = bpr * 32;
+    const int ii = min(tid, nitems - 1);
+    const f32x4 v0 = *reinterpret_cast<const f32x4 *>(x + (size_t)ii * 8);
+    const f32x4 v1 = *reinterpret_cast<const f32x4 *>(x + (size_t)ii * 8 + 4);
+    gload(0);
+    for (int b = tid; b < bpr; b += NT)
+        *reinterpret_cast<u32x4 *>(lds + (size_t)b * TAB + 1024) = u32x4{0u, 0u, 0u, 0u};
+    {
+        float amax = fmaxf(fmaxf(fmaxf(fabsf(v0[0]), fabsf(v0[1])), fmaxf(fabsf(v0[2]), fabsf(v0[3]))),
+                           fmaxf(fmaxf(fabsf(v1[0]), fabsf(v1[1])), fmaxf(fabsf(v1[2]), fabsf(v1[3]))));
+        float sum = ((v0[0] + v0[1]) + (v0[2] + v0[3])) + ((v1[0] + v1[1]) + (v1[2] + v1[3]));
+        amax = fmaxf(amax, quad_xor<1>(amax));
+        amax = fmaxf(amax, quad_xor<2>(amax));
+        sum += quad_xor<1>(sum);  // the 16 values of this half
+        if (tid < nitems) {
+            int e = 0;  // x*2^e puts the sub-block's largest |x| in [2^13, 2^14)
+            if (amax > 0.0f && amax <= 3.402823466e38f) {
+                int ex;
+                frexpf(amax, &ex);
+                e = std::min(std::max(14 - ex, -90), 140);
+            }
+            const int b = tid >> 5, j = (tid >> 2) & 7, kg = tid & 3;
+            if (kg == 0) meta[b * META + j] = ldexpf(1.0f, 24 - e);
+            if ((kg & 1) == 0) meta[b * META + 8 + 2 * j + (kg >> 1)] = sum;
+            // slot s holds position {0,2,1,3,4,6,5,7}[s] of the 8 (the B operand's order)
+            const float xs[8] = {v0[0], v0[2], v0[1], v0[3], v1[0], v1[2], v1[1], v1[3]};
+            u32x4 hh, hl;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float a0 = ldexpf(xs[2 * q], e), a1 = ldexpf(xs[2 * q + 1], e);
+                const auto hp = __builtin_amdgcn_cvt_pkrtz(a0, a1);
+                const auto lp = __builtin_amdgcn_cvt_pkrtz(a0 - (float)hp[0], a1 - (float)hp[1]);
+                hh[q] = __builtin_bit_cast(uint32_t, hp);
+                hl[q] = __builtin_bit_cast(uint32_t, lp);
+            }
+            uint8_t *ent = lds + (size_t)b * TAB + (size_t)((j * 4 + kg) * 2) * 16;
+            *reinterpret_cast<u32x4 *>(ent) = hh;
+            *reinterpret_cast<u32x4 *>(ent + 16) = hl;
+        }
+    }
+    lstore();
+    gload(1);
+    __syncthreads();
+
+    // ---- per-lane constants --------------------------------------------------
+    const int n16 = lane & 15, g = lane >> 4;
+    uint32_t aoff[8];  // A operand of sub-block c: entry (c, g, part) or the zero slot
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const bool hit = (n16 >> 2) == (c & 3) && ((n16 >> 1) & 1) == (g >> 1);
+        aoff[c] = hit ? (uint32_t)(((c * 4 + g) * 2 + (n16 & 1)) * 16) : 1024u;
+    }
+    const uint8_t *stage = lds + Lo.stage;
+    // 8 bytes at an even LDS offset: the three aligned dwords around them
+    auto ld8 = [&](uint32_t off, uint32_t &d0, uint32_t &d1) {
+        const uint32_t *p = reinterpret_cast<const uint32_t *>(stage + (off & ~3u));
+        const uint32_t sh = off & 3u, p0 = p[0], p1 = p[1], p2 = p[2];
+        d0 = __builtin_amdgcn_alignbyte(p1, p0, sh);
+        d1 = __builtin_amdgcn_alignbyte(p2, p1, sh);
+    };
+
+    for (int q = 0; q < my_groups; ++q) {
+        float yacc = 0.0f;
+        for (int b = wave; b < bpr; b += NW) {
+            const uint32_t rb = (uint32_t)(n16 * RB + b * BB);
+            f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int gh = 0; gh < 2; ++gh) {  // positions 128gh ..
+                uint32_t qlA0, qlA1, qlB0, qlB1, qh0, qh1;
+                ld8(rb + 64 * gh + 8 * g, qlA0, qlA1);       // quads 0, 2
+                ld8(rb + 64 * gh + 32 + 8 * g, qlB0, qlB1);  // quads 1, 3
+                ld8(rb + 128 + 32 * gh + 8 * g, qh0, qh1);
+#pragma unroll
+                for (int quad = 0; quad < 4; ++quad) {
+                    const int c = 4 * gh + quad;
+                    const uint32_t s0 = (quad & 1) ? qlB0 : qlA0, s1 = (quad & 1) ? qlB1 : qlA1;
+                    const uint32_t n0 = (quad >> 1) ? ((s0 >> 4) & 0x0F0F0F0Fu) : (s0 & 0x0F0F0F0Fu);
+                    const uint32_t n1 = (quad >> 1) ? ((s1 >> 4) & 0x0F0F0F0Fu) : (s1 & 0x0F0F0F0Fu);
+                    const uint32_t q0 = n0 | (((qh0 >> (2 * quad)) & 0x03030303u) << 4);
+                    const uint32_t q1 = n1 | (((qh1 >> (2 * quad)) & 0x03030303u) << 4);
+                    const u32x4 bop = {q0 & 0x00FF00FFu, (q0 >> 8) & 0x00FF00FFu,
+                                       q1 & 0x00FF00FFu, (q1 >> 8) & 0x00FF00FFu};
+                    const half8 aop = *reinterpret_cast<const half8 *>(lds + (uint32_t)b * TAB + aoff[c]);
+                    acc[gh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, __builtin_bit_cast(half8, bop),
+                                                                     acc[gh], 0, 0, 0);
+                }
+            }
+            // this lane's sub-blocks g (acc[0]) and 4 + g (acc[1]) of row n16
+            const float d = half_bits_finite((uint32_t)stage[rb + 208] | ((uint32_t)stage[rb + 209] << 8));
+            const float *mb = meta + b * META;
+#pragma unroll
+            for (int a = 0; a < 2; ++a) {
+                const int j = 4 * a + g;
+                const float sc0 = (float)(int8_t)stage[rb + 192 + 2 * j];
+                const float sc1 = (float)(int8_t)stage[rb + 193 + 2 * j];
+                const float s0 = acc[a][0] + acc[a][1], s1 = acc[a][2] + acc[a][3];
+                yacc += d * (mb[j] * (sc0 * s0 + sc1 * s1) -
+                             32.0f * (sc0 * mb[8 + 2 * j] + sc1 * mb[9 + 2 * j]));
+            }
+        }
+        // row n16's sum over the 4 lane groups, then over the wavefronts
+        yacc += __shfl_xor(yacc, 16, 64);
+        yacc += __shfl_xor(yacc, 32, 64);
+        if (lane < 16) aux[wave * R + lane] = yacc;
+        __syncthreads();  // every wavefront is done with the stage and aux
+        if (tid < R) {
+            float s = 0.0f;
+            for (int wv = 0; wv < NW; ++wv) s += aux[wv * R + tid];
+            ybuf[q * R + tid] = s;
+        }
+        lstore();       // group q + 1 (a clamped duplicate after the last)
+        gload(q + 2);   // issued unconditionally, so every wait is exact
+        __syncthreads();
+    }
+    for (int i = tid; i < my_groups * R; i += NT) {
+        const int r = ((int)blockIdx.x + (i / R) * (int)gridDim.x) * R + (i % R);
+        if (r < n) y[r] = ybuf[i];
+    }
+}
+
+hipError_t gemv_q6k_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                                hipStream_t stream) {
+    using namespace q6m;
+    if (bpr > MAX_BPR || (((uintptr_t)w | (uintptr_t)x) & 15u) || (((long)n * bpr * BB) % 16))
+        return hipErrorNotSupported;
+    static hipError_t attr = hipFuncSetAttribute((const void *)gemv_q6k_mfma_kernel,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 160 * 1024);
+    if (attr != hipSuccess) return attr;
+    static int occ = 0;
+    if (occ == 0) {
+        int o = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, (const void *)gemv_q6k_mfma_kernel, NT,
+                                                         q6m_layout(MAX_BPR, 32).total) != hipSuccess ||
+            o <= 0)
+            o = 1;
+        occ = o;
+    }
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    const long groups = (n + R - 1) / R;
+    const long maxgrid = (long)cus * occ;
+    const long rounds = (groups + maxgrid - 1) / maxgrid;
+    const long grid = (groups + rounds - 1) / rounds;
+    const size_t lds = q6m_layout(bpr, (int)rounds).total;
+    if (lds > 160 * 1024) return hipErrorNotSupported;
+    gemv_q6k_mfma_kernel<<<(unsigned)grid, NT, lds, stream>>>(w, x, y, n, bpr, (int)rounds);
+    return hipGetLastError();
+}
+
+}  // namespace mgq
