@@ -1,17 +1,24 @@
 // Q6_K matvec on the gfx950 matrix cores (launch_matvec_q6k, rocm.rs:482-485;
 // canonical order of dequantize_row_q6_k, gguf.rs:441-477), for 16-byte
-// aligned weights and x with K <= kQ6mMaxBpr * 256 (the attention and lm_head
-// shapes of 7B-class models).
+// aligned weights and x. Two kernels share the decode: whole-row stages for
+// K <= kQ6mMaxBpr * 256 (attention, lm_head) and K-chunked per-row stages for
+// longer rows (ffn_down).
 //
 // Q6_K block, 210 B / 256 weights: ql[128] | qh[64] | int8 sc[16] | d f16.
 // Position p = 128g' + 32quad + l (l < 32) is sub-block j = 4g' + quad:
 // q = (nibble (quad >> 1) of ql[64g' + 32(quad & 1) + l]) | (2 bits (2quad) of
 // qh[32g' + l]) << 4, and w = d * sc[2j + l/16] * (q - 32).
 //
-// Work-group = 16 rows x all K, persistent over row groups; 7 wavefronts.
-//   * Stage: a row group's 16 rows are one contiguous byte range (16 x RB,
-//     RB = 210 bpr, a multiple of 16 bytes), copied flat into LDS as whole
-//     16-byte chunks; the next group's chunks wait in registers.
+// Work-group = 16 rows x all K, persistent over row groups; 7 wavefronts
+// (16 for the K-chunked kernel).
+//   * Whole-row stage: a row group's 16 rows are one contiguous byte range
+//     (16 x RB, RB = 210 bpr), copied flat into LDS as whole 16-byte chunks;
+//     the next group's chunks wait in registers.
+//   * K-chunked stage (bpr > kQ6mMaxBpr): a stage is 14 blocks of each of the
+//     16 rows; row r's segment is copied as the 16-byte chunks from the
+//     16-byte boundary at or below its start into its own LDS slot, and the
+//     segment's offset in that chunk (s & 15) moves the lane's reads. Row sums
+//     carry over the chunks of a group; the table covers the whole row.
 //   * One v_mfma_f32_16x16x32_f16 per sub-block: B = weights (lane (n, g):
 //     row n, positions 8g..8g+7 of the sub-block; the 6-bit q are f16
 //     subnormals q*2^-24, exact), A = the activation table built once per
@@ -39,8 +46,14 @@ constexpr int R = 16, NW = 7, NT = NW * 64;
 constexpr int BB = 210;                   // Q6_K block bytes
 constexpr int MAX_BPR = 14;               // whole-row stages
 constexpr int CPL = (R * MAX_BPR * BB / 16 + NT - 1) / NT;  // 16-byte chunks per lane (7)
-constexpr int TAB = 1040;                 // per block: 1 KiB of A operands + a zero slot
+constexpr int TAB = 1024;                 // per block: 1 KiB of A operands
 constexpr int META = 24;                  // floats per block: corr[8] | X[16]
+constexpr int SEG = 14;                   // blocks per K-chunk of a long row
+// wavefronts of the K-chunked kernel: a long-row shape has few row groups
+// (ffn_down: 224 for 256 CUs), so one work-group per CU carries the latency
+// hiding (7 -> 16 waves: 25.5 -> 20.9 us on 3584x18944)
+constexpr int LONG_NW = 16;
+constexpr int SLOTC = (15 + SEG * BB + 15) / 16;            // 16-byte chunks per row slot (185)
 }  // namespace q6m
 
 constexpr int kQ6mMaxBpr = q6m::MAX_BPR;
@@ -50,16 +63,149 @@ struct Q6mLayout {
     size_t total;
 };
 
-__host__ __device__ inline Q6mLayout q6m_layout(int bpr, int rounds) {
+// chunked = false: whole-row stages (bpr <= MAX_BPR); true: K-chunked slots;
+// nw = wavefronts per work-group
+__host__ __device__ inline Q6mLayout q6m_layout(int bpr, int rounds, bool chunked,
+                                                int nw = q6m::NW) {
     using namespace q6m;
     Q6mLayout L;
     L.meta = (uint32_t)bpr * TAB;
     L.stage = L.meta + (uint32_t)bpr * META * 4;
     // + 16: the 3-dword window around the last bytes of row 15 may end past them
-    L.aux = L.stage + (uint32_t)(R * bpr * BB) + 16;
-    L.ybuf = L.aux + (uint32_t)NW * R * 4;
+    L.aux = L.stage + (chunked ? (uint32_t)(R * SLOTC * 16) : (uint32_t)(R * bpr * BB)) + 16;
+    L.ybuf = L.aux + (uint32_t)nw * R * 4;
     L.total = (size_t)L.ybuf + (size_t)R * rounds * 4;
     return L;
+}
+
+// Activation-table item i = 8 floats (v0, v1) of x: block i/32, sub-block
+// (i/4)%8, lane group i%4. Every lane calls it (the quad reductions are
+// cross-lane); only lanes with `valid` store. x*2^e = xh + xl with e putting
+// the sub-block's largest |x| in [2^13, 2^14); slot s of the 8 holds position
+// {0,2,1,3,4,6,5,7}[s] (the B operand's order).
+__device__ __forceinline__ void q6m_item(uint8_t *lds, float *meta, int i, bool valid, f32x4 v0,
+                                         f32x4 v1) {
+    using namespace q6m;
+    float amax = fmaxf(fmaxf(fmaxf(fabsf(v0[0]), fabsf(v0[1])), fmaxf(fabsf(v0[2]), fabsf(v0[3]))),
+                       fmaxf(fmaxf(fabsf(v1[0]), fabsf(v1[1])), fmaxf(fabsf(v1[2]), fabsf(v1[3]))));
+    float sum = ((v0[0] + v0[1]) + (v0[2] + v0[3])) + ((v1[0] + v1[1]) + (v1[2] + v1[3]));
+    amax = fmaxf(amax, quad_xor<1>(amax));
+    amax = fmaxf(amax, quad_xor<2>(amax));
+    sum += quad_xor<1>(sum);  // the 16 values of this half
+    if (!valid) return;
+    int e = 0;
+    if (amax > 0.0f && amax <= 3.402823466e38f) {
+        int ex;
+        frexpf(amax, &ex);
+        e = std::min(std::max(14 - ex, -90), 140);
+    }
+    const int b = i >> 5, j = (i >> 2) & 7, kg = i & 3;
+    if (kg == 0) meta[b * META + j] = ldexpf(1.0f, 24 - e);
+    if ((kg & 1) == 0) meta[b * META + 8 + 2 * j + (kg >> 1)] = sum;
+    const float xs[8] = {v0[0], v0[2], v0[1], v0[3], v1[0], v1[2], v1[1], v1[3]};
+    u32x4 hh, hl;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float a0 = ldexpf(xs[2 * q], e), a1 = ldexpf(xs[2 * q + 1], e);
+        const auto hp = __builtin_amdgcn_cvt_pkrtz(a0, a1);
+        const auto lp = __builtin_amdgcn_cvt_pkrtz(a0 - (float)hp[0], a1 - (float)hp[1]);
+        hh[q] = __builtin_bit_cast(uint32_t, hp);
+        hl[q] = __builtin_bit_cast(uint32_t, lp);
+    }
+    uint8_t *ent = lds + (size_t)b * TAB + (size_t)((j * 4 + kg) * 2) * 16;
+    *reinterpret_cast<u32x4 *>(ent) = hh;
+    *reinterpret_cast<u32x4 *>(ent + 16) = hl;
+}
+
+// Lane (n16, g) supplies A row n16, k-slice g of every MFMA. Row n16 is
+// nonzero only in the MFMAs of sub-blocks c with c % 4 = n16 / 4, and only in
+// its half's k-slices (g / 2 = (n16 / 2) % 2): there it is table entry
+// (c, g, part = n16 % 2), at byte 128 c + e of the block's table. hitq is
+// that quad (-1: the lane's A data is zero in every MFMA).
+struct Q6mLane {
+    uint32_t e;
+    int hitq;
+};
+__device__ __forceinline__ Q6mLane q6m_lane(int lane) {
+    const int n16 = lane & 15, g = lane >> 4;
+    Q6mLane L;
+    L.e = (uint32_t)((g * 2 + (n16 & 1)) * 16);
+    L.hitq = (((n16 >> 1) & 1) == (g >> 1)) ? (n16 >> 2) : -1;
+    return L;
+}
+
+// One Q6_K block of row n16 staged at LDS byte rb (2-byte aligned), against
+// table entry b: this lane's part of d * sum_j (corr_j (sc s_0 + sc s_1) -
+// 32 (sc X_0 + sc X_1)) over its sub-blocks g and 4 + g. aop holds the A
+// operands: zero (set once by the caller) except where the lane's row is
+// nonzero, which only those lanes reload, block by block.
+__device__ __forceinline__ float q6m_block(const uint8_t *lds, const uint8_t *stage, uint32_t rb,
+                                           int b, Q6mLane ln, half8 (&aop)[8], const float *meta,
+                                           int g) {
+    using namespace q6m;
+    // 8 bytes at an even LDS offset: the three aligned dwords around them
+    const uint32_t sh = rb & 3u;
+    const uint32_t *rw = reinterpret_cast<const uint32_t *>(stage + (rb & ~3u));
+    auto ld8 = [&](uint32_t off, uint32_t &d0, uint32_t &d1) {  // off: a multiple of 4
+        const uint32_t p0 = rw[off / 4], p1 = rw[off / 4 + 1], p2 = rw[off / 4 + 2];
+        d0 = __builtin_amdgcn_alignbyte(p1, p0, sh);
+        d1 = __builtin_amdgcn_alignbyte(p2, p1, sh);
+    };
+    const uint8_t *tb = lds + (uint32_t)b * TAB + ln.e;
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+        if ((c & 3) == ln.hitq) aop[c] = *reinterpret_cast<const half8 *>(tb + 128 * c);
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int gh = 0; gh < 2; ++gh) {  // positions 128gh ..
+        uint32_t qlA0, qlA1, qlB0, qlB1, qh0, qh1;
+        ld8(64 * gh + 8 * g, qlA0, qlA1);       // quads 0, 2
+        ld8(64 * gh + 32 + 8 * g, qlB0, qlB1);  // quads 1, 3
+        ld8(128 + 32 * gh + 8 * g, qh0, qh1);
+#pragma unroll
+        for (int quad = 0; quad < 4; ++quad) {
+            const int c = 4 * gh + quad;
+            const uint32_t s0 = (quad & 1) ? qlB0 : qlA0, s1 = (quad & 1) ? qlB1 : qlA1;
+            const uint32_t n0 = (quad >> 1) ? ((s0 >> 4) & 0x0F0F0F0Fu) : (s0 & 0x0F0F0F0Fu);
+            const uint32_t n1 = (quad >> 1) ? ((s1 >> 4) & 0x0F0F0F0Fu) : (s1 & 0x0F0F0F0Fu);
+            const uint32_t q0 = n0 | (((qh0 >> (2 * quad)) & 0x03030303u) << 4);
+            const uint32_t q1 = n1 | (((qh1 >> (2 * quad)) & 0x03030303u) << 4);
+            const u32x4 bop = {q0 & 0x00FF00FFu, (q0 >> 8) & 0x00FF00FFu, q1 & 0x00FF00FFu,
+                               (q1 >> 8) & 0x00FF00FFu};
+            acc[gh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop[c], __builtin_bit_cast(half8, bop),
+                                                             acc[gh], 0, 0, 0);
+        }
+    }
+    // this lane's sub-blocks g (acc[0]) and 4 + g (acc[1]) of row n16
+    const float d = half_bits_finite((uint32_t)stage[rb + 208] | ((uint32_t)stage[rb + 209] << 8));
+    const float *mb = meta + b * META;
+    float y = 0.0f;
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+        const int j = 4 * a + g;
+        const float sc0 = (float)(int8_t)stage[rb + 192 + 2 * j];
+        const float sc1 = (float)(int8_t)stage[rb + 193 + 2 * j];
+        const float s0 = acc[a][0] + acc[a][1], s1 = acc[a][2] + acc[a][3];
+        y += d * (mb[j] * (sc0 * s0 + sc1 * s1) - 32.0f * (sc0 * mb[8 + 2 * j] + sc1 * mb[9 + 2 * j]));
+    }
+    return y;
+}
+
+// Row n16's sum over the 4 lane groups and the wavefronts -> ybuf[slot];
+// ends with every wavefront done with the stage and aux.
+template <int NW = q6m::NW>
+__device__ __forceinline__ void q6m_row_sums(float yacc, float *aux, float *ybuf, int tid, int lane,
+                                             int wave) {
+    constexpr int R = q6m::R;
+    yacc += __shfl_xor(yacc, 16, 64);
+    yacc += __shfl_xor(yacc, 32, 64);
+    if (lane < 16) aux[wave * R + lane] = yacc;
+    __syncthreads();
+    if (tid < R) {
+        float s = 0.0f;
+        for (int wv = 0; wv < NW; ++wv) s += aux[wv * R + tid];
+        ybuf[tid] = s;
+    }
 }
 
 __global__ __launch_bounds__(q6m::NT) void gemv_q6k_mfma_kernel(const uint8_t *__restrict__ w,
@@ -68,7 +214,7 @@ __global__ __launch_bounds__(q6m::NT) void gemv_q6k_mfma_kernel(const uint8_t *_
                                                                 int bpr, int rounds) {
     using namespace q6m;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    const Q6mLayout Lo = q6m_layout(bpr, rounds);
+    const Q6mLayout Lo = q6m_layout(bpr, rounds, false);
     float *meta = reinterpret_cast<float *>(lds + Lo.meta);
     float *aux = reinterpret_cast<float *>(lds + Lo.aux);
     float *ybuf = reinterpret_cast<float *>(lds + Lo.ybuf);
@@ -100,118 +246,28 @@ __global__ __launch_bounds__(q6m::NT) void gemv_q6k_mfma_kernel(const uint8_t *_
     };
 
     // ---- prologue: the activation table (x loads first, then the weights) --
-    // item i = 8 floats: block i/32, sub-block (i/4)%8, lane group kg = i%4;
     // bpr <= 14 makes it at most one item per thread
     const int nitems = bpr * 32;
     const int ii = min(tid, nitems - 1);
     const f32x4 v0 = *reinterpret_cast<const f32x4 *>(x + (size_t)ii * 8);
     const f32x4 v1 = *reinterpret_cast<const f32x4 *>(x + (size_t)ii * 8 + 4);
     gload(0);
-    for (int b = tid; b < bpr; b += NT)
-        *reinterpret_cast<u32x4 *>(lds + (size_t)b * TAB + 1024) = u32x4{0u, 0u, 0u, 0u};
-    {
-        float amax = fmaxf(fmaxf(fmaxf(fabsf(v0[0]), fabsf(v0[1])), fmaxf(fabsf(v0[2]), fabsf(v0[3]))),
-                           fmaxf(fmaxf(fabsf(v1[0]), fabsf(v1[1])), fmaxf(fabsf(v1[2]), fabsf(v1[3]))));
-        float sum = ((v0[0] + v0[1]) + (v0[2] + v0[3])) + ((v1[0] + v1[1]) + (v1[2] + v1[3]));
-        amax = fmaxf(amax, quad_xor<1>(amax));
-        amax = fmaxf(amax, quad_xor<2>(amax));
-        sum += quad_xor<1>(sum);  // the 16 values of this half
-        if (tid < nitems) {
-            int e = 0;  // x*2^e puts the sub-block's largest |x| in [2^13, 2^14)
-            if (amax > 0.0f && amax <= 3.402823466e38f) {
-                int ex;
-                frexpf(amax, &ex);
-                e = std::min(std::max(14 - ex, -90), 140);
-            }
-            const int b = tid >> 5, j = (tid >> 2) & 7, kg = tid & 3;
-            if (kg == 0) meta[b * META + j] = ldexpf(1.0f, 24 - e);
-            if ((kg & 1) == 0) meta[b * META + 8 + 2 * j + (kg >> 1)] = sum;
-            // slot s holds position {0,2,1,3,4,6,5,7}[s] of the 8 (the B operand's order)
-            const float xs[8] = {v0[0], v0[2], v0[1], v0[3], v1[0], v1[2], v1[1], v1[3]};
-            u32x4 hh, hl;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float a0 = ldexpf(xs[2 * q], e), a1 = ldexpf(xs[2 * q + 1], e);
-                const auto hp = __builtin_amdgcn_cvt_pkrtz(a0, a1);
-                const auto lp = __builtin_amdgcn_cvt_pkrtz(a0 - (float)hp[0], a1 - (float)hp[1]);
-                hh[q] = __builtin_bit_cast(uint32_t, hp);
-                hl[q] = __builtin_bit_cast(uint32_t, lp);
-            }
-            uint8_t *ent = lds + (size_t)b * TAB + (size_t)((j * 4 + kg) * 2) * 16;
-            *reinterpret_cast<u32x4 *>(ent) = hh;
-            *reinterpret_cast<u32x4 *>(ent + 16) = hl;
-        }
-    }
+    q6m_item(lds, meta, tid, tid < nitems, v0, v1);
     lstore();
     gload(1);
     __syncthreads();
 
-    // ---- per-lane constants --------------------------------------------------
     const int n16 = lane & 15, g = lane >> 4;
-    uint32_t aoff[8];  // A operand of sub-block c: entry (c, g, part) or the zero slot
+    const Q6mLane ln = q6m_lane(lane);
+    half8 aop[8];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-        const bool hit = (n16 >> 2) == (c & 3) && ((n16 >> 1) & 1) == (g >> 1);
-        aoff[c] = hit ? (uint32_t)(((c * 4 + g) * 2 + (n16 & 1)) * 16) : 1024u;
-    }
+    for (int c = 0; c < 8; ++c) aop[c] = half8{};
     const uint8_t *stage = lds + Lo.stage;
-    // 8 bytes at an even LDS offset: the three aligned dwords around them
-    auto ld8 = [&](uint32_t off, uint32_t &d0, uint32_t &d1) {
-        const uint32_t *p = reinterpret_cast<const uint32_t *>(stage + (off & ~3u));
-        const uint32_t sh = off & 3u, p0 = p[0], p1 = p[1], p2 = p[2];
-        d0 = __builtin_amdgcn_alignbyte(p1, p0, sh);
-        d1 = __builtin_amdgcn_alignbyte(p2, p1, sh);
-    };
-
     for (int q = 0; q < my_groups; ++q) {
         float yacc = 0.0f;
-        for (int b = wave; b < bpr; b += NW) {
-            const uint32_t rb = (uint32_t)(n16 * RB + b * BB);
-            f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-            for (int gh = 0; gh < 2; ++gh) {  // positions 128gh ..
-                uint32_t qlA0, qlA1, qlB0, qlB1, qh0, qh1;
-                ld8(rb + 64 * gh + 8 * g, qlA0, qlA1);       // quads 0, 2
-                ld8(rb + 64 * gh + 32 + 8 * g, qlB0, qlB1);  // quads 1, 3
-                ld8(rb + 128 + 32 * gh + 8 * g, qh0, qh1);
-#pragma unroll
-                for (int quad = 0; quad < 4; ++quad) {
-                    const int c = 4 * gh + quad;
-                    const uint32_t s0 = (quad & 1) ? qlB0 : qlA0, s1 = (quad & 1) ? qlB1 : qlA1;
-                    const uint32_t n0 = (quad >> 1) ? ((s0 >> 4) & 0x0F0F0F0Fu) : (s0 & 0x0F0F0F0Fu);
-                    const uint32_t n1 = (quad >> 1) ? ((s1 >> 4) & 0x0F0F0F0Fu) : (s1 & 0x0F0F0F0Fu);
-                    const uint32_t q0 = n0 | (((qh0 >> (2 * quad)) & 0x03030303u) << 4);
-                    const uint32_t q1 = n1 | (((qh1 >> (2 * quad)) & 0x03030303u) << 4);
-                    const u32x4 bop = {q0 & 0x00FF00FFu, (q0 >> 8) & 0x00FF00FFu,
-                                       q1 & 0x00FF00FFu, (q1 >> 8) & 0x00FF00FFu};
-                    const half8 aop = *reinterpret_cast<const half8 *>(lds + (uint32_t)b * TAB + aoff[c]);
-                    acc[gh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, __builtin_bit_cast(half8, bop),
-                                                                     acc[gh], 0, 0, 0);
-                }
-            }
-            // this lane's sub-blocks g (acc[0]) and 4 + g (acc[1]) of row n16
-            const float d = half_bits_finite((uint32_t)stage[rb + 208] | ((uint32_t)stage[rb + 209] << 8));
-            const float *mb = meta + b * META;
-#pragma unroll
-            for (int a = 0; a < 2; ++a) {
-                const int j = 4 * a + g;
-                const float sc0 = (float)(int8_t)stage[rb + 192 + 2 * j];
-                const float sc1 = (float)(int8_t)stage[rb + 193 + 2 * j];
-                const float s0 = acc[a][0] + acc[a][1], s1 = acc[a][2] + acc[a][3];
-                yacc += d * (mb[j] * (sc0 * s0 + sc1 * s1) -
-                             32.0f * (sc0 * mb[8 + 2 * j] + sc1 * mb[9 + 2 * j]));
-            }
-        }
-        // row n16's sum over the 4 lane groups, then over the wavefronts
-        yacc += __shfl_xor(yacc, 16, 64);
-        yacc += __shfl_xor(yacc, 32, 64);
-        if (lane < 16) aux[wave * R + lane] = yacc;
-        __syncthreads();  // every wavefront is done with the stage and aux
-        if (tid < R) {
-            float s = 0.0f;
-            for (int wv = 0; wv < NW; ++wv) s += aux[wv * R + tid];
-            ybuf[q * R + tid] = s;
-        }
+        for (int b = wave; b < bpr; b += NW)
+            yacc += q6m_block(lds, stage, (uint32_t)(n16 * RB + b * BB), b, ln, aop, meta, g);
+        q6m_row_sums(yacc, aux, ybuf + q * R, tid, lane, wave);
         lstore();       // group q + 1 (a clamped duplicate after the last)
         gload(q + 2);   // issued unconditionally, so every wait is exact
         __syncthreads();
@@ -222,36 +278,177 @@ __global__ __launch_bounds__(q6m::NT) void gemv_q6k_mfma_kernel(const uint8_t *_
     }
 }
 
-hipError_t gemv_q6k_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
-                                hipStream_t stream) {
-    using namespace q6m;
-    if (bpr > MAX_BPR || (((uintptr_t)w | (uintptr_t)x) & 15u) || (((long)n * bpr * BB) % 16))
-        return hipErrorNotSupported;
-    static hipError_t attr = hipFuncSetAttribute((const void *)gemv_q6k_mfma_kernel,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 160 * 1024);
-    if (attr != hipSuccess) return attr;
-    static int occ = 0;
-    if (occ == 0) {
-        int o = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, (const void *)gemv_q6k_mfma_kernel, NT,
-                                                         q6m_layout(MAX_BPR, 32).total) != hipSuccess ||
-            o <= 0)
-            o = 1;
-        occ = o;
+// Long rows: stage t = (group t / nck, K-chunk t % nck) of this work-group;
+// chunk kc covers blocks [14 kc, min(14 kc + 14, bpr)) of the group's 16 rows.
+template <int NW, int XI>
+__global__ __launch_bounds__(NW * 64) void gemv_q6k_mfma_long_kernel(const uint8_t *__restrict__ w,
+                                                                     const float *__restrict__ x,
+                                                                     float *__restrict__ y, int n,
+                                                                     int bpr, int rounds) {
+    using q6m::R, q6m::BB, q6m::TAB, q6m::SEG, q6m::SLOTC;
+    constexpr int NT = NW * 64, LCPL = (R * SLOTC + NT - 1) / NT;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const Q6mLayout Lo = q6m_layout(bpr, rounds, true, NW);
+    float *meta = reinterpret_cast<float *>(lds + Lo.meta);
+    float *aux = reinterpret_cast<float *>(lds + Lo.aux);
+    float *ybuf = reinterpret_cast<float *>(lds + Lo.ybuf);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const long RB = (long)bpr * BB;
+    const int groups = (n + R - 1) / R;
+    const int my_groups = (groups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int nck = (bpr + SEG - 1) / SEG;
+    const int T = my_groups * nck;
+    const u32x4 *wc = reinterpret_cast<const u32x4 *>(w);
+    const long last_chunk = (long)n * RB / 16 - 1;
+
+    // ---- stage loads: stage t, clamped (unconditional) ----------------------
+    // slot chunk c = 16-byte chunk (c % SLOTC) of row c / SLOTC's segment,
+    // taken from the 16-byte boundary at or below the segment's start
+    u32x4 reg[LCPL];
+    auto gload = [&](int t) {
+        t = min(t, T - 1);
+        const int q = t / nck, kc = t - q * nck;
+        const int b0 = kc * SEG, cb = min(SEG, bpr - b0);
+        const int row0 = ((int)blockIdx.x + q * (int)gridDim.x) * R;
+#pragma unroll
+        for (int k = 0; k < LCPL; ++k) {
+            const int c = min(tid + k * NT, R * SLOTC - 1);
+            const int r = c / SLOTC, col = c - r * SLOTC;
+            const long s = (long)min(row0 + r, n - 1) * RB + (long)b0 * BB;
+            const int nch = (int)(((s & 15) + cb * BB + 15) >> 4);
+            reg[k] = wc[min((s >> 4) + min(col, nch - 1), last_chunk)];
+        }
+    };
+    auto lstore = [&]() {
+#pragma unroll
+        for (int k = 0; k < LCPL; ++k) {
+            const int c = tid + k * NT;
+            if (c < R * SLOTC) *reinterpret_cast<u32x4 *>(lds + Lo.stage + 16 * c) = reg[k];
+        }
+    };
+
+    // ---- prologue: the whole row's activation table, XI items per thread ---
+    const int nitems = bpr * 32;
+    f32x4 xv[2 * XI];
+#pragma unroll
+    for (int k = 0; k < XI; ++k) {
+        const int ii = min(tid + k * NT, nitems - 1);
+        xv[2 * k] = *reinterpret_cast<const f32x4 *>(x + (size_t)ii * 8);
+        xv[2 * k + 1] = *reinterpret_cast<const f32x4 *>(x + (size_t)ii * 8 + 4);
     }
+    gload(0);
+#pragma unroll
+    for (int k = 0; k < XI; ++k)
+        q6m_item(lds, meta, tid + k * NT, tid + k * NT < nitems, xv[2 * k], xv[2 * k + 1]);
+    lstore();
+    gload(1);
+    __syncthreads();
+
+    const int n16 = lane & 15, g = lane >> 4;
+    const Q6mLane ln = q6m_lane(lane);
+    half8 aop[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) aop[c] = half8{};
+    const uint8_t *stage = lds + Lo.stage;
+    float yacc = 0.0f;
+    for (int t = 0; t < T; ++t) {
+        const int q = t / nck, kc = t - q * nck;
+        const int b0 = kc * SEG, cb = min(SEG, bpr - b0);
+        const int row = min(((int)blockIdx.x + q * (int)gridDim.x) * R + n16, n - 1);
+        const uint32_t rb0 =
+            (uint32_t)(n16 * SLOTC * 16) + (uint32_t)(((long)row * RB + (long)b0 * BB) & 15);
+        for (int bl = wave; bl < cb; bl += NW)
+            yacc += q6m_block(lds, stage, rb0 + (uint32_t)(bl * BB), b0 + bl, ln, aop, meta, g);
+        if (kc == nck - 1) {
+            q6m_row_sums<NW>(yacc, aux, ybuf + q * R, tid, lane, wave);
+            yacc = 0.0f;
+        } else {
+            __syncthreads();  // every wavefront is done with the stage
+        }
+        lstore();       // stage t + 1 (a clamped duplicate after the last)
+        gload(t + 2);   // issued unconditionally, so every wait is exact
+        __syncthreads();
+    }
+    for (int i = tid; i < my_groups * R; i += NT) {
+        const int r = ((int)blockIdx.x + (i / R) * (int)gridDim.x) * R + (i % R);
+        if (r < n) y[r] = ybuf[i];
+    }
+}
+
+namespace {
+
+int cu_count() {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
         cus = 256;
+    return cus;
+}
+
+// Persistent launch of `kern` with the occupancy at `probe_lds` bytes: grid
+// balanced so every work-group gets the same number of row groups.
+template <typename K>
+hipError_t q6m_launch(K kern, bool chunked, int nw, const uint8_t *w, const float *x, float *y,
+                      int n, int bpr, int probe_bpr, int &occ, hipError_t &attr,
+                      hipStream_t stream) {
+    using namespace q6m;
+    if (attr != hipSuccess) return attr;
+    if (occ == 0) {
+        int o = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, (const void *)kern, nw * 64,
+                                                         q6m_layout(probe_bpr, 32, chunked, nw).total) !=
+                hipSuccess ||
+            o <= 0)
+            o = 1;
+        occ = o;
+    }
     const long groups = (n + R - 1) / R;
-    const long maxgrid = (long)cus * occ;
+    const long maxgrid = (long)cu_count() * occ;
     const long rounds = (groups + maxgrid - 1) / maxgrid;
     const long grid = (groups + rounds - 1) / rounds;
-    const size_t lds = q6m_layout(bpr, (int)rounds).total;
+    const size_t lds = q6m_layout(bpr, (int)rounds, chunked, nw).total;
     if (lds > 160 * 1024) return hipErrorNotSupported;
-    gemv_q6k_mfma_kernel<<<(unsigned)grid, NT, lds, stream>>>(w, x, y, n, bpr, (int)rounds);
+    kern<<<(unsigned)grid, nw * 64, lds, stream>>>(w, x, y, n, bpr, (int)rounds);
     return hipGetLastError();
+}
+
+template <int NW, int XI>
+hipError_t q6m_long_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                           hipStream_t stream) {
+    static hipError_t attr = hipFuncSetAttribute((const void *)gemv_q6k_mfma_long_kernel<NW, XI>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 160 * 1024);
+    static int occ = 0;
+    // occupancy at the largest row this instance serves
+    const int probe = std::min(XI * NW * 64 / 32, 100);
+    return q6m_launch(gemv_q6k_mfma_long_kernel<NW, XI>, true, NW, w, x, y, n, bpr, probe, occ,
+                      attr, stream);
+}
+
+}  // namespace
+
+hipError_t gemv_q6k_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                                hipStream_t stream) {
+    using namespace q6m;
+    if ((((uintptr_t)w | (uintptr_t)x) & 15u) || (((long)n * bpr * BB) % 16))
+        return hipErrorNotSupported;
+    if (bpr <= MAX_BPR) {
+        static hipError_t attr = hipFuncSetAttribute((const void *)gemv_q6k_mfma_kernel,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     160 * 1024);
+        static int occ = 0;
+        return q6m_launch(gemv_q6k_mfma_kernel, false, NW, w, x, y, n, bpr, MAX_BPR, occ, attr,
+                          stream);
+    }
+    constexpr int LNW = LONG_NW, LNT = LNW * 64;
+    const int need = (bpr * 32 + LNT - 1) / LNT;  // table items per thread
+    if (need <= 1) return q6m_long_launch<LNW, 1>(w, x, y, n, bpr, stream);
+    if (need <= 2) return q6m_long_launch<LNW, 2>(w, x, y, n, bpr, stream);
+    if (need <= 4) return q6m_long_launch<LNW, 4>(w, x, y, n, bpr, stream);
+    if (need <= 6) return q6m_long_launch<LNW, 6>(w, x, y, n, bpr, stream);
+    if (need <= 8) return q6m_long_launch<LNW, 8>(w, x, y, n, bpr, stream);
+    return hipErrorNotSupported;
 }
 
 }  // namespace mgq

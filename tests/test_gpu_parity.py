@@ -495,7 +495,11 @@ def test_dp4a_nonfinite_rows_are_zero(L, orc):
 @pytest.mark.parametrize("fmt", [176, 210])
 @pytest.mark.parametrize("n,bpr", [(1, 1), (5, 3), (64, 14), (3584, 14), (300, 74), (4099, 2),
                                    (7, 15), (33, 29), (20000, 14), (9001, 3), (8, 1), (40, 1),
-                                   (24, 3), (136, 7), (1000, 14), (4096, 2)])
+                                   (24, 3), (136, 7), (1000, 14), (4096, 2),
+                                   # Q6_K K-chunked stages: chunk remainders, odd bpr (2-byte
+                                   # aligned rows), a partial last group, 2 rounds, 8 items/thread
+                                   (16, 15), (48, 29), (520, 43), (9600, 16), (3584, 74),
+                                   (232, 101)])
 def test_kquant_matvec_matches_oracle(L, orc, fmt, n, bpr):
     from tests.gpu_util import random_kquant_bytes
     note(f"{'q5k' if fmt == 176 else 'q6k'} n={n} bpr={bpr}")
