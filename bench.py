@@ -539,17 +539,19 @@ def run_decode_q4km(torch, q4k, args):
                         f"{launches[0]} launches), one graph",
             "us_per_launch": round(ms * 1e3 / launches[0], 3), "gbs": qbytes / (ms * 1e-3) / 1e9,
             "bytes_per_launch": qbytes // launches[0], "parity": parity,
-            "kernel": "mgq::gemv_mfma_kernel + mgq::gemv_q6k_staged_kernel",
+            "kernel": "mgq::gemv_mfma_kernel + mgq::gemv_q6k_mfma_kernel / _long_kernel",
             "tokens_per_s": 1000.0 / ms, "ms_per_step": ms}
 
 
 def run_kquant(torch, q4k, args):
     """Q5_K (176 B / 256 weights) on the gate and down shapes, or Q6_K
-    (210 B / 256) on the lm_head shape -- the K-quants real GGUFs mix in."""
+    (210 B / 256) on the lm_head and ffn_down shapes -- the K-quants real
+    GGUFs mix in (Q4_K_M: Q6_K output and half the ffn_down layers). Each
+    shape is also timed alone, in a graph of its own copies."""
     from oracle import oracle as orc
     fmt = 176 if args.workload == "q5k" else 210
     shapes = [("gate", INTER, HIDDEN), ("down", HIDDEN, INTER)] if fmt == 176 else \
-        [("lm_head", VOCAB, HIDDEN)]
+        [("lm_head", VOCAB, HIDDEN), ("down", HIDDEN, INTER)]
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0x5150 + fmt)
     per = sum(n * (k // BLOCK_ELEMS) * fmt for _, n, k in shapes)
@@ -575,6 +577,16 @@ def run_kquant(torch, q4k, args):
             fn(w.data_ptr(), x.data_ptr(), y.data_ptr(), n, k // BLOCK_ELEMS, st)
     ms = time_captured(torch, launch, args.steps, args.warmup)
     nbytes = sum(n * (k // BLOCK_ELEMS) * fmt + 4 * (n + k) for _, _, _, _, n, k in items)
+    per_shape = {}
+    for sname, n, k in shapes:
+        mine = [it for it in items if it[0] == sname]
+
+        def launch_one(st, mine=mine):
+            for _, w, x, y, n_, k_ in mine:
+                fn(w.data_ptr(), x.data_ptr(), y.data_ptr(), n_, k_ // BLOCK_ELEMS, st)
+        us = time_captured(torch, launch_one, args.steps, args.warmup) * 1e3 / len(mine)
+        wb = n * (k // BLOCK_ELEMS) * fmt
+        per_shape[f"{sname} {n}x{k}"] = {"us": round(us, 2), "gbs": round(wb / (us * 1e-6) / 1e9, 1)}
     worst, parity = 0.0, None
     for name, w, x, y, n, k in items[-len(shapes):]:
         bpr = k // BLOCK_ELEMS
@@ -587,11 +599,12 @@ def run_kquant(torch, q4k, args):
             parity = f"FAIL {name}: max err/absdot {r.max():.3e}"
     parity = parity or f"ok (max err/absdot {worst:.2e} <= 1e-4)"
     label = "q5k: Q5_K gate 18944x3584 + down 3584x18944" if fmt == 176 else \
-        "q6k: Q6_K lm_head 152064x3584"
+        "q6k: Q6_K lm_head 152064x3584 + down 3584x18944"
     return {"workload": f"{label}, {copies} rotating copies, one graph",
             "us_per_launch": round(ms * 1e3 / len(items), 3), "gbs": nbytes / (ms * 1e-3) / 1e9,
-            "bytes_per_launch": nbytes // len(items), "parity": parity,
-            "kernel": "mgq::gemv_q5k_kernel" if fmt == 176 else "mgq::gemv_q6k_kernel"}
+            "bytes_per_launch": nbytes // len(items), "parity": parity, "per_shape": per_shape,
+            "kernel": "mgq::gemv_mfma_kernel (Q5_K mode)" if fmt == 176 else
+            "mgq::gemv_q6k_mfma_kernel + mgq::gemv_q6k_mfma_long_kernel"}
 
 
 TRAFFIC_PROFILES = {"decode7b": "gemv_mfma_decode7b_pmc.txt",
@@ -640,6 +653,8 @@ def run_side_workload(torch, q4k, args) -> int:
     for key in ("tokens_per_s", "ms_per_step", "unfused_ms_per_step", "unfused_tokens_per_s"):
         if key in r:
             out[key] = round(r[key], 4)
+    if "per_shape" in r:
+        out["per_shape"] = r["per_shape"]
     log(f"{r['workload']}: {r['us_per_launch']} us per launch; parity {r['parity']}")
     print(json.dumps(out), flush=True)
     return 0
