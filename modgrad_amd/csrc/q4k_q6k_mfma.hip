@@ -21,7 +21,9 @@
 //     carry over the chunks of a group; the table covers the whole row.
 //   * One v_mfma_f32_16x16x32_f16 per sub-block: B = weights (lane (n, g):
 //     row n, positions 8g..8g+7 of the sub-block; the 6-bit q are f16
-//     subnormals q*2^-24, exact), A = the activation table built once per
+//     subnormals q*2^-24, exact, or 16q*2^-24 for the high-nibble sub-blocks,
+//     whose halves are the nibble in place plus the qh bits as the high byte:
+//     one byte permute per operand dword), A = the activation table built once per
 //     work-group: x*2^e = xh + xl (f16) with one exponent per sub-block, in
 //     A row m = 4(j % 4) + 2 half + part, so sub-blocks 0-3 and 4-7 of a block
 //     land in two accumulators and lane (n, g) holds both halves (xh, xl) of
@@ -100,7 +102,8 @@ __device__ __forceinline__ void q6m_item(uint8_t *lds, float *meta, int i, bool 
         e = std::min(std::max(14 - ex, -90), 140);
     }
     const int b = i >> 5, j = (i >> 2) & 7, kg = i & 3;
-    if (kg == 0) meta[b * META + j] = ldexpf(1.0f, 24 - e);
+    // sub-blocks 2, 3, 6, 7 (high nibbles) arrive as 16q: their corr is / 16
+    if (kg == 0) meta[b * META + j] = ldexpf(1.0f, ((j & 2) ? 20 : 24) - e);
     if ((kg & 1) == 0) meta[b * META + 8 + 2 * j + (kg >> 1)] = sum;
     const float xs[8] = {v0[0], v0[2], v0[1], v0[3], v1[0], v1[2], v1[1], v1[3]};
     u32x4 hh, hl;
@@ -166,12 +169,25 @@ __device__ __forceinline__ float q6m_block(const uint8_t *lds, const uint8_t *st
         for (int quad = 0; quad < 4; ++quad) {
             const int c = 4 * gh + quad;
             const uint32_t s0 = (quad & 1) ? qlB0 : qlA0, s1 = (quad & 1) ? qlB1 : qlA1;
-            const uint32_t n0 = (quad >> 1) ? ((s0 >> 4) & 0x0F0F0F0Fu) : (s0 & 0x0F0F0F0Fu);
-            const uint32_t n1 = (quad >> 1) ? ((s1 >> 4) & 0x0F0F0F0Fu) : (s1 & 0x0F0F0F0Fu);
-            const uint32_t q0 = n0 | (((qh0 >> (2 * quad)) & 0x03030303u) << 4);
-            const uint32_t q1 = n1 | (((qh1 >> (2 * quad)) & 0x03030303u) << 4);
-            const u32x4 bop = {q0 & 0x00FF00FFu, (q0 >> 8) & 0x00FF00FFu, q1 & 0x00FF00FFu,
-                               (q1 >> 8) & 0x00FF00FFu};
+            u32x4 bop;
+            if (quad < 2) {
+                // low nibbles: the 6-bit q bytes (nibble | qh bits << 4), then
+                // bytes 0,2 and 1,3 into the low bytes of f16 halves: q*2^-24
+                const int sh = 4 - 2 * quad;
+                const uint32_t q0 = ((qh0 << sh) & 0x30303030u) | (s0 & 0x0F0F0F0Fu);
+                const uint32_t q1 = ((qh1 << sh) & 0x30303030u) | (s1 & 0x0F0F0F0Fu);
+                bop = u32x4{__builtin_amdgcn_perm(0u, q0, 0x0C020C00u), __builtin_amdgcn_perm(0u, q0, 0x0C030C01u),
+                            __builtin_amdgcn_perm(0u, q1, 0x0C020C00u), __builtin_amdgcn_perm(0u, q1, 0x0C030C01u)};
+            } else {
+                // high nibbles in place (16*nibble) as a half's low byte and
+                // the 2 qh bits as its high byte: 16*nibble + 256*qh = 16q,
+                // i.e. 16q*2^-24 (the sub-block's corr carries the 1/16)
+                const uint32_t m0 = s0 & 0xF0F0F0F0u, m1 = s1 & 0xF0F0F0F0u;
+                const uint32_t h0 = (qh0 >> (2 * quad)) & 0x03030303u;
+                const uint32_t h1 = (qh1 >> (2 * quad)) & 0x03030303u;
+                bop = u32x4{__builtin_amdgcn_perm(h0, m0, 0x06020400u), __builtin_amdgcn_perm(h0, m0, 0x07030501u),
+                            __builtin_amdgcn_perm(h1, m1, 0x06020400u), __builtin_amdgcn_perm(h1, m1, 0x07030501u)};
+            }
             acc[gh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop[c], __builtin_bit_cast(half8, bop),
                                                              acc[gh], 0, 0, 0);
         }
