@@ -373,18 +373,6 @@ __global__ __launch_bounds__(512) void gemv_batched_mfma_kernel(const uint8_t *_
     }
 }
 
-static int cu_count() {
-    static int cus[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cus[dev] == 0) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
-            v = 256;
-        cus[dev] = v;
-    }
-    return cus[dev];
-}
 
 template <int R, int SETS, int PF>
 static hipError_t batched_main_launch(const uint8_t *w, const uint8_t *ws, float *Y, int n, int bpr,
@@ -400,7 +388,7 @@ static hipError_t batched_main_launch(const uint8_t *w, const uint8_t *ws, float
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)kern, 512,
                                                      base + 8 * R * BP * 4) != hipSuccess || occ <= 0)
         occ = 1;
-    const long maxgrid = (long)cu_count() * occ;
+    const long maxgrid = (long)device_cus() * occ;
     const long rounds = (groups + maxgrid - 1) / maxgrid;
     const long grid = (groups + rounds - 1) / rounds;
     const size_t lds = base + (size_t)rounds * R * BP * 4;
@@ -421,7 +409,7 @@ hipError_t gemv_batched_mfma_launch(const uint8_t *w, const float *X, float *Y, 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // 16-row groups when 32-row groups would leave CUs idle
-    const bool small = (n + 31) / 32 < cu_count();
+    const bool small = (n + 31) / 32 < device_cus();
     if (sets == 1)
         return small ? batched_main_launch<16, 1, 2>(w, ws, Y, n, bpr, batch, stream)
                      : batched_main_launch<32, 1, 2>(w, ws, Y, n, bpr, batch, stream);

@@ -682,18 +682,6 @@ static int env_int(const char *name, int dflt) {
     return (s && *s) ? std::atoi(s) : dflt;
 }
 
-static int device_cus() {
-    static int cus[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cus[dev] == 0) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
-            v = 256;
-        cus[dev] = v;
-    }
-    return cus[dev];
-}
 
 // Activation operands of one launch: f32 x, or (Q8) int8 xq with its
 // per-sub-block scale xd and sum xsum.

@@ -6,6 +6,21 @@
 
 namespace mgq {
 
+// Compute units of the current device, cached per device (the persistent
+// launches size their grids from it on every call).
+inline int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+            v = 256;
+        cus[dev] = v;
+    }
+    return cus[dev];
+}
+
 // Bit-exact canonical dequant of n_blocks super-blocks; q must be 4-B aligned.
 hipError_t dequant_launch(const uint8_t *q, int n_blocks, float *out, hipStream_t stream);
 
@@ -60,7 +75,8 @@ hipError_t gemv_q8_generic_launch(const uint8_t *w, const int8_t *xq, const floa
 hipError_t gemv_q5k_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                                 hipStream_t stream);
 
-// Matrix-core Q6_K matvec for K <= 3584; hipErrorNotSupported for longer K,
+// Matrix-core Q6_K matvec (whole-row stages for K <= 3584, K-chunked stages
+// beyond, up to ~100 blocks per row); hipErrorNotSupported for longer K,
 // misaligned w or x, or a tensor that does not end on a 16-byte boundary.
 hipError_t gemv_q6k_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                                 hipStream_t stream);

@@ -394,13 +394,6 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_mfma_long_kernel(const uint8
 
 namespace {
 
-int cu_count() {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-        cus = 256;
-    return cus;
-}
 
 // Persistent launch of `kern` with the occupancy at `probe_lds` bytes: grid
 // balanced so every work-group gets the same number of row groups.
@@ -420,7 +413,7 @@ hipError_t q6m_launch(K kern, bool chunked, int nw, const uint8_t *w, const floa
         occ = o;
     }
     const long groups = (n + R - 1) / R;
-    const long maxgrid = (long)cu_count() * occ;
+    const long maxgrid = (long)device_cus() * occ;
     const long rounds = (groups + maxgrid - 1) / maxgrid;
     const long grid = (groups + rounds - 1) / rounds;
     const size_t lds = q6m_layout(bpr, (int)rounds, chunked, nw).total;
