@@ -192,6 +192,18 @@ hipError_t launch_geglu(const float *gate, const float *up, float *out, int n);
 hipError_t launch_glu_ex(const float *gate, const float *up, float *out, int n, int act,
                          hipStream_t stream);
 
+/* Replaces launch_residual_add (decl rocm.rs:503, def kernels/
+ * transformer_ops.hip:10-19): h[i] += x[i] for i < n. Also the bias add of
+ * the resident linear layer (hipblasSgemv's beta = 1 on a bias-filled y,
+ * rocm.rs:2000-2056). hipErrorInvalidValue for n <= 0 or a null pointer. */
+hipError_t launch_residual_add(float *h, const float *x, int n);
+hipError_t launch_residual_add_ex(float *h, const float *x, int n, hipStream_t stream);
+
+/* Replaces launch_scale (decl rocm.rs:504, def kernels/transformer_ops.hip:
+ * 21-30): h[i] *= s for i < n. hipErrorInvalidValue for n <= 0 or null h. */
+hipError_t launch_scale(float *h, float s, int n);
+hipError_t launch_scale_ex(float *h, float s, int n, hipStream_t stream);
+
 /* Fused RMSNorm -> Q4_K matvec: y = W * rms_norm(x, norm_w, eps) for one
  * activation row of K = blocks_per_row*256, replacing the reference decode's
  * launch_rms_norm + launch_matvec_q4k pair (rocm_gemma.rs:439-440, 477-478).

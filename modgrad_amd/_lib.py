@@ -45,6 +45,10 @@ SIGNATURES = {
     "launch_rms_norm_ex": (I, [P, P, P, I, I, F, P]),
     "launch_geglu": (I, [P, P, P, I]),
     "launch_glu_ex": (I, [P, P, P, I, I, P]),
+    "launch_residual_add": (I, [P, P, I]),
+    "launch_residual_add_ex": (I, [P, P, I, P]),
+    "launch_scale": (I, [P, F, I]),
+    "launch_scale_ex": (I, [P, F, I, P]),
     "launch_matvec_q4k_rmsnorm_ex": (I, [P, P, P, F, P, I, I, P]),
     "launch_matvec_q4k_glu_ex": (I, [P, P, P, P, F, I, P, I, I, P]),
     "mgq_chain_create": (I, [P, I, P]),

@@ -261,6 +261,22 @@ hipError_t launch_geglu(const float *gate, const float *up, float *out, int n) {
     return launch_glu_ex(gate, up, out, n, MGQ_ACT_GELU_TANH, nullptr);
 }
 
+hipError_t launch_residual_add_ex(float *h, const float *x, int n, hipStream_t stream) {
+    if (n <= 0 || !h || !x) return hipErrorInvalidValue;
+    return mgq::residual_add_launch(h, x, n, stream);
+}
+
+hipError_t launch_residual_add(float *h, const float *x, int n) {
+    return launch_residual_add_ex(h, x, n, nullptr);
+}
+
+hipError_t launch_scale_ex(float *h, float s, int n, hipStream_t stream) {
+    if (n <= 0 || !h) return hipErrorInvalidValue;
+    return mgq::scale_launch(h, s, n, stream);
+}
+
+hipError_t launch_scale(float *h, float s, int n) { return launch_scale_ex(h, s, n, nullptr); }
+
 namespace {
 bool misaligned16(const void *p) { return ((uintptr_t)p & 15u) != 0; }
 }  // namespace

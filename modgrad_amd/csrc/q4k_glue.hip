@@ -58,4 +58,28 @@ hipError_t glu_launch(const float *gate, const float *up, float *out, int n, int
     return hipGetLastError();
 }
 
+// h[i] += x[i] (kernels/transformer_ops.hip:10-19): the residual add after the
+// attention and FFN projections, and the bias add of a resident linear layer.
+__global__ __launch_bounds__(256) void residual_add_kernel(float *__restrict__ h,
+                                                           const float *__restrict__ x, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) h[i] += x[i];
+}
+
+hipError_t residual_add_launch(float *h, const float *x, int n, hipStream_t stream) {
+    residual_add_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(h, x, n);
+    return hipGetLastError();
+}
+
+// h[i] *= s (kernels/transformer_ops.hip:21-30).
+__global__ __launch_bounds__(256) void scale_kernel(float *__restrict__ h, float s, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) h[i] *= s;
+}
+
+hipError_t scale_launch(float *h, float s, int n, hipStream_t stream) {
+    scale_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(h, s, n);
+    return hipGetLastError();
+}
+
 }  // namespace mgq

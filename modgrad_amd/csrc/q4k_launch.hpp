@@ -102,6 +102,9 @@ hipError_t rms_norm_launch(const float *x, const float *w, float *y, int rows, i
                            float eps, hipStream_t stream);
 hipError_t glu_launch(const float *gate, const float *up, float *out, int n, int act,
                       hipStream_t stream);
+// h += x and h *= s, elementwise over n.
+hipError_t residual_add_launch(float *h, const float *x, int n, hipStream_t stream);
+hipError_t scale_launch(float *h, float s, int n, hipStream_t stream);
 
 hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n, int bpr,
                            int m_tokens, hipStream_t stream);

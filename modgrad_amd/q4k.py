@@ -4,11 +4,14 @@ Names, argument meaning and error behaviour follow the reference's Rust host
 (crates/modgrad-device/src/backend/rocm.rs, ops.rs and
 crates/modgrad-compute/src/neuron.rs), so tests read like the reference's:
 
+  BackendError        backend/mod.rs:107-123
   HipBuffer           rocm.rs:603-935  (RAII device buffer; here a torch
                                         uint8 CUDA tensor holds the memory)
   HipBuffer.matvec_q4k / matvec_q4k_into   rocm.rs:681-738
-  kern.matvec_q4k, kern.hip_sync           rocm.rs:942-963
+  HipBuffer.matvec_q5k / matvec_q5k_into   rocm.rs:743-776
+  kern.*                                   rocm.rs:943-996
   ops.dequant_q4k_resident                 ops.rs:531-539
+  GpuVec, ResidencyError                   compute/src/backend.rs:35-278
   LinearResidentQuantized                  neuron.rs:897-1108
 
 PyTorch is only the device-memory allocator here; every computation goes
@@ -57,8 +60,14 @@ class HipBuffer:
 
     def __init__(self, nbytes: int):
         torch = _torch()
+        if nbytes < 0:
+            raise BackendError("Runtime", f"hipMalloc({nbytes}): negative size")
         # round up to 16 B so 128-bit loads of the tail stay in the allocation
-        self._t = torch.empty(max(16, (nbytes + 15) // 16 * 16), dtype=torch.uint8, device="cuda")
+        try:
+            self._t = torch.empty(max(16, (nbytes + 15) // 16 * 16), dtype=torch.uint8,
+                                  device="cuda")
+        except torch.cuda.OutOfMemoryError as e:
+            raise BackendError("OutOfMemory", f"hipMalloc({nbytes})") from e
         self._bytes = nbytes
 
     @classmethod
@@ -86,6 +95,12 @@ class HipBuffer:
     def f32_at(self, index: int) -> int:
         return self.u8_at(4 * index)
 
+    def f32_ptr(self) -> int:
+        return self.device_ptr()
+
+    def u8_ptr(self) -> int:
+        return self.device_ptr()
+
     def copy_from_host_bytes(self, src) -> None:
         torch = _torch()
         a = np.frombuffer(bytes(src), dtype=np.uint8) if not isinstance(src, np.ndarray) else src
@@ -94,16 +109,49 @@ class HipBuffer:
             raise BackendError("Runtime", f"copy_from_host_bytes: src {a.size} > buf {self._bytes}")
         self._t[: a.size].copy_(torch.from_numpy(a))
 
+    def copy_from_host_bytes_at(self, off: int, src) -> None:
+        """Stage host bytes at a byte offset, for packing many tensors into
+        one allocation (rocm.rs:917-934)."""
+        torch = _torch()
+        a = np.frombuffer(bytes(src), dtype=np.uint8) if not isinstance(src, np.ndarray) else src
+        a = np.ascontiguousarray(a, dtype=np.uint8).ravel()
+        if off < 0 or off + a.size > self._bytes:
+            raise BackendError("Runtime", f"copy_from_host_bytes_at: off {off} + {a.size} > "
+                                          f"buf {self._bytes}")
+        self._t[off: off + a.size].copy_(torch.from_numpy(a))
+
     def copy_from_host(self, src) -> None:
         a = np.ascontiguousarray(src, dtype=np.float32).ravel()
         if a.nbytes > self._bytes:
-            raise BackendError("Runtime", f"copy_from_host: src {a.nbytes} > buf {self._bytes}")
+            raise BackendError("Runtime", f"upload_f32: src is {a.nbytes} bytes, device buffer "
+                                          f"is {self._bytes} bytes")
         self.copy_from_host_bytes(a.view(np.uint8))
 
     def copy_to_host(self, n_f32: int | None = None) -> np.ndarray:
-        _torch().cuda.synchronize()
+        """The first `n_f32` floats (all of them by default); asking for more
+        than the buffer holds is an error (rocm.rs:779-781, 873-895)."""
         n = self.len_f32() if n_f32 is None else n_f32
+        if n < 0 or 4 * n > self._bytes:
+            raise BackendError("Runtime", f"download_f32: dst is {4 * n} bytes, device buffer "
+                                          f"is {self._bytes} bytes")
+        _torch().cuda.synchronize()
         return self._t[: 4 * n].cpu().numpy().view(np.float32).copy()
+
+    def copy_range_from(self, src: "HipBuffer", src_offset_f32: int, dst_offset_f32: int,
+                        len_f32: int) -> None:
+        """Device-to-device copy of `len_f32` floats from `src` at
+        `src_offset_f32` into this buffer at `dst_offset_f32`, both ranges
+        bounds-checked (rocm.rs:791-837)."""
+        if min(src_offset_f32, dst_offset_f32, len_f32) < 0:
+            raise BackendError("Runtime", "copy_range_from: negative offset or length")
+        nb, so, do = 4 * len_f32, 4 * src_offset_f32, 4 * dst_offset_f32
+        if so + nb > src._bytes:
+            raise BackendError("Runtime", f"copy_range_from: src range [{so},{so + nb}) bytes "
+                                          f"exceeds src buffer ({src._bytes} bytes)")
+        if do + nb > self._bytes:
+            raise BackendError("Runtime", f"copy_range_from: dst range [{do},{do + nb}) bytes "
+                                          f"exceeds dst buffer ({self._bytes} bytes)")
+        self._t[do: do + nb].copy_(src._t[so: so + nb])
 
     def matvec_q4k(self, x, out_dim: int, blocks_per_row: int) -> np.ndarray:
         """y = dequant(self) @ x with host x in and host y out (rocm.rs:681-709)."""
@@ -121,6 +169,22 @@ class HipBuffer:
                         blocks_per_row)
         kern.hip_sync()
 
+    def matvec_q5k(self, x, out_dim: int, blocks_per_row: int) -> np.ndarray:
+        """Q5_K twin of matvec_q4k (rocm.rs:743-761)."""
+        in_dim = blocks_per_row * Q4K_BLOCK_ELEMS
+        x_dev = HipBuffer(in_dim * 4)
+        x_dev.copy_from_host(np.asarray(x, np.float32)[:in_dim])
+        y_dev = HipBuffer(out_dim * 4)
+        self.matvec_q5k_into(x_dev, y_dev, out_dim, blocks_per_row)
+        return y_dev.copy_to_host(out_dim)
+
+    def matvec_q5k_into(self, x_dev: "HipBuffer", y_dev: "HipBuffer", out_dim: int,
+                        blocks_per_row: int) -> None:
+        """Q5_K twin of matvec_q4k_into (rocm.rs:765-776)."""
+        kern.matvec_q5k(self.device_ptr(), x_dev.device_ptr(), y_dev.device_ptr(), out_dim,
+                        blocks_per_row)
+        kern.hip_sync()
+
 
 class kern:
     """Launch-only wrappers, null stream, no sync (rocm.rs:942-979)."""
@@ -128,6 +192,21 @@ class kern:
     @staticmethod
     def hip_sync() -> None:
         _torch().cuda.synchronize()
+
+    @staticmethod
+    def vram_free_total() -> tuple[int, int]:
+        """(free, total) device memory in bytes (rocm.rs:956-961)."""
+        return tuple(int(v) for v in _torch().cuda.mem_get_info())
+
+    @staticmethod
+    def residual_add(h: int, x: int, n: int, stream=None) -> None:
+        """rocm.rs:984-986: h += x over n floats."""
+        _chk(_lib.load().launch_residual_add_ex(h, x, n, _stream_ptr(stream)), "residual_add")
+
+    @staticmethod
+    def scale(h: int, s: float, n: int, stream=None) -> None:
+        """rocm.rs:987-989: h *= s over n floats."""
+        _chk(_lib.load().launch_scale_ex(h, s, n, _stream_ptr(stream)), "scale")
 
     @staticmethod
     def matvec_q4k(w: int, x: int, y: int, out_dim: int, bpr: int) -> None:
@@ -290,6 +369,116 @@ class Chain:
             pass
 
 
+class ResidencyError(Exception):
+    """Error of a device-resident dispatch (compute/src/backend.rs:244-278):
+    either a wrapped BackendError (`backend`) or a GpuVec of the wrong
+    residency variant handed to a Hip-only entry point (`expected`, `got`)."""
+
+    def __init__(self, backend: BackendError | None = None, expected: str | None = None,
+                 got: str | None = None):
+        self.backend, self.expected, self.got = backend, expected, got
+        if backend is not None:
+            super().__init__(str(backend))
+        else:
+            super().__init__(f"wrong GpuVec variant: expected {expected}, got {got}")
+
+    @classmethod
+    def wrong_variant(cls, expected: str, got: str) -> "ResidencyError":
+        return cls(expected=expected, got=got)
+
+
+class GpuVec:
+    """An f32 vector on the host heap or resident on the device
+    (compute/src/backend.rs:35-205).
+
+    Variants are "Heap" (a numpy array) and "Hip" (a HipBuffer). The
+    reference's third variant, "Vram", is its gfx1102 KFD arena mapped
+    through the PCIe BAR; this build has no such arena, so try_vram takes
+    the reference's own fallback and returns a Heap vector.
+    """
+
+    def __init__(self, heap: np.ndarray | None = None, hip: HipBuffer | None = None):
+        if (heap is None) == (hip is None):
+            raise ValueError("GpuVec holds exactly one of a heap array or a HipBuffer")
+        self._heap = None if heap is None else np.ascontiguousarray(heap, np.float32).ravel()
+        self._hip = hip
+
+    @classmethod
+    def heap(cls, n: int) -> "GpuVec":
+        return cls(heap=np.zeros(n, np.float32))
+
+    @classmethod
+    def from_host(cls, v) -> "GpuVec":
+        """From<Vec<f32>>: a Heap vector."""
+        return cls(heap=np.array(v, np.float32, copy=True).ravel())
+
+    @classmethod
+    def try_vram(cls, n: int) -> "GpuVec":
+        return cls.heap(n)
+
+    @classmethod
+    def try_hip(cls, n: int) -> "GpuVec":
+        """A device-resident vector of n floats; allocation failure raises
+        ResidencyError wrapping the BackendError."""
+        try:
+            return cls(hip=HipBuffer.new(4 * n))
+        except BackendError as e:
+            raise ResidencyError(backend=e) from e
+
+    def variant_name(self) -> str:
+        return "Heap" if self._hip is None else "Hip"
+
+    def hip_buffer(self) -> HipBuffer:
+        """The HipBuffer of a Hip vector; WrongVariant otherwise."""
+        if self._hip is None:
+            raise ResidencyError.wrong_variant("Hip", self.variant_name())
+        return self._hip
+
+    def __len__(self) -> int:
+        return self._heap.size if self._hip is None else self._hip.len_f32()
+
+    def len(self) -> int:
+        return len(self)
+
+    def is_host_visible(self) -> bool:
+        return self._hip is None
+
+    def copy_from(self, src) -> None:
+        """Copy a host slice into the front of this vector (an explicit
+        host-to-device copy for Hip)."""
+        a = np.ascontiguousarray(src, np.float32).ravel()
+        if self._hip is None:
+            if a.size > self._heap.size:
+                raise ValueError(f"copy_from: src {a.size} > len {self._heap.size}")
+            self._heap[: a.size] = a
+        else:
+            self._hip.copy_from_host(a)
+
+    def as_slice(self) -> np.ndarray:
+        """The host array of a Heap vector. A Hip vector is not host-visible
+        and raises, as the reference panics (backend.rs:139-151)."""
+        if self._hip is not None:
+            raise ResidencyError.wrong_variant("Heap or Vram", "Hip")
+        return self._heap
+
+    def copy_to_host(self) -> np.ndarray:
+        """A host copy of the contents (a device-to-host copy for Hip)."""
+        return self._heap.copy() if self._hip is None else self._hip.copy_to_host()
+
+    def clone(self) -> "GpuVec":
+        """Always a Heap vector; a Hip vector is downloaded first
+        (backend.rs:45-61)."""
+        return GpuVec(heap=self.copy_to_host())
+
+
+def _hip_of(v, what: str) -> HipBuffer:
+    if isinstance(v, HipBuffer):
+        return v
+    if isinstance(v, GpuVec):
+        return v.hip_buffer()
+    raise ResidencyError.wrong_variant("Hip", f"{type(v).__name__} ({what})")
+
+
 class LinearResidentQuantized:
     """Q4_K-quantised resident linear layer (neuron.rs:897-1108).
 
@@ -316,9 +505,14 @@ class LinearResidentQuantized:
         """Wrap already-quantized bytes (the reference's from_linear quantizes on
         the host with quantize_row_q4_k, gguf.rs:581-663, neuron.rs:931-951)."""
         if (in_dim * out_dim) % Q4K_BLOCK_ELEMS:
-            raise BackendError("WrongVariant", "weight len not aligned to Q4_K block")
+            raise ResidencyError.wrong_variant("weight len multiple of 256",
+                                               "weight len not aligned to Q4_K block")
         if np.asarray(q4k_bytes).size != in_dim * out_dim // 256 * Q4K_BLOCK_BYTES:
-            raise BackendError("WrongVariant", "q4k byte count does not match dims")
+            raise ResidencyError.wrong_variant("q4k bytes of (in_dim*out_dim/256)*144",
+                                               "q4k byte count does not match dims")
+        if np.asarray(bias).size != out_dim:
+            raise ResidencyError.wrong_variant("bias of out_dim floats",
+                                               f"bias of {np.asarray(bias).size}")
         return cls(q4k_bytes, bias, in_dim, out_dim)
 
     def in_dim(self) -> int:
@@ -352,14 +546,16 @@ class LinearResidentQuantized:
     def evict(self) -> None:
         self.weight_q4k_dev = self.weight_dev = self.bias_dev = None
 
-    def forward(self, x_dev: HipBuffer, out_dev: HipBuffer, auto_evict: bool = False,
-                stream=None) -> None:
-        """out = W x + b, W the canonical dequant of the resident Q4_K bytes."""
+    def forward(self, x_dev, out_dev, auto_evict: bool = False, stream=None) -> None:
+        """out = W x + b, W the canonical dequant of the resident Q4_K bytes
+        (neuron.rs:1059-1108). x_dev and out_dev are HipBuffers or Hip
+        GpuVecs; a Heap GpuVec raises ResidencyError WrongVariant, as in the
+        reference. The bias is added after the product, one rounding, as
+        hipblasSgemv's beta = 1 on a bias-filled y does (rocm.rs:2000-2056)."""
+        x_buf, out_buf = _hip_of(x_dev, "x"), _hip_of(out_dev, "out")
         self.ensure_resident()
-        kern.matvec_q4k_ex(self.weight_q4k_dev.device_ptr(), x_dev.device_ptr(),
-                           out_dev.device_ptr(), self._out, self._in, _lib.LAYOUT_FLAT, stream)
-        torch = _torch()
-        y = out_dev.tensor()[: 4 * self._out].view(torch.float32)
-        y.add_(self.bias_dev.tensor()[: 4 * self._out].view(torch.float32))
+        kern.matvec_q4k_ex(self.weight_q4k_dev.device_ptr(), x_buf.device_ptr(),
+                           out_buf.device_ptr(), self._out, self._in, _lib.LAYOUT_FLAT, stream)
+        kern.residual_add(out_buf.device_ptr(), self.bias_dev.device_ptr(), self._out, stream)
         if auto_evict:
             self.evict()

@@ -116,12 +116,42 @@ def test_chain_rejects_bad_descs(L):
 
 
 def test_host_api_rejects_misshaped_weights():
+    # neuron.rs:933-938: a weight that is not a whole number of Q4_K blocks is
+    # ResidencyError::WrongVariant
     import numpy as np
-    from modgrad_amd.q4k import BackendError, LinearResidentQuantized
-    with pytest.raises(BackendError):
+    from modgrad_amd.q4k import LinearResidentQuantized, ResidencyError
+    with pytest.raises(ResidencyError) as e:
         LinearResidentQuantized.from_q4k(np.zeros(144, np.uint8), np.zeros(3), 100, 3)
-    with pytest.raises(BackendError):
+    assert e.value.backend is None and e.value.got == "weight len not aligned to Q4_K block"
+    with pytest.raises(ResidencyError):
         LinearResidentQuantized.from_q4k(np.zeros(100, np.uint8), np.zeros(4), 64, 4)
+    with pytest.raises(ResidencyError):
+        LinearResidentQuantized.from_q4k(np.zeros(144, np.uint8), np.zeros(3), 64, 4)
+
+
+def test_gpuvec_heap_variant():
+    # backend.rs:35-205: the Heap variant is host-visible, clones to Heap, and
+    # a Hip-only entry point rejects it with WrongVariant
+    import numpy as np
+    from modgrad_amd.q4k import GpuVec, LinearResidentQuantized, ResidencyError
+    v = GpuVec.heap(8)
+    assert v.variant_name() == "Heap" and len(v) == 8 and v.is_host_visible()
+    v.copy_from([1.0, 2.0, 3.0])
+    assert v.as_slice()[:4].tolist() == [1.0, 2.0, 3.0, 0.0]
+    c = v.clone()
+    c.as_slice()[0] = 9.0
+    assert v.as_slice()[0] == 1.0 and c.variant_name() == "Heap"
+    assert GpuVec.try_vram(4).variant_name() == "Heap"  # no KFD BAR arena here
+    assert GpuVec.from_host([5.0, 6.0]).copy_to_host().tolist() == [5.0, 6.0]
+    with pytest.raises(ResidencyError) as e:
+        v.hip_buffer()
+    assert (e.value.expected, e.value.got) == ("Hip", "Heap")
+    assert str(e.value) == "wrong GpuVec variant: expected Hip, got Heap"
+    lin = LinearResidentQuantized.from_q4k(np.zeros(144, np.uint8), np.zeros(1, np.float32),
+                                           256, 1)
+    with pytest.raises(ResidencyError):
+        lin.forward(GpuVec.heap(256), GpuVec.heap(1))
+    assert not lin.is_resident()  # the variant check comes before any allocation
 
 
 def test_host_size_savings():
@@ -142,6 +172,11 @@ def test_glue_rejects_bad_args(L):
     assert L.launch_geglu(FAKE, FAKE, FAKE, 0) == INVALID
     assert L.launch_geglu(FAKE, None, FAKE, 16) == INVALID
     assert L.launch_glu_ex(FAKE, FAKE, FAKE, 16, 2, None) == INVALID  # unknown activation
+    assert L.launch_residual_add(FAKE, FAKE, 0) == INVALID
+    assert L.launch_residual_add(None, FAKE, 16) == INVALID
+    assert L.launch_residual_add_ex(FAKE, None, 16, None) == INVALID
+    assert L.launch_scale(FAKE, 2.0, -1) == INVALID
+    assert L.launch_scale_ex(None, 2.0, 16, None) == INVALID
 
 
 def test_fused_matvecs_reject_bad_args(L):

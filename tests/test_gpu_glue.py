@@ -60,6 +60,31 @@ def test_glu_matches_oracle(L, orc, n, act):
     assert np.all(np.abs(out.astype(np.float64) - ref) <= 2e-6 * np.abs(g * u) + 1e-30)
 
 
+@pytest.mark.parametrize("n", [3584, 1, 257, 18944])
+def test_residual_add_and_scale_are_exact(L, n):
+    # transformer_ops.hip:10-30: h += x and h *= s are single IEEE f32
+    # operations per element, so the result is the correctly rounded one that
+    # numpy's float32 arithmetic gives, bit for bit, specials included
+    note(f"residual_add / scale n={n}")
+    rng = np.random.default_rng(n)
+    h = (rng.standard_normal(n) * 10).astype(np.float32)
+    x = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+    if n >= 4:
+        h[:4] = [np.inf, -0.0, 3.0e38, np.nan]
+        x[:4] = [1.0, 0.0, 3.0e38, 1.0]
+    ht, xt = dev(h), dev(x)
+    _lib.check("launch_residual_add", L.launch_residual_add(ptr(ht), ptr(xt), n))
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = h + x
+    got = host(ht)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    s = np.float32(0.7071068)
+    _lib.check("launch_scale_ex", L.launch_scale_ex(ptr(ht), float(s), n, None))
+    with np.errstate(invalid="ignore"):
+        ref_s = ref * s
+    assert np.array_equal(host(ht).view(np.uint32), ref_s.view(np.uint32))
+
+
 def _weights(orc, seed, n, bpr):
     return orc.seeded_weight(seed, n, bpr * 256)
 

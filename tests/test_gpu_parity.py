@@ -343,6 +343,72 @@ def test_linear_resident_quantized_forward_and_evict(L, orc):
     assert np.array_equal(lin.weight_dev.copy_to_host().view(np.uint32), first.view(np.uint32))
 
 
+def test_linear_forward_takes_hip_gpuvecs(L, orc):
+    # neuron.rs:1059-1108 with GpuVec::Hip operands: out = fl(W x + b), the bias
+    # added after the product in one rounding, as hipblasSgemv's beta = 1 on a
+    # bias-filled y (rocm.rs:2000-2056)
+    note("LinearResidentQuantized.forward on Hip GpuVecs 1024->512")
+    from modgrad_amd import _lib as lib
+    from modgrad_amd.q4k import GpuVec, HipBuffer, LinearResidentQuantized, kern
+    in_dim, out_dim = 1024, 512
+    w = orc.seeded_weight(0xB1A5, out_dim, in_dim)
+    bias = orc.normal(0xB1A6, out_dim, 0.3)
+    lin = LinearResidentQuantized.from_q4k(w, bias, in_dim, out_dim)
+    xv, yv = GpuVec.try_hip(in_dim), GpuVec.try_hip(out_dim)
+    assert xv.variant_name() == "Hip" and not xv.is_host_visible() and len(yv) == out_dim
+    x = orc.normal(0xB1A7, in_dim)
+    xv.copy_from(x)
+    lin.forward(xv, yv)
+    y = yv.copy_to_host()
+    plain = HipBuffer(out_dim * 4)
+    kern.matvec_q4k_ex(lin.weight_q4k_dev.device_ptr(), xv.hip_buffer().device_ptr(),
+                       plain.device_ptr(), out_dim, in_dim, lib.LAYOUT_FLAT)
+    y0 = plain.copy_to_host()
+    assert np.array_equal(y.view(np.uint32), (y0 + bias).view(np.uint32))
+    y_ref, a = orc.gemv_flat(w, x, out_dim, in_dim)
+    assert_gemv_close(y0, y_ref, a + 1e-30)
+    assert yv.clone().variant_name() == "Heap"
+    with pytest.raises(Exception):
+        yv.as_slice()  # Hip memory is not host-visible (backend.rs:139-151)
+
+
+def test_hipbuffer_range_copies_and_q5k(L, orc):
+    # rocm.rs:791-837 copy_range_from, rocm.rs:917-934 copy_from_host_bytes_at,
+    # rocm.rs:743-776 matvec_q5k / matvec_q5k_into
+    note("HipBuffer copy_range_from / copy_from_host_bytes_at / matvec_q5k")
+    from modgrad_amd.q4k import BackendError, HipBuffer, kern
+    a = HipBuffer(64 * 4)
+    a.copy_from_host(np.arange(64, dtype=np.float32))
+    b = HipBuffer(32 * 4)
+    b.copy_from_host(np.full(32, -1.0, np.float32))
+    b.copy_range_from(a, 10, 4, 20)
+    got = b.copy_to_host()
+    assert got[:4].tolist() == [-1.0] * 4 and got[24:].tolist() == [-1.0] * 8
+    assert got[4:24].tolist() == list(range(10, 30))
+    with pytest.raises(BackendError):
+        b.copy_range_from(a, 50, 0, 20)   # past the end of src
+    with pytest.raises(BackendError):
+        b.copy_range_from(a, 0, 20, 20)   # past the end of dst
+    with pytest.raises(BackendError):
+        b.copy_to_host(33)
+    arena = HipBuffer(256)
+    arena.copy_from_host_bytes_at(100, np.arange(50, dtype=np.uint8))
+    assert np.array_equal(arena.tensor()[100:150].cpu().numpy(), np.arange(50, dtype=np.uint8))
+    with pytest.raises(BackendError):
+        arena.copy_from_host_bytes_at(250, np.zeros(7, np.uint8))
+    free, total = kern.vram_free_total()
+    assert 0 < free <= total
+    from tests.gpu_util import random_kquant_bytes
+    n, bpr = 96, 3
+    w5 = random_kquant_bytes(np.random.default_rng(0x55), n * bpr, 176)
+    wb = HipBuffer(w5.size)
+    wb.copy_from_host_bytes(w5)
+    x = orc.normal(0x56, bpr * 256)
+    y = wb.matvec_q5k(x, n, bpr)
+    y_ref, aa = orc.gemv_kquant(176, w5, x, n, bpr)
+    assert_gemv_close(y, y_ref, aa)
+
+
 def test_hipbuffer_matvec_q4k_host_roundtrip(L, orc):
     # rocm.rs:681-709 path (host x in, host y out)
     note("HipBuffer.matvec_q4k")
