@@ -143,6 +143,29 @@ struct GemvFuse {
     int act;            // kActGeluTanh or kActSilu
 };
 
+// Row-group schedule of a persistent launch (G = gridDim.x work-groups). In
+// rounds j < shared every work-group b takes group b + j*G; the groups past
+// shared*G go to the `lead` lowest-numbered work-groups only, strided by lead.
+// {lead = G, shared = 0} is the plain strided schedule. With two work-groups
+// per CU the hardware dispatches the lower-numbered one of each pair first and
+// issues its waves first, so it streams faster; giving those `lead` = #CUs
+// work-groups the extra rounds lets both members of a pair finish together.
+struct GemvSched {
+    int lead, shared;
+};
+
+__device__ __forceinline__ int sched_group(const GemvSched &s, int b, int G, int j) {
+    return j < s.shared ? b + j * G : s.shared * G + (j - s.shared) * s.lead + b;
+}
+
+// groups work-group b takes out of `groups`
+__host__ __device__ inline int sched_count(const GemvSched &s, int b, int G, int groups) {
+    if (b >= groups) return 0;
+    const int own = std::min(s.shared, (groups - b - 1) / G + 1);
+    const int rest = groups - s.shared * G;
+    return own + ((b < s.lead && rest > b) ? (rest - b - 1) / s.lead + 1 : 0);
+}
+
 // rounds = row groups per work-group (persistent launch); their results stay
 // in LDS (ybuf) until the stream ends, so no global store sits between the
 // staged loads (a store would force the compiler to drain every load).
@@ -204,7 +227,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
                                                             const float *__restrict__ xdv,
                                                             const float *__restrict__ xsv,
                                                             float *__restrict__ y, int n,
-                                                            int bpr, int rounds, GemvFuse fz) {
+                                                            int bpr, int rounds, GemvFuse fz,
+                                                            GemvSched sch) {
     static_assert(Q8 ? (FUSE == 0 || FUSE == kFuseQuant) : (FUSE & kFuseQuant) == 0,
                   "fused glue runs on f32 activations; quantization only in Q8 mode");
     static_assert(!(FUSE & kFmtQ5K) || FUSE == kFmtQ5K, "Q5_K weights: plain f32 matvec only");
@@ -222,7 +246,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     const size_t row_bytes = (size_t)bpr * BB;
     const int stages = (bpr + C - 1) / C;
     const int groups = (n + R - 1) / R;
-    const int my_groups = (groups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int my_groups = sched_count(sch, (int)blockIdx.x, (int)gridDim.x, groups);
     const int Q = my_groups * VM * stages;        // stages this work-group streams
     constexpr int PIECES = R * BP * C;            // 16-byte pieces per stage
     constexpr int IPW = ((PIECES + 63) / 64 + NW - 1) / NW;  // wave loads per wavefront
@@ -252,7 +276,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     auto gload = [&](int q, u32x4(&dst)[IPW]) {
         q = std::min(q, Q - 1);
         const int vg = q / stages;  // pass index: row group vg / VM, matrix vg % VM
-        const uint32_t r0 = ((uint32_t)blockIdx.x + (uint32_t)(vg / VM) * gridDim.x) * R;
+        const uint32_t r0 =
+            (uint32_t)sched_group(sch, (int)blockIdx.x, (int)gridDim.x, vg / VM) * R;
         const uint8_t *wm = (VM == 2 && (vg & 1)) ? fz.w2 : w;
         const uint32_t tcol = (uint32_t)((q % stages) * C * BB);
         const uint32_t rlast = (uint32_t)(n - 1), rb = (uint32_t)row_bytes;
@@ -662,7 +687,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     }
     const float *yb = reinterpret_cast<const float *>(lds + Lo.ybuf);
     for (int i = tid; i < my_groups * R; i += NW * 64) {
-        const int r = ((int)blockIdx.x + (i / R) * (int)gridDim.x) * R + (i % R);
+        const int r = sched_group(sch, (int)blockIdx.x, (int)gridDim.x, i / R) * R + (i % R);
         if (r < n) {
             if constexpr (VM == 2) {
                 // pass 2j = gate rows of group j, 2j+1 = up rows
@@ -676,6 +701,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         }
     }
 }
+
+// Share of the row groups, in percent of the average, that the
+// second-dispatched work-group of each CU pair takes in a persistent launch
+// (GemvSched); 0 keeps the plain strided schedule.
+constexpr int kGemvSkew = 70;
 
 static int env_int(const char *name, int dflt) {
     const char *s = std::getenv(name);
@@ -717,22 +747,35 @@ static hipError_t launch_xit(const uint8_t *w, const GemvAct &a, const GemvFuse 
     if (attr != hipSuccess) return attr;
     const long groups = (n + R - 1) / R;
     long grid = groups, rounds = 1;
+    GemvSched sch{(int)groups, 0};
     if (persistent) {
         static const int occ_env = env_int("MGQ_GEMV_OCC", 0);
+        static const int skew = std::min(100, env_int("MGQ_GEMV_SKEW", kGemvSkew));
         const size_t base = mfma_layout(bpr, R, C, NW, 8, DB, Q8, FUSE).total;
         int occ = 0;  // resident work-groups per CU (registers and LDS)
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)kern, NW * 64,
                                                          base) != hipSuccess || occ <= 0)
             occ = (int)std::min<size_t>(4, (160 * 1024) / base);
         if (occ_env > 0) occ = occ_env;
-        const long maxgrid = (long)device_cus() * std::max(1, occ);
+        const long cus = device_cus();
+        const long maxgrid = cus * std::max(1, occ);
         rounds = (groups + maxgrid - 1) / maxgrid;
         grid = (groups + rounds - 1) / rounds;  // balanced: every WG gets `rounds` groups (or one fewer)
+        sch = GemvSched{(int)grid, 0};
+        if (skew > 0 && occ == 2 && groups >= 2 * maxgrid) {
+            // pairs per CU: the second-dispatched work-group of each pair
+            // (ids >= cus) takes `skew` percent of the average share
+            grid = maxgrid;
+            const long shared = groups * skew / (100 * grid);
+            const long rest = groups - shared * grid;
+            sch = GemvSched{(int)cus, (int)shared};
+            rounds = shared + (rest + cus - 1) / cus;
+        }
     }
     const MfmaLayout Lo = mfma_layout(bpr, R, C, NW, (int)rounds, DB, Q8, FUSE);
     if (Lo.total > 160 * 1024) return hipErrorNotSupported;
     kern<<<(unsigned)grid, NW * 64, Lo.total, stream>>>(w, a.x, a.xq, a.xd, a.xsum, y, n, bpr,
-                                                        (int)rounds, fz);
+                                                        (int)rounds, fz, sch);
     return hipGetLastError();
 }
 
