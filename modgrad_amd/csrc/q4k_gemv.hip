@@ -143,29 +143,6 @@ struct GemvFuse {
     int act;            // kActGeluTanh or kActSilu
 };
 
-// Row-group schedule of a persistent launch (G = gridDim.x work-groups). In
-// rounds j < shared every work-group b takes group b + j*G; the groups past
-// shared*G go to the `lead` lowest-numbered work-groups only, strided by lead.
-// {lead = G, shared = 0} is the plain strided schedule. With two work-groups
-// per CU the hardware dispatches the lower-numbered one of each pair first and
-// issues its waves first, so it streams faster; giving those `lead` = #CUs
-// work-groups the extra rounds lets both members of a pair finish together.
-struct GemvSched {
-    int lead, shared;
-};
-
-__device__ __forceinline__ int sched_group(const GemvSched &s, int b, int G, int j) {
-    return j < s.shared ? b + j * G : s.shared * G + (j - s.shared) * s.lead + b;
-}
-
-// groups work-group b takes out of `groups`
-__host__ __device__ inline int sched_count(const GemvSched &s, int b, int G, int groups) {
-    if (b >= groups) return 0;
-    const int own = std::min(s.shared, (groups - b - 1) / G + 1);
-    const int rest = groups - s.shared * G;
-    return own + ((b < s.lead && rest > b) ? (rest - b - 1) / s.lead + 1 : 0);
-}
-
 // rounds = row groups per work-group (persistent launch); their results stay
 // in LDS (ybuf) until the stream ends, so no global store sits between the
 // staged loads (a store would force the compiler to drain every load).
@@ -702,11 +679,6 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     }
 }
 
-// Share of the row groups, in percent of the average, that the
-// second-dispatched work-group of each CU pair takes in a persistent launch
-// (GemvSched); 0 keeps the plain strided schedule.
-constexpr int kGemvSkew = 70;
-
 static int env_int(const char *name, int dflt) {
     const char *s = std::getenv(name);
     return (s && *s) ? std::atoi(s) : dflt;
@@ -750,27 +722,16 @@ static hipError_t launch_xit(const uint8_t *w, const GemvAct &a, const GemvFuse 
     GemvSched sch{(int)groups, 0};
     if (persistent) {
         static const int occ_env = env_int("MGQ_GEMV_OCC", 0);
-        static const int skew = std::min(100, env_int("MGQ_GEMV_SKEW", kGemvSkew));
         const size_t base = mfma_layout(bpr, R, C, NW, 8, DB, Q8, FUSE).total;
         int occ = 0;  // resident work-groups per CU (registers and LDS)
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)kern, NW * 64,
                                                          base) != hipSuccess || occ <= 0)
             occ = (int)std::min<size_t>(4, (160 * 1024) / base);
         if (occ_env > 0) occ = occ_env;
-        const long cus = device_cus();
-        const long maxgrid = cus * std::max(1, occ);
-        rounds = (groups + maxgrid - 1) / maxgrid;
-        grid = (groups + rounds - 1) / rounds;  // balanced: every WG gets `rounds` groups (or one fewer)
-        sch = GemvSched{(int)grid, 0};
-        if (skew > 0 && occ == 2 && groups >= 2 * maxgrid) {
-            // pairs per CU: the second-dispatched work-group of each pair
-            // (ids >= cus) takes `skew` percent of the average share
-            grid = maxgrid;
-            const long shared = groups * skew / (100 * grid);
-            const long rest = groups - shared * grid;
-            sch = GemvSched{(int)cus, (int)shared};
-            rounds = shared + (rest + cus - 1) / cus;
-        }
+        const PersistPlan p = persistent_plan(groups, occ);
+        grid = p.grid;
+        rounds = p.rounds;
+        sch = p.sch;
     }
     const MfmaLayout Lo = mfma_layout(bpr, R, C, NW, (int)rounds, DB, Q8, FUSE);
     if (Lo.total > 160 * 1024) return hipErrorNotSupported;

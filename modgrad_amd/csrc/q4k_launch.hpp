@@ -4,6 +4,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+#include <cstdlib>
+
 namespace mgq {
 
 // Compute units of the current device, cached per device (the persistent
@@ -19,6 +22,72 @@ inline int device_cus() {
         cus[dev] = v;
     }
     return cus[dev];
+}
+
+// Row-group schedule of a persistent launch (G = gridDim.x work-groups). In
+// rounds j < shared every work-group b takes group b + j*G; the groups past
+// shared*G go to the `lead` lowest-numbered work-groups only, strided by lead.
+// {lead = G, shared = 0} is the plain strided schedule. With two work-groups
+// per CU the hardware dispatches the lower-numbered one of each pair first and
+// issues its waves first, so it streams faster; giving those `lead` = #CUs
+// work-groups the extra rounds lets both members of a pair finish together.
+struct GemvSched {
+    int lead, shared;
+};
+
+__device__ __forceinline__ int sched_group(const GemvSched &s, int b, int G, int j) {
+    return j < s.shared ? b + j * G : s.shared * G + (j - s.shared) * s.lead + b;
+}
+
+// groups work-group b takes out of `groups`
+__host__ __device__ inline int sched_count(const GemvSched &s, int b, int G, int groups) {
+    if (b >= groups) return 0;
+    const int own = std::min(s.shared, (groups - b - 1) / G + 1);
+    const int rest = groups - s.shared * G;
+    return own + ((b < s.lead && rest > b) ? (rest - b - 1) / s.lead + 1 : 0);
+}
+
+// Share of the row groups, in percent of the average, that the
+// second-dispatched work-group of each CU pair takes in a persistent launch
+// (MGQ_GEMV_SKEW overrides; 0 keeps the plain strided schedule).
+constexpr int kGemvSkew = 70;
+
+inline int gemv_skew() {
+    static const int v = [] {
+        const char *s = std::getenv("MGQ_GEMV_SKEW");
+        return std::max(0, std::min(100, (s && *s) ? std::atoi(s) : kGemvSkew));
+    }();
+    return v;
+}
+
+// Grid, per-work-group rounds (the LDS result buffer is sized for them) and
+// schedule of a persistent launch of `groups` row groups at `occ` resident
+// work-groups per CU. Balanced by default: every work-group gets `rounds`
+// groups or one fewer. With two per CU and at least two full rounds of
+// pairs, the grid is exactly 2 x #CUs and the younger member of each pair
+// (ids >= #CUs) takes gemv_skew() percent of the average share.
+struct PersistPlan {
+    long grid, rounds;
+    GemvSched sch;
+};
+
+inline PersistPlan persistent_plan(long groups, int occ) {
+    const long cus = device_cus();
+    const long maxgrid = cus * std::max(1, occ);
+    PersistPlan p;
+    p.rounds = (groups + maxgrid - 1) / maxgrid;
+    p.grid = (groups + p.rounds - 1) / p.rounds;
+    p.sch = GemvSched{(int)p.grid, 0};
+    const int skew = gemv_skew();
+    if (skew > 0 && occ == 2 && groups >= 2 * maxgrid) {
+        // at least one round each: the kernels assume every work-group owns a group
+        const long shared = std::max(1L, groups * skew / (100 * maxgrid));
+        const long rest = groups - shared * maxgrid;
+        p.grid = maxgrid;
+        p.sch = GemvSched{(int)cus, (int)shared};
+        p.rounds = shared + (rest + cus - 1) / cus;
+    }
+    return p;
 }
 
 // Bit-exact canonical dequant of n_blocks super-blocks; q must be 4-B aligned.

@@ -227,7 +227,8 @@ __device__ __forceinline__ void q6m_row_sums(float yacc, float *aux, float *ybuf
 __global__ __launch_bounds__(q6m::NT) void gemv_q6k_mfma_kernel(const uint8_t *__restrict__ w,
                                                                 const float *__restrict__ x,
                                                                 float *__restrict__ y, int n,
-                                                                int bpr, int rounds) {
+                                                                int bpr, int rounds,
+                                                                GemvSched sch) {
     using namespace q6m;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const Q6mLayout Lo = q6m_layout(bpr, rounds, false);
@@ -238,7 +239,7 @@ __global__ __launch_bounds__(q6m::NT) void gemv_q6k_mfma_kernel(const uint8_t *_
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int RB = bpr * BB;            // row bytes; a group is RB 16-byte chunks
     const int groups = (n + R - 1) / R;
-    const int my_groups = (groups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int my_groups = sched_count(sch, (int)blockIdx.x, (int)gridDim.x, groups);
     const u32x4 *wc = reinterpret_cast<const u32x4 *>(w);
     const long last_chunk = (long)n * RB / 16 - 1;
 
@@ -246,7 +247,7 @@ __global__ __launch_bounds__(q6m::NT) void gemv_q6k_mfma_kernel(const uint8_t *_
     u32x4 reg[CPL];
     auto gload = [&](int q) {
         q = min(q, my_groups - 1);
-        const long base = (long)((int)blockIdx.x + q * (int)gridDim.x) * RB;
+        const long base = (long)sched_group(sch, (int)blockIdx.x, (int)gridDim.x, q) * RB;
 #pragma unroll
         for (int k = 0; k < CPL; ++k) {
             const int c = min(tid + k * NT, RB - 1);
@@ -289,7 +290,7 @@ __global__ __launch_bounds__(q6m::NT) void gemv_q6k_mfma_kernel(const uint8_t *_
         __syncthreads();
     }
     for (int i = tid; i < my_groups * R; i += NT) {
-        const int r = ((int)blockIdx.x + (i / R) * (int)gridDim.x) * R + (i % R);
+        const int r = sched_group(sch, (int)blockIdx.x, (int)gridDim.x, i / R) * R + (i % R);
         if (r < n) y[r] = ybuf[i];
     }
 }
@@ -300,7 +301,8 @@ template <int NW, int XI>
 __global__ __launch_bounds__(NW * 64) void gemv_q6k_mfma_long_kernel(const uint8_t *__restrict__ w,
                                                                      const float *__restrict__ x,
                                                                      float *__restrict__ y, int n,
-                                                                     int bpr, int rounds) {
+                                                                     int bpr, int rounds,
+                                                                     GemvSched sch) {
     using q6m::R, q6m::BB, q6m::TAB, q6m::SEG, q6m::SLOTC;
     constexpr int NT = NW * 64, LCPL = (R * SLOTC + NT - 1) / NT;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -312,7 +314,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_mfma_long_kernel(const uint8
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const long RB = (long)bpr * BB;
     const int groups = (n + R - 1) / R;
-    const int my_groups = (groups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int my_groups = sched_count(sch, (int)blockIdx.x, (int)gridDim.x, groups);
     const int nck = (bpr + SEG - 1) / SEG;
     const int T = my_groups * nck;
     const u32x4 *wc = reinterpret_cast<const u32x4 *>(w);
@@ -326,7 +328,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_mfma_long_kernel(const uint8
         t = min(t, T - 1);
         const int q = t / nck, kc = t - q * nck;
         const int b0 = kc * SEG, cb = min(SEG, bpr - b0);
-        const int row0 = ((int)blockIdx.x + q * (int)gridDim.x) * R;
+        const int row0 = sched_group(sch, (int)blockIdx.x, (int)gridDim.x, q) * R;
 #pragma unroll
         for (int k = 0; k < LCPL; ++k) {
             const int c = min(tid + k * NT, R * SLOTC - 1);
@@ -371,7 +373,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_mfma_long_kernel(const uint8
     for (int t = 0; t < T; ++t) {
         const int q = t / nck, kc = t - q * nck;
         const int b0 = kc * SEG, cb = min(SEG, bpr - b0);
-        const int row = min(((int)blockIdx.x + q * (int)gridDim.x) * R + n16, n - 1);
+        const int row = min(sched_group(sch, (int)blockIdx.x, (int)gridDim.x, q) * R + n16, n - 1);
         const uint32_t rb0 =
             (uint32_t)(n16 * SLOTC * 16) + (uint32_t)(((long)row * RB + (long)b0 * BB) & 15);
         for (int bl = wave; bl < cb; bl += NW)
@@ -387,7 +389,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_mfma_long_kernel(const uint8
         __syncthreads();
     }
     for (int i = tid; i < my_groups * R; i += NT) {
-        const int r = ((int)blockIdx.x + (i / R) * (int)gridDim.x) * R + (i % R);
+        const int r = sched_group(sch, (int)blockIdx.x, (int)gridDim.x, i / R) * R + (i % R);
         if (r < n) y[r] = ybuf[i];
     }
 }
@@ -395,8 +397,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_mfma_long_kernel(const uint8
 namespace {
 
 
-// Persistent launch of `kern` with the occupancy at `probe_lds` bytes: grid
-// balanced so every work-group gets the same number of row groups.
+// Persistent launch of `kern` with the occupancy at `probe_lds` bytes
+// (persistent_plan: balanced, or age-skewed for pairs of work-groups per CU).
 template <typename K>
 hipError_t q6m_launch(K kern, bool chunked, int nw, const uint8_t *w, const float *x, float *y,
                       int n, int bpr, int probe_bpr, int &occ, hipError_t &attr,
@@ -412,13 +414,10 @@ hipError_t q6m_launch(K kern, bool chunked, int nw, const uint8_t *w, const floa
             o = 1;
         occ = o;
     }
-    const long groups = (n + R - 1) / R;
-    const long maxgrid = (long)device_cus() * occ;
-    const long rounds = (groups + maxgrid - 1) / maxgrid;
-    const long grid = (groups + rounds - 1) / rounds;
-    const size_t lds = q6m_layout(bpr, (int)rounds, chunked, nw).total;
+    const PersistPlan p = persistent_plan((n + R - 1) / R, occ);
+    const size_t lds = q6m_layout(bpr, (int)p.rounds, chunked, nw).total;
     if (lds > 160 * 1024) return hipErrorNotSupported;
-    kern<<<(unsigned)grid, nw * 64, lds, stream>>>(w, x, y, n, bpr, (int)rounds);
+    kern<<<(unsigned)p.grid, nw * 64, lds, stream>>>(w, x, y, n, bpr, (int)p.rounds, p.sch);
     return hipGetLastError();
 }
 
