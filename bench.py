@@ -107,8 +107,19 @@ def time_graph(torch, q4k, wl: Workload, steps: int, warmup: int):
     t1.record(stream)
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
+    # Spread, in a separate pass after the timed region: each step between its
+    # own event pair (the events add a small gap between steps, so these are
+    # reported beside the value, never as it).
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(max(1, steps))]
+    for a, b in ev:
+        a.record(stream)
+        chain.launch(stream)
+        b.record(stream)
+    torch.cuda.synchronize()
+    spread = _spread(np.array([a.elapsed_time(b) for a, b in ev]))
     chain.close()
-    return ms
+    return ms, spread
 
 
 def check_parity(torch, wl: Workload, rows: int = 256) -> str:
@@ -176,7 +187,27 @@ def time_captured(torch, launch, steps: int, warmup: int) -> float:
         g.replay()
     t1.record(cur)
     torch.cuda.synchronize()
-    return t0.elapsed_time(t1) / steps
+    ms = t0.elapsed_time(t1) / steps
+    # per-replay spread, a separate pass after the timed region
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(max(1, steps))]
+    for a, b in ev:
+        a.record(cur)
+        g.replay()
+        b.record(cur)
+    torch.cuda.synchronize()
+    SPREADS.append(_spread(np.array([a.elapsed_time(b) for a, b in ev])))
+    return ms
+
+
+# per-pass (p10, median, p90) ms of every time_captured call, in call order
+SPREADS: list = []
+
+
+def _spread(per) -> dict:
+    return {"p10": round(float(np.percentile(per, 10)), 5),
+            "median": round(float(np.median(per)), 5),
+            "p90": round(float(np.percentile(per, 90)), 5), "n": int(per.size)}
 
 
 def run_config1(torch, q4k, args):
@@ -210,7 +241,7 @@ def run_config1(torch, q4k, args):
     return {"workload": "config1: 4864x896 flattened Q4_K (LinearResidentQuantized layout), "
                         f"{copies} rotating copies, one graph", "us_per_launch": round(us, 3),
             "gbs": gbs, "bytes_per_launch": nbytes // copies, "parity": parity,
-            "kernel": "mgq::gemv_generic_kernel<false>"}
+            "kernel": "mgq::gemv_flat_kernel<2>"}
 
 
 def run_batched(torch, q4k, args):
@@ -633,6 +664,10 @@ def run_side_workload(torch, q4k, args) -> int:
           "decode7b_glue": run_decode_glue, "decode7b_q4km": run_decode_q4km}[args.workload]
     r = fn(torch, q4k, args)
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           # ms per graph replay of the headline measurement (dp4a and glue time
+           # their two-launch / unfused baseline first)
+           "pass_ms_spread": SPREADS[1 if args.workload in ("decode7b_dp4a", "decode7b_glue")
+                                     else 0] if SPREADS else None,
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": "synthetic",
            "config": {"workload": r["workload"]}, "parity": r["parity"]}
     if "tflops" in r:
@@ -702,8 +737,8 @@ def main() -> int:
     torch.cuda.synchronize()
     log(f"{len(wl.launches)} launches, {wl.weight_bytes / 1e9:.3f} GB weights resident")
 
-    ms = time_graph(torch, q4k, wl, args.steps, args.warmup)
-    log(f"timed {args.steps} steps: {ms:.4f} ms/step")
+    ms, spread = time_graph(torch, q4k, wl, args.steps, args.warmup)
+    log(f"timed {args.steps} steps: {ms:.4f} ms/step; per-step events {spread}")
     parity = "skipped" if args.no_parity else check_parity(torch, wl)
     log(f"parity: {parity}")
     # The timed region is back-to-back GEMV launches (one graph per step), so
@@ -723,6 +758,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
+        "step_ms_spread": spread,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -44,6 +44,8 @@ hipError_t launch_matvec_q4k_ex(const unsigned char *w_q4, const float *x, float
         if (((int64_t)out_dim * k_elems) % 256 != 0) return hipErrorInvalidValue;
         if (k_elems % 256 == 0)
             return mgq::gemv_rows_launch(w_q4, x, y, out_dim, k_elems / 256, stream);
+        const hipError_t e = mgq::gemv_flat_launch(w_q4, x, y, out_dim, k_elems, stream);
+        if (e != hipErrorNotSupported) return e;
         return mgq::gemv_generic_launch(w_q4, x, y, out_dim, k_elems, stream);
     }
     return hipErrorInvalidValue;

@@ -85,6 +85,87 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const uint8_t *__rest
     if (lane == 0) y[row] = acc;
 }
 
+// Flat-stream layout with k % 32 == 0 (k % 256 != 0): every sub-block lies
+// inside one row, and U = 256 / gcd(k, 256) consecutive rows (a unit) are
+// BPU = U*k/256 whole blocks. One wavefront per unit: lane (bi, j) = (lane/8,
+// lane%8) takes 16-byte qs chunk j of block bi (+8 per pass), i.e. the 16 low
+// nibbles of sub-block 2(j/2) and the 16 high nibbles of sub-block 2(j/2)+1,
+// with 16-byte loads of the 16 matching x values each. Per sub-block half:
+// d*sc * sum(q x) - dmin*m * sum(x), added to the accumulator of its row.
+template <int U>
+__global__ __launch_bounds__(256) void gemv_flat_kernel(const uint8_t *__restrict__ w,
+                                                        const float *__restrict__ x,
+                                                        float *__restrict__ y, int n, int k,
+                                                        int bpu, int units, int64_t nblocks) {
+    const int lane = threadIdx.x & 63;
+    const int u = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (u >= units) return;  // uniform per wavefront
+    const int64_t ub = (int64_t)u * bpu;
+    const int nb = (int)std::min<int64_t>(bpu, nblocks - ub);
+    const int bi = lane >> 3, j = lane & 7, G = j >> 1;
+    float acc[U];
+#pragma unroll
+    for (int r = 0; r < U; ++r) acc[r] = 0.0f;
+    for (int bl = bi; bl < nb; bl += 8) {
+        const uint8_t *blk = w + (ub + bl) * kBlockBytes;
+        const u32x4 hd = *reinterpret_cast<const u32x4 *>(blk);
+        const u32x4 qs = *reinterpret_cast<const u32x4 *>(blk + 16 + 16 * j);
+        const float d = half_bits_finite(hd[0]), dmin = half_bits_finite(hd[0] >> 16);
+        uint32_t sc_lo, m_lo, sc_hi, m_hi;
+        scale_min(2 * G, hd[1], hd[2], hd[3], sc_lo, m_lo);
+        scale_min(2 * G + 1, hd[1], hd[2], hd[3], sc_hi, m_hi);
+        const int f_lo = 256 * bl + 64 * G + 16 * (j & 1);  // unit-relative flat index
+        const int r_lo = f_lo / k, r_hi = (f_lo + 32) / k;
+        const f32x4 *xl = reinterpret_cast<const f32x4 *>(x + (f_lo - r_lo * k));
+        const f32x4 *xh = reinterpret_cast<const f32x4 *>(x + (f_lo + 32 - r_hi * k));
+        float dl = 0.0f, sl = 0.0f, dh = 0.0f, sh = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const f32x4 a = xl[c], b = xh[c];
+            const uint32_t v = qs[c];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                dl += (float)((v >> (8 * t)) & 15u) * a[t];
+                dh += (float)((v >> (8 * t + 4)) & 15u) * b[t];
+                sl += a[t];
+                sh += b[t];
+            }
+        }
+        const float vl = (d * (float)sc_lo) * dl - (dmin * (float)m_lo) * sl;
+        const float vh = (d * (float)sc_hi) * dh - (dmin * (float)m_hi) * sh;
+#pragma unroll
+        for (int r = 0; r < U; ++r) acc[r] += (r_lo == r ? vl : 0.0f) + (r_hi == r ? vh : 0.0f);
+    }
+#pragma unroll
+    for (int r = 0; r < U; ++r) {
+        float v = acc[r];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        const int row = u * U + r;
+        if (lane == 0 && row < n) y[row] = v;
+    }
+}
+
+hipError_t gemv_flat_launch(const uint8_t *w, const float *x, float *y, int n, int k,
+                            hipStream_t stream) {
+    if (k % 32 != 0 || (((uintptr_t)w | (uintptr_t)x) & 15u)) return hipErrorNotSupported;
+    int g = 256;
+    while (k % g) g >>= 1;  // gcd(k, 256), >= 32 here
+    const int U = 256 / g;
+    if ((int64_t)U * k > 0x7FFFFFFFLL) return hipErrorNotSupported;  // unit-relative indices are int
+    const int bpu = (int)((int64_t)U * k / kBlockElems);
+    const int units = (n + U - 1) / U;
+    const int64_t nblocks = (int64_t)n * k / kBlockElems;
+    const unsigned grid = (unsigned)((units + 3) / 4);
+    switch (U) {
+    case 1: gemv_flat_kernel<1><<<grid, 256, 0, stream>>>(w, x, y, n, k, bpu, units, nblocks); break;
+    case 2: gemv_flat_kernel<2><<<grid, 256, 0, stream>>>(w, x, y, n, k, bpu, units, nblocks); break;
+    case 4: gemv_flat_kernel<4><<<grid, 256, 0, stream>>>(w, x, y, n, k, bpu, units, nblocks); break;
+    default: gemv_flat_kernel<8><<<grid, 256, 0, stream>>>(w, x, y, n, k, bpu, units, nblocks); break;
+    }
+    return hipGetLastError();
+}
+
 hipError_t gemv_generic_launch(const uint8_t *w, const float *x, float *y, int n, int k,
                                hipStream_t stream) {
     const unsigned grid = (unsigned)((n + 3) / 4);

@@ -98,6 +98,10 @@ hipError_t dequant_launch(const uint8_t *q, int n_blocks, float *out, hipStream_
 // layout (k % 256 == 0) when the fast kernel does not apply.
 hipError_t gemv_generic_launch(const uint8_t *w, const float *x, float *y, int n, int k,
                                hipStream_t stream);
+// Flat-stream layout with k % 32 == 0 (whole sub-blocks per row), w and x
+// 16-byte aligned; hipErrorNotSupported otherwise (then: generic).
+hipError_t gemv_flat_launch(const uint8_t *w, const float *x, float *y, int n, int k,
+                            hipStream_t stream);
 
 // Matrix-core GEMV for the row-aligned layout. Returns hipErrorNotSupported
 // when the shape or alignment does not fit it (caller then uses generic).

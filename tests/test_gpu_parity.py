@@ -191,7 +191,10 @@ def test_matvec_generic_kernel_on_misaligned_weights(L, orc):
     assert_gemv_close(y, y_ref, a)
 
 
-@pytest.mark.parametrize("n,k", [(4864, 896), (8, 96), (128, 258), (3, 256 * 3)])
+# (n, k): rows of U = 256/gcd(k, 256) rows per unit (U = 2, 8, 4, 2, 8 with a
+# 153-block unit), k % 32 != 0 (vector-ALU kernel), k % 256 == 0 (row layout)
+@pytest.mark.parametrize("n,k", [(4864, 896), (8, 96), (16, 320), (64, 1152), (40, 4896),
+                                 (128, 258), (3, 256 * 3)])
 def test_matvec_flat_layout(L, orc, n, k):
     note(f"matvec flat {n}x{k}")
     w = orc.seeded_weight(0xC0F1 + k, n, k)
@@ -202,6 +205,30 @@ def test_matvec_flat_layout(L, orc, n, k):
     y = host(yt)
     y_ref, a = orc.gemv_flat(w, x, n, k)
     assert_gemv_close(y, y_ref, a)
+
+
+def test_matvec_flat_layout_random_bytes_and_misaligned_x(L, orc):
+    # random blocks (non-finite d / dmin included) on the whole-unit kernel,
+    # then x 4 bytes off 16-byte alignment (the vector-ALU kernel), same result
+    note("matvec flat 4864x896 random bytes; x offset 4 B")
+    import torch
+    n, k = 4864, 896
+    rng = np.random.default_rng(0xF1A7)
+    w = random_q4k_bytes(rng, n * k // 256, finite_scales=False)
+    x = rng.standard_normal(k).astype(np.float32)
+    wt, yt = dev(w), empty_f32(n)
+    xt = torch.zeros(k + 4, dtype=torch.float32, device="cuda")
+    xt[1:k + 1].copy_(torch.from_numpy(x))
+    y_ref, a = orc.gemv_flat(w, x, n, k)
+    ok = np.isfinite(y_ref)
+    xa = dev(x)  # 16-byte aligned copy
+    for off in (4, 0):
+        xp = ptr(xt) + off if off else ptr(xa)
+        _lib.check("launch_matvec_q4k_ex",
+                   L.launch_matvec_q4k_ex(ptr(wt), xp, ptr(yt), n, k, _lib.LAYOUT_FLAT, None))
+        y = host(yt)
+        assert np.array_equal(np.isfinite(y), ok)
+        assert_gemv_close(y[ok], y_ref[ok], a[ok])
 
 
 # ------------------------------------------------------------------ batched --
