@@ -14,7 +14,7 @@
 //    for the dmin*m term.
 //
 // 2. gemv_batched_mfma_kernel streams the weights exactly as the GEMV does
-//    (fully coalesced 16-byte loads -> registers -> LDS stage of 32 rows x 8
+//    (fully coalesced 16-byte loads -> registers -> LDS stage of 16 rows x 8
 //    blocks) and keeps the batch on the MFMA M dimension, so one weight
 //    operand serves 8 batch rows per v_mfma_f32_16x16x32_f16:
 //      * B operand = sc*q: the nibble masked in place is the f16 subnormal
@@ -166,7 +166,7 @@ __device__ __forceinline__ uint32_t byte_to_h2(uint32_t src, uint32_t sel) {
     return __builtin_bit_cast(uint32_t, r);
 }
 
-// Work-group = 8 waves; stage = R (16 or 32) rows x 8 blocks (single LDS
+// Work-group = 8 waves; stage = R (16; 32 also compiles) rows x 8 blocks (single LDS
 // buffer), PF stages in flight; persistent over row groups. SETS = batch sets
 // of 8.
 template <int R, int SETS, int PF>
@@ -408,13 +408,12 @@ hipError_t gemv_batched_mfma_launch(const uint8_t *w, const float *X, float *Y, 
         X, batch, bpr, sets, ((uintptr_t)X & 15u) == 0, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    // 16-row groups when 32-row groups would leave CUs idle
-    const bool small = (n + 31) / 32 < device_cus();
-    if (sets == 1)
-        return small ? batched_main_launch<16, 1, 2>(w, ws, Y, n, bpr, batch, stream)
-                     : batched_main_launch<32, 1, 2>(w, ws, Y, n, bpr, batch, stream);
-    return small ? batched_main_launch<16, 2, 1>(w, ws, Y, n, bpr, batch, stream)
-                 : batched_main_launch<32, 2, 1>(w, ws, Y, n, bpr, batch, stream);
+    // 16-row groups: at one 8-wave work-group per CU, 32-row groups leave a
+    // coarser last round (gate 18944x3584: 3 rounds of 32 rows on 198
+    // work-groups against 5 of 16 on 237; 14.6 against 16.6 us at B = 8, and
+    // slower at B = 4 and 16 too)
+    if (sets == 1) return batched_main_launch<16, 1, 2>(w, ws, Y, n, bpr, batch, stream);
+    return batched_main_launch<16, 2, 1>(w, ws, Y, n, bpr, batch, stream);
 }
 
 }  // namespace mgq
