@@ -76,8 +76,16 @@ __device__ __forceinline__ int split_exponent(float amax) {
 // grid (bpr, sets), 256 threads: thread = (batch b' = tid/32, 8-float chunk)
 __global__ __launch_bounds__(256) void batched_table_kernel(const float *__restrict__ X, int batch,
                                                             int bpr, int sets, bool x_aligned16,
-                                                            uint8_t *__restrict__ ws) {
+                                                            uint8_t *__restrict__ ws,
+                                                            float *__restrict__ yzero, int ytotal) {
     __shared__ float xs[8][256];
+    // Y = 0 ahead of a K-split main kernel (it adds its partials atomically)
+    {
+        const int nthr = (int)(gridDim.x * gridDim.y) * 256;
+        for (int i = (int)(blockIdx.y * gridDim.x + blockIdx.x) * 256 + (int)threadIdx.x; i < ytotal;
+             i += nthr)
+            yzero[i] = 0.0f;
+    }
     __shared__ float xsum[8][8];
     const int j = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
     const int bl = tid >> 5, ch = tid & 31, b = s * 8 + bl;
@@ -173,7 +181,8 @@ template <int R, int SETS, int PF>
 __global__ __launch_bounds__(512) void gemv_batched_mfma_kernel(const uint8_t *__restrict__ w,
                                                                 const uint8_t *__restrict__ ws,
                                                                 float *__restrict__ Y, int n,
-                                                                int bpr, int batch, int rounds) {
+                                                                int bpr, int batch, int rounds,
+                                                                int kparts) {
     constexpr int C = 8, NW = 8, BP = 8 * SETS, TILES = R / 16;
     constexpr int RP = (9 * C) | 1;               // LDS pieces per staged row (odd: no bank conflicts)
     constexpr int STAGE_BYTES = R * RP * 16;
@@ -187,9 +196,16 @@ __global__ __launch_bounds__(512) void gemv_batched_mfma_kernel(const uint8_t *_
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const size_t row_bytes = (size_t)bpr * kBlockBytes;
-    const int slices = (bpr + C - 1) / C;
+    // K split: work-group id = kp * G + bx; K part kp takes slices
+    // [sl0, sl0 + slices) of all of them (kparts <= slices overall)
+    const int G = (int)gridDim.x / kparts;
+    const int kp = (int)blockIdx.x / G, bx = (int)blockIdx.x - kp * G;
+    const int all_slices = (bpr + C - 1) / C;
+    const int spk = (all_slices + kparts - 1) / kparts;
+    const int sl0 = kp * spk;
+    const int slices = std::min(all_slices, sl0 + spk) - sl0;
     const int groups = (n + R - 1) / R;
-    const int my_groups = (groups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int my_groups = (groups - bx + G - 1) / G;
     const int Q = my_groups * slices;  // stage q = (slice q / my_groups, group q % my_groups)
 
     u32x4 stg[PF][IPW];
@@ -207,8 +223,8 @@ __global__ __launch_bounds__(512) void gemv_batched_mfma_kernel(const uint8_t *_
     auto gload = [&](int q, u32x4(&dst)[IPW]) {
         q = std::min(q, Q - 1);
         const int sl = q / my_groups, t = q - sl * my_groups;
-        const uint32_t r0 = ((uint32_t)blockIdx.x + (uint32_t)t * gridDim.x) * R;
-        const uint32_t tcol = (uint32_t)(sl * C * kBlockBytes);
+        const uint32_t r0 = ((uint32_t)bx + (uint32_t)t * (uint32_t)G) * R;
+        const uint32_t tcol = (uint32_t)((sl0 + sl) * C * kBlockBytes);
         const uint32_t rlast = (uint32_t)(n - 1), rb = (uint32_t)row_bytes;
 #pragma unroll
         for (int k = 0; k < IPW; ++k) {
@@ -235,7 +251,7 @@ __global__ __launch_bounds__(512) void gemv_batched_mfma_kernel(const uint8_t *_
     u32x4 areg[SETS][kBatchOps], anext[SETS][kBatchOps];
     f32x4 mreg[SETS], mnext[SETS];  // (corr, corr_min) of batches 2g, 2g+1 of each set
     auto load_a = [&](int sl, u32x4(&a)[SETS][kBatchOps], f32x4(&mr)[SETS]) {
-        const int jb = std::min(sl * C + wave, bpr - 1);
+        const int jb = std::min((sl0 + sl) * C + wave, bpr - 1);
 #pragma unroll
         for (int s = 0; s < SETS; ++s) {
             const uint8_t *base = ws + ((size_t)jb * SETS + s) * kBatchOps * 1024 + lane * 16;
@@ -259,7 +275,7 @@ __global__ __launch_bounds__(512) void gemv_batched_mfma_kernel(const uint8_t *_
                 for (int c = 0; c < kBatchOps; ++c) areg[s][c] = anext[s][c];
             }
         }
-        const int jb = sl * C + wave;  // this wave's block of the slice
+        const int jb = (sl0 + sl) * C + wave;  // this wave's block of the slice
         float *aux = aux0 + (q & 1) * (AUX_BYTES / 4);
         if (jb < bpr) {
 #pragma unroll
@@ -368,15 +384,22 @@ __global__ __launch_bounds__(512) void gemv_batched_mfma_kernel(const uint8_t *_
     // Y[b][r], rows fastest
     for (int i = tid; i < my_groups * R * BP; i += NW * 64) {
         const int t = i / (R * BP), rem = i - t * R * BP, b = rem / R, r = rem - b * R;
-        const int row = ((int)blockIdx.x + t * (int)gridDim.x) * R + r;
-        if (row < n && b < batch) Y[(size_t)b * n + row] = ybuf[(t * R + r) * BP + b];
+        const int row = (bx + t * G) * R + r;
+        if (row < n && b < batch) {
+            const float v = ybuf[(t * R + r) * BP + b];
+            // two K parts: 0 + a + b rounds the same in either order
+            if (kparts > 1)
+                atomicAdd(&Y[(size_t)b * n + row], v);
+            else
+                Y[(size_t)b * n + row] = v;
+        }
     }
 }
 
 
 template <int R, int SETS, int PF>
 static hipError_t batched_main_launch(const uint8_t *w, const uint8_t *ws, float *Y, int n, int bpr,
-                                      int batch, hipStream_t stream) {
+                                      int batch, int kparts, hipStream_t stream) {
     auto kern = gemv_batched_mfma_kernel<R, SETS, PF>;
     static const hipError_t attr = hipFuncSetAttribute(
         (const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -393,7 +416,8 @@ static hipError_t batched_main_launch(const uint8_t *w, const uint8_t *ws, float
     const long grid = (groups + rounds - 1) / rounds;
     const size_t lds = base + (size_t)rounds * R * BP * 4;
     if (lds > 160 * 1024) return hipErrorNotSupported;
-    kern<<<(unsigned)grid, 512, lds, stream>>>(w, ws, Y, n, bpr, batch, (int)rounds);
+    kern<<<(unsigned)(grid * kparts), 512, lds, stream>>>(w, ws, Y, n, bpr, batch, (int)rounds,
+                                                          kparts);
     return hipGetLastError();
 }
 
@@ -404,16 +428,22 @@ hipError_t gemv_batched_mfma_launch(const uint8_t *w, const float *X, float *Y, 
     if (workspace_bytes < batched_ws(bpr, sets).total) return hipErrorInvalidValue;
     if (((uintptr_t)w & 15u) || ((uintptr_t)workspace & 15u)) return hipErrorNotSupported;
     uint8_t *ws = static_cast<uint8_t *>(workspace);
+    // Few row groups and a long K (ffn_down): 32-row groups, K split in two,
+    // so every CU is busy and each work-group reads the operand table for 32
+    // rows instead of 16. Otherwise 16-row groups: at one 8-wave work-group
+    // per CU, 32-row groups leave a coarser last round (gate 18944x3584: 3
+    // rounds of 32 rows on 198 work-groups against 5 of 16 on 237; 14.6
+    // against 16.6 us at B = 8, and slower at B = 4 and 16 too).
+    const bool ksplit = (n + 15) / 16 <= device_cus() && (bpr + 7) / 8 >= 4;
     batched_table_kernel<<<dim3((unsigned)bpr, (unsigned)sets), 256, 0, stream>>>(
-        X, batch, bpr, sets, ((uintptr_t)X & 15u) == 0, ws);
+        X, batch, bpr, sets, ((uintptr_t)X & 15u) == 0, ws, Y, ksplit ? batch * n : 0);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    // 16-row groups: at one 8-wave work-group per CU, 32-row groups leave a
-    // coarser last round (gate 18944x3584: 3 rounds of 32 rows on 198
-    // work-groups against 5 of 16 on 237; 14.6 against 16.6 us at B = 8, and
-    // slower at B = 4 and 16 too)
-    if (sets == 1) return batched_main_launch<16, 1, 2>(w, ws, Y, n, bpr, batch, stream);
-    return batched_main_launch<16, 2, 1>(w, ws, Y, n, bpr, batch, stream);
+    if (ksplit)
+        return sets == 1 ? batched_main_launch<32, 1, 2>(w, ws, Y, n, bpr, batch, 2, stream)
+                         : batched_main_launch<32, 2, 1>(w, ws, Y, n, bpr, batch, 2, stream);
+    if (sets == 1) return batched_main_launch<16, 1, 2>(w, ws, Y, n, bpr, batch, 1, stream);
+    return batched_main_launch<16, 2, 1>(w, ws, Y, n, bpr, batch, 1, stream);
 }
 
 }  // namespace mgq

@@ -285,6 +285,23 @@ def test_matvec_batched_matches_gemv_and_is_deterministic(L, orc):
         assert_gemv_close(y, y_ref, a)
 
 
+@pytest.mark.parametrize("n,bpr,batch", [(45, 33, 8), (300, 74, 16), (3584, 74, 5)])
+def test_matvec_batched_k_split(L, orc, n, bpr, batch):
+    # few row groups and K >= 4 slices of 8 blocks: 32-row groups, K split in
+    # two, partials added onto a zeroed Y. Odd slice count (33 blocks: 3 + 2
+    # slices, the last one block), a ragged row group, two batch sets, the
+    # ffn_down shape; two K parts add in either order to the same bits
+    note(f"batched K split n={n} bpr={bpr} B={batch}")
+    w = orc.seeded_weight(71 + n, n, bpr * 256)
+    X = orc.normal(72 + bpr, batch * bpr * 256).reshape(batch, -1)
+    Y1 = run_batched(L, w, X, n, bpr, batch)
+    Y2 = run_batched(L, w, X, n, bpr, batch)
+    assert np.array_equal(Y1.view(np.uint32), Y2.view(np.uint32))
+    Y_ref, A = orc.gemv_batched(w, X, n, bpr)
+    for b in range(batch):
+        assert_gemv_close(Y1[b], Y_ref[b], A[b])
+
+
 def test_matvec_batched_single_row_is_the_matvec(L, orc):
     # batch 1 runs the matvec itself (no operand-table pass): bit-identical
     note("batched B=1 == gemv")
