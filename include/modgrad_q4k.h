@@ -150,7 +150,9 @@ hipError_t launch_dequant_q4k_ex(const unsigned char *q4k, int n_blocks, float *
  * mgq_batched_workspace_bytes(blocks_per_row, batch) bytes, 16-byte aligned;
  * it holds X converted to matrix-core operands for the duration of the call,
  * so calls that may overlap need distinct workspaces. A smaller or null
- * workspace -> hipErrorInvalidValue. */
+ * workspace -> hipErrorInvalidValue. Y must not overlap X, W or the
+ * workspace: for long K and few rows the call zeroes Y first and adds two
+ * K-half partials into it (bit-identical from call to call). */
 size_t mgq_batched_workspace_bytes(int blocks_per_row, int batch);
 hipError_t launch_matvec_q4k_batched(const unsigned char *w_q4, const float *X, float *Y,
                                      int out_dim, int blocks_per_row, int batch,

@@ -28,6 +28,9 @@
 //        blocks 8s..8s+7, then s+1), so wave w keeps the A operands of block
 //        8s+w in registers for the whole slice; per-stage partial sums are
 //        reduced across waves into an LDS row buffer.
+//      * Shapes with few row groups and a long K split K in two: the table
+//        kernel zeroes Y and each half adds its partials atomically (two
+//        addends onto 0 round the same in either order).
 #include "q4k_device.hpp"
 #include "q4k_launch.hpp"
 
