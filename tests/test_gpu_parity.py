@@ -160,6 +160,25 @@ def test_matvec_baseline_layer_shapes(L, orc, name, n, k, t):
     print(f"{name}: worst err/absdot = {worst:.3e}")
 
 
+@pytest.mark.parametrize("fmt", [144, 210])
+def test_matvec_lm_head_full_size(L, orc, fmt):
+    # BASELINE lm_head 152064x3584: the longest persistent schedule (19 rounds
+    # of row groups per work-group, the older member of each CU pair taking
+    # the extra rounds); every row against the f64 oracle
+    from tests.gpu_util import random_kquant_bytes
+    n, bpr = 152064, 14
+    note(f"{'q4k' if fmt == 144 else 'q6k'} lm_head {n}x{bpr * 256}")
+    rng = np.random.default_rng(0x1A4EAD + fmt)
+    w = (random_q4k_bytes(rng, n * bpr) if fmt == 144
+         else random_kquant_bytes(rng, n * bpr, 210))
+    x = rng.standard_normal(bpr * 256).astype(np.float32)
+    wt, xt, yt = dev(w), dev(x), empty_f32(n)
+    fn = L.launch_matvec_q4k if fmt == 144 else L.launch_matvec_q6k
+    _lib.check("lm_head", fn(ptr(wt), ptr(xt), ptr(yt), n, bpr))
+    y_ref, a = orc.gemv_kquant(fmt, w, x, n, bpr)
+    assert_gemv_close(host(yt), y_ref, a)
+
+
 @pytest.mark.parametrize("n,bpr", [(3584, 14), (3584, 74), (40, 148)])
 def test_matvec_is_deterministic(L, orc, n, bpr):
     # shapes that split K across work-groups: the last arriver sums the
