@@ -12,6 +12,7 @@ crates/modgrad-compute/src/neuron.rs), so tests read like the reference's:
   kern.*                                   rocm.rs:943-996
   ops.dequant_q4k_resident                 ops.rs:531-539
   GpuVec, ResidencyError                   compute/src/backend.rs:35-278
+  HipBatch                                 rocm.rs:1089-1211
   LinearResidentQuantized                  neuron.rs:897-1108
 
 PyTorch is only the device-memory allocator here; every computation goes
@@ -369,6 +370,58 @@ class Chain:
             pass
 
 
+class HipBatch:
+    """Dispatch counter that drains the device every `sync_every` queued
+    kernels (rocm.rs:1089-1211), so long runs of resident dispatches cannot
+    pile up unsynchronized. Resident ops call note_dispatch() after queueing
+    a kernel; flush() drains now; a batch with pending work drains when it is
+    dropped."""
+
+    DEFAULT_SYNC_EVERY = 256
+
+    def __init__(self, sync_every: int = DEFAULT_SYNC_EVERY):
+        if sync_every < 1:
+            raise ValueError("HipBatch::with_sync_every: n must be >= 1")
+        self.sync_every = sync_every
+        self.pending = 0
+
+    @classmethod
+    def new(cls) -> "HipBatch":
+        return cls()
+
+    @classmethod
+    def with_sync_every(cls, n: int) -> "HipBatch":
+        return cls(n)
+
+    def note_dispatch(self) -> None:
+        n = self.pending + 1
+        if n >= self.sync_every:
+            self.pending = 0  # reset even when the drain fails
+            self._sync("HipBatch sync (every %d)" % self.sync_every)
+        else:
+            self.pending = n
+
+    def flush(self) -> None:
+        self.pending = 0
+        self._sync("HipBatch::flush")
+
+    @staticmethod
+    def _sync(what: str) -> None:
+        try:
+            _torch().cuda.synchronize()
+        except BackendError:
+            raise
+        except RuntimeError as e:
+            raise BackendError("Runtime", f"{what}: {e}") from e
+
+    def __del__(self):
+        if getattr(self, "pending", 0) > 0:
+            try:
+                _torch().cuda.synchronize()
+            except Exception:
+                pass
+
+
 class ResidencyError(Exception):
     """Error of a device-resident dispatch (compute/src/backend.rs:244-278):
     either a wrapped BackendError (`backend`) or a GpuVec of the wrong
@@ -531,7 +584,9 @@ class LinearResidentQuantized:
     def dequant_size_bytes(self) -> int:
         return self.host_weight_q4k.size + self._in * self._out * 4 + self.host_bias.size * 4
 
-    def ensure_resident(self) -> None:
+    def ensure_resident(self, batch: HipBatch | None = None) -> None:
+        """Upload, dequantize and stage the bias unless resident
+        (neuron.rs:1018-1038); the dequant kernel counts against `batch`."""
         if self.is_resident():
             return
         q = HipBuffer(self.host_weight_q4k.size)
@@ -539,6 +594,8 @@ class LinearResidentQuantized:
         wf = HipBuffer(self._in * self._out * 4)
         ops.dequant_q4k_resident(q.device_ptr(), wf.device_ptr(),
                                  self.host_weight_q4k.size // Q4K_BLOCK_BYTES)
+        if batch is not None:
+            batch.note_dispatch()
         b = HipBuffer(self.host_bias.size * 4)
         b.copy_from_host(self.host_bias)
         self.weight_q4k_dev, self.weight_dev, self.bias_dev = q, wf, b
@@ -546,16 +603,22 @@ class LinearResidentQuantized:
     def evict(self) -> None:
         self.weight_q4k_dev = self.weight_dev = self.bias_dev = None
 
-    def forward(self, x_dev, out_dev, auto_evict: bool = False, stream=None) -> None:
+    def forward(self, x_dev, out_dev, auto_evict: bool = False, stream=None,
+                batch: HipBatch | None = None) -> None:
         """out = W x + b, W the canonical dequant of the resident Q4_K bytes
         (neuron.rs:1059-1108). x_dev and out_dev are HipBuffers or Hip
         GpuVecs; a Heap GpuVec raises ResidencyError WrongVariant, as in the
         reference. The bias is added after the product, one rounding, as
-        hipblasSgemv's beta = 1 on a bias-filled y does (rocm.rs:2000-2056)."""
+        hipblasSgemv's beta = 1 on a bias-filled y does (rocm.rs:2000-2056).
+        With a HipBatch, every kernel queued here counts against it."""
         x_buf, out_buf = _hip_of(x_dev, "x"), _hip_of(out_dev, "out")
-        self.ensure_resident()
+        self.ensure_resident(batch)
         kern.matvec_q4k_ex(self.weight_q4k_dev.device_ptr(), x_buf.device_ptr(),
                            out_buf.device_ptr(), self._out, self._in, _lib.LAYOUT_FLAT, stream)
+        if batch is not None:
+            batch.note_dispatch()
         kern.residual_add(out_buf.device_ptr(), self.bias_dev.device_ptr(), self._out, stream)
+        if batch is not None:
+            batch.note_dispatch()
         if auto_evict:
             self.evict()

@@ -154,6 +154,20 @@ def test_gpuvec_heap_variant():
     assert not lin.is_resident()  # the variant check comes before any allocation
 
 
+def test_hipbatch_counts_dispatches():
+    # rocm.rs:1089-1211: a cadence below 1 is rejected; below the cadence a
+    # dispatch only counts (the drain itself needs a device)
+    from modgrad_amd.q4k import HipBatch
+    with pytest.raises(ValueError):
+        HipBatch.with_sync_every(0)
+    b = HipBatch.new()
+    assert b.sync_every == HipBatch.DEFAULT_SYNC_EVERY == 256
+    for i in range(255):
+        b.note_dispatch()
+    assert b.pending == 255
+    b.pending = 0  # nothing queued on a device here: let it drop quietly
+
+
 def test_host_size_savings():
     # neuron.rs:2002-2028: a 1024->256 layer's Q4_K host footprint < 16% of f32
     import numpy as np

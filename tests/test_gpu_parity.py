@@ -433,6 +433,17 @@ def test_linear_forward_takes_hip_gpuvecs(L, orc):
     assert yv.clone().variant_name() == "Heap"
     with pytest.raises(Exception):
         yv.as_slice()  # Hip memory is not host-visible (backend.rs:139-151)
+    # with a HipBatch (neuron.rs:1059-1108): every queued kernel counts and the
+    # batch drains at its cadence; the result is unchanged
+    from modgrad_amd.q4k import HipBatch
+    batch = HipBatch.with_sync_every(3)
+    lin.evict()
+    lin.ensure_resident(batch)       # dequant: 1
+    assert batch.pending == 1
+    lin.forward(xv, yv, batch=batch)  # matvec + bias add: 3 -> drained
+    assert batch.pending == 0
+    assert np.array_equal(yv.copy_to_host().view(np.uint32), y.view(np.uint32))
+    batch.flush()
 
 
 def test_hipbuffer_range_copies_and_q5k(L, orc):
