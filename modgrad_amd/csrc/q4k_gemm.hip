@@ -5,13 +5,15 @@
 // canonical dequantized value (gguf.rs:364-404) with d*sc and dmin*m rounded
 // to f16 and the weight itself computed and rounded in f16.
 //
-// Work-group tile: 128 W rows x 128 tokens, 4 wavefronts of 64x64 outputs
-// (4x4 v_mfma_f32_16x16x32_f16, W rows as the A operand, tokens as the B
-// operand, so a lane's 4 accumulators are 4 consecutive W rows of one token:
-// one 16-byte store into C's [M][N]).
+// Work-group tile: BN W rows x 128 tokens (BN = 128, or 160 when 128-row
+// tiles would leave a second, mostly empty round of the two resident
+// work-groups per CU), 4 wavefronts of BN/2 x 64 outputs (BN/32 x 4
+// v_mfma_f32_16x16x32_f16, W rows as the A operand, tokens as the B operand,
+// so a lane's 4 accumulators are 4 consecutive W rows of one token: one
+// 16-byte store into C's [M][N]).
 //
 // Memory path. Global loads are whole cache lines: the W tile of a
-// super-block (128 rows x 144 B) is copied raw into LDS as 1152 contiguous
+// super-block (BN rows x 144 B) is copied raw into LDS as 9*BN contiguous
 // 16-byte pieces (a wavefront's 64 pieces cover ~7 rows), once per 8 MFMA
 // k-steps; the activation tile of a 64-wide K step is 128 tokens x 128 B,
 // 8 lanes per token. Loads for the next super-block / K step are in flight
@@ -33,15 +35,15 @@
 #include "q4k_device.hpp"
 #include "q4k_launch.hpp"
 
+#include <cstdlib>
+
 namespace mgq {
 
 namespace gemm {
-constexpr int BN = 128;        // W rows per work-group
 constexpr int BM = 128;        // tokens per work-group
 constexpr int BK = 64;         // k per step (one 32-byte qs group: 2 sub-blocks)
 constexpr int AROW = 72;       // halves per activation LDS row (64 + 8 pad, 144 B)
 constexpr int SROW = 10;       // dwords per scale row (8 + 2 pad: conflict-free b64 reads)
-constexpr int RAW_PIECES = BN * kBlockBytes / 16;  // 1152 16-byte pieces per super-block
 constexpr int NXCD = 8;        // XCDs the hardware deals work-groups across, round robin
 }  // namespace gemm
 
@@ -89,13 +91,19 @@ __device__ __forceinline__ u32x4 act_order(u32x4 v) {
     return r;
 }
 
+// BN = W rows per work-group (128 or 160): two wavefronts along N of BN/2
+// rows = TI 16-row MFMA tiles each.
+template <int BN>
 __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__restrict__ w,
                                                            const uint16_t *__restrict__ a,
                                                            float *__restrict__ c, int n, int bpr,
                                                            int m_tokens, int tiles_n, int tiles_m) {
     using namespace gemm;
-    __shared__ __attribute__((aligned(16))) uint8_t sRaw[BN * kBlockBytes];  // 18432 B
-    __shared__ __attribute__((aligned(16))) uint32_t sScl[BN * SROW];        // 5120 B
+    constexpr int TI = BN / 32;                            // 16-row tiles per wavefront
+    constexpr int RAW_PIECES = BN * kBlockBytes / 16;      // 16-byte pieces per super-block
+    constexpr int NPL = (RAW_PIECES + 255) / 256;          // raw loads per thread
+    __shared__ __attribute__((aligned(16))) uint8_t sRaw[BN * kBlockBytes];
+    __shared__ __attribute__((aligned(16))) uint32_t sScl[BN * SROW];
     __shared__ __attribute__((aligned(16))) _Float16 sA[2][BM * AROW];      // 36864 B
 
     // work-group -> tile: the hardware sends work-group i to XCD i % 8; give
@@ -111,40 +119,40 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__r
     const int T = bpr * 4;  // K steps
     const size_t row_bytes = (size_t)bpr * kBlockBytes;
 
-    // raw W loader: piece p = tid + 256*k (k < 4, and k = 4 for tid < 128)
-    // is bytes 16*(p%9) .. +15 of row p/9's super-block
-    const uint8_t *rsrc[5];
+    // raw W loader: piece p = tid + 256*k (k < NPL - 1, and the last k for
+    // tid < RAW_PIECES - 256 (NPL - 1)) is bytes 16*(p%9) .. +15 of row p/9's
+    // super-block
+    const uint8_t *rsrc[NPL];
 #pragma unroll
-    for (int k = 0; k < 5; ++k) {
+    for (int k = 0; k < NPL; ++k) {
         const int p = min(tid + 256 * k, RAW_PIECES - 1);
         rsrc[k] = w + (size_t)min(n0 + p / 9, n - 1) * row_bytes + 16 * (p % 9);
     }
-    const bool has5 = tid < RAW_PIECES - 1024;
+    const bool haslast = tid < RAW_PIECES - 256 * (NPL - 1);
     // the lane holding a row's header piece decodes that row's scales
     int hk = -1, hrow = 0;
 #pragma unroll
-    for (int k = 0; k < 5; ++k) {
+    for (int k = 0; k < NPL; ++k) {
         const int p = tid + 256 * k;
         if (p < RAW_PIECES && p % 9 == 0) {
             hk = k;
             hrow = p / 9;
         }
     }
-    u32x4 R[5];
-    auto rload = [&](int b) {  // piece 4 is loaded by every lane (clamped address): no branch
+    u32x4 R[NPL];
+    auto rload = [&](int b) __attribute__((always_inline)) {  // piece 4 is loaded by every lane (clamped address): no branch
 #pragma unroll
-        for (int k = 0; k < 5; ++k)
+        for (int k = 0; k < NPL; ++k)
             R[k] = *reinterpret_cast<const u32x4 *>(rsrc[k] + (size_t)b * kBlockBytes);
     };
-    auto rstore = [&]() {
+    auto rstore = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) *reinterpret_cast<u32x4 *>(&sRaw[16 * (tid + 256 * k)]) = R[k];
-        if (has5) *reinterpret_cast<u32x4 *>(&sRaw[16 * (tid + 1024)]) = R[4];
+        for (int k = 0; k < NPL - 1; ++k) *reinterpret_cast<u32x4 *>(&sRaw[16 * (tid + 256 * k)]) = R[k];
+        if (haslast) *reinterpret_cast<u32x4 *>(&sRaw[16 * (tid + 256 * (NPL - 1))]) = R[NPL - 1];
         if (hk >= 0) {
-            u32x4 h = R[0];
-#pragma unroll
-            for (int k = 1; k < 5; ++k)
-                if (hk == k) h = R[k];
+            // this lane stored the row's header piece just above; reading it
+            // back from LDS avoids indexing R with the runtime hk
+            const u32x4 h = *reinterpret_cast<const u32x4 *>(&sRaw[16 * 9 * hrow]);
             const float d = half_bits_finite(h[0]), dmin = half_bits_finite(h[0] >> 16);
             uint32_t pr[8];
 #pragma unroll
@@ -169,12 +177,12 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__r
     for (int k = 0; k < 4; ++k)
         asrc[k] = a + (size_t)min(m0 + (tid >> 3) + 32 * k, m_tokens - 1) * K + 8 * ap;
     u32x4 Areg[2][4];  // two register sets: step t+2's loads fly while t+1's are stored
-    auto aload = [&](int t, int set) {
+    auto aload = [&](int t, int set) __attribute__((always_inline)) {
 #pragma unroll
         for (int k = 0; k < 4; ++k)
             Areg[set][k] = *reinterpret_cast<const u32x4 *>(asrc[k] + (size_t)t * BK);
     };
-    auto astore = [&](int set, int buf) {
+    auto astore = [&](int set, int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int k = 0; k < 4; ++k)
             *reinterpret_cast<u32x4 *>(&sA[buf][((tid >> 3) + 32 * k) * AROW + 8 * ap]) =
@@ -182,20 +190,20 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__r
     };
 
     // compute roles
-    const int wn = (wave >> 1) * 64, wm = (wave & 1) * 64;  // wave's W-row / token offsets
+    const int wn = (wave >> 1) * (BN / 2), wm = (wave & 1) * 64;  // wave's W-row / token offsets
     const int l16 = lane & 15, q = lane >> 4;
-    f32x4 acc[4][4];
+    f32x4 acc[TI][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) acc[i][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // magic 0x64006400 in a VGPR (the VOP3 constant bus takes one SGPR: the mask)
     const uint32_t magic = __builtin_amdgcn_readfirstlane(0x64006400u) + (uint32_t)(tid >> 16);
-    auto compute = [&](int G, int buf) {
-        half8 wlo[4], whi[4];
+    auto compute = [&](int G, int buf) __attribute__((always_inline)) {
+        half8 wlo[TI], whi[TI];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < TI; ++i) {
             const int row = wn + 16 * i + l16;
             const u32x2 wq = *reinterpret_cast<const u32x2 *>(&sRaw[row * kBlockBytes + 16 + 32 * G + 8 * q]);
             const u32x2 sp = *reinterpret_cast<const u32x2 *>(&sScl[row * SROW + 2 * G]);
@@ -211,7 +219,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__r
                 tb[jj] = *reinterpret_cast<const half8 *>(
                     &sA[buf][(wm + 16 * jj + l16) * AROW + 32 * h + 8 * q]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < TI; ++i)
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj)
                     acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(h ? whi[i] : wlo[i], tb[jj],
@@ -257,7 +265,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__r
         const int m = m0 + wm + 16 * jj + l16;
         if (m >= m_tokens) continue;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < TI; ++i) {
             const int r = n0 + wn + 16 * i + 4 * q;
             float *dst = c + (size_t)m * n + r;
             if (vec && r + 3 < n) {
@@ -271,15 +279,31 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__r
     }
 }
 
-hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n, int bpr,
-                           int m_tokens, hipStream_t stream) {
-    if (((uintptr_t)w & 15u) || ((uintptr_t)a & 15u)) return hipErrorInvalidValue;
-    const int tn = (n + gemm::BN - 1) / gemm::BN, tm = (m_tokens + gemm::BM - 1) / gemm::BM;
+template <int BN>
+static hipError_t gemm_launch_bn(const uint8_t *w, const uint16_t *a, float *c, int n, int bpr,
+                                 int m_tokens, hipStream_t stream) {
+    const int tn = (n + BN - 1) / BN, tm = (m_tokens + gemm::BM - 1) / gemm::BM;
     const long ntiles = (long)tn * tm;
     const long grid = (ntiles + gemm::NXCD - 1) / gemm::NXCD * gemm::NXCD;
     if (grid > 0x7FFFFFFFL) return hipErrorInvalidValue;
-    gemm_q4k_f16_kernel<<<(unsigned)grid, 256, 0, stream>>>(w, a, c, n, bpr, m_tokens, tn, tm);
+    gemm_q4k_f16_kernel<BN><<<(unsigned)grid, 256, 0, stream>>>(w, a, c, n, bpr, m_tokens, tn, tm);
     return hipGetLastError();
+}
+
+hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n, int bpr,
+                           int m_tokens, hipStream_t stream) {
+    if (((uintptr_t)w & 15u) || ((uintptr_t)a & 15u)) return hipErrorInvalidValue;
+    // 160-row tiles when 128-row tiles would spill into a second round of the
+    // two resident work-groups per CU and 160-row ones would not
+    static const int bn_env = [] {
+        const char *v = std::getenv("MGQ_GEMM_BN");
+        return (v && *v) ? std::atoi(v) : 0;
+    }();
+    const long tm = (m_tokens + gemm::BM - 1) / gemm::BM, slots = 2L * device_cus();
+    const long t128 = (n + 127) / 128 * tm, t160 = (n + 159) / 160 * tm;
+    const bool wide = bn_env ? bn_env == 160 : (t128 > slots && t160 <= slots);
+    return wide ? gemm_launch_bn<160>(w, a, c, n, bpr, m_tokens, stream)
+                : gemm_launch_bn<128>(w, a, c, n, bpr, m_tokens, stream);
 }
 
 }  // namespace mgq

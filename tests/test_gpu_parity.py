@@ -344,8 +344,10 @@ def test_matvec_batched_vector_alu_fallback(L, orc):
 
 
 # --------------------------------------------------------------------- GEMM --
+# (70000, 1, 16): 547 tiles of 128 rows but 438 of 160 for 512 resident
+# slots, so the 160-row tile runs; the others, ragged tiles of either height
 @pytest.mark.parametrize("n,bpr,m", [(64, 2, 8), (100, 14, 33), (256, 1, 1), (300, 5, 130),
-                                     (1030, 3, 257), (130, 9, 384)])
+                                     (1030, 3, 257), (130, 9, 384), (70000, 1, 16)])
 def test_gemm_f16_small(L, orc, n, bpr, m):
     note(f"gemm n={n} bpr={bpr} m={m}")
     w = orc.seeded_weight(61, n, bpr * 256)
