@@ -5,9 +5,8 @@
 // canonical dequantized value (gguf.rs:364-404) with d*sc and dmin*m rounded
 // to f16 and the weight itself computed and rounded in f16.
 //
-// Work-group tile: BN W rows x 128 tokens (BN = 128, or 160 when 128-row
-// tiles would leave a second, mostly empty round of the two resident
-// work-groups per CU), 4 wavefronts of BN/2 x 64 outputs (BN/32 x 4
+// Work-group tile: BN W rows x 128 tokens (BN = 128 or 160, whichever gives
+// the busiest CU fewer rows to compute), 4 wavefronts of BN/2 x 64 outputs (BN/32 x 4
 // v_mfma_f32_16x16x32_f16, W rows as the A operand, tokens as the B operand,
 // so a lane's 4 accumulators are 4 consecutive W rows of one token: one
 // 16-byte store into C's [M][N]).
@@ -293,15 +292,19 @@ static hipError_t gemm_launch_bn(const uint8_t *w, const uint16_t *a, float *c, 
 hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n, int bpr,
                            int m_tokens, hipStream_t stream) {
     if (((uintptr_t)w & 15u) || ((uintptr_t)a & 15u)) return hipErrorInvalidValue;
-    // 160-row tiles when 128-row tiles would spill into a second round of the
-    // two resident work-groups per CU and 160-row ones would not
+    // Tile height by the rows the busiest CU computes: ceil(tiles / #CUs) x
+    // BN, the lower one, ties to 160 (a second resident tile on a CU adds
+    // only part of a tile's throughput). Measured on 18944 x 3584 (us, 128 vs
+    // 160 rows): M = 256 80 / 65, 512 129 / 110, 640 136 / 145, 768 161 /
+    // 146, 1024 193 / 180. MGQ_GEMM_BN=128 or 160 forces one.
     static const int bn_env = [] {
         const char *v = std::getenv("MGQ_GEMM_BN");
         return (v && *v) ? std::atoi(v) : 0;
     }();
-    const long tm = (m_tokens + gemm::BM - 1) / gemm::BM, slots = 2L * device_cus();
-    const long t128 = (n + 127) / 128 * tm, t160 = (n + 159) / 160 * tm;
-    const bool wide = bn_env ? bn_env == 160 : (t128 > slots && t160 <= slots);
+    const long tm = (m_tokens + gemm::BM - 1) / gemm::BM, cus = device_cus();
+    const long c128 = ((n + 127) / 128 * tm + cus - 1) / cus * 128;
+    const long c160 = ((n + 159) / 160 * tm + cus - 1) / cus * 160;
+    const bool wide = bn_env ? bn_env == 160 : c160 <= c128;
     return wide ? gemm_launch_bn<160>(w, a, c, n, bpr, m_tokens, stream)
                 : gemm_launch_bn<128>(w, a, c, n, bpr, m_tokens, stream);
 }
