@@ -247,8 +247,9 @@ hipError_t mgq_chain_create(const mgq_gemv_desc *descs, int n, void **chain_out)
 hipError_t mgq_chain_launch(void *chain, hipStream_t stream);
 hipError_t mgq_chain_destroy(void *chain);
 
-/* Prepares the current device: sets the GEMV kernels' LDS attributes (every
- * launcher also does this on first use). Allocates nothing; the library keeps
+/* Prepares the current device: sets the GEMV kernels' LDS attributes, which
+ * belong to a device (every launcher also does this on its first use on a
+ * device). Allocates nothing; the library keeps
  * no device memory and no mutable device state, so launches on different
  * streams may run concurrently. Safe to call more than once. */
 hipError_t mgq_prepare(void);

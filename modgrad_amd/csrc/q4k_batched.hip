@@ -404,8 +404,8 @@ template <int R, int SETS, int PF>
 static hipError_t batched_main_launch(const uint8_t *w, const uint8_t *ws, float *Y, int n, int bpr,
                                       int batch, int kparts, hipStream_t stream) {
     auto kern = gemv_batched_mfma_kernel<R, SETS, PF>;
-    static const hipError_t attr = hipFuncSetAttribute(
-        (const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    static std::atomic<int> lds_state[64];
+    const hipError_t attr = allow_full_lds((const void *)kern, lds_state);
     if (attr != hipSuccess) return attr;
     constexpr int BP = 8 * SETS;
     constexpr size_t base = (size_t)R * ((9 * 8) | 1) * 16 + 2 * (size_t)8 * R * BP * 4;

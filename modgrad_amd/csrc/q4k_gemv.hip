@@ -777,10 +777,9 @@ struct GemvAct {
 // Allows the kernel the whole 160 KiB of gfx950 LDS (once per process).
 template <int R, int C, int NW, int PF, bool DB, int XIT, bool Q8, int FUSE>
 static hipError_t lds_attr() {
-    static const hipError_t attr = hipFuncSetAttribute(
-        (const void *)gemv_mfma_kernel<R, C, NW, PF, DB, XIT, Q8, FUSE>,
-        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    return attr;
+    static std::atomic<int> lds_state[64];
+    return allow_full_lds((const void *)gemv_mfma_kernel<R, C, NW, PF, DB, XIT, Q8, FUSE>,
+                          lds_state);
 }
 
 template <int R, int C, int NW, int PF, bool DB, bool Q8, int FUSE = 0>

@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 
 namespace mgq {
@@ -22,6 +23,20 @@ inline int device_cus() {
         cus[dev] = v;
     }
     return cus[dev];
+}
+
+// Allows `kern` the whole 160 KiB of gfx950 LDS. The attribute belongs to the
+// current device, so it is set once per (kernel, device); `state` is the
+// call site's per-device record (0 = not yet set, else hipError_t + 1).
+inline hipError_t allow_full_lds(const void *kern, std::atomic<int> (&state)[64]) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    int s = state[dev].load(std::memory_order_acquire);
+    if (s == 0) {
+        s = (int)hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) + 1;
+        state[dev].store(s, std::memory_order_release);
+    }
+    return (hipError_t)(s - 1);
 }
 
 // Row-group schedule of a persistent launch (G = gridDim.x work-groups). In

@@ -424,9 +424,8 @@ hipError_t q6m_launch(K kern, bool chunked, int nw, const uint8_t *w, const floa
 template <int NW, int XI>
 hipError_t q6m_long_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                            hipStream_t stream) {
-    static hipError_t attr = hipFuncSetAttribute((const void *)gemv_q6k_mfma_long_kernel<NW, XI>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 160 * 1024);
+    static std::atomic<int> lds_state[64];
+    hipError_t attr = allow_full_lds((const void *)gemv_q6k_mfma_long_kernel<NW, XI>, lds_state);
     static int occ = 0;
     // occupancy at the largest row this instance serves
     const int probe = std::min(XI * NW * 64 / 32, 100);
@@ -442,9 +441,8 @@ hipError_t gemv_q6k_mfma_launch(const uint8_t *w, const float *x, float *y, int 
     if ((((uintptr_t)w | (uintptr_t)x) & 15u) || (((long)n * bpr * BB) % 16))
         return hipErrorNotSupported;
     if (bpr <= MAX_BPR) {
-        static hipError_t attr = hipFuncSetAttribute((const void *)gemv_q6k_mfma_kernel,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                     160 * 1024);
+        static std::atomic<int> lds_state[64];
+        hipError_t attr = allow_full_lds((const void *)gemv_q6k_mfma_kernel, lds_state);
         static int occ = 0;
         return q6m_launch(gemv_q6k_mfma_kernel, false, NW, w, x, y, n, bpr, MAX_BPR, occ, attr,
                           stream);
