@@ -50,7 +50,7 @@ struct GemvSched {
     int lead, shared;
 };
 
-__device__ __forceinline__ int sched_group(const GemvSched &s, int b, int G, int j) {
+__host__ __device__ __forceinline__ int sched_group(const GemvSched &s, int b, int G, int j) {
     return j < s.shared ? b + j * G : s.shared * G + (j - s.shared) * s.lead + b;
 }
 
