@@ -141,30 +141,69 @@ def check_parity(torch, wl: Workload, rows: int = 256) -> str:
     return f"ok (max err/absdot {worst:.2e} <= 1e-4)"
 
 
-def cpu_baseline(torch, wl: Workload, target_s: float, threads: int, launches: int = 32):
-    """The reference CPU GEMV restated (oracle), on the first `launches`
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads() -> int:
+    """Threads for the multi-core leg: every core this process may run on
+    (its affinity set), capped at OMP_NUM_THREADS when that is set -- the GPU
+    boxes allot each GPU a share of the host's cores and set it there."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def cpu_baseline(torch, wl: Workload, target_s: float, threads: int, launches: int = 32,
+                 target_1t_s: float = 5.0):
+    """The reference CPU GEMV restated (oracle): kfd::llm::matvec
+    (llm.rs:468-534, rows in parallel as its rayon pool does, llm.rs:506-511)
+    with the AVX-512 dot (llm.rs:748-806). Timed on the first `launches`
     launches of the workload (8 decode layers = 1.05 GB, above any host
-    cache, so the CPU streams from DRAM like the GPU streams from HBM)."""
+    cache, so the CPU streams from DRAM like the GPU streams from HBM), on
+    `threads` threads and on one thread."""
     from oracle import oracle as orc
     sample = [(name, w.cpu().numpy(), x.cpu().numpy(), n, k)
               for name, w, x, _, n, k in wl.launches[:launches]]
     nbytes = sum(gemv_bytes(n, k) for _, _, _, n, k in sample)
     ys = [np.empty(n, np.float32) for _, _, _, n, _ in sample]
-    for (name, w, x, n, k), y in zip(sample, ys):  # warm-up
-        orc.cpu_matvec(w, x, y, n, k // BLOCK_ELEMS, threads)
-    reps, t_total = 0, 0.0
-    while t_total < target_s:
-        t = time.perf_counter()
-        for (name, w, x, n, k), y in zip(sample, ys):
-            orc.cpu_matvec(w, x, y, n, k // BLOCK_ELEMS, threads)
-        t_total += time.perf_counter() - t
-        reps += 1
-    gbs = nbytes * reps / t_total / 1e9
+
+    def timed(nthreads: int, budget: float):
+        for (name, w, x, n, k), y in zip(sample, ys):  # warm-up
+            orc.cpu_matvec(w, x, y, n, k // BLOCK_ELEMS, nthreads)
+        reps, t_total = 0, 0.0
+        while t_total < budget:
+            t = time.perf_counter()
+            for (name, w, x, n, k), y in zip(sample, ys):
+                orc.cpu_matvec(w, x, y, n, k // BLOCK_ELEMS, nthreads)
+            t_total += time.perf_counter() - t
+            reps += 1
+        return nbytes * reps / t_total / 1e9, reps, t_total
+
+    gbs, reps, t_total = timed(threads, target_s)
+    gbs1, reps1, t1 = timed(1, target_1t_s) if threads > 1 else (gbs, reps, t_total)
     names = f"{sample[0][0]}..{sample[-1][0]} ({len(sample)} launches)"
     return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{names}, {nbytes / 1e6:.1f} MB of Q4_K + activations, x {reps} passes, "
-                      f"{t_total:.1f} s; AVX-512={'yes' if orc.cpu_has_avx512() else 'no'}",
-            "tokens_per_s_equiv": round(gbs * 1e9 / wl.bytes_per_pass, 3)}
+                      f"{t_total:.1f} s on {threads} threads; 1 thread: x {reps1} passes, "
+                      f"{t1:.1f} s; AVX-512={'yes' if orc.cpu_has_avx512() else 'no'}",
+            "value_1thread": round(gbs1, 3),
+            "cpu_model": cpu_model(),
+            "host_logical_cpus": os.cpu_count(),
+            "tokens_per_s_equiv": round(gbs * 1e9 / wl.bytes_per_pass, 3),
+            "tokens_per_s_equiv_1thread": round(gbs1 * 1e9 / wl.bytes_per_pass, 4)}
 
 
 def time_captured(torch, launch, steps: int, warmup: int) -> float:
@@ -776,8 +815,8 @@ def main() -> int:
                      "avg_launch_us": round(avg_s * 1e6, 3), "avg_launch_bytes": int(avg_b)},
     }
     if not args.no_cpu:
-        threads = min(16, os.cpu_count() or 1)
-        log(f"cpu baseline ({threads} threads, ~{args.cpu_seconds:.0f} s)")
+        threads = cpu_threads()
+        log(f"cpu baseline ({threads} threads, ~{args.cpu_seconds:.0f} s, then 1 thread ~5 s)")
         out["cpu_baseline"] = cpu_baseline(torch, wl, args.cpu_seconds, threads)
     print(json.dumps(out), flush=True)
     return 0

@@ -3,7 +3,9 @@
 // Reference-compatible launchers keep the reference's conventions
 // (matvec_q4k.hip:110-124, dequant_q4k.hip:147-157): null stream, no
 // synchronization, hipErrorInvalidValue on non-positive sizes, otherwise the
-// launch status from hipGetLastError().
+// launch status from hipGetLastError(). Quantized weight bytes (and int8
+// activations) may start at any byte, as the reference's byte-reading
+// kernels allow; float pointers need float (4-byte) alignment, f16 ones 2.
 #include "../../include/modgrad_q4k.h"
 #include "q4k_launch.hpp"
 
@@ -23,7 +25,7 @@ extern "C" {
 hipError_t launch_dequant_q4k_ex(const unsigned char *q4k, int n_blocks, float *fp32_out,
                                  hipStream_t stream) {
     if (n_blocks <= 0 || !q4k || !fp32_out) return hipErrorInvalidValue;
-    if (misaligned4(q4k) || misaligned4(fp32_out)) return hipErrorInvalidValue;
+    if (misaligned4(fp32_out)) return hipErrorInvalidValue;
     if ((int64_t)n_blocks * 32 > kMaxI32 * 256LL) return hipErrorInvalidValue;
     return mgq::dequant_launch(q4k, n_blocks, fp32_out, stream);
 }
@@ -35,7 +37,7 @@ hipError_t launch_dequant_q4k(const unsigned char *q4k, int n_blocks, float *fp3
 hipError_t launch_matvec_q4k_ex(const unsigned char *w_q4, const float *x, float *y,
                                 int out_dim, int k_elems, int layout, hipStream_t stream) {
     if (out_dim <= 0 || k_elems <= 0 || !w_q4 || !x || !y) return hipErrorInvalidValue;
-    if (misaligned4(w_q4) || misaligned4(x) || misaligned4(y)) return hipErrorInvalidValue;
+    if (misaligned4(x) || misaligned4(y)) return hipErrorInvalidValue;
     if (layout == MGQ_LAYOUT_ROWS) {
         if (k_elems % 256 != 0) return hipErrorInvalidValue;
         return mgq::gemv_rows_launch(w_q4, x, y, out_dim, k_elems / 256, stream);
@@ -69,7 +71,7 @@ hipError_t launch_matvec_q4k_batched(const unsigned char *w_q4, const float *X, 
                                      void *workspace, size_t workspace_bytes,
                                      hipStream_t stream) {
     if (out_dim <= 0 || blocks_per_row <= 0 || batch <= 0 || batch > 16) return hipErrorInvalidValue;
-    if (!w_q4 || !X || !Y || misaligned4(w_q4) || misaligned4(X) || misaligned4(Y))
+    if (!w_q4 || !X || !Y || misaligned4(X) || misaligned4(Y))
         return hipErrorInvalidValue;
     if ((int64_t)blocks_per_row * 256 > kMaxI32) return hipErrorInvalidValue;
     if (!workspace || workspace_bytes < mgq::batched_workspace_bytes(blocks_per_row, batch))
@@ -85,8 +87,7 @@ hipError_t launch_matvec_q4k_batched(const unsigned char *w_q4, const float *X, 
 hipError_t launch_quantize_q8_1_ex(const float *x, signed char *xq, float *xd, float *xsum, int n,
                                    hipStream_t stream) {
     if (n < 32) return hipErrorInvalidValue;
-    if (!x || !xq || !xd || !xsum || misaligned4(x) || misaligned4(xq) || misaligned4(xd) ||
-        misaligned4(xsum))
+    if (!x || !xq || !xd || !xsum || misaligned4(x) || misaligned4(xd) || misaligned4(xsum))
         return hipErrorInvalidValue;
     return mgq::quantize_q8_1_launch(x, reinterpret_cast<int8_t *>(xq), xd, xsum, n, stream);
 }
@@ -99,8 +100,7 @@ hipError_t launch_matvec_q4k_dp4a_ex(const unsigned char *w, const signed char *
                                      const float *xd, const float *xsum, float *y, int out_dim,
                                      int bpr, hipStream_t stream) {
     if (out_dim <= 0 || bpr <= 0) return hipErrorInvalidValue;
-    if (!w || !xq || !xd || !xsum || !y || misaligned4(w) || misaligned4(xq) || misaligned4(xd) ||
-        misaligned4(xsum) || misaligned4(y))
+    if (!w || !xq || !xd || !xsum || !y || misaligned4(xd) || misaligned4(xsum) || misaligned4(y))
         return hipErrorInvalidValue;
     if ((int64_t)bpr * 256 > kMaxI32) return hipErrorInvalidValue;
     return mgq::gemv_q8_launch(w, reinterpret_cast<const int8_t *>(xq), xd, xsum, y, out_dim, bpr,
@@ -124,7 +124,7 @@ hipError_t launch_quantize_matvec_q4k_dp4a_ex(const unsigned char *w, const floa
                                               int out_dim, int bpr, hipStream_t stream) {
     if (out_dim <= 0 || bpr <= 0 || !w || !x || !y) return hipErrorInvalidValue;
     if ((int64_t)bpr * 256 > kMaxI32) return hipErrorInvalidValue;
-    if ((((uintptr_t)w | (uintptr_t)x) & 15u) || misaligned4(y)) return hipErrorInvalidValue;
+    if (misaligned4(x) || misaligned4(y)) return hipErrorInvalidValue;
     return mgq::gemv_q8x_launch(w, x, y, out_dim, bpr, stream);
 }
 
@@ -170,7 +170,7 @@ hipError_t launch_gemm_q4k_f16(const unsigned char *w_q4, const uint16_t *a_f16,
                                int out_dim, int blocks_per_row, int m_tokens,
                                hipStream_t stream) {
     if (out_dim <= 0 || blocks_per_row <= 0 || m_tokens <= 0) return hipErrorInvalidValue;
-    if (!w_q4 || !a_f16 || !c || misaligned4(w_q4) || misaligned4(a_f16) || misaligned4(c))
+    if (!w_q4 || !a_f16 || !c || ((uintptr_t)a_f16 & 1u) || misaligned4(c))
         return hipErrorInvalidValue;
     if ((int64_t)blocks_per_row * 256 > kMaxI32) return hipErrorInvalidValue;
     return mgq::gemm_f16_launch(w_q4, a_f16, c, out_dim, blocks_per_row, m_tokens, stream);
@@ -279,17 +279,13 @@ hipError_t launch_scale_ex(float *h, float s, int n, hipStream_t stream) {
 
 hipError_t launch_scale(float *h, float s, int n) { return launch_scale_ex(h, s, n, nullptr); }
 
-namespace {
-bool misaligned16(const void *p) { return ((uintptr_t)p & 15u) != 0; }
-}  // namespace
-
 hipError_t launch_matvec_q4k_rmsnorm_ex(const unsigned char *w_q4, const float *x,
                                         const float *norm_w, float eps, float *y, int out_dim,
                                         int blocks_per_row, hipStream_t stream) {
     if (out_dim <= 0 || blocks_per_row <= 0 || !w_q4 || !x || !norm_w || !y)
         return hipErrorInvalidValue;
     if ((int64_t)blocks_per_row * 256 > kMaxI32) return hipErrorInvalidValue;
-    if (misaligned16(w_q4) || misaligned16(x) || misaligned16(norm_w) || misaligned4(y))
+    if (misaligned4(x) || misaligned4(norm_w) || misaligned4(y))
         return hipErrorInvalidValue;
     return mgq::gemv_fused_launch(w_q4, nullptr, x, norm_w, eps, MGQ_ACT_GELU_TANH, y, out_dim,
                                   blocks_per_row, stream);
@@ -303,8 +299,7 @@ hipError_t launch_matvec_q4k_glu_ex(const unsigned char *w_gate, const unsigned 
         return hipErrorInvalidValue;
     if (act != MGQ_ACT_GELU_TANH && act != MGQ_ACT_SILU) return hipErrorInvalidValue;
     if ((int64_t)blocks_per_row * 256 > kMaxI32) return hipErrorInvalidValue;
-    if (misaligned16(w_gate) || misaligned16(w_up) || misaligned16(x) ||
-        (norm_w && misaligned16(norm_w)) || misaligned4(y))
+    if (misaligned4(x) || (norm_w && misaligned4(norm_w)) || misaligned4(y))
         return hipErrorInvalidValue;
     return mgq::gemv_fused_launch(w_gate, w_up, x, norm_w, eps, act, y, out_dim, blocks_per_row,
                                   stream);

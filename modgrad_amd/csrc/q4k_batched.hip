@@ -99,8 +99,8 @@ __global__ __launch_bounds__(256) void batched_table_kernel(const float *__restr
     if (b < batch) {
         const float *xp = X + (size_t)b * K + (size_t)j * kBlockElems + ch * 8;
         if (x_aligned16) {
-            const f32x4 a = *reinterpret_cast<const f32x4 *>(xp);
-            const f32x4 c = *reinterpret_cast<const f32x4 *>(xp + 4);
+            const f32x4 a = ld_f32x4(xp);
+            const f32x4 c = ld_f32x4(xp + 4);
             v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
             v[4] = c[0]; v[5] = c[1]; v[6] = c[2]; v[7] = c[3];
         } else {
@@ -233,7 +233,7 @@ __global__ __launch_bounds__(512) void gemv_batched_mfma_kernel(const uint8_t *_
         for (int k = 0; k < IPW; ++k) {
             const uint32_t rr = std::min(r0 + prow[k], rlast);
             const uint32_t col = std::min(tcol + pcol[k], plast[k]);
-            dst[k] = *reinterpret_cast<const u32x4 *>(w + (uint64_t)rr * rb + col);
+            dst[k] = ld_u32x4(w + (uint64_t)rr * rb + col);
         }
     };
     auto lstore = [&](const u32x4(&src)[IPW]) {
@@ -429,7 +429,7 @@ hipError_t gemv_batched_mfma_launch(const uint8_t *w, const float *X, float *Y, 
                                     hipStream_t stream) {
     const int sets = (batch + 7) / 8;
     if (workspace_bytes < batched_ws(bpr, sets).total) return hipErrorInvalidValue;
-    if (((uintptr_t)w & 15u) || ((uintptr_t)workspace & 15u)) return hipErrorNotSupported;
+    if ((uintptr_t)workspace & 15u) return hipErrorNotSupported;
     uint8_t *ws = static_cast<uint8_t *>(workspace);
     // Few row groups and a long K (ffn_down): 32-row groups, K split in two,
     // so every CU is busy and each work-group reads the operand table for 32

@@ -55,9 +55,29 @@ __device__ __forceinline__ uint32_t mins4(int j, uint32_t s1, uint32_t s2) {
                   : (((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u));
 }
 
+// Loads of caller data at any byte alignment. The reference reads weight
+// bytes one at a time and accepts any address (matvec_q4k.hip:66-96), and its
+// engine packs tensors back to back in one arena (rocm_gemma.rs:214-215), so
+// a tensor can start at any byte. The types below carry alignment 1 (floats:
+// 4); for gfx950 under the HSA ABI, which runs with unaligned access enabled,
+// the compiler still emits single global_load_dword / _dwordx4 instructions,
+// so an aligned pointer costs nothing extra and a misaligned one stays
+// correct.
+typedef uint32_t u32_a1 __attribute__((aligned(1)));
+typedef uint32_t u32x4_a1 __attribute__((ext_vector_type(4), aligned(1)));
+typedef uint32_t u32x2_a1 __attribute__((ext_vector_type(2), aligned(1)));
+typedef float f32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
 __device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) {
-    return *reinterpret_cast<const uint32_t *>(p);
+    return *reinterpret_cast<const u32_a1 *>(p);
 }
+__device__ __forceinline__ u32x4 ld_u32x4(const void *p) {
+    return *reinterpret_cast<const u32x4_a1 *>(p);
+}
+__device__ __forceinline__ f32x4 ld_f32x4(const float *p) {
+    return *reinterpret_cast<const f32x4_a4 *>(p);
+}
+__device__ __forceinline__ void st_u32(void *p, uint32_t v) { *reinterpret_cast<u32_a1 *>(p) = v; }
 
 // v from lane (lane ^ MASK) within each group of 4 lanes (DPP quad_perm).
 template <int MASK>

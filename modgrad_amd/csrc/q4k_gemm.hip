@@ -142,7 +142,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__r
     auto rload = [&](int b) __attribute__((always_inline)) {  // piece 4 is loaded by every lane (clamped address): no branch
 #pragma unroll
         for (int k = 0; k < NPL; ++k)
-            R[k] = *reinterpret_cast<const u32x4 *>(rsrc[k] + (size_t)b * kBlockBytes);
+            R[k] = ld_u32x4(rsrc[k] + (size_t)b * kBlockBytes);
     };
     auto rstore = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -179,7 +179,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__r
     auto aload = [&](int t, int set) __attribute__((always_inline)) {
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-            Areg[set][k] = *reinterpret_cast<const u32x4 *>(asrc[k] + (size_t)t * BK);
+            Areg[set][k] = ld_u32x4(asrc[k] + (size_t)t * BK);
     };
     auto astore = [&](int set, int buf) __attribute__((always_inline)) {
 #pragma unroll
@@ -291,7 +291,7 @@ static hipError_t gemm_launch_bn(const uint8_t *w, const uint16_t *a, float *c, 
 
 hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n, int bpr,
                            int m_tokens, hipStream_t stream) {
-    if (((uintptr_t)w & 15u) || ((uintptr_t)a & 15u)) return hipErrorInvalidValue;
+    if ((uintptr_t)a & 1u) return hipErrorInvalidValue;
     // Tile height by the rows the busiest CU computes: ceil(tiles / #CUs) x
     // BN, the lower one, ties to 160 (a second resident tile on a CU adds
     // only part of a tile's throughput). Measured on 18944 x 3584 (us, 128 vs

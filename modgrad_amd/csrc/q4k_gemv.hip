@@ -108,20 +108,20 @@ __global__ __launch_bounds__(256) void gemv_flat_kernel(const uint8_t *__restric
     for (int r = 0; r < U; ++r) acc[r] = 0.0f;
     for (int bl = bi; bl < nb; bl += 8) {
         const uint8_t *blk = w + (ub + bl) * kBlockBytes;
-        const u32x4 hd = *reinterpret_cast<const u32x4 *>(blk);
-        const u32x4 qs = *reinterpret_cast<const u32x4 *>(blk + 16 + 16 * j);
+        const u32x4 hd = ld_u32x4(blk);
+        const u32x4 qs = ld_u32x4(blk + 16 + 16 * j);
         const float d = half_bits_finite(hd[0]), dmin = half_bits_finite(hd[0] >> 16);
         uint32_t sc_lo, m_lo, sc_hi, m_hi;
         scale_min(2 * G, hd[1], hd[2], hd[3], sc_lo, m_lo);
         scale_min(2 * G + 1, hd[1], hd[2], hd[3], sc_hi, m_hi);
         const int f_lo = 256 * bl + 64 * G + 16 * (j & 1);  // unit-relative flat index
         const int r_lo = f_lo / k, r_hi = (f_lo + 32) / k;
-        const f32x4 *xl = reinterpret_cast<const f32x4 *>(x + (f_lo - r_lo * k));
-        const f32x4 *xh = reinterpret_cast<const f32x4 *>(x + (f_lo + 32 - r_hi * k));
+        const float *xl = x + (f_lo - r_lo * k);
+        const float *xh = x + (f_lo + 32 - r_hi * k);
         float dl = 0.0f, sl = 0.0f, dh = 0.0f, sh = 0.0f;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const f32x4 a = xl[c], b = xh[c];
+            const f32x4 a = ld_f32x4(xl + 4 * c), b = ld_f32x4(xh + 4 * c);
             const uint32_t v = qs[c];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void gemv_flat_kernel(const uint8_t *__restric
 
 hipError_t gemv_flat_launch(const uint8_t *w, const float *x, float *y, int n, int k,
                             hipStream_t stream) {
-    if (k % 32 != 0 || (((uintptr_t)w | (uintptr_t)x) & 15u)) return hipErrorNotSupported;
+    if (k % 32 != 0) return hipErrorNotSupported;
     int g = 256;
     while (k % g) g >>= 1;  // gcd(k, 256), >= 32 here
     const int U = 256 / g;
@@ -194,7 +194,8 @@ __device__ __forceinline__ int pair_byte_offset(int p, int h) {
 //   stage 2 (1 if bpr <= C) x SB bytes: weight bytes of R rows x C blocks,
 //         row-major over (row, block, 16-byte piece), rows padded to an odd
 //         number of pieces
-//   aux   NW*32*4 B: cross-wave reduction buffer (32 row sums per wavefront)
+//   aux   2 x NW*32*4 B: cross-wave reduction buffers (32 row sums per
+//         wavefront), alternating by row group
 //   ybuf  rounds x R row results (x2 with kFuseGlu: gate and up)
 //   normp 16 f32 sum(x^2) partials (kFuseNorm only)
 struct MfmaLayout {
@@ -248,7 +249,7 @@ __host__ __device__ inline MfmaLayout mfma_layout(int bpr, int R, int C, int NW,
     L.stage_bytes = (uint32_t)(R * stage_row_pieces(C, bp) * 16);
     // two stage buffers when double-buffered and K needs more than one stage
     L.aux = L.stage + ((db && bpr > C) ? 2u : 1u) * L.stage_bytes;
-    L.ybuf = L.aux + (uint32_t)NW * 128u;
+    L.ybuf = L.aux + (uint32_t)NW * 256u;
     // kFuseGlu: gate and up results of every row group (2x rounds);
     // kFuseNorm: one sum(x^2) partial per wavefront
     const int vm = (fuse & kFuseGlu) ? 2 : 1;
@@ -344,7 +345,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
             const uint32_t rr = std::min(r0 + prow[k], rlast);
             const uint32_t col = std::min(tcol + pcol[k], plast[k]);
             const uint64_t off = (uint64_t)rr * rb + col;  // one v_mad_u64_u32
-            dst[k] = *reinterpret_cast<const u32x4 *>(wm + off);
+            dst[k] = ld_u32x4(wm + off);
         }
     };
     auto lstore = [&](int buf, const u32x4(&src)[IPW]) {
@@ -370,8 +371,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     for (int it = 0; it < XIT; ++it) {
         if (it >= its) break;
         const int i = std::min(tid + it * NW * 64, nitems - 1);
-        xv0[it] = *reinterpret_cast<const f32x4 *>(x + (size_t)i * 8);
-        xv1[it] = *reinterpret_cast<const f32x4 *>(x + (size_t)i * 8 + 4);
+        xv0[it] = ld_f32x4(x + (size_t)i * 8);
+        xv1[it] = ld_f32x4(x + (size_t)i * 8 + 4);
     }
 #pragma unroll
     for (int f = 0; f < PF; ++f) gload(f, stg[f]);
@@ -425,7 +426,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         const uint8_t *src = i < nq ? reinterpret_cast<const uint8_t *>(xq) + (size_t)i * 16
                            : i < nq + 2 * bpr ? reinterpret_cast<const uint8_t *>(xdv + (size_t)(i - nq) * 4)
                                               : reinterpret_cast<const uint8_t *>(xsv + (size_t)(i - nq - 2 * bpr) * 4);
-        cv[it] = *reinterpret_cast<const u32x4 *>(src);
+        cv[it] = ld_u32x4(src);
     }
 #pragma unroll
     for (int f = 0; f < PF; ++f) gload(f, stg[f]);
@@ -450,11 +451,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     for (int it = 0; it < XIT; ++it) {
         if (it >= its) break;
         const int i = std::min(tid + it * NW * 64, nitems - 1);
-        xv0[it] = *reinterpret_cast<const f32x4 *>(x + (size_t)i * 8);
-        xv1[it] = *reinterpret_cast<const f32x4 *>(x + (size_t)i * 8 + 4);
+        xv0[it] = ld_f32x4(x + (size_t)i * 8);
+        xv1[it] = ld_f32x4(x + (size_t)i * 8 + 4);
         if constexpr (NORM) {
-            nv0[it] = *reinterpret_cast<const f32x4 *>(fz.nw + (size_t)i * 8);
-            nv1[it] = *reinterpret_cast<const f32x4 *>(fz.nw + (size_t)i * 8 + 4);
+            nv0[it] = ld_f32x4(fz.nw + (size_t)i * 8);
+            nv1[it] = ld_f32x4(fz.nw + (size_t)i * 8 + 4);
         }
     }
     float ssq = 0.0f;  // kFuseNorm: this lane's sum of x^2
@@ -685,6 +686,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
           }
         }
         const bool group_end = (t == stages - 1);
+        // The row group's aux buffer alternates with the group's parity. With
+        // one stage per group the next group's sums are written before any
+        // barrier of its step, while the first R threads may still be reading
+        // this group's: the buffer they read is the other one, and reusing it
+        // two groups later is ordered by the barrier between.
+        float *auxg = aux + ((q / stages) & 1) * (NW * 32);
         if (group_end) {
             // sum the 4 lanes (g = 0..3) of each row, then one value per row
             // and tile into aux (free after the prologue)
@@ -693,8 +700,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
             yaccB += __shfl_xor(yaccB, 16, 64);
             yaccB += __shfl_xor(yaccB, 32, 64);
             if (lane < 16) {
-                aux[wave * 32 + lane] = yaccA;
-                aux[wave * 32 + 16 + lane] = yaccB;
+                auxg[wave * 32 + lane] = yaccA;
+                auxg[wave * 32 + 16 + lane] = yaccB;
             }
         }
         if (more) {
@@ -704,11 +711,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         }
         __syncthreads();
         if (group_end) {
-            // cross-wave reduction of this row group; the next group's
-            // reduction writes aux only after at least one more barrier
+            // cross-wave reduction of this row group (its own aux buffer)
             if (tid < R) {
                 float sum = 0.0f;
-                for (int wv = 0; wv < NW; ++wv) sum += aux[wv * 32 + tid];
+                for (int wv = 0; wv < NW; ++wv) sum += auxg[wv * 32 + tid];
                 reinterpret_cast<float *>(lds + Lo.ybuf)[(q / stages) * R + tid] = sum;
             }
             yaccA = 0.0f;
@@ -920,8 +926,6 @@ static hipError_t mfma_dispatch(const uint8_t *w, const GemvAct &a, float *y, in
 hipError_t gemv_fused_launch(const uint8_t *w_gate, const uint8_t *w_up, const float *x,
                              const float *norm_w, float eps, int act, float *y, int n, int bpr,
                              hipStream_t stream) {
-    if (((uintptr_t)w_gate | (uintptr_t)w_up | (uintptr_t)x | (uintptr_t)norm_w) & 15u)
-        return hipErrorNotSupported;
     const GemvAct a{x, nullptr, nullptr, nullptr};
     const GemvFuse fz{w_up, norm_w, eps, act};
     if (w_up == nullptr) {
@@ -935,30 +939,24 @@ hipError_t gemv_fused_launch(const uint8_t *w_gate, const uint8_t *w_up, const f
 
 hipError_t gemv_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                             hipStream_t stream) {
-    if (((uintptr_t)w & 15u) || ((uintptr_t)x & 15u)) return hipErrorNotSupported;
     return mfma_dispatch<false>(w, GemvAct{x, nullptr, nullptr, nullptr}, y, n, bpr, stream);
 }
 
 hipError_t gemv_q5k_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                                 hipStream_t stream) {
-    if (((uintptr_t)w | (uintptr_t)x) & 15u) return hipErrorNotSupported;
     return mfma_dispatch<false, kFmtQ5K>(w, GemvAct{x, nullptr, nullptr, nullptr}, y, n, bpr, stream);
 }
 
 hipError_t gemv_q8x_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                            hipStream_t stream) {
-    if (((uintptr_t)w | (uintptr_t)x) & 15u) return hipErrorNotSupported;
     return mfma_dispatch<true, kFuseQuant>(w, GemvAct{x, nullptr, nullptr, nullptr}, y, n, bpr,
                                            stream);
 }
 
 hipError_t gemv_q8_launch(const uint8_t *w, const int8_t *xq, const float *xd, const float *xsum,
                           float *y, int n, int bpr, hipStream_t stream) {
-    const bool aligned = !(((uintptr_t)w | (uintptr_t)xq | (uintptr_t)xd | (uintptr_t)xsum) & 15u);
-    if (aligned) {
-        const hipError_t e = mfma_dispatch<true>(w, GemvAct{nullptr, xq, xd, xsum}, y, n, bpr, stream);
-        if (e != hipErrorNotSupported) return e;
-    }
+    const hipError_t e = mfma_dispatch<true>(w, GemvAct{nullptr, xq, xd, xsum}, y, n, bpr, stream);
+    if (e != hipErrorNotSupported) return e;
     return gemv_q8_generic_launch(w, xq, xd, xsum, y, n, bpr, stream);
 }
 

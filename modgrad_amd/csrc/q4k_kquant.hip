@@ -11,13 +11,12 @@
 //   Q6_K, 210 B / 256 values: ql[128] | qh[64] | int8 scales[16] | d f16;
 //     q = (nibble | 2 qh bits << 4) - 32, one scale per 16 values.
 //
-// Vector-ALU kernels, one wavefront per row. gemv_q5k_kernel,
-// gemv_q6k_kernel and gemv_q6k_q8_kernel read bytes: lane l owns positions
-// l, l+64, l+128, l+192 of every block, so each byte array of a block is read
-// by the wavefront as consecutive bytes and the activations as consecutive
-// floats; they serve any 2-byte alignment. For 16-byte aligned Q6_K weights
-// and x, gemv_q6k_staged_kernel streams whole 16-byte chunks through LDS
-// instead.
+// Vector-ALU kernels, one wavefront per row. gemv_q5k_kernel and
+// gemv_q6k_q8_kernel read bytes: lane l owns positions l, l+64, l+128, l+192
+// of every block, so each byte array of a block is read by the wavefront as
+// consecutive bytes and the activations as consecutive floats; they serve any
+// alignment. gemv_q6k_staged_kernel streams Q6_K rows as whole 16-byte
+// chunks through LDS (the fallback behind the matrix-core Q6_K kernels).
 #include "q4k_device.hpp"
 #include "q4k_launch.hpp"
 
@@ -72,43 +71,10 @@ __global__ __launch_bounds__(256) void gemv_q5k_kernel(const uint8_t *__restrict
     if (lane == 0) y[row] = acc;
 }
 
-__global__ __launch_bounds__(256) void gemv_q6k_kernel(const uint8_t *__restrict__ w,
-                                                       const float *__restrict__ x,
-                                                       float *__restrict__ y, int n, int bpr) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= n) return;
-    const uint8_t *wr = w + (size_t)row * bpr * kQ6Bytes;
-    const int l31 = lane & 31, hi32 = lane >> 5;
-    float acc = 0.0f;
-    for (int b = 0; b < bpr; ++b) {
-        const uint8_t *blk = wr + (size_t)b * kQ6Bytes;
-        const float d = half_at(blk + 208);
-        const int8_t *sc = reinterpret_cast<const int8_t *>(blk + 192);
-        const float *xb = x + (size_t)b * kBlockElems + lane;
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            // positions 128g + lane (quad = hi32, low nibble) and
-            // 128g + 64 + lane (quad = 2 + hi32, high nibble) share ql[64g + lane]
-            const uint32_t qb = blk[64 * g + lane];
-            const uint32_t hb = blk[128 + 32 * g + l31];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int quad = hi32 + 2 * h;
-                const int q = (int)(((h ? (qb >> 4) : (qb & 15u)) | (((hb >> (2 * quad)) & 3u) << 4))) - 32;
-                const float s = (float)sc[8 * g + (l31 >> 4) + 2 * quad];
-                acc += (d * s) * (float)q * xb[128 * g + 64 * h];
-            }
-        }
-    }
-    acc = wave_sum(acc);
-    if (lane == 0) y[row] = acc;
-}
-
 // Q6_K on Q8_1 activations: y[r] = sum_s xd[s]*d*(sc_lo*isum_lo + sc_hi*isum_hi),
 // isum over the 16-value halves of sub-block s (exact integer dots). Lane l
-// owns the same positions as above; the 16 lanes of a half combine their
-// integer products with xor shuffles, so the dots stay exact.
+// owns positions l, l+64, l+128, l+192 of every block; the 16 lanes of a half
+// combine their integer products with xor shuffles, so the dots stay exact.
 __global__ __launch_bounds__(256) void gemv_q6k_q8_kernel(const uint8_t *__restrict__ w,
                                                           const int8_t *__restrict__ xq,
                                                           const float *__restrict__ xd,
@@ -163,7 +129,8 @@ __global__ __launch_bounds__(256) void gemv_q6k_q8_kernel(const uint8_t *__restr
 // with scales sc[P/16] and sc[P/16 + 4]. Blocks are only 2-byte aligned, so a
 // dword is read as the aligned pair around it (ds_read2_b32) and shifted into
 // place (v_alignbyte_b32). y[r] = sum d*(sc_lo*(sum q x - 32 sum x) + ...).
-// Needs w and x 16-byte aligned; the tensor's last row, whose final chunk
+// Takes any w (windows start at the 16-byte boundary at or below the
+// segment) and float-aligned x; the tensor's last row, whose final chunk
 // would reach past the tensor when its end is not 16-byte aligned, is decoded
 // with byte loads instead.
 constexpr int kQ6Seg = 14;  // blocks per segment: 2940 B window per wavefront
@@ -249,8 +216,8 @@ __global__ __launch_bounds__(256) void gemv_q6k_staged_kernel(const uint8_t *__r
                 const float sl = (float)(int8_t)win[si], sh = (float)(int8_t)win[si + 4];
                 const float d = half_bits_finite((uint32_t)win[bo + 208] | ((uint32_t)win[bo + 209] << 8));
                 const float *xb = x + (size_t)(s * SEG + bb) * kBlockElems + 128 * g + 4 * (l2 & 15);
-                const f32x4 xl = *reinterpret_cast<const f32x4 *>(xb);
-                const f32x4 xh = *reinterpret_cast<const f32x4 *>(xb + 64);
+                const f32x4 xl = ld_f32x4(xb);
+                const f32x4 xh = ld_f32x4(xb + 64);
                 const uint32_t lo = (ql & 0x0F0F0F0Fu) | (((qh >> (2 * q0)) & 0x03030303u) << 4);
                 const uint32_t hi = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * q0 + 4)) & 0x03030303u) << 4);
                 float dl = 0.0f, dh = 0.0f;
@@ -285,10 +252,10 @@ hipError_t gemv_q6k_launch(const uint8_t *w, const float *x, float *y, int n, in
                            hipStream_t stream) {
     const hipError_t e = gemv_q6k_mfma_launch(w, x, y, n, bpr, stream);
     if (e != hipErrorNotSupported) return e;
-    if ((((uintptr_t)w | (uintptr_t)x) & 15u) == 0)
-        gemv_q6k_staged_kernel<<<(unsigned)((n + 3) / 4), 256, 0, stream>>>(w, x, y, n, bpr);
-    else
-        gemv_q6k_kernel<<<(unsigned)((n + 3) / 4), 256, 0, stream>>>(w, x, y, n, bpr);
+    // the staged kernel reads 16-byte windows aligned below each segment and
+    // byte-decodes the tensor's last row when the tensor end is misaligned,
+    // so it takes any w; x needs only float alignment
+    gemv_q6k_staged_kernel<<<(unsigned)((n + 3) / 4), 256, 0, stream>>>(w, x, y, n, bpr);
     return hipGetLastError();
 }
 

@@ -1,6 +1,6 @@
 // Q6_K matvec on the gfx950 matrix cores (launch_matvec_q6k, rocm.rs:482-485;
 // canonical order of dequantize_row_q6_k, gguf.rs:441-477), for 16-byte
-// aligned weights and x. Two kernels share the decode: whole-row stages for
+// aligned weights and float-aligned x. Two kernels share the decode: whole-row stages for
 // K <= kQ6mMaxBpr * 256 (attention, lm_head) and K-chunked per-row stages for
 // longer rows (ffn_down).
 //
@@ -266,8 +266,8 @@ __global__ __launch_bounds__(q6m::NT) void gemv_q6k_mfma_kernel(const uint8_t *_
     // bpr <= 14 makes it at most one item per thread
     const int nitems = bpr * 32;
     const int ii = min(tid, nitems - 1);
-    const f32x4 v0 = *reinterpret_cast<const f32x4 *>(x + (size_t)ii * 8);
-    const f32x4 v1 = *reinterpret_cast<const f32x4 *>(x + (size_t)ii * 8 + 4);
+    const f32x4 v0 = ld_f32x4(x + (size_t)ii * 8);
+    const f32x4 v1 = ld_f32x4(x + (size_t)ii * 8 + 4);
     gload(0);
     q6m_item(lds, meta, tid, tid < nitems, v0, v1);
     lstore();
@@ -352,8 +352,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_mfma_long_kernel(const uint8
 #pragma unroll
     for (int k = 0; k < XI; ++k) {
         const int ii = min(tid + k * NT, nitems - 1);
-        xv[2 * k] = *reinterpret_cast<const f32x4 *>(x + (size_t)ii * 8);
-        xv[2 * k + 1] = *reinterpret_cast<const f32x4 *>(x + (size_t)ii * 8 + 4);
+        xv[2 * k] = ld_f32x4(x + (size_t)ii * 8);
+        xv[2 * k + 1] = ld_f32x4(x + (size_t)ii * 8 + 4);
     }
     gload(0);
 #pragma unroll
@@ -438,7 +438,9 @@ hipError_t q6m_long_launch(const uint8_t *w, const float *x, float *y, int n, in
 hipError_t gemv_q6k_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                                 hipStream_t stream) {
     using namespace q6m;
-    if ((((uintptr_t)w | (uintptr_t)x) & 15u) || (((long)n * bpr * BB) % 16))
+    // whole 16-byte chunks from w up to the tensor end: w 16-byte aligned and
+    // a tensor size that is a multiple of 16 (x needs only float alignment)
+    if (((uintptr_t)w & 15u) || (((long)n * bpr * BB) % 16))
         return hipErrorNotSupported;
     if (bpr <= MAX_BPR) {
         static std::atomic<int> lds_state[64];

@@ -27,7 +27,7 @@ __global__ __launch_bounds__(256) void quantize_q8_1_kernel(const float *__restr
     if (live) {
         const float *xp = x + (size_t)s * 32 + part * 4;
         if (aligned16) {
-            const f32x4 a = *reinterpret_cast<const f32x4 *>(xp);
+            const f32x4 a = ld_f32x4(xp);
             v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
         } else {
             v[0] = xp[0]; v[1] = xp[1]; v[2] = xp[2]; v[3] = xp[3];
@@ -57,7 +57,7 @@ __global__ __launch_bounds__(256) void quantize_q8_1_kernel(const float *__restr
     sum += __shfl_xor(sum, 2, 64);
     sum += __shfl_xor(sum, 4, 64);
     if (!live) return;
-    *reinterpret_cast<uint32_t *>(xq + (size_t)s * 32 + part * 4) = packed;
+    st_u32(xq + (size_t)s * 32 + part * 4, packed);
     if (part == 0) {
         xd[s] = d;
         xsum[s] = (float)sum;
@@ -98,7 +98,7 @@ __global__ __launch_bounds__(256) void gemv_q8_generic_kernel(const uint8_t *__r
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const uint32_t nib = (ld_u32(qs + 4 * j) >> shift) & 0x0F0F0F0Fu;
-            isum = __builtin_amdgcn_sdot4((int)nib, *reinterpret_cast<const int *>(xv + 4 * j), isum,
+            isum = __builtin_amdgcn_sdot4((int)nib, (int)ld_u32(reinterpret_cast<const uint8_t *>(xv) + 4 * j), isum,
                                           false);
         }
         acc += xd[s] * (d * (float)sc * (float)isum - dmin * (float)m * xsum[s]);

@@ -524,6 +524,27 @@ class GpuVec:
         return GpuVec(heap=self.copy_to_host())
 
 
+# Where the reference quantizer takes sub-block `is` of each 256-element block
+# from: elements start[is] .. start[is] + 31 (gguf.rs:590-601, its "legacy"
+# order), while every decoder -- the reference's own host dequantize_row_q4_k
+# (gguf.rs:364-404), its CPU matvec (llm.rs:684-806) and this library -- puts
+# sub-block is at elements 32*is .. 32*is + 31 (canonical ggml order).
+LEGACY_SUBBLOCK_START = (0, 128, 32, 160, 64, 192, 96, 224)
+_LEGACY_POS = np.concatenate([np.arange(s, s + 32) for s in LEGACY_SUBBLOCK_START])
+
+
+def legacy_quantizer_input(weight) -> np.ndarray:
+    """The flattened weight reordered so that a legacy-order quantizer emits
+    canonical Q4_K bytes: within each 256-element block, x'[start[is] + l] =
+    w[32*is + l]. The quantizer reads sub-block is from x'[start[is] ..] =
+    w[32*is ..] and packs it where the canonical decoder looks for sub-block
+    is, so the bytes decode to (a quantization of) w itself, in place."""
+    w = np.ascontiguousarray(weight, dtype=np.float32).reshape(-1, Q4K_BLOCK_ELEMS)
+    out = np.empty_like(w)
+    out[:, _LEGACY_POS] = w
+    return out.ravel()
+
+
 def _hip_of(v, what: str) -> HipBuffer:
     if isinstance(v, HipBuffer):
         return v
@@ -567,6 +588,29 @@ class LinearResidentQuantized:
             raise ResidencyError.wrong_variant("bias of out_dim floats",
                                                f"bias of {np.asarray(bias).size}")
         return cls(q4k_bytes, bias, in_dim, out_dim)
+
+    @classmethod
+    def from_linear(cls, weight, bias, in_dim: int, out_dim: int, quantize_row_q4_k,
+                    legacy_order: bool = True) -> "LinearResidentQuantized":
+        """neuron.rs:931-951: quantize the flattened [out_dim x in_dim] f32
+        weight on the host and keep the f32 bias. `quantize_row_q4_k` is the
+        host's own quantizer (the reference's gguf.rs:581-663 stays on the
+        Rust side; it maps n*256 floats to n*144 bytes). That quantizer packs
+        sub-blocks in its legacy order; with legacy_order the weight is first
+        reordered by legacy_quantizer_input, so the bytes are canonical and
+        forward() computes W x + b of this very W. (legacy_order=False is for
+        a quantizer that is canonical already.) A weight whose length is not
+        a multiple of 256 is WrongVariant, as in the reference."""
+        w = np.ascontiguousarray(weight, dtype=np.float32).ravel()
+        if w.size != in_dim * out_dim:
+            raise ResidencyError.wrong_variant("weight of out_dim*in_dim floats",
+                                               f"weight of {w.size}")
+        if w.size % Q4K_BLOCK_ELEMS:
+            raise ResidencyError.wrong_variant("weight len multiple of 256",
+                                               "weight len not aligned to Q4_K block")
+        q = np.asarray(quantize_row_q4_k(legacy_quantizer_input(w) if legacy_order else w),
+                       dtype=np.uint8)
+        return cls.from_q4k(q, bias, in_dim, out_dim)
 
     def in_dim(self) -> int:
         return self._in

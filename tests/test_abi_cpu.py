@@ -42,11 +42,13 @@ def test_matvec_rejects_nonpositive_dims(L):
 
 
 def test_dp4a_path_rejects_bad_args(L):
-    # launch_quantize_q8_1: fewer than one 32-value sub-block, null, misaligned
+    # launch_quantize_q8_1: fewer than one 32-value sub-block, null, a float
+    # pointer off float alignment (the int8 xq may start at any byte)
     assert L.launch_quantize_q8_1(FAKE, FAKE, FAKE, FAKE, 31) == INVALID
     assert L.launch_quantize_q8_1(FAKE, FAKE, FAKE, FAKE, 0) == INVALID
     assert L.launch_quantize_q8_1(None, FAKE, FAKE, FAKE, 64) == INVALID
-    assert L.launch_quantize_q8_1(FAKE, FAKE + 1, FAKE, FAKE, 64) == INVALID
+    assert L.launch_quantize_q8_1(FAKE + 2, FAKE, FAKE, FAKE, 64) == INVALID
+    assert L.launch_quantize_q8_1(FAKE, FAKE + 1, FAKE + 1, FAKE, 64) == INVALID
     # launch_matvec_q4k_dp4a: reference checks (matvec_q4k_dp4a.hip:111) + pointers
     assert L.launch_matvec_q4k_dp4a(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 14) == INVALID
     assert L.launch_matvec_q4k_dp4a(FAKE, FAKE, FAKE, FAKE, FAKE, 16, 0) == INVALID
@@ -64,11 +66,13 @@ def test_q5k_q6k_reject_bad_args(L):
     assert L.launch_matvec_q6k_dp4a(FAKE, None, FAKE, FAKE, FAKE, 8, 1) == INVALID
 
 
-def test_matvec_rejects_null_and_misaligned(L):
+def test_matvec_rejects_null_and_misaligned_floats(L):
+    # weight bytes may start at any byte (the GPU tests run +1/+2/+4 offsets);
+    # x and y are float pointers and need float alignment
     assert L.launch_matvec_q4k(None, FAKE, FAKE, 16, 1) == INVALID
     assert L.launch_matvec_q4k(FAKE, None, FAKE, 16, 1) == INVALID
-    assert L.launch_matvec_q4k(FAKE + 2, FAKE, FAKE, 16, 1) == INVALID
-    assert L.launch_matvec_q4k(FAKE, FAKE + 1, FAKE, 16, 1) == INVALID
+    assert L.launch_matvec_q4k(FAKE + 1, FAKE + 1, FAKE, 16, 1) == INVALID
+    assert L.launch_matvec_q4k(FAKE + 3, FAKE, FAKE + 2, 16, 1) == INVALID
 
 
 def test_matvec_ex_layout_rules(L):
@@ -198,13 +202,13 @@ def test_fused_matvecs_reject_bad_args(L):
     assert rms(FAKE, FAKE, FAKE, 1e-6, FAKE, 0, 14, None) == INVALID
     assert rms(FAKE, FAKE, FAKE, 1e-6, FAKE, 16, 0, None) == INVALID
     assert rms(FAKE, FAKE, None, 1e-6, FAKE, 16, 14, None) == INVALID   # norm weights required
-    assert rms(FAKE + 4, FAKE, FAKE, 1e-6, FAKE, 16, 14, None) == INVALID  # w not 16-B aligned
-    assert rms(FAKE, FAKE, FAKE + 8, 1e-6, FAKE, 16, 14, None) == INVALID  # norm_w not 16-B aligned
+    assert rms(FAKE + 1, FAKE + 2, FAKE, 1e-6, FAKE, 16, 14, None) == INVALID  # x off float alignment
+    assert rms(FAKE + 1, FAKE, FAKE + 2, 1e-6, FAKE, 16, 14, None) == INVALID  # norm_w likewise
     glu = L.launch_matvec_q4k_glu_ex
     assert glu(FAKE, None, FAKE, None, 0.0, 0, FAKE, 16, 14, None) == INVALID  # up matrix required
     assert glu(FAKE, FAKE, FAKE, None, 0.0, 7, FAKE, 16, 14, None) == INVALID  # unknown activation
-    assert glu(FAKE, FAKE + 4, FAKE, None, 0.0, 0, FAKE, 16, 14, None) == INVALID
-    assert glu(FAKE, FAKE, FAKE, FAKE + 4, 0.0, 0, FAKE, 16, 14, None) == INVALID
+    assert glu(FAKE, FAKE + 1, FAKE + 2, None, 0.0, 0, FAKE, 16, 14, None) == INVALID
+    assert glu(FAKE, FAKE, FAKE, FAKE + 2, 0.0, 0, FAKE, 16, 14, None) == INVALID
     assert glu(FAKE, FAKE, FAKE, None, 0.0, 1, FAKE, -1, 14, None) == INVALID
 
 
@@ -213,5 +217,5 @@ def test_fused_quantize_dp4a_rejects_bad_args(L):
     assert fn(FAKE, FAKE, FAKE, 0, 14, None) == INVALID
     assert fn(FAKE, FAKE, FAKE, 16, 0, None) == INVALID
     assert fn(FAKE, None, FAKE, 16, 14, None) == INVALID
-    assert fn(FAKE + 4, FAKE, FAKE, 16, 14, None) == INVALID   # w not 16-B aligned
-    assert fn(FAKE, FAKE + 8, FAKE, 16, 14, None) == INVALID   # x not 16-B aligned
+    assert fn(FAKE + 1, FAKE + 2, FAKE, 16, 14, None) == INVALID   # x off float alignment
+    assert fn(FAKE + 1, FAKE, FAKE + 2, 16, 14, None) == INVALID   # y likewise

@@ -199,17 +199,6 @@ def test_matvec_is_deterministic(L, orc, n, bpr):
     del torch
 
 
-def test_matvec_generic_kernel_on_misaligned_weights(L, orc):
-    # a 4-byte-aligned (not 16) weight pointer takes the vector-ALU kernel
-    note("matvec generic path (w offset 4 B)")
-    n, bpr = 70, 14
-    w = orc.seeded_weight(41, n, bpr * 256)
-    x = orc.normal(42, bpr * 256)
-    y = run_gemv(L, w, x, n, bpr, w_offset=4)
-    y_ref, a = orc.gemv(w, x, n, bpr)
-    assert_gemv_close(y, y_ref, a)
-
-
 # (n, k): rows of U = 256/gcd(k, 256) rows per unit (U = 2, 8, 4, 2, 8 with a
 # 153-block unit), k % 32 != 0 (vector-ALU kernel), k % 256 == 0 (row layout)
 @pytest.mark.parametrize("n,k", [(4864, 896), (8, 96), (16, 320), (64, 1152), (40, 4896),
@@ -228,7 +217,7 @@ def test_matvec_flat_layout(L, orc, n, k):
 
 def test_matvec_flat_layout_random_bytes_and_misaligned_x(L, orc):
     # random blocks (non-finite d / dmin included) on the whole-unit kernel,
-    # then x 4 bytes off 16-byte alignment (the vector-ALU kernel), same result
+    # with x 16-byte aligned and 4 bytes past that, same result
     note("matvec flat 4864x896 random bytes; x offset 4 B")
     import torch
     n, k = 4864, 896
@@ -329,18 +318,6 @@ def test_matvec_batched_single_row_is_the_matvec(L, orc):
     x = orc.normal(64, bpr * 256)
     Y = run_batched(L, w, x.reshape(1, -1), n, bpr, 1)
     assert np.array_equal(Y[0], run_gemv(L, w, x, n, bpr))
-
-
-def test_matvec_batched_vector_alu_fallback(L, orc):
-    # weights only 4-byte aligned: the vector-ALU batched kernel runs
-    note("batched misaligned weights")
-    n, bpr, batch = 70, 3, 6
-    w = orc.seeded_weight(71, n, bpr * 256)
-    X = orc.normal(72, batch * bpr * 256).reshape(batch, -1)
-    Y = run_batched(L, w, X, n, bpr, batch, w_offset=4)
-    Y_ref, A = orc.gemv_batched(w, X, n, bpr)
-    for b in range(batch):
-        assert_gemv_close(Y[b], Y_ref[b], A[b])
 
 
 # --------------------------------------------------------------------- GEMM --
@@ -557,9 +534,11 @@ def test_dp4a_matvec_matches_oracle(L, orc, n, bpr):
 
 
 def test_dp4a_vector_alu_fallback_matches_oracle(L, orc):
-    # xq only 4-byte aligned: the vector-ALU dp4a kernel runs
-    note("dp4a misaligned activations")
-    n, bpr = 45, 5
+    # K = 102400: the Q8 activation staging exceeds the matrix-core kernel's
+    # per-lane item count, so the vector-ALU dp4a kernel runs; xq at a 4-byte
+    # offset
+    note("dp4a vector-ALU kernel (bpr 400, xq offset 4)")
+    n, bpr = 8, 400
     rng = np.random.default_rng(93)
     w = random_q4k_bytes(rng, n * bpr)
     x = rng.standard_normal(bpr * 256).astype(np.float32)
@@ -655,10 +634,12 @@ def test_kquant_matvec_matches_oracle(L, orc, fmt, n, bpr):
     assert_gemv_close(host(yt), y_ref, a)
 
 
-def test_q5k_matvec_misaligned_weights_use_the_vector_alu_kernel(L, orc):
+def test_q5k_matvec_long_rows_use_the_vector_alu_kernel(L, orc):
+    # K = 37888 exceeds the matrix-core kernel's activation staging: the
+    # byte-reading vector-ALU Q5_K kernel runs (weights at a 4-byte offset)
     from tests.gpu_util import random_kquant_bytes
-    note("q5k weights 4-byte aligned")
-    n, bpr = 70, 3
+    note("q5k vector-ALU kernel (bpr 148, w offset 4)")
+    n, bpr = 10, 148
     w = random_kquant_bytes(np.random.default_rng(8), n * bpr, 176)
     x = np.random.default_rng(9).standard_normal(bpr * 256).astype(np.float32)
     import torch
