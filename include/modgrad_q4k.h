@@ -159,6 +159,23 @@ hipError_t launch_matvec_q4k_batched(const unsigned char *w_q4, const float *X, 
                                      void *workspace, size_t workspace_bytes,
                                      hipStream_t stream);
 
+/* No counterpart in the reference. launch_matvec_q4k_batched without a
+ * workspace argument and without any device allocation, for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The operand table lives in a fixed
+ * MGQ_NOALLOC_SCRATCH_BYTES array of the library on each GPU (held until
+ * the process ends; its device address is looked up once per device, by
+ * mgq_prepare or the first call). Same results as launch_matvec_q4k_batched
+ * with a workspace. Shapes whose workspace
+ * (mgq_batched_workspace_bytes) exceeds the array return
+ * hipErrorInvalidValue: up to blocks_per_row 451 for batch <= 8, 225 for
+ * batch <= 16. Calls on one GPU share the array: calls that may overlap (on
+ * unordered streams) race and must not be issued. */
+#define MGQ_NOALLOC_SCRATCH_BYTES ((size_t)4 << 20)
+hipError_t launch_matvec_q4k_batched_noalloc(const unsigned char *w_q4, const float *X, float *Y,
+                                             int out_dim, int blocks_per_row, int batch,
+                                             hipStream_t stream);
+
 /* Prefill dequant-GEMM: C[m][r] = sum_k dequant(W)[r][k] * A[m][k] for
  * m < m_tokens, with A f16 [m_tokens][blocks_per_row*256] (IEEE half bits)
  * and C f32 [m_tokens][out_dim]. Weights are dequantized to f16 tiles and
@@ -249,9 +266,11 @@ hipError_t mgq_chain_destroy(void *chain);
 
 /* Prepares the current device: sets the GEMV kernels' LDS attributes, which
  * belong to a device (every launcher also does this on its first use on a
- * device). Allocates nothing; the library keeps
- * no device memory and no mutable device state, so launches on different
- * streams may run concurrently. Safe to call more than once. */
+ * device), and looks up the device address of the fixed scratch array of
+ * launch_matvec_q4k_batched_noalloc. Allocates nothing. Apart from that array
+ * (used by that entry point only) the library keeps no device memory and no
+ * mutable device state, so launches on different streams may run
+ * concurrently. Safe to call more than once. */
 hipError_t mgq_prepare(void);
 
 /* Library version string, e.g. "modgrad_q4k 0.1.0 gfx950". */

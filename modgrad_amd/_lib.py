@@ -39,6 +39,7 @@ SIGNATURES = {
     "launch_dequant_q4k_ex": (I, [P, I, P, P]),
     "mgq_batched_workspace_bytes": (S, [I, I]),
     "launch_matvec_q4k_batched": (I, [P, P, P, I, I, I, P, S, P]),
+    "launch_matvec_q4k_batched_noalloc": (I, [P, P, P, I, I, I, P]),
     "launch_gemm_q4k_f16": (I, [P, P, P, I, I, I, P]),
     "launch_quantize_matvec_q4k_dp4a_ex": (I, [P, P, P, I, I, P]),
     "launch_rms_norm": (I, [P, P, P, I, I, F]),

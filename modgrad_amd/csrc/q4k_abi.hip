@@ -305,7 +305,10 @@ hipError_t launch_matvec_q4k_glu_ex(const unsigned char *w_gate, const unsigned 
                                   stream);
 }
 
-hipError_t mgq_prepare(void) { return mgq::gemv_prepare(); }
+hipError_t mgq_prepare(void) {
+    const hipError_t e = mgq::gemv_prepare();
+    return e != hipSuccess ? e : mgq::noalloc_prepare();
+}
 
 const char *mgq_version(void) { return "modgrad_q4k 0.1.0 gfx950"; }
 

@@ -126,6 +126,10 @@ hipError_t gemv_mfma_launch(const uint8_t *w, const float *x, float *y, int n, i
 // One-time kernel attribute setup (dynamic LDS limit); safe to call often.
 hipError_t gemv_prepare();
 
+// Looks up the current device's address of the no-allocation entry point's
+// fixed scratch array (once per device).
+hipError_t noalloc_prepare();
+
 // Row-aligned GEMV: picks the matrix-core kernel when it applies.
 hipError_t gemv_rows_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                             hipStream_t stream);
