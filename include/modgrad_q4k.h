@@ -13,7 +13,12 @@
  *   - reference-compatible launchers enqueue on the null stream; the *_ex
  *     variants take an explicit hipStream_t;
  *   - the return value is a hipError_t (0 = hipSuccess); non-positive sizes
- *     return hipErrorInvalidValue and enqueue nothing.
+ *     return hipErrorInvalidValue and enqueue nothing;
+ *   - quantized weight bytes and int8 activations may start at any byte
+ *     address, as the reference's byte-reading kernels allow (its engine
+ *     packs tensors back to back, rocm_gemma.rs:214-215); the same kernels
+ *     run at every offset. Float pointers need 4-byte alignment and f16
+ *     pointers 2-byte (hipErrorInvalidValue otherwise).
  *
  * Q4_K super-block (144 bytes, 256 weights): +0 d:f16, +2 dmin:f16,
  * +4 scales[12] (6-bit scale/min pairs), +16 qs[128] (4-bit quants).
@@ -122,8 +127,7 @@ hipError_t launch_matvec_q4k_dp4a_ex(const unsigned char *w, const signed char *
  * matvec quantizes x (blocks_per_row*256 f32) to Q8_1 itself, with the same
  * steps as launch_quantize_q8_1, so y is bit-identical to the two-launch
  * sequence (rocm_gemma.rs:298-306) while x, xq, xd and xsum never go to
- * memory. w and x must be 16-byte aligned (hipErrorInvalidValue otherwise);
- * hipErrorNotSupported when K exceeds the kernel's LDS staging. */
+ * memory. hipErrorNotSupported when K exceeds the kernel's LDS staging. */
 hipError_t launch_quantize_matvec_q4k_dp4a_ex(const unsigned char *w, const float *x, float *y,
                                               int out_dim, int bpr, hipStream_t stream);
 
@@ -229,8 +233,7 @@ hipError_t launch_scale_ex(float *h, float s, int n, hipStream_t stream);
  * Computed as rstd * (W * (x .* norm_w)): the matvec's activation staging
  * multiplies by norm_w and reduces sum(x^2) on the way, so the normalized
  * vector never goes to memory. Same per-row bound as launch_matvec_q4k
- * against the f64 matvec of the normalized vector. w, x and norm_w must be
- * 16-byte aligned (hipErrorInvalidValue otherwise); hipErrorNotSupported when
+ * against the f64 matvec of the normalized vector. hipErrorNotSupported when
  * K exceeds the kernel's LDS staging (blocks_per_row > ~110). */
 hipError_t launch_matvec_q4k_rmsnorm_ex(const unsigned char *w_q4, const float *x,
                                         const float *norm_w, float eps, float *y, int out_dim,
@@ -241,7 +244,7 @@ hipError_t launch_matvec_q4k_rmsnorm_ex(const unsigned char *w_q4, const float *
  * xn = x). Replaces the reference FFN's launch_rms_norm + two
  * launch_matvec_q4k + launch_geglu (rocm_gemma.rs:477-481): one launch, and
  * gate/up never go to memory. W_gate and W_up are out_dim x blocks_per_row
- * row-aligned Q4_K, both 16-byte aligned, as are x and norm_w. */
+ * row-aligned Q4_K. */
 hipError_t launch_matvec_q4k_glu_ex(const unsigned char *w_gate, const unsigned char *w_up,
                                     const float *x, const float *norm_w, float eps, int act,
                                     float *y, int out_dim, int blocks_per_row,

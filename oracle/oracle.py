@@ -48,6 +48,7 @@ def lib() -> ctypes.CDLL:
         "orq_pack_scales_mins": (None, [P, P, P]),
         "orq_dequantize_row_q4_k": (None, [P, P, z, z]),
         "orq_quantize_row_q4_k": (z, [P, z, P]),
+        "orq_quantize_row_q4_k_offsets": (z, [P, z, P, P]),
         "orq_rng_init": (None, [P, u64]),
         "orq_rng_next_u64": (u64, [P]),
         "orq_rng_next_f32": (f, [P]),
@@ -124,6 +125,20 @@ def quantize(x: np.ndarray) -> np.ndarray:
         raise ValueError(f"quantize: len {x.size} not a multiple of {BLOCK_ELEMS}")
     out = np.zeros(x.size // BLOCK_ELEMS * BLOCK_BYTES, dtype=np.uint8)
     n = lib().orq_quantize_row_q4_k(_p(x), x.size, _p(out))
+    assert n == out.size
+    return out
+
+
+def quantize_with_offsets(x: np.ndarray, offsets) -> np.ndarray:
+    """quantize() with the sub-block table of gguf.rs:601 replaced by
+    `offsets` (offsets[is] = first element of sub-block is)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    if x.size % BLOCK_ELEMS:
+        raise ValueError(f"quantize: len {x.size} not a multiple of {BLOCK_ELEMS}")
+    offs = np.ascontiguousarray(offsets, dtype=np.int32)
+    assert offs.size == 8
+    out = np.zeros(x.size // BLOCK_ELEMS * BLOCK_BYTES, dtype=np.uint8)
+    n = lib().orq_quantize_row_q4_k_offsets(_p(x), x.size, _p(out), _p(offs))
     assert n == out.size
     return out
 

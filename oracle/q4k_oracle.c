@@ -161,11 +161,9 @@ static void quantize_sub_block(const float *x, uint8_t *sc, uint8_t *m, uint8_t 
         q[i] = d1 > 0.0f ? round_clamp_u8((x[i] + m1) / d1, 15.0f) : 0;
 }
 
-/* gguf.rs:581-663. Sub-block `is` reads x[OFFS[is] .. +32] (the reference's
- * all-low-then-all-high table at gguf.rs:590-601), so its bytes decode, in the
- * canonical order above, to a 32-element-chunk permutation of x. */
-size_t orq_quantize_row_q4_k(const float *x, size_t n, uint8_t *out) {
-    static const int OFFS[8] = {0, 128, 32, 160, 64, 192, 96, 224};
+/* gguf.rs:581-663 with its sub-block table (gguf.rs:601) as a parameter:
+ * sub-block `is` reads x[OFFS[is] .. +32]. */
+size_t orq_quantize_row_q4_k_offsets(const float *x, size_t n, uint8_t *out, const int *OFFS) {
     if (n % ORQ_BLOCK_ELEMS != 0) return 0;
     size_t n_blocks = n / ORQ_BLOCK_ELEMS;
     for (size_t blk = 0; blk < n_blocks; ++blk) {
@@ -193,6 +191,14 @@ size_t orq_quantize_row_q4_k(const float *x, size_t n, uint8_t *out) {
         }
     }
     return n_blocks * ORQ_BLOCK_BYTES;
+}
+
+/* gguf.rs:581-663 as the reference ships it: the all-low-then-all-high table
+ * of gguf.rs:590-601, so its bytes decode, in the canonical order above, to
+ * a 32-element-chunk permutation of x. */
+size_t orq_quantize_row_q4_k(const float *x, size_t n, uint8_t *out) {
+    static const int OFFS[8] = {0, 128, 32, 160, 64, 192, 96, 224};
+    return orq_quantize_row_q4_k_offsets(x, n, out, OFFS);
 }
 
 /* ---------------------------------------------------------------- RNG ---- */

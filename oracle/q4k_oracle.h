@@ -39,6 +39,10 @@ void orq_dequantize_row_q4_k(const uint8_t *data, float *out, size_t out_len,
 /* gguf.rs:509-663 -- the reference's own quantizer (legacy sub-block order).
  * Returns bytes written, or 0 when n % 256 != 0 (the reference asserts). */
 size_t orq_quantize_row_q4_k(const float *x, size_t n, uint8_t *out);
+/* The same quantizer with the sub-block table of gguf.rs:601 given: offs[is]
+ * is the first element of sub-block is ({0,32,..,224} is the one-line
+ * canonical-order patch of that table). */
+size_t orq_quantize_row_q4_k_offsets(const float *x, size_t n, uint8_t *out, const int *offs);
 
 /* SimpleRng: crates/modgrad-compute/src/neuron.rs:1345-1367 */
 typedef struct { uint64_t s; } orq_rng;

@@ -89,3 +89,15 @@ def test_from_linear_rejects_a_weight_of_partial_blocks(orc):
     with pytest.raises(ResidencyError):
         LinearResidentQuantized.from_linear(np.zeros(512, np.float32), np.zeros(4), 256, 4,
                                             orc.quantize)
+
+
+def test_canonical_table_patch_gives_the_reordered_bytes(orc):
+    # the one-line alternative at gguf.rs:601 (sub-block table {0, 32, .., 224})
+    # emits exactly the bytes that from_linear's reordering gets out of the
+    # shipped quantizer: each sub-block's scale, min and nibbles depend only
+    # on its own 32 values and the block-wide maxima
+    w = linear_new_weight(orc, 1024, 64)
+    patched = orc.quantize_with_offsets(w, [0, 32, 64, 96, 128, 160, 192, 224])
+    assert np.array_equal(patched, orc.quantize(legacy_quantizer_input(w)))
+    # and the shipped table through the same entry is the shipped quantizer
+    assert np.array_equal(orc.quantize_with_offsets(w, LEGACY_SUBBLOCK_START), orc.quantize(w))
