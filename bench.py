@@ -93,9 +93,16 @@ class Workload:
         self.weight_bytes = sum(w.numel() for _, w, _, _, _, _ in self.launches)
 
 
-def time_graph(torch, q4k, wl: Workload, steps: int, warmup: int):
+CHAIN_MODES = {"auto": 0, "graph": 1, "persistent": 2}
+
+
+def time_graph(torch, q4k, wl: Workload, steps: int, warmup: int, mode: str = "auto"):
+    """ms per step of the workload's matvecs as one mgq_chain (the persistent
+    chain kernel, or a HIP graph of the per-matvec launches), the per-step
+    spread, and the chain's implementation."""
     chain = q4k.Chain([(w.data_ptr(), x.data_ptr(), y.data_ptr(), n, k // BLOCK_ELEMS)
-                       for _, w, x, y, n, k in wl.launches])
+                       for _, w, x, y, n, k in wl.launches], CHAIN_MODES[mode])
+    impl = "persistent" if chain.mode() == CHAIN_MODES["persistent"] else "graph"
     stream = torch.cuda.current_stream()
     for i in range(warmup):
         chain.launch(stream)
@@ -118,8 +125,11 @@ def time_graph(torch, q4k, wl: Workload, steps: int, warmup: int):
         b.record(stream)
     torch.cuda.synchronize()
     spread = _spread(np.array([a.elapsed_time(b) for a, b in ev]))
+    faults = chain.faults()
     chain.close()
-    return ms, spread
+    if faults:
+        raise RuntimeError("the persistent chain reported a timed-out grid-wide wait")
+    return ms, spread, impl
 
 
 def check_parity(torch, wl: Workload, rows: int = 256) -> str:
@@ -681,11 +691,11 @@ TRAFFIC_PROFILES = {"decode7b": "gemv_mfma_decode7b_pmc.txt",
                     "prefill": "gemm_q4k_f16_prefill_pmc.txt"}
 
 
-def profiled_traffic(workload: str):
+def profiled_traffic(workload: str, impl: str = "graph"):
     """HBM bytes per launch of the workload's dominant kernel from the
-    committed FETCH_SIZE / WRITE_SIZE summary of this same workload
-    (calibrated against a plain copy), or None."""
-    name = TRAFFIC_PROFILES.get(workload)
+    committed FETCH_SIZE / WRITE_SIZE summary of this same workload and
+    chain implementation (calibrated against a plain copy), or None."""
+    name = TRAFFIC_PROFILES.get(workload if impl == "graph" else f"{workload}/{impl}")
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name or "")
     if name is None or not os.path.exists(path):
         return None
@@ -746,6 +756,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--chain", default="auto", choices=sorted(CHAIN_MODES),
+                    help="decode7b/layer/gateup: the chain's implementation")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -776,17 +788,21 @@ def main() -> int:
     torch.cuda.synchronize()
     log(f"{len(wl.launches)} launches, {wl.weight_bytes / 1e9:.3f} GB weights resident")
 
-    ms, spread = time_graph(torch, q4k, wl, args.steps, args.warmup)
-    log(f"timed {args.steps} steps: {ms:.4f} ms/step; per-step events {spread}")
+    ms, spread, impl = time_graph(torch, q4k, wl, args.steps, args.warmup, args.chain)
+    log(f"timed {args.steps} steps ({impl} chain): {ms:.4f} ms/step; per-step events {spread}")
     parity = "skipped" if args.no_parity else check_parity(torch, wl)
     log(f"parity: {parity}")
-    # The timed region is back-to-back GEMV launches (one graph per step), so
-    # the kernel's average launch duration is the step time over its launches.
     nl = len(wl.launches)
-    avg_s = ms * 1e-3 / nl
-    avg_b = wl.bytes_per_pass / nl
+    if impl == "persistent":
+        # one cooperative launch per step runs all the matvecs: the kernel's
+        # launch is the step, its bytes the step's
+        kernel, avg_s, avg_b = "mgq::chain_kernel<2>", ms * 1e-3, wl.bytes_per_pass
+    else:
+        # back-to-back GEMV launches (one graph per step): the kernel's average
+        # launch duration is the step time over its launches
+        kernel, avg_s, avg_b = "mgq::gemv_mfma_kernel", ms * 1e-3 / nl, wl.bytes_per_pass / nl
     achieved = avg_b / avg_s / 1e9
-    log(f"kernel avg {avg_s * 1e6:.3f} us over {nl} launches, {achieved:.1f} GB/s")
+    log(f"kernel {kernel} avg {avg_s * 1e6:.3f} us per launch, {achieved:.1f} GB/s")
 
     value = wl.bytes_per_pass / (ms * 1e-3) / 1e9
     out = {
@@ -803,7 +819,8 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": desc, "launches_per_step": len(wl.launches),
+        "config": {"workload": desc, "matvecs_per_step": nl, "chain": impl,
+                   "launches_per_step": 1 if impl == "persistent" else nl,
                    "bytes_per_step": wl.bytes_per_pass, "weights": "q4_k (144 B / 256 weights)",
                    "batch": 1},
         "tokens_per_s": round(1000.0 / ms, 2) if args.workload == "decode7b" else None,
@@ -811,7 +828,7 @@ def main() -> int:
         "parity": parity,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": profiled_traffic(args.workload), "kernel": "mgq::gemv_mfma_kernel",
+                     "traffic": profiled_traffic(args.workload, impl), "kernel": kernel,
                      "avg_launch_us": round(avg_s * 1e6, 3), "avg_launch_bytes": int(avg_b)},
     }
     if not args.no_cpu:

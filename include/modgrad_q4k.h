@@ -259,12 +259,42 @@ typedef struct mgq_gemv_desc {
     int blocks_per_row;
 } mgq_gemv_desc;
 
-/* Records the n matvecs, in order, into a HIP graph (stream capture on a
- * private stream), so a whole decode step replays with one launch. The graph
- * keeps the descriptors' pointers: buffers must outlive the chain. */
+/* A decode step's matvecs as one launchable chain (the reference's per-layer
+ * chain, rocm_gemma.rs:429-489). A launch runs the n matvecs with the
+ * ordering of launching them one after another on a stream: matvec d sees
+ * everything matvecs < d wrote (its x is typically an earlier y). A matvec's
+ * y must not alias its own x or any weights. The chain keeps the
+ * descriptors' pointers: buffers must outlive it.
+ *
+ * Two implementations:
+ *   MGQ_CHAIN_PERSISTENT  one cooperative launch for the whole chain: a
+ *       persistent kernel streams the next matvec's weights while it waits
+ *       for the previous matvec's output (grid-wide completion counters, no
+ *       fences). Row-aligned Q4_K with blocks_per_row <= 84. A launch is not
+ *       capturable into a HIP graph, and launches of one chain must be
+ *       ordered (one stream, or synchronized): the chain owns its counters.
+ *       Measured on MI355X it is slower than the graph (one 15-wave
+ *       work-group per CU streams weights at ~0.7x the standalone kernels'
+ *       rate), so it is opt-in.
+ *   MGQ_CHAIN_GRAPH       the n launch_matvec_q4k_ex launches recorded into
+ *       a HIP graph (stream capture on a private stream).
+ * MGQ_CHAIN_AUTO takes the graph (environment MGQ_CHAIN=persistent selects
+ * the persistent kernel where it can run). MGQ_CHAIN_PERSISTENT returns
+ * hipErrorNotSupported when it cannot run. */
+#define MGQ_CHAIN_AUTO 0
+#define MGQ_CHAIN_GRAPH 1
+#define MGQ_CHAIN_PERSISTENT 2
+hipError_t mgq_chain_create_ex(const mgq_gemv_desc *descs, int n, int mode, void **chain_out);
+/* mgq_chain_create_ex with MGQ_CHAIN_AUTO. */
 hipError_t mgq_chain_create(const mgq_gemv_desc *descs, int n, void **chain_out);
-/* Replays the chain on `stream`; ordered after prior work on that stream. */
+/* Launches the chain on `stream`; ordered after prior work on that stream. */
 hipError_t mgq_chain_launch(void *chain, hipStream_t stream);
+/* The chain's implementation (MGQ_CHAIN_GRAPH / MGQ_CHAIN_PERSISTENT) and,
+ * for the persistent kernel, its fault word: nonzero when a grid-wide wait
+ * gave up (bounded at seconds) in some launch, i.e. results are not to be
+ * trusted. Reading it synchronizes with the device. Either pointer may be
+ * null. */
+hipError_t mgq_chain_info(void *chain, int *mode, unsigned *faults);
 hipError_t mgq_chain_destroy(void *chain);
 
 /* Prepares the current device: sets the GEMV kernels' LDS attributes, which

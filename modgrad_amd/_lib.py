@@ -53,6 +53,8 @@ SIGNATURES = {
     "launch_matvec_q4k_rmsnorm_ex": (I, [P, P, P, F, P, I, I, P]),
     "launch_matvec_q4k_glu_ex": (I, [P, P, P, P, F, I, P, I, I, P]),
     "mgq_chain_create": (I, [P, I, P]),
+    "mgq_chain_create_ex": (I, [P, I, I, P]),
+    "mgq_chain_info": (I, [P, P, P]),
     "mgq_chain_launch": (I, [P, P]),
     "mgq_chain_destroy": (I, [P]),
     "mgq_prepare": (I, []),
@@ -63,6 +65,9 @@ ACT_GELU_TANH = 0
 ACT_SILU = 1
 LAYOUT_ROWS = 0
 LAYOUT_FLAT = 1
+CHAIN_AUTO = 0
+CHAIN_GRAPH = 1
+CHAIN_PERSISTENT = 2
 
 
 class GemvDesc(ctypes.Structure):

@@ -18,7 +18,7 @@ OBJ = os.path.join(HERE, "_obj")
 SO = os.path.join(HERE, "libmodgrad_q4k.so")
 AR = os.path.join(HERE, "libmodgrad_q4k.a")
 
-SOURCES = ["q4k_abi.hip", "q4k_dequant.hip", "q4k_gemv.hip", "q4k_batched.hip", "q4k_q8.hip", "q4k_kquant.hip", "q4k_gemm.hip", "q4k_glue.hip", "q4k_q6k_mfma.hip", "q4k_noalloc.hip"]
+SOURCES = ["q4k_abi.hip", "q4k_dequant.hip", "q4k_gemv.hip", "q4k_batched.hip", "q4k_q8.hip", "q4k_kquant.hip", "q4k_gemm.hip", "q4k_glue.hip", "q4k_q6k_mfma.hip", "q4k_noalloc.hip", "q4k_chain.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = [

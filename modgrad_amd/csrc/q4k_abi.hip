@@ -9,6 +9,8 @@
 #include "../../include/modgrad_q4k.h"
 #include "q4k_launch.hpp"
 
+#include <cstdlib>
+#include <cstring>
 #include <new>
 #include <vector>
 
@@ -181,18 +183,43 @@ hipError_t launch_gemm_q4k_f16(const unsigned char *w_q4, const uint16_t *a_f16,
 struct mgq_chain {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    mgq::PersistentChain *pers = nullptr;
 };
 
-hipError_t mgq_chain_create(const mgq_gemv_desc *descs, int n, void **chain_out) {
+static bool env_chain_persistent() {
+    const char *s = std::getenv("MGQ_CHAIN");
+    return s && std::strcmp(s, "persistent") == 0;
+}
+
+hipError_t mgq_chain_create_ex(const mgq_gemv_desc *descs, int n, int mode, void **chain_out) {
     if (!chain_out || !descs || n <= 0) return hipErrorInvalidValue;
+    if (mode != MGQ_CHAIN_AUTO && mode != MGQ_CHAIN_GRAPH && mode != MGQ_CHAIN_PERSISTENT)
+        return hipErrorInvalidValue;
     *chain_out = nullptr;
     for (int i = 0; i < n; ++i) {
         const mgq_gemv_desc &d = descs[i];
         if (d.out_dim <= 0 || d.blocks_per_row <= 0 || !d.w_q4 || !d.x || !d.y)
             return hipErrorInvalidValue;
+        if (misaligned4(d.x) || misaligned4(d.y)) return hipErrorInvalidValue;
+        if ((int64_t)d.blocks_per_row * 256 > kMaxI32) return hipErrorInvalidValue;
     }
     hipError_t e = mgq::gemv_prepare();  // not allowed to happen mid-capture
     if (e != hipSuccess) return e;
+    if (mode == MGQ_CHAIN_PERSISTENT || (mode == MGQ_CHAIN_AUTO && env_chain_persistent())) {
+        mgq::PersistentChain *p = nullptr;
+        e = mgq::chain_persistent_create(descs, n, &p);
+        if (e == hipSuccess) {
+            auto *ch = new (std::nothrow) mgq_chain;
+            if (!ch) {
+                mgq::chain_persistent_destroy(p);
+                return hipErrorOutOfMemory;
+            }
+            ch->pers = p;
+            *chain_out = ch;
+            return hipSuccess;
+        }
+        if (mode == MGQ_CHAIN_PERSISTENT) return e;
+    }
     hipStream_t s = nullptr;
     e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
     if (e != hipSuccess) return e;
@@ -226,14 +253,36 @@ hipError_t mgq_chain_create(const mgq_gemv_desc *descs, int n, void **chain_out)
     return hipSuccess;
 }
 
+hipError_t mgq_chain_create(const mgq_gemv_desc *descs, int n, void **chain_out) {
+    return mgq_chain_create_ex(descs, n, MGQ_CHAIN_AUTO, chain_out);
+}
+
 hipError_t mgq_chain_launch(void *chain, hipStream_t stream) {
     if (!chain) return hipErrorInvalidValue;
-    return hipGraphLaunch(static_cast<mgq_chain *>(chain)->exec, stream);
+    auto *ch = static_cast<mgq_chain *>(chain);
+    if (ch->pers) return mgq::chain_persistent_launch(ch->pers, stream);
+    return hipGraphLaunch(ch->exec, stream);
+}
+
+hipError_t mgq_chain_info(void *chain, int *mode, unsigned *faults) {
+    if (!chain) return hipErrorInvalidValue;
+    auto *ch = static_cast<mgq_chain *>(chain);
+    if (mode) *mode = ch->pers ? MGQ_CHAIN_PERSISTENT : MGQ_CHAIN_GRAPH;
+    if (faults) {
+        *faults = 0;
+        if (ch->pers) return mgq::chain_persistent_faults(ch->pers, faults);
+    }
+    return hipSuccess;
 }
 
 hipError_t mgq_chain_destroy(void *chain) {
     if (!chain) return hipErrorInvalidValue;
     auto *ch = static_cast<mgq_chain *>(chain);
+    if (ch->pers) {
+        const hipError_t e = mgq::chain_persistent_destroy(ch->pers);
+        delete ch;
+        return e;
+    }
     hipError_t e1 = ch->exec ? hipGraphExecDestroy(ch->exec) : hipSuccess;
     hipError_t e2 = ch->graph ? hipGraphDestroy(ch->graph) : hipSuccess;
     delete ch;

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/modgrad_q4k.h"
+
 #include <algorithm>
 #include <atomic>
 #include <cstdlib>
@@ -197,6 +199,14 @@ hipError_t glu_launch(const float *gate, const float *up, float *out, int n, int
 // h += x and h *= s, elementwise over n.
 hipError_t residual_add_launch(float *h, const float *x, int n, hipStream_t stream);
 hipError_t scale_launch(float *h, float s, int n, hipStream_t stream);
+
+// Persistent decode-step chain (q4k_chain.hip): one cooperative launch runs
+// a list of row-aligned Q4_K matvecs in order.
+struct PersistentChain;
+hipError_t chain_persistent_create(const mgq_gemv_desc *descs, int n, PersistentChain **out);
+hipError_t chain_persistent_launch(PersistentChain *p, hipStream_t stream);
+hipError_t chain_persistent_faults(PersistentChain *p, unsigned *faults);
+hipError_t chain_persistent_destroy(PersistentChain *p);
 
 hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n, int bpr,
                            int m_tokens, hipStream_t stream);

@@ -344,19 +344,36 @@ class ops:
 
 
 class Chain:
-    """A recorded sequence of row-aligned matvecs replayed as one HIP graph."""
+    """A decode step's row-aligned matvecs as one launchable chain
+    (mgq_chain_create_ex): a persistent kernel (mode CHAIN_PERSISTENT) or a
+    HIP graph (CHAIN_GRAPH); CHAIN_AUTO picks the persistent kernel when it
+    applies. Each launch runs the matvecs in order, each seeing the earlier
+    ones' outputs."""
 
-    def __init__(self, descs):
+    def __init__(self, descs, mode: int = _lib.CHAIN_AUTO):
         arr = (_lib.GemvDesc * len(descs))()
         for i, (w, x, y, out_dim, bpr) in enumerate(descs):
             arr[i] = _lib.GemvDesc(w, x, y, out_dim, bpr)
         h = ctypes.c_void_p()
-        _chk(_lib.load().mgq_chain_create(arr, len(descs), ctypes.byref(h)), "mgq_chain_create")
+        _chk(_lib.load().mgq_chain_create_ex(arr, len(descs), mode, ctypes.byref(h)),
+             "mgq_chain_create_ex")
         self._h = h
         self.n = len(descs)
 
     def launch(self, stream=None) -> None:
         _chk(_lib.load().mgq_chain_launch(self._h, _stream_ptr(stream)), "mgq_chain_launch")
+
+    def mode(self) -> int:
+        m = ctypes.c_int(-1)
+        _chk(_lib.load().mgq_chain_info(self._h, ctypes.byref(m), None), "mgq_chain_info")
+        return m.value
+
+    def faults(self) -> int:
+        """Nonzero when a grid-wide wait of the persistent kernel gave up in
+        some launch (synchronizes with the device)."""
+        f = ctypes.c_uint(0)
+        _chk(_lib.load().mgq_chain_info(self._h, None, ctypes.byref(f)), "mgq_chain_info")
+        return f.value
 
     def close(self) -> None:
         if self._h:
