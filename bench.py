@@ -367,7 +367,7 @@ def run_prefill(torch, q4k, args):
               if elem_ok and frob <= 1e-3 else f"FAIL: frobenius rel {frob:.3e}, elementwise {elem_ok}")
     return {"workload": f"config5: prefill 18944x3584 Q4_K x f16 [512x3584], {copies} weight copies",
             "us_per_launch": round(s * 1e6, 3), "tflops": tflops, "parity": parity,
-            "kernel": "mgq::gemm_q4k_f16_kernel"}
+            "kernel": "mgq::gemm_q4k_f16_lds_kernel"}
 
 
 def run_decode_dp4a(torch, q4k, args):

@@ -355,7 +355,8 @@ hipError_t launch_matvec_q4k_glu_ex(const unsigned char *w_gate, const unsigned 
 }
 
 hipError_t mgq_prepare(void) {
-    const hipError_t e = mgq::gemv_prepare();
+    hipError_t e = mgq::gemv_prepare();
+    if (e == hipSuccess) e = mgq::gemm_prepare();
     return e != hipSuccess ? e : mgq::noalloc_prepare();
 }
 

@@ -2,10 +2,17 @@
 //   C[m][r] = sum_k dequant(W)[r][k] * A[m][k],  A f16 [M][K], C f32 [M][N].
 // No counterpart in the reference (its prefill is a per-token GEMV loop,
 // crates/modgrad-gemma/examples/gemma4_rocm.rs:26-34); each weight is the
-// canonical dequantized value (gguf.rs:364-404) with d*sc and dmin*m rounded
-// to f16 and the weight itself computed and rounded in f16.
+// canonical dequantized value (gguf.rs:364-404) times a per-row power of two
+// 2^e (row_range_exp: keeps every |weight| of the row below 2^15, so f16
+// neither overflows nor goes subnormal), with d*sc*2^e and dmin*m*2^e
+// rounded to f16 and the weight computed and rounded in f16; C is scaled
+// back by 2^-e exactly.
 //
-// Work-group tile: BN W rows x 128 tokens (BN = 128 or 160, whichever gives
+// Two kernels. M >= 384: gemm_q4k_f16_lds_kernel (below), which dequantizes
+// each W element once per work-group into an f16 LDS tile. Smaller M:
+// gemm_q4k_f16_kernel, whose 128-token tiles keep every CU busy.
+//
+// gemm_q4k_f16_kernel -- work-group tile: BN W rows x 128 tokens (BN = 128 or 160, whichever gives
 // the busiest CU fewer rows to compute), 4 wavefronts of BN/2 x 64 outputs (BN/32 x 4
 // v_mfma_f32_16x16x32_f16, W rows as the A operand, tokens as the B operand,
 // so a lane's 4 accumulators are 4 consecutive W rows of one token: one
@@ -34,6 +41,7 @@
 #include "q4k_device.hpp"
 #include "q4k_launch.hpp"
 
+#include <atomic>
 #include <cstdlib>
 
 namespace mgq {
@@ -90,6 +98,41 @@ __device__ __forceinline__ u32x4 act_order(u32x4 v) {
     return r;
 }
 
+// Power-of-two range scale of one W row: e such that every dequantized
+// |weight| of the row times 2^e is below 2^15 (|q*d*sc - dmin*m| <=
+// 945*|d| + 63*|dmin|), so the f16 weights neither overflow nor fall into
+// f16 subnormals when d is small. The caller's threads split the blocks:
+// this one reads blocks j0, j0 + step, ..., eight header loads in flight.
+__device__ __forceinline__ float row_range_bound(const uint8_t *row, int j0, int step, int bpr) {
+    float bound = 0.0f;
+    for (int j = j0; j < bpr; j += 8 * step) {
+        uint32_t hv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            hv[i] = ld_u32(row + (size_t)min(j + step * i, bpr - 1) * kBlockBytes);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float d = half_bits_finite(hv[i]), dm = half_bits_finite(hv[i] >> 16);
+            bound = fmaxf(bound, fabsf(d) * 945.0f + fabsf(dm) * 63.0f);
+        }
+    }
+    return bound;
+}
+
+__device__ __forceinline__ int range_exp(float bound) {
+    int e = 0;
+    if (bound > 0.0f && bound <= 3.402823466e38f) {
+        int ex;
+        frexpf(bound, &ex);  // bound in [2^(ex-1), 2^ex)
+        e = min(max(15 - ex, -120), 120);
+    }
+    return e;
+}
+
+__device__ __forceinline__ int row_range_exp(const uint8_t *row, int j0, int step, int bpr) {
+    return range_exp(row_range_bound(row, j0, step, bpr));
+}
+
 // BN = W rows per work-group (128 or 160): two wavefronts along N of BN/2
 // rows = TI 16-row MFMA tiles each.
 template <int BN>
@@ -104,6 +147,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__r
     __shared__ __attribute__((aligned(16))) uint8_t sRaw[BN * kBlockBytes];
     __shared__ __attribute__((aligned(16))) uint32_t sScl[BN * SROW];
     __shared__ __attribute__((aligned(16))) _Float16 sA[2][BM * AROW];      // 36864 B
+    __shared__ __attribute__((aligned(16))) float sInv[BN];                  // 2^-e per row
 
     // work-group -> tile: the hardware sends work-group i to XCD i % 8; give
     // XCD x a contiguous range of tiles (token tiles of a W tile adjacent)
@@ -138,6 +182,14 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__r
             hrow = p / 9;
         }
     }
+    // ... and the row's power-of-two range scale (row_range_scale), from all
+    // of its block headers; C is scaled back by the inverse in the epilogue
+    float srow = 1.0f;
+    if (hk >= 0) {
+        const int e = row_range_exp(w + (size_t)min(n0 + hrow, n - 1) * row_bytes, 0, 1, bpr);
+        srow = ldexpf(1.0f, e);
+        sInv[hrow] = ldexpf(1.0f, -e);
+    }
     u32x4 R[NPL];
     auto rload = [&](int b) __attribute__((always_inline)) {  // piece 4 is loaded by every lane (clamped address): no branch
 #pragma unroll
@@ -158,9 +210,9 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__r
             for (int j = 0; j < 8; ++j) {
                 uint32_t sc, m;
                 scale_min(j, h[1], h[2], h[3], sc, m);
-                _Float16 d1 = (_Float16)(d * (float)sc);
-                if (j & 1) d1 = d1 * (_Float16)0.0625f;  // high nibbles arrive as 16*q
-                const _Float16 nm1 = (_Float16)(-(dmin * (float)m));
+                // high nibbles arrive as 16*q
+                const _Float16 d1 = (_Float16)(d * (float)sc * srow * ((j & 1) ? 0.0625f : 1.0f));
+                const _Float16 nm1 = (_Float16)(-(dmin * (float)m * srow));
                 pr[j] = __builtin_bit_cast(uint32_t, (h2_t){d1, nm1});
             }
             u32x2 *dst = reinterpret_cast<u32x2 *>(&sScl[hrow * SROW]);
@@ -266,16 +318,346 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__r
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
             const int r = n0 + wn + 16 * i + 4 * q;
+            const f32x4 v4 = acc[i][jj] * *reinterpret_cast<const f32x4 *>(&sInv[wn + 16 * i + 4 * q]);
             float *dst = c + (size_t)m * n + r;
             if (vec && r + 3 < n) {
-                *reinterpret_cast<f32x4 *>(dst) = acc[i][jj];
+                *reinterpret_cast<f32x4 *>(dst) = v4;
             } else {
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
-                    if (r + v < n) dst[v] = acc[i][jj][v];
+                    if (r + v < n) dst[v] = v4[v];
             }
         }
     }
+}
+
+// ---------------------------------------------------------------------------
+// Large-M prefill GEMM: the work-group dequantizes its W slice ONCE per K
+// step into an f16 LDS tile and runs a plain f16 matrix-core GEMM on it.
+//
+// Work-group tile: 160 W rows x 256 tokens, 8 wavefronts as 2 (W rows) x 4
+// (tokens), each 80 rows x 64 tokens = 5 x 4 v_mfma_f32_16x16x32_f16 tiles
+// (W rows the A operand, tokens the B operand, so a lane's 4 accumulators
+// are 4 consecutive W rows of one token: one 16-byte store into C [M][N]).
+// One work-group per CU (120 KiB of LDS); at M = 512 and N = 18944 the 238
+// tiles are one round on the 256 CUs.
+//
+// K step = 64 (one 32-byte qs group: sub-blocks 2G and 2G+1 of a
+// super-block). Per step the work-group loads 160 x 16-byte qs pieces x 2
+// and 256 tokens x 128 B of activations into registers, two steps ahead of
+// the one being computed; a step's registers are written to a double-
+// buffered LDS stage (the activations as they are, the weights dequantized
+// to f16 in natural k order by the thread that loaded them), one barrier per
+// step.
+//
+// Range. Each W row gets a power-of-two scale 2^e chosen from its block
+// headers so that every dequantized |weight| of the row is below 2^15: the
+// f16 weights neither overflow (d*sc*q up to ~6e7) nor fall into f16
+// subnormals for small d; C is multiplied by 2^-e (exact) at the end. The
+// weight itself is q*(d*sc*2^e) + (-dmin*m*2^e) with both factors rounded
+// to f16 once and one f16 fused multiply-add.
+// Tile shape as template parameters: WN x WM wavefronts, each TI x TJ
+// 16x16 MFMA tiles (16*TI W rows x 16*TJ tokens). ASETS = activation
+// register sets (2: loaded two steps ahead, like the weights; 1: one step
+// ahead). PRE: a step's MFMA operands are all read from LDS before its
+// first MFMA.
+template <int WN_, int WM_, int TI_, int TJ_, int ASETS_, bool PRE_, int PITCH_ = 72, int OCC_ = 1>
+struct G2 {
+    static constexpr int WN = WN_, WM = WM_, TI = TI_, TJ = TJ_, ASETS = ASETS_;
+    static constexpr bool PRE = PRE_;
+    static constexpr int OCC = OCC_;              // resident work-groups per CU
+    static constexpr int BN = WN * 16 * TI;       // W rows per work-group
+    static constexpr int BM = WM * 16 * TJ;       // tokens per work-group
+    static constexpr int NT = 64 * WN * WM;       // threads
+    static constexpr int KS = 64;                 // k per step
+    static constexpr int PITCH = PITCH_;          // halves per LDS row (64 + pad)
+    static constexpr int WP = BN * 2;             // 16-byte qs pieces per step
+    static constexpr int WPT = (WP + NT - 1) / NT;
+    static constexpr int APT = BM * 8 / NT;       // activation pieces per thread per step
+    static constexpr uint32_t SW = BN * PITCH * 2, SA = BM * PITCH * 2;
+    static constexpr uint32_t LDS = 2 * SW + 2 * SA + BN * 4;
+    static_assert(BM * 8 % NT == 0, "whole activation pieces per thread");
+};
+
+#ifndef MGQ_GEMM_CFG
+#define MGQ_GEMM_CFG 2
+#endif
+#if MGQ_GEMM_CFG == 0
+using G2Cfg = G2<2, 4, 5, 4, 2, false>;
+#elif MGQ_GEMM_CFG == 1
+using G2Cfg = G2<2, 4, 5, 4, 1, false>;
+#elif MGQ_GEMM_CFG == 2
+using G2Cfg = G2<2, 4, 5, 4, 1, true>;
+#elif MGQ_GEMM_CFG == 3
+using G2Cfg = G2<1, 4, 10, 4, 2, false>;
+#elif MGQ_GEMM_CFG == 4
+using G2Cfg = G2<1, 4, 10, 4, 2, true>;
+#elif MGQ_GEMM_CFG == 5
+using G2Cfg = G2<1, 4, 10, 4, 1, true>;
+#elif MGQ_GEMM_CFG == 6
+using G2Cfg = G2<2, 2, 5, 4, 1, true, 68, 2>;
+#elif MGQ_GEMM_CFG == 7
+using G2Cfg = G2<2, 2, 5, 4, 2, true, 68, 2>;
+#endif
+
+template <class Cfg>
+__global__ __launch_bounds__(Cfg::NT, Cfg::OCC * Cfg::NT / 256) void gemm_q4k_f16_lds_kernel(
+    const uint8_t *__restrict__ w, const uint16_t *__restrict__ a, float *__restrict__ c, int n,
+    int bpr, int m_tokens, int tiles_n, int tiles_m) {
+    constexpr int WN = Cfg::WN, TI = Cfg::TI, TJ = Cfg::TJ, BN = Cfg::BN, BM = Cfg::BM;
+    constexpr int NT = Cfg::NT, KS = Cfg::KS, PITCH = Cfg::PITCH, WP = Cfg::WP, WPT = Cfg::WPT;
+    constexpr int APT = Cfg::APT, AS = Cfg::ASETS;
+    constexpr uint32_t SW = Cfg::SW, SA = Cfg::SA;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    _Float16 *sW = reinterpret_cast<_Float16 *>(lds);
+    _Float16 *sA = reinterpret_cast<_Float16 *>(lds + 2 * SW);
+    float *sE = reinterpret_cast<float *>(lds + 2 * SW + 2 * SA);
+
+    // work-group -> tile: work-group i runs on XCD i % 8; XCD x takes a
+    // contiguous range of tiles, so the token tiles of one W tile share an L2
+    const int ntiles = tiles_n * tiles_m;
+    const int per_xcd = (ntiles + gemm::NXCD - 1) / gemm::NXCD;
+    const int tile = (int)(blockIdx.x % gemm::NXCD) * per_xcd + (int)(blockIdx.x / gemm::NXCD);
+    if (tile >= ntiles) return;  // uniform
+    const int n0 = (tile / tiles_m) * BN, m0 = (tile % tiles_m) * BM;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int K = bpr * kBlockElems;
+    const int T = bpr * 4;  // K steps
+    const size_t row_bytes = (size_t)bpr * kBlockBytes;
+
+    // this thread's qs pieces: W row wr (clamped past n), bytes 16*wh.. of the
+    // step's 32-byte qs group
+    bool wown[WPT];
+    int wr[WPT], wh[WPT];
+    const uint8_t *wrow[WPT];
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) {
+        const int p = tid + NT * k;
+        wown[k] = p < WP;
+        wr[k] = min(p >> 1, BN - 1);
+        wh[k] = p & 1;
+        wrow[k] = w + (size_t)min(n0 + wr[k], n - 1) * row_bytes;
+    }
+
+    // ---- per-row range: bound on |weight| over the row's blocks ------------
+    // (two threads per row, blocks wh, wh+2, ..., eight loads in flight)
+    float bound[WPT];
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) bound[k] = row_range_bound(wrow[k], wh[k], 2, bpr);
+
+    // ---- step loaders (registers) ------------------------------------------
+    const uint16_t *aptr[APT];
+    uint32_t alds[APT];
+#pragma unroll
+    for (int k = 0; k < APT; ++k) {
+        const int p = tid + NT * k, tok = p >> 3, part = p & 7;
+        aptr[k] = a + (size_t)min(m0 + tok, m_tokens - 1) * K + 8 * part;
+        alds[k] = (uint32_t)((tok * PITCH + 8 * part) * 2);
+    }
+    u32x4 Ar[AS][APT], Wq[2][WPT], Wh[2][WPT];
+    auto loadA = [&](int t, int set) __attribute__((always_inline)) {
+        t = min(t, T - 1);
+#pragma unroll
+        for (int k = 0; k < APT; ++k) Ar[set][k] = ld_u32x4(aptr[k] + (size_t)t * KS);
+    };
+    auto loadW = [&](int t, int set) __attribute__((always_inline)) {
+        t = min(t, T - 1);
+        const int b = t >> 2, G = t & 3;
+#pragma unroll
+        for (int k = 0; k < WPT; ++k) {
+            const uint8_t *blk = wrow[k] + (size_t)b * kBlockBytes;
+            Wq[set][k] = ld_u32x4(blk + 16 + 32 * G + 16 * wh[k]);
+            Wh[set][k] = ld_u32x4(blk);
+        }
+    };
+
+    // row scales (need the header loads above, issued before any step load)
+    float srow[WPT];
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) {
+        const int e = range_exp(fmaxf(bound[k], __shfl_xor(bound[k], 1, 64)));
+        srow[k] = ldexpf(1.0f, e);
+        if (wown[k] && wh[k] == 0) sE[wr[k]] = ldexpf(1.0f, -e);
+    }
+
+    // step t -> LDS buffer: activations copied, weights dequantized
+    const uint32_t magic = __builtin_amdgcn_readfirstlane(0x64006400u) + (uint32_t)(tid >> 16);
+    auto storeA = [&](int set, int buf) __attribute__((always_inline)) {
+        uint8_t *dA = lds + 2 * SW + buf * SA;
+#pragma unroll
+        for (int k = 0; k < APT; ++k) *reinterpret_cast<u32x4 *>(dA + alds[k]) = Ar[set][k];
+    };
+    auto storeW = [&](int t, int set, int buf) __attribute__((always_inline)) {
+        t = min(t, T - 1);
+        const int G = t & 3;
+#pragma unroll
+        for (int k = 0; k < WPT; ++k) {
+            if (!wown[k]) continue;
+            const u32x4 h = Wh[set][k];
+            const float d = half_bits_finite(h[0]), dmin = half_bits_finite(h[0] >> 16);
+            uint32_t sc0, mn0, sc1, mn1;
+            scale_min(2 * G, h[1], h[2], h[3], sc0, mn0);
+            scale_min(2 * G + 1, h[1], h[2], h[3], sc1, mn1);
+            const float sr = srow[k];
+            const _Float16 dl = (_Float16)(d * (float)sc0 * sr);
+            const _Float16 nl = (_Float16)(-(dmin * (float)mn0 * sr));
+            const _Float16 dh = (_Float16)(d * (float)sc1 * sr * 0.0625f);  // high nibbles arrive as 16*q
+            const _Float16 nh = (_Float16)(-(dmin * (float)mn1 * sr));
+            const h2_t dl2 = {dl, dl}, nl2 = {nl, nl}, dh2 = {dh, dh}, nh2 = {nh, nh};
+            u32x4 lo[2], hi[2];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t v = Wq[set][k][u];
+                const uint32_t p0 = __builtin_amdgcn_perm(v, v, 0x0C010C00u);  // bytes 0, 1 -> 0, 2
+                const uint32_t p1 = __builtin_amdgcn_perm(v, v, 0x0C030C02u);  // bytes 2, 3 -> 0, 2
+                lo[u >> 1][2 * (u & 1)] = dq2(p0, 0x000F000Fu, magic, dl2, nl2);
+                lo[u >> 1][2 * (u & 1) + 1] = dq2(p1, 0x000F000Fu, magic, dl2, nl2);
+                hi[u >> 1][2 * (u & 1)] = dq2(p0, 0x00F000F0u, magic, dh2, nh2);
+                hi[u >> 1][2 * (u & 1) + 1] = dq2(p1, 0x00F000F0u, magic, dh2, nh2);
+            }
+            // low nibbles: k = 16*wh + 0..15 of the step; high nibbles: 32 + that
+            uint8_t *dW = lds + buf * SW + (size_t)(wr[k] * PITCH + 16 * wh[k]) * 2;
+            *reinterpret_cast<u32x4 *>(dW) = lo[0];
+            *reinterpret_cast<u32x4 *>(dW + 16) = lo[1];
+            *reinterpret_cast<u32x4 *>(dW + 64) = hi[0];
+            *reinterpret_cast<u32x4 *>(dW + 80) = hi[1];
+        }
+    };
+
+    // ---- compute roles -----------------------------------------------------
+    const int wn = (wave % WN) * (16 * TI), wm = (wave / WN) * (16 * TJ);
+    const int l16 = lane & 15, q = lane >> 4;
+    f32x4 acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](int buf) __attribute__((always_inline)) {
+        const _Float16 *W_ = sW + buf * (BN * PITCH);
+        const _Float16 *A_ = sA + buf * (BM * PITCH);
+        if constexpr (Cfg::PRE) {
+            half8 wa[2][TI], tb[2][TJ];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int i = 0; i < TI; ++i)
+                    wa[h][i] = *reinterpret_cast<const half8 *>(&W_[(wn + 16 * i + l16) * PITCH + 32 * h + 8 * q]);
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+                    tb[h][j] = *reinterpret_cast<const half8 *>(&A_[(wm + 16 * j + l16) * PITCH + 32 * h + 8 * q]);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < TI; ++i)
+#pragma unroll
+                    for (int j = 0; j < TJ; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[h][i], tb[h][j], acc[i][j], 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < KS; kk += 32) {
+                half8 wa[TI], tb[TJ];
+#pragma unroll
+                for (int i = 0; i < TI; ++i)
+                    wa[i] = *reinterpret_cast<const half8 *>(&W_[(wn + 16 * i + l16) * PITCH + kk + 8 * q]);
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+                    tb[j] = *reinterpret_cast<const half8 *>(&A_[(wm + 16 * j + l16) * PITCH + kk + 8 * q]);
+#pragma unroll
+                for (int i = 0; i < TI; ++i)
+#pragma unroll
+                    for (int j = 0; j < TJ; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[i], tb[j], acc[i][j], 0, 0, 0);
+            }
+        }
+    };
+
+    // ---- pipeline ----------------------------------------------------------
+    // Step t computes buffer t & 1, then writes step t+1 into the other
+    // buffer and refills the registers it came from: weights with step t+3
+    // (two sets), activations with step t+3 (two sets) or t+2 (one set).
+    // Loads past the last step re-read it (clamped), so every load is
+    // unconditional and the load counter waits only for the data it needs.
+    constexpr int AD = AS == 2 ? 3 : 2;  // activation prefetch distance
+    loadA(0, 0);
+    loadW(0, 0);
+    if constexpr (AS == 2) loadA(1, 1);
+    loadW(1, 1);
+    storeA(0, 0);
+    storeW(0, 0, 0);
+    loadA(AD - 1, 0);
+    loadW(2, 0);
+    __syncthreads();
+    auto stage = [&](int t, auto par, bool dq_first) __attribute__((always_inline)) {
+        constexpr int P = decltype(par)::value;  // t & 1
+        constexpr int NS = (P + 1) & 1;           // buffer / weight set of step t+1
+        constexpr int AN = AS == 2 ? NS : 0;      // activation set of step t+1
+        if (!dq_first) compute(P);
+        storeA(AN, NS);
+        storeW(t + 1, NS, NS);
+        loadA(t + AD, AN);
+        loadW(t + 3, NS);
+        if (dq_first) compute(P);
+        __syncthreads();
+    };
+    // Wavefronts w and w + 4 share a SIMD: with 8 wavefronts the first
+    // computes and then dequantizes, the second dequantizes and then
+    // computes, so one's dequant VALU work runs while the other's MFMAs
+    // occupy the matrix core.
+    if (NT / 64 <= 4 || wave < 4) {
+        for (int t = 0; t < T; t += 2) {
+            stage(t, std::integral_constant<int, 0>{}, false);
+            stage(t + 1, std::integral_constant<int, 1>{}, false);  // T % 4 == 0
+        }
+    } else {
+        for (int t = 0; t < T; t += 2) {
+            stage(t, std::integral_constant<int, 0>{}, true);
+            stage(t + 1, std::integral_constant<int, 1>{}, true);
+        }
+    }
+
+    // ---- epilogue: lane holds W rows wn+16i+4q+v of token wm+16j+l16 --------
+    const bool vec = (n % 4) == 0 && (((uintptr_t)c & 15u) == 0);
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+        const int rl = wn + 16 * i + 4 * q;
+        const f32x4 sc = *reinterpret_cast<const f32x4 *>(&sE[rl]);
+        const int r = n0 + rl;
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int m = m0 + wm + 16 * j + l16;
+            if (m >= m_tokens) continue;
+            const f32x4 v = acc[i][j] * sc;
+            float *dst = c + (size_t)m * n + r;
+            if (vec && r + 3 < n) {
+                *reinterpret_cast<f32x4 *>(dst) = v;
+            } else {
+#pragma unroll
+                for (int x = 0; x < 4; ++x)
+                    if (r + x < n) dst[x] = v[x];
+            }
+        }
+    }
+}
+
+static std::atomic<int> g_gemm_lds_state[64];
+
+hipError_t gemm_prepare() {
+    return allow_full_lds((const void *)gemm_q4k_f16_lds_kernel<G2Cfg>, g_gemm_lds_state);
+}
+
+static hipError_t gemm_lds_launch(const uint8_t *w, const uint16_t *a, float *c, int n, int bpr,
+                                  int m_tokens, hipStream_t stream) {
+    const hipError_t attr = gemm_prepare();
+    if (attr != hipSuccess) return attr;
+    const int tn = (n + G2Cfg::BN - 1) / G2Cfg::BN, tm = (m_tokens + G2Cfg::BM - 1) / G2Cfg::BM;
+    const long ntiles = (long)tn * tm;
+    const long grid = (ntiles + gemm::NXCD - 1) / gemm::NXCD * gemm::NXCD;
+    if (grid > 0x7FFFFFFFL) return hipErrorInvalidValue;
+    gemm_q4k_f16_lds_kernel<G2Cfg><<<(unsigned)grid, G2Cfg::NT, G2Cfg::LDS, stream>>>(
+        w, a, c, n, bpr, m_tokens, tn, tm);
+    return hipGetLastError();
 }
 
 template <int BN>
@@ -292,6 +674,12 @@ static hipError_t gemm_launch_bn(const uint8_t *w, const uint16_t *a, float *c, 
 hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n, int bpr,
                            int m_tokens, hipStream_t stream) {
     if ((uintptr_t)a & 1u) return hipErrorInvalidValue;
+    static const int big_env = [] {
+        const char *v = std::getenv("MGQ_GEMM_LDS");
+        return (v && *v) ? std::atoi(v) : -1;
+    }();
+    if (big_env == 1 || (big_env < 0 && m_tokens >= 384))
+        return gemm_lds_launch(w, a, c, n, bpr, m_tokens, stream);
     // Tile height by the rows the busiest CU computes: ceil(tiles / #CUs) x
     // BN, the lower one, ties to 160 (a second resident tile on a CU adds
     // only part of a tile's throughput). Measured on 18944 x 3584 (us, 128 vs

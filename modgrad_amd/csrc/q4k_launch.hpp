@@ -210,5 +210,7 @@ hipError_t chain_persistent_destroy(PersistentChain *p);
 
 hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n, int bpr,
                            int m_tokens, hipStream_t stream);
+// One-time LDS attribute of the large-M GEMM kernel (safe to call often).
+hipError_t gemm_prepare();
 
 }  // namespace mgq

@@ -338,6 +338,43 @@ def test_gemm_f16_small(L, orc, n, bpr, m):
     assert np.linalg.norm(C - C_ref) <= 1e-3 * np.linalg.norm(C_ref)
 
 
+# Random-byte blocks across the f16 range of d/dmin: tiny (f16 subnormal d,
+# weights ~1e-4), huge (weights up to ~6e7, past f16's 65504), ten decades
+# mixed inside one row, and raw random header bytes (Inf/NaN d read as 0).
+# M = 40 runs the 128-token-tile kernel, M = 384 the LDS-dequant kernel.
+def _range_weight(rng, n, bpr, kind):
+    nb = n * bpr
+    if kind == "random":
+        return random_q4k_bytes(rng, nb, finite_scales=False)
+    b = rng.integers(0, 256, size=(nb, 144), dtype=np.uint8)
+    if kind == "tiny":
+        d = rng.uniform(1e-8, 3e-6, size=(nb, 2))
+    elif kind == "huge":
+        d = rng.uniform(1e2, 6e4, size=(nb, 2))
+    else:  # mixed
+        d = 10.0 ** rng.uniform(-7, 1, size=(nb, 2))
+    b[:, 0:4] = d.astype(np.float16).view(np.uint8).reshape(nb, 4)
+    return b.ravel()
+
+
+@pytest.mark.parametrize("m", [40, 384])
+@pytest.mark.parametrize("kind", ["tiny", "huge", "mixed", "random"])
+def test_gemm_f16_dynamic_range(L, orc, kind, m):
+    n, bpr = 200, 4
+    note(f"gemm range {kind} n={n} bpr={bpr} m={m}")
+    rng = np.random.default_rng(0x6E11 + m)
+    w = _range_weight(rng, n, bpr, kind)
+    a = rng.normal(0, 1, size=(m, bpr * 256)).astype(np.float16)
+    wt, at, ct = dev(w), dev(a.view(np.uint16)), empty_f32(m * n)
+    _lib.check("gemm", L.launch_gemm_q4k_f16(ptr(wt), ptr(at), ptr(ct), n, bpr, m, None))
+    C = host(ct).reshape(m, n).astype(np.float64)
+    C_ref, A = orc.gemm_f16(w, a.view(np.uint16), n, bpr)
+    k = bpr * 256
+    assert np.all(np.isfinite(C))
+    assert np.all(np.abs(C - C_ref) <= 1e-2 * A / np.sqrt(k))
+    assert np.linalg.norm(C - C_ref) <= 1e-3 * np.linalg.norm(C_ref)
+
+
 # -------------------------------------------------------------------- chain --
 def test_chain_replays_the_recorded_matvecs(L, orc):
     note("chain of 3 matvecs")
