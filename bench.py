@@ -249,6 +249,33 @@ def time_captured(torch, launch, steps: int, warmup: int) -> float:
     return ms
 
 
+def time_op_chain(torch, q4k, ops, steps: int, warmup: int) -> float:
+    """ms per launch of a chain of mgq_op_desc kernels (one HIP graph recorded
+    by the library, mgq_chain_create_ops), timed like time_captured."""
+    chain = q4k.Chain.from_ops(ops)
+    stream = torch.cuda.current_stream()
+    for _ in range(max(1, warmup)):
+        chain.launch(stream)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(steps):
+        chain.launch(stream)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(max(1, steps))]
+    for a, b in ev:
+        a.record(stream)
+        chain.launch(stream)
+        b.record(stream)
+    torch.cuda.synchronize()
+    SPREADS.append(_spread(np.array([a.elapsed_time(b) for a, b in ev])))
+    chain.close()
+    return ms
+
+
 # per-pass (p10, median, p90) ms of every time_captured call, in call order
 SPREADS: list = []
 
@@ -566,32 +593,31 @@ def run_decode_q4km(torch, q4k, args):
     hs = [torch.randn(HIDDEN, device="cuda", generator=gen) for _ in range(2 * LAYERS + 1)]
     att = [torch.randn(NQ * HEAD, device="cuda", generator=gen) for _ in range(LAYERS)]
     xn, qk, vv, o, glu, dn, logits = f(HIDDEN), f(HIDDEN + kv), f(kv), f(HIDDEN), f(INTER), f(HIDDEN), f(VOCAB)
-    launches = [0]
-
-    def step(st):
-        k, A, n = q4k.kern, arena, 0
-        for l in range(LAYERS):
-            p = f"blk.{l}."
-            h0, h1 = hs[2 * l].data_ptr(), hs[2 * l + 1].data_ptr()
-            if A.dtype[p + "attn_v.weight"] == Q4:
-                A.qmatvec_rmsnorm(p + "attn_qk.weight", h0, p + "attn_norm.weight", eps, qk.data_ptr(), st)
-                A.qmatvec_rmsnorm(p + "attn_v.weight", h0, p + "attn_norm.weight", eps, vv.data_ptr(), st)
-                n += 2
-            else:
-                k.rms_norm(h0, A.ptr(p + "attn_norm.weight"), xn.data_ptr(), 1, HIDDEN, eps, st)
-                A.qmatvec(p + "attn_qk.weight", xn.data_ptr(), qk.data_ptr(), st)
-                A.qmatvec(p + "attn_v.weight", xn.data_ptr(), vv.data_ptr(), st)
-                n += 3
-            A.qmatvec(p + "attn_output.weight", att[l].data_ptr(), o.data_ptr(), st)
-            A.qmatvec_glu(p + "ffn_gate.weight", p + "ffn_up.weight", h1, glu.data_ptr(),
-                          norm=p + "ffn_norm.weight", eps=eps, stream=st)
-            A.qmatvec(p + "ffn_down.weight", glu.data_ptr(), dn.data_ptr(), st)
-            n += 3
-        k.rms_norm(hs[-1].data_ptr(), A.ptr("output_norm.weight"), xn.data_ptr(), 1, HIDDEN, eps, st)
-        A.qmatvec("output.weight", xn.data_ptr(), logits.data_ptr(), st)
-        launches[0] = n + 2
-
-    ms = time_captured(torch, step, args.steps, args.warmup)
+    # the step as mgq_op_desc descriptors, recorded into one graph through the
+    # C ABI (mgq_chain_create_ops): what a Rust host would record
+    A, ops = arena, []
+    for l in range(LAYERS):
+        p = f"blk.{l}."
+        h0, h1 = hs[2 * l].data_ptr(), hs[2 * l + 1].data_ptr()
+        if A.dtype[p + "attn_v.weight"] == Q4:
+            ops.append(A.op_qmatvec_rmsnorm(p + "attn_qk.weight", h0, p + "attn_norm.weight", eps,
+                                            qk.data_ptr()))
+            ops.append(A.op_qmatvec_rmsnorm(p + "attn_v.weight", h0, p + "attn_norm.weight", eps,
+                                            vv.data_ptr()))
+        else:
+            ops.append(q4k.op_rms_norm(h0, A.ptr(p + "attn_norm.weight"), xn.data_ptr(), 1, HIDDEN,
+                                       eps))
+            ops.append(A.op_qmatvec(p + "attn_qk.weight", xn.data_ptr(), qk.data_ptr()))
+            ops.append(A.op_qmatvec(p + "attn_v.weight", xn.data_ptr(), vv.data_ptr()))
+        ops.append(A.op_qmatvec(p + "attn_output.weight", att[l].data_ptr(), o.data_ptr()))
+        ops.append(A.op_qmatvec_glu(p + "ffn_gate.weight", p + "ffn_up.weight", h1, glu.data_ptr(),
+                                    norm=p + "ffn_norm.weight", eps=eps))
+        ops.append(A.op_qmatvec(p + "ffn_down.weight", glu.data_ptr(), dn.data_ptr()))
+    ops.append(q4k.op_rms_norm(hs[-1].data_ptr(), A.ptr("output_norm.weight"), xn.data_ptr(), 1,
+                               HIDDEN, eps))
+    ops.append(A.op_qmatvec("output.weight", xn.data_ptr(), logits.data_ptr()))
+    launches = [len(ops)]
+    ms = time_op_chain(torch, q4k, ops, args.steps, args.warmup)
     # parity: the last layer's Q6_K or Q4_K down (its GLU input as produced)
     # and the Q6_K lm_head, sampled rows against the oracle
     worst, fail = 0.0, None
@@ -616,7 +642,7 @@ def run_decode_q4km(torch, q4k, args):
     n6 = sum(1 for nm, _, t in entries if t == Q6)
     return {"workload": f"decode7b_q4km: Q4_K_M 7B-class decode step from one weight arena "
                         f"({n6} Q6_K tensors incl. lm_head, the rest Q4_K; fused RMSNorm/GeGLU; "
-                        f"{launches[0]} launches), one graph",
+                        f"{launches[0]} launches), one mgq_chain_create_ops graph",
             "us_per_launch": round(ms * 1e3 / launches[0], 3), "gbs": qbytes / (ms * 1e-3) / 1e9,
             "bytes_per_launch": qbytes // launches[0], "parity": parity,
             "kernel": "mgq::gemv_mfma_kernel + mgq::gemv_q6k_mfma_kernel / _long_kernel",

@@ -297,6 +297,62 @@ hipError_t mgq_chain_launch(void *chain, hipStream_t stream);
 hipError_t mgq_chain_info(void *chain, int *mode, unsigned *faults);
 hipError_t mgq_chain_destroy(void *chain);
 
+/* One kernel of a decode-step chain recorded by mgq_chain_create_ops: the
+ * reference's per-layer sequence (rocm_gemma.rs:429-489, with the weight
+ * type dispatch of RocmGemma::qmatvec, rocm_gemma.rs:291-309) for a real
+ * GGUF mix of Q4_K, Q5_K and Q6_K tensors, including the fused glue matvecs.
+ * Fields an op does not use are ignored (keep them zero/null).
+ *
+ *   MGQ_OP_MATVEC        y = W x; dtype Q4_K (layout MGQ_LAYOUT_ROWS or
+ *                        MGQ_LAYOUT_FLAT, in_dim = K), Q5_K or Q6_K
+ *                        (in_dim % 256 == 0); out_dim rows.
+ *   MGQ_OP_MATVEC_NORM   y = W rms_norm(x, norm_w, eps); Q4_K, rows layout
+ *                        (launch_matvec_q4k_rmsnorm_ex).
+ *   MGQ_OP_MATVEC_GLU    y = act(W xn) .* (W2 xn), xn = rms_norm(x, norm_w,
+ *                        eps) when norm_w is not null, else x; Q4_K, rows
+ *                        layout (launch_matvec_q4k_glu_ex).
+ *   MGQ_OP_RMS_NORM      y = rms_norm(x, norm_w, eps) over `rows` rows of
+ *                        in_dim (launch_rms_norm_ex).
+ *   MGQ_OP_GLU           y = act(x) .* x2 over out_dim (launch_glu_ex).
+ *   MGQ_OP_RESIDUAL_ADD  y += x over out_dim (launch_residual_add_ex).
+ * No counterpart in the reference's C ABI: its chain is Rust code that
+ * launches these kernels one by one; this records them into one graph. */
+#define MGQ_OP_MATVEC 0
+#define MGQ_OP_MATVEC_NORM 1
+#define MGQ_OP_MATVEC_GLU 2
+#define MGQ_OP_RMS_NORM 3
+#define MGQ_OP_GLU 4
+#define MGQ_OP_RESIDUAL_ADD 5
+/* GGML tensor types (gguf.rs:9-40) of the quantized weights */
+#define MGQ_DTYPE_Q4_K 12
+#define MGQ_DTYPE_Q5_K 13
+#define MGQ_DTYPE_Q6_K 14
+typedef struct mgq_op_desc {
+    int op;                   /* MGQ_OP_* */
+    int dtype;                /* MGQ_DTYPE_* (matvec ops) */
+    int layout;               /* MGQ_LAYOUT_* (MGQ_OP_MATVEC on Q4_K) */
+    int act;                  /* MGQ_ACT_* (GLU ops) */
+    const unsigned char *w;   /* weights (the gate matrix for MGQ_OP_MATVEC_GLU) */
+    const unsigned char *w2;  /* MGQ_OP_MATVEC_GLU: the up matrix */
+    const float *x;           /* input */
+    const float *x2;          /* MGQ_OP_GLU: the up vector */
+    const float *norm_w;      /* RMSNorm weights */
+    float *y;                 /* output (MGQ_OP_RESIDUAL_ADD: the accumulated h) */
+    int out_dim;              /* matvec rows / elementwise length */
+    int in_dim;               /* matvec K / RMSNorm row length */
+    int rows;                 /* MGQ_OP_RMS_NORM: rows */
+    float eps;                /* RMSNorm epsilon */
+} mgq_op_desc;
+
+/* A chain of mgq_op_desc kernels recorded into one HIP graph (the chain's
+ * MGQ_CHAIN_GRAPH implementation; same launch/info/destroy calls and the
+ * same ordering and lifetime rules as mgq_chain_create_ex). Every
+ * descriptor is validated before any device call: hipErrorInvalidValue
+ * names no device work; hipErrorNotSupported comes from an op whose fused
+ * kernel cannot take the shape (e.g. MGQ_OP_MATVEC_NORM past its LDS
+ * staging), and then no chain is created. */
+hipError_t mgq_chain_create_ops(const mgq_op_desc *ops, int n, void **chain_out);
+
 /* Prepares the current device: sets the GEMV kernels' LDS attributes, which
  * belong to a device (every launcher also does this on its first use on a
  * device), and looks up the device address of the fixed scratch array of

@@ -54,6 +54,7 @@ SIGNATURES = {
     "launch_matvec_q4k_glu_ex": (I, [P, P, P, P, F, I, P, I, I, P]),
     "mgq_chain_create": (I, [P, I, P]),
     "mgq_chain_create_ex": (I, [P, I, I, P]),
+    "mgq_chain_create_ops": (I, [P, I, P]),
     "mgq_chain_info": (I, [P, P, P]),
     "mgq_chain_launch": (I, [P, P]),
     "mgq_chain_destroy": (I, [P]),
@@ -68,11 +69,27 @@ LAYOUT_FLAT = 1
 CHAIN_AUTO = 0
 CHAIN_GRAPH = 1
 CHAIN_PERSISTENT = 2
+OP_MATVEC = 0
+OP_MATVEC_NORM = 1
+OP_MATVEC_GLU = 2
+OP_RMS_NORM = 3
+OP_GLU = 4
+OP_RESIDUAL_ADD = 5
+DTYPE_Q4_K = 12
+DTYPE_Q5_K = 13
+DTYPE_Q6_K = 14
 
 
 class GemvDesc(ctypes.Structure):
     """mgq_gemv_desc."""
     _fields_ = [("w_q4", P), ("x", P), ("y", P), ("out_dim", I), ("blocks_per_row", I)]
+
+
+class OpDesc(ctypes.Structure):
+    """mgq_op_desc (one kernel of an op chain)."""
+    _fields_ = [("op", I), ("dtype", I), ("layout", I), ("act", I), ("w", P), ("w2", P),
+                ("x", P), ("x2", P), ("norm_w", P), ("y", P), ("out_dim", I), ("in_dim", I),
+                ("rows", I), ("eps", F)]
 
 
 class HipError(RuntimeError):

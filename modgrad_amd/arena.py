@@ -26,7 +26,7 @@ import numpy as np
 
 from . import _lib
 from .gguf import GgmlType, GgufFile, data_size
-from .q4k import BackendError, _stream_ptr, kern
+from .q4k import BackendError, _stream_ptr, kern, op_matvec, op_matvec_glu, op_matvec_norm
 
 ALIGN = 256
 
@@ -159,6 +159,38 @@ class WeightArena:
             self._need(norm, GgmlType.F32)
             nw = self.ptr(norm)
         kern.matvec_q4k_glu(self.ptr(gate), self.ptr(up), x, y, n, k // 256, nw, eps, act, stream)
+
+    # -- the same calls as mgq_op_desc descriptors, for a recorded chain
+    #    (q4k.Chain.from_ops): RocmGemma's per-layer chain through the C ABI
+    def op_qmatvec(self, name: str, x: int, y: int) -> "_lib.OpDesc":
+        """Descriptor of y = W x, the kernel picked by W's dtype."""
+        n, k = self.shape(name)
+        t = self.dtype[name]
+        if t not in (GgmlType.Q4_K, GgmlType.Q5_K, GgmlType.Q6_K):
+            raise BackendError("Unsupported", f"{name}: no matvec for {t.name}")
+        if k % 256:
+            raise BackendError("Runtime", f"{name}: in_dim {k} is not a multiple of 256")
+        return op_matvec(int(t), self.ptr(name), x, y, n, k)
+
+    def op_qmatvec_rmsnorm(self, name: str, x: int, norm: str, eps: float,
+                           y: int) -> "_lib.OpDesc":
+        n, k = self.shape(name)
+        self._need(name, GgmlType.Q4_K)
+        self._need(norm, GgmlType.F32)
+        return op_matvec_norm(self.ptr(name), x, self.ptr(norm), eps, y, n, k)
+
+    def op_qmatvec_glu(self, gate: str, up: str, x: int, y: int, norm: str | None = None,
+                       eps: float = 0.0, act: int = _lib.ACT_GELU_TANH) -> "_lib.OpDesc":
+        n, k = self.shape(gate)
+        if self.shape(up) != (n, k):
+            raise BackendError("Runtime", f"{gate} and {up} differ in shape")
+        self._need(gate, GgmlType.Q4_K)
+        self._need(up, GgmlType.Q4_K)
+        nw = None
+        if norm is not None:
+            self._need(norm, GgmlType.F32)
+            nw = self.ptr(norm)
+        return op_matvec_glu(self.ptr(gate), self.ptr(up), x, y, n, k, nw, eps, act)
 
     def _need(self, name: str, t: GgmlType) -> None:
         if self.dtype[name] != t:

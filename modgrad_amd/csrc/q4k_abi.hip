@@ -186,6 +186,43 @@ struct mgq_chain {
     mgq::PersistentChain *pers = nullptr;
 };
 
+}  // extern "C"
+
+// Records launches 0..n-1 (enqueue(i, stream)) into a HIP graph through
+// stream capture on a private stream, and instantiates it.
+template <class F>
+static hipError_t chain_record(int n, void **chain_out, F enqueue) {
+    hipStream_t s = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e != hipSuccess) return e;
+    auto *ch = new (std::nothrow) mgq_chain;
+    if (!ch) {
+        hipStreamDestroy(s);
+        return hipErrorOutOfMemory;
+    }
+    e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    hipError_t launch_err = hipSuccess;
+    if (e == hipSuccess) {
+        for (int i = 0; i < n && launch_err == hipSuccess; ++i) launch_err = enqueue(i, s);
+        hipGraph_t g = nullptr;
+        e = hipStreamEndCapture(s, &g);
+        ch->graph = g;
+        if (e == hipSuccess) e = launch_err;
+        if (e == hipSuccess) e = hipGraphInstantiate(&ch->exec, ch->graph, nullptr, nullptr, 0);
+    }
+    hipStreamDestroy(s);
+    if (e != hipSuccess) {
+        if (ch->exec) hipGraphExecDestroy(ch->exec);
+        if (ch->graph) hipGraphDestroy(ch->graph);
+        delete ch;
+        return e;
+    }
+    *chain_out = ch;
+    return hipSuccess;
+}
+
+extern "C" {
+
 static bool env_chain_persistent() {
     const char *s = std::getenv("MGQ_CHAIN");
     return s && std::strcmp(s, "persistent") == 0;
@@ -220,37 +257,87 @@ hipError_t mgq_chain_create_ex(const mgq_gemv_desc *descs, int n, int mode, void
         }
         if (mode == MGQ_CHAIN_PERSISTENT) return e;
     }
-    hipStream_t s = nullptr;
-    e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
-    if (e != hipSuccess) return e;
-    auto *ch = new (std::nothrow) mgq_chain;
-    if (!ch) {
-        hipStreamDestroy(s);
-        return hipErrorOutOfMemory;
-    }
-    e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
-    hipError_t launch_err = hipSuccess;
-    if (e == hipSuccess) {
-        for (int i = 0; i < n && launch_err == hipSuccess; ++i) {
-            const mgq_gemv_desc &d = descs[i];
-            launch_err = launch_matvec_q4k_ex(d.w_q4, d.x, d.y, d.out_dim, d.blocks_per_row * 256,
-                                              MGQ_LAYOUT_ROWS, s);
+    return chain_record(n, chain_out, [descs](int i, hipStream_t s) {
+        const mgq_gemv_desc &d = descs[i];
+        return launch_matvec_q4k_ex(d.w_q4, d.x, d.y, d.out_dim, d.blocks_per_row * 256,
+                                    MGQ_LAYOUT_ROWS, s);
+    });
+}
+
+// ---------------------------------------------------------- op chains --
+
+static bool bad_f32(const float *p) { return !p || misaligned4(p); }
+
+// Host-side checks of one op descriptor (the launchers check again).
+static hipError_t op_check(const mgq_op_desc &o) {
+    switch (o.op) {
+    case MGQ_OP_MATVEC:
+        if (!o.w || bad_f32(o.x) || bad_f32(o.y) || o.out_dim <= 0 || o.in_dim <= 0)
+            return hipErrorInvalidValue;
+        if (o.dtype == MGQ_DTYPE_Q4_K) {
+            if (o.layout != MGQ_LAYOUT_ROWS && o.layout != MGQ_LAYOUT_FLAT) return hipErrorInvalidValue;
+            if (o.layout == MGQ_LAYOUT_ROWS && o.in_dim % 256) return hipErrorInvalidValue;
+            if (o.layout == MGQ_LAYOUT_FLAT && ((int64_t)o.out_dim * o.in_dim) % 256)
+                return hipErrorInvalidValue;
+            return hipSuccess;
         }
-        hipGraph_t g = nullptr;
-        e = hipStreamEndCapture(s, &g);
-        ch->graph = g;
-        if (e == hipSuccess) e = launch_err;
-        if (e == hipSuccess) e = hipGraphInstantiate(&ch->exec, ch->graph, nullptr, nullptr, 0);
+        if (o.dtype != MGQ_DTYPE_Q5_K && o.dtype != MGQ_DTYPE_Q6_K) return hipErrorInvalidValue;
+        return o.in_dim % 256 ? hipErrorInvalidValue : hipSuccess;
+    case MGQ_OP_MATVEC_NORM:
+    case MGQ_OP_MATVEC_GLU: {
+        if (o.dtype != MGQ_DTYPE_Q4_K || !o.w || bad_f32(o.x) || bad_f32(o.y)) return hipErrorInvalidValue;
+        if (o.out_dim <= 0 || o.in_dim <= 0 || o.in_dim % 256) return hipErrorInvalidValue;
+        if (o.op == MGQ_OP_MATVEC_NORM) return bad_f32(o.norm_w) ? hipErrorInvalidValue : hipSuccess;
+        if (!o.w2 || (o.norm_w && misaligned4(o.norm_w))) return hipErrorInvalidValue;
+        return (o.act == MGQ_ACT_GELU_TANH || o.act == MGQ_ACT_SILU) ? hipSuccess : hipErrorInvalidValue;
     }
-    hipStreamDestroy(s);
-    if (e != hipSuccess) {
-        if (ch->exec) hipGraphExecDestroy(ch->exec);
-        if (ch->graph) hipGraphDestroy(ch->graph);
-        delete ch;
-        return e;
+    case MGQ_OP_RMS_NORM:
+        if (bad_f32(o.x) || bad_f32(o.y) || bad_f32(o.norm_w) || o.rows <= 0 || o.in_dim <= 0)
+            return hipErrorInvalidValue;
+        return (int64_t)o.rows * o.in_dim > kMaxI32 * 4LL ? hipErrorInvalidValue : hipSuccess;
+    case MGQ_OP_GLU:
+        if (bad_f32(o.x) || bad_f32(o.x2) || bad_f32(o.y) || o.out_dim <= 0) return hipErrorInvalidValue;
+        return (o.act == MGQ_ACT_GELU_TANH || o.act == MGQ_ACT_SILU) ? hipSuccess : hipErrorInvalidValue;
+    case MGQ_OP_RESIDUAL_ADD:
+        return (bad_f32(o.x) || bad_f32(o.y) || o.out_dim <= 0) ? hipErrorInvalidValue : hipSuccess;
+    default:
+        return hipErrorInvalidValue;
     }
-    *chain_out = ch;
-    return hipSuccess;
+}
+
+static hipError_t op_launch(const mgq_op_desc &o, hipStream_t s) {
+    switch (o.op) {
+    case MGQ_OP_MATVEC:
+        if (o.dtype == MGQ_DTYPE_Q4_K)
+            return launch_matvec_q4k_ex(o.w, o.x, o.y, o.out_dim, o.in_dim, o.layout, s);
+        if (o.dtype == MGQ_DTYPE_Q5_K)
+            return launch_matvec_q5k_ex(o.w, o.x, o.y, o.out_dim, o.in_dim / 256, s);
+        return launch_matvec_q6k_ex(o.w, o.x, o.y, o.out_dim, o.in_dim / 256, s);
+    case MGQ_OP_MATVEC_NORM:
+        return launch_matvec_q4k_rmsnorm_ex(o.w, o.x, o.norm_w, o.eps, o.y, o.out_dim,
+                                            o.in_dim / 256, s);
+    case MGQ_OP_MATVEC_GLU:
+        return launch_matvec_q4k_glu_ex(o.w, o.w2, o.x, o.norm_w, o.eps, o.act, o.y, o.out_dim,
+                                        o.in_dim / 256, s);
+    case MGQ_OP_RMS_NORM:
+        return launch_rms_norm_ex(o.x, o.norm_w, o.y, o.rows, o.in_dim, o.eps, s);
+    case MGQ_OP_GLU:
+        return launch_glu_ex(o.x, o.x2, o.y, o.out_dim, o.act, s);
+    default:
+        return launch_residual_add_ex(o.y, o.x, o.out_dim, s);
+    }
+}
+
+hipError_t mgq_chain_create_ops(const mgq_op_desc *ops, int n, void **chain_out) {
+    if (!chain_out || !ops || n <= 0) return hipErrorInvalidValue;
+    *chain_out = nullptr;
+    for (int i = 0; i < n; ++i) {
+        const hipError_t e = op_check(ops[i]);
+        if (e != hipSuccess) return e;
+    }
+    hipError_t e = mgq::gemv_prepare();  // not allowed to happen mid-capture
+    if (e != hipSuccess) return e;
+    return chain_record(n, chain_out, [ops](int i, hipStream_t s) { return op_launch(ops[i], s); });
 }
 
 hipError_t mgq_chain_create(const mgq_gemv_desc *descs, int n, void **chain_out) {

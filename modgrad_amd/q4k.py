@@ -343,6 +343,43 @@ class ops:
         _chk(_lib.load().launch_dequant_q4k(q4k_dev, n_blocks, fp32_dev), "launch_dequant_q4k")
 
 
+def op_matvec(dtype: int, w: int, x: int, y: int, out_dim: int, in_dim: int,
+              layout: int = _lib.LAYOUT_ROWS) -> "_lib.OpDesc":
+    """y = W x for a Q4_K/Q5_K/Q6_K weight (mgq_op_desc MGQ_OP_MATVEC)."""
+    return _lib.OpDesc(op=_lib.OP_MATVEC, dtype=dtype, layout=layout, w=w, x=x, y=y,
+                       out_dim=out_dim, in_dim=in_dim)
+
+
+def op_matvec_norm(w: int, x: int, norm_w: int, eps: float, y: int, out_dim: int,
+                   in_dim: int) -> "_lib.OpDesc":
+    """y = W rms_norm(x) (Q4_K, one fused kernel)."""
+    return _lib.OpDesc(op=_lib.OP_MATVEC_NORM, dtype=_lib.DTYPE_Q4_K, w=w, x=x, norm_w=norm_w,
+                       eps=eps, y=y, out_dim=out_dim, in_dim=in_dim)
+
+
+def op_matvec_glu(w_gate: int, w_up: int, x: int, y: int, out_dim: int, in_dim: int,
+                  norm_w: int | None = None, eps: float = 0.0,
+                  act: int = _lib.ACT_GELU_TANH) -> "_lib.OpDesc":
+    """y = act(W_gate xn) * (W_up xn), xn = rms_norm(x) if norm_w (Q4_K)."""
+    return _lib.OpDesc(op=_lib.OP_MATVEC_GLU, dtype=_lib.DTYPE_Q4_K, act=act, w=w_gate, w2=w_up,
+                       x=x, norm_w=norm_w, eps=eps, y=y, out_dim=out_dim, in_dim=in_dim)
+
+
+def op_rms_norm(x: int, norm_w: int, y: int, rows: int, hidden: int,
+                eps: float) -> "_lib.OpDesc":
+    return _lib.OpDesc(op=_lib.OP_RMS_NORM, x=x, norm_w=norm_w, y=y, rows=rows, in_dim=hidden,
+                       eps=eps)
+
+
+def op_glu(gate: int, up: int, y: int, n: int, act: int = _lib.ACT_GELU_TANH) -> "_lib.OpDesc":
+    return _lib.OpDesc(op=_lib.OP_GLU, act=act, x=gate, x2=up, y=y, out_dim=n)
+
+
+def op_residual_add(h: int, x: int, n: int) -> "_lib.OpDesc":
+    """h += x."""
+    return _lib.OpDesc(op=_lib.OP_RESIDUAL_ADD, x=x, y=h, out_dim=n)
+
+
 class Chain:
     """A decode step's row-aligned matvecs as one launchable chain
     (mgq_chain_create_ex): a persistent kernel (mode CHAIN_PERSISTENT) or a
@@ -351,6 +388,8 @@ class Chain:
     ones' outputs."""
 
     def __init__(self, descs, mode: int = _lib.CHAIN_AUTO):
+        if descs is None:  # from_ops
+            return
         arr = (_lib.GemvDesc * len(descs))()
         for i, (w, x, y, out_dim, bpr) in enumerate(descs):
             arr[i] = _lib.GemvDesc(w, x, y, out_dim, bpr)
@@ -359,6 +398,21 @@ class Chain:
              "mgq_chain_create_ex")
         self._h = h
         self.n = len(descs)
+
+    @classmethod
+    def from_ops(cls, ops) -> "Chain":
+        """A chain of mgq_op_desc kernels (mixed Q4_K/Q5_K/Q6_K matvecs, fused
+        RMSNorm/GLU matvecs and the glue kernels) recorded into one HIP graph
+        (mgq_chain_create_ops)."""
+        ops = list(ops)
+        arr = (_lib.OpDesc * len(ops))(*ops)
+        h = ctypes.c_void_p()
+        _chk(_lib.load().mgq_chain_create_ops(arr, len(ops), ctypes.byref(h)),
+             "mgq_chain_create_ops")
+        self = cls(None)
+        self._h = h
+        self.n = len(ops)
+        return self
 
     def launch(self, stream=None) -> None:
         _chk(_lib.load().mgq_chain_launch(self._h, _stream_ptr(stream)), "mgq_chain_launch")

@@ -219,3 +219,30 @@ def test_fused_quantize_dp4a_rejects_bad_args(L):
     assert fn(FAKE, None, FAKE, 16, 14, None) == INVALID
     assert fn(FAKE + 1, FAKE + 2, FAKE, 16, 14, None) == INVALID   # x off float alignment
     assert fn(FAKE + 1, FAKE, FAKE + 2, 16, 14, None) == INVALID   # y likewise
+
+
+def test_op_chain_rejects_bad_descriptors_before_any_device_call(L):
+    """mgq_chain_create_ops validates every descriptor on the host first, so
+    these return hipErrorInvalidValue without touching a device."""
+    import ctypes
+    h = ctypes.c_void_p()
+    good = dict(op=_lib.OP_MATVEC, dtype=_lib.DTYPE_Q4_K, layout=_lib.LAYOUT_ROWS, w=FAKE, x=FAKE,
+                y=FAKE, out_dim=16, in_dim=256)
+    bad = [dict(op=99), dict(dtype=15), dict(w=None), dict(x=FAKE + 2), dict(in_dim=300),
+           dict(out_dim=0), dict(layout=7), dict(dtype=_lib.DTYPE_Q6_K, in_dim=512 + 32),
+           dict(op=_lib.OP_MATVEC_NORM),                      # no norm weights
+           dict(op=_lib.OP_MATVEC_GLU, w2=FAKE, act=5),       # bad activation
+           dict(op=_lib.OP_MATVEC_GLU, dtype=_lib.DTYPE_Q6_K, w2=FAKE),
+           dict(op=_lib.OP_RMS_NORM, norm_w=FAKE, rows=0),
+           dict(op=_lib.OP_GLU, x2=None),
+           dict(op=_lib.OP_RESIDUAL_ADD, out_dim=-1)]
+    for change in bad:
+        d = dict(good)
+        d.update(change)
+        arr = (_lib.OpDesc * 2)(_lib.OpDesc(**good), _lib.OpDesc(**d))
+        assert L.mgq_chain_create_ops(arr, 2, ctypes.byref(h)) == INVALID, change
+        assert h.value is None
+    arr = (_lib.OpDesc * 1)(_lib.OpDesc(**good))
+    assert L.mgq_chain_create_ops(arr, 0, ctypes.byref(h)) == INVALID
+    assert L.mgq_chain_create_ops(None, 1, ctypes.byref(h)) == INVALID
+    assert L.mgq_chain_create_ops(arr, 1, None) == INVALID

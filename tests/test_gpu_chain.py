@@ -130,3 +130,91 @@ def test_persistent_chain_rejects_long_rows(L, orc):
     for (y_ref, a), (_, _, yt) in zip(refs, bufs):
         assert_gemv_close(host(yt), y_ref, a)
     ch.close()
+
+
+# ------------------------------------------------ op chains (mixed dtypes) --
+def _glu_ref(g: np.ndarray, u: np.ndarray, act: int) -> np.ndarray:
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    if act == 0:
+        a = 0.5 * g64 * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (g64 + 0.044715 * g64 ** 3)))
+    else:
+        a = g64 / (1.0 + np.exp(-g64))
+    return a, a * u64
+
+
+def test_op_chain_mixed_dtypes_and_glue(L, orc):
+    """mgq_chain_create_ops on one recorded graph of the reference's layer
+    sequence (rocm_gemma.rs:429-489) over a GGUF-like mix: RMSNorm, Q6_K and
+    Q5_K matvecs on its output, the fused RMSNorm Q4_K matvec, the fused
+    gate/up GLU matvec on that, a Q4_K down matvec on the GLU output, the
+    standalone GLU, a residual add and a flat-layout Q4_K matvec reading the
+    residual sum. Every output is checked against the oracle applied to the
+    inputs the GPU actually produced, on three replays."""
+    from modgrad_amd import q4k
+    from tests.gpu_util import random_kquant_bytes
+    note("op chain: Q4_K/Q5_K/Q6_K matvecs, fused norm/GLU matvecs, glue")
+    rng = np.random.default_rng(0xC4A1)
+    H, I, KV, eps = 512, 768, 256, 1e-5
+    h0 = (rng.standard_normal(H) * 1.5).astype(np.float32)
+    nw1 = (rng.standard_normal(H) * 0.3 + 1.0).astype(np.float32)
+    nw2 = (rng.standard_normal(H) * 0.3 + 1.0).astype(np.float32)
+    w6 = random_kquant_bytes(rng, KV * H // 256, 210)
+    w5 = random_kquant_bytes(rng, KV * H // 256, 176)
+    w4 = orc.seeded_weight(11, H, H)
+    wg = orc.seeded_weight(12, I, H)
+    wu = orc.seeded_weight(13, I, H)
+    wd = orc.seeded_weight(14, H, I)
+    wf = random_q4k_bytes(rng, 8 * 96 // 256)  # flat 8 x 96
+    dv = {k: dev(v) for k, v in dict(h0=h0, nw1=nw1, nw2=nw2, w6=w6, w5=w5, w4=w4, wg=wg,
+                                          wu=wu, wd=wd, wf=wf).items()}
+    out = {k: empty_f32(n) for k, n in dict(xn=H, q=KV, v=KV, y3=H, g=I, d=H, z=KV,
+                                            yf=8).items()}
+    P = lambda k: ptr(dv[k]) if k in dv else ptr(out[k])
+    Q4, Q5, Q6 = _lib.DTYPE_Q4_K, _lib.DTYPE_Q5_K, _lib.DTYPE_Q6_K
+    ops = [
+        q4k.op_rms_norm(P("h0"), P("nw1"), P("xn"), 1, H, eps),
+        q4k.op_matvec(Q6, P("w6"), P("xn"), P("q"), KV, H),
+        q4k.op_matvec(Q5, P("w5"), P("xn"), P("v"), KV, H),
+        q4k.op_matvec_norm(P("w4"), P("h0"), P("nw1"), eps, P("y3"), H, H),
+        q4k.op_matvec_glu(P("wg"), P("wu"), P("y3"), P("g"), I, H, P("nw2"), eps, _lib.ACT_SILU),
+        q4k.op_matvec(Q4, P("wd"), P("g"), P("d"), H, I),
+        q4k.op_glu(P("q"), P("v"), P("z"), KV, _lib.ACT_GELU_TANH),
+        q4k.op_residual_add(P("d"), P("y3"), H),
+        q4k.op_matvec(Q4, P("wf"), P("d"), P("yf"), 8, 96, _lib.LAYOUT_FLAT),
+    ]
+    ch = q4k.Chain.from_ops(ops)
+    assert ch.mode() == _lib.CHAIN_GRAPH
+    first = None
+    for rep in range(3):
+        for t in out.values():
+            t.fill_(float("nan"))
+        ch.launch()
+        r = {k: host(t) for k, t in out.items()}
+        xn_ref = orc.rms_norm(h0, nw1, 1, H, eps)
+        assert np.all(np.abs(r["xn"].astype(np.float64) - xn_ref) <= 4e-6 * np.abs(xn_ref) + 1e-30)
+        y, A = orc.gemv_kquant(210, w6, r["xn"], KV, H // 256)
+        assert_gemv_close(r["q"], y, A)
+        y, A = orc.gemv_kquant(176, w5, r["xn"], KV, H // 256)
+        assert_gemv_close(r["v"], y, A)
+        y, A = orc.gemv(w4, xn_ref, H, H // 256)
+        assert_gemv_close(r["y3"], y, A)
+        xn2 = orc.rms_norm(r["y3"], nw2, 1, H, eps)
+        gg, Ag = orc.gemv(wg, xn2, I, H // 256)
+        uu, Au = orc.gemv(wu, xn2, I, H // 256)
+        a, ref = _glu_ref(gg, uu, _lib.ACT_SILU)
+        bound = 1e-4 * (1.13 * Ag * np.abs(uu) + np.abs(a) * Au) + 1e-5 * np.abs(ref) + 1e-30
+        assert np.all(np.abs(r["g"].astype(np.float64) - ref) <= bound)
+        # d = Wd g, then d += y3 (one f32 add per element)
+        dd, Ad = orc.gemv(wd, r["g"], H, I // 256)
+        res = r["d"].astype(np.float64) - r["y3"]
+        assert np.all(np.abs(res - dd) <= 1e-4 * Ad + 2 ** -23 * np.abs(r["d"]) + 1e-30)
+        zref = orc.glu(r["q"], r["v"], 0)
+        assert np.all(np.abs(r["z"].astype(np.float64) - zref) <= 2e-6 * np.abs(r["q"] * r["v"]) + 1e-30)
+        y, A = orc.gemv_flat(wf, r["d"][:96], 8, 96)
+        assert_gemv_close(r["yf"], y, A)
+        if first is None:
+            first = r
+        else:
+            for k in r:
+                assert np.array_equal(r[k].view(np.uint32), first[k].view(np.uint32)), k
+    ch.close()
