@@ -8,8 +8,9 @@
 // rounded to f16 and the weight computed and rounded in f16; C is scaled
 // back by 2^-e exactly.
 //
-// Two kernels. M >= 384: gemm_q4k_f16_lds_kernel (below), which dequantizes
-// each W element once per work-group into an f16 LDS tile. Smaller M:
+// Two kernels: gemm_q4k_f16_lds_kernel (below), which dequantizes each W
+// element once per work-group into an f16 LDS tile, where its 160 x 256
+// tiles make one full round (config 5: M = 512, N = 18944); otherwise
 // gemm_q4k_f16_kernel, whose 128-token tiles keep every CU busy.
 //
 // gemm_q4k_f16_kernel -- work-group tile: BN W rows x 128 tokens (BN = 128 or 160, whichever gives
@@ -49,7 +50,14 @@ namespace mgq {
 namespace gemm {
 constexpr int BM = 128;        // tokens per work-group
 constexpr int BK = 64;         // k per step (one 32-byte qs group: 2 sub-blocks)
-constexpr int AROW = 72;       // halves per activation LDS row (64 + 8 pad, 144 B)
+#ifndef MGQ_AROW
+#define MGQ_AROW 80
+#endif
+// halves per activation LDS row: 64 + 16 pad (160 B). At this pitch the 16
+// lanes of a b128 operand read hit distinct banks (measured: 4 cycles per
+// read against 8 at a 72-half pitch, and ~60 when rows are not 16-byte
+// aligned).
+constexpr int AROW = MGQ_AROW;
 constexpr int SROW = 10;       // dwords per scale row (8 + 2 pad: conflict-free b64 reads)
 constexpr int NXCD = 8;        // XCDs the hardware deals work-groups across, round robin
 }  // namespace gemm
@@ -361,8 +369,10 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__r
 // register sets (2: loaded two steps ahead, like the weights; 1: one step
 // ahead). PRE: a step's MFMA operands are all read from LDS before its
 // first MFMA.
-template <int WN_, int WM_, int TI_, int TJ_, int ASETS_, bool PRE_, int PITCH_ = 72, int OCC_ = 1>
+template <int WN_, int WM_, int TI_, int TJ_, int ASETS_, bool PRE_, int PITCH_ = 80, int OCC_ = 1,
+          int ABUF_ = 2>
 struct G2 {
+    static constexpr int ABUF = ABUF_;            // activation LDS buffers (1: two barriers per step)
     static constexpr int WN = WN_, WM = WM_, TI = TI_, TJ = TJ_, ASETS = ASETS_;
     static constexpr bool PRE = PRE_;
     static constexpr int OCC = OCC_;              // resident work-groups per CU
@@ -371,11 +381,12 @@ struct G2 {
     static constexpr int NT = 64 * WN * WM;       // threads
     static constexpr int KS = 64;                 // k per step
     static constexpr int PITCH = PITCH_;          // halves per LDS row (64 + pad)
+    static_assert(PITCH % 8 == 0, "16-byte aligned LDS rows (b128 accesses)");
     static constexpr int WP = BN * 2;             // 16-byte qs pieces per step
     static constexpr int WPT = (WP + NT - 1) / NT;
     static constexpr int APT = BM * 8 / NT;       // activation pieces per thread per step
     static constexpr uint32_t SW = BN * PITCH * 2, SA = BM * PITCH * 2;
-    static constexpr uint32_t LDS = 2 * SW + 2 * SA + BN * 4;
+    static constexpr uint32_t LDS = 2 * SW + ABUF * SA + BN * 4;
     static_assert(BM * 8 % NT == 0, "whole activation pieces per thread");
 };
 
@@ -398,6 +409,16 @@ using G2Cfg = G2<1, 4, 10, 4, 1, true>;
 using G2Cfg = G2<2, 2, 5, 4, 1, true, 68, 2>;
 #elif MGQ_GEMM_CFG == 7
 using G2Cfg = G2<2, 2, 5, 4, 2, true, 68, 2>;
+#elif MGQ_GEMM_CFG == 8
+using G2Cfg = G2<2, 2, 5, 4, 1, true, 72, 2, 1>;
+#elif MGQ_GEMM_CFG == 9
+using G2Cfg = G2<2, 2, 5, 4, 2, true, 72, 2, 1>;
+#elif MGQ_GEMM_CFG == 10
+using G2Cfg = G2<2, 8, 5, 2, 1, false>;
+#elif MGQ_GEMM_CFG == 11
+using G2Cfg = G2<2, 8, 5, 2, 1, true>;
+#elif MGQ_GEMM_CFG == 12
+using G2Cfg = G2<2, 8, 5, 2, 2, false>;
 #endif
 
 template <class Cfg>
@@ -406,12 +427,12 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC * Cfg::NT / 256) void gemm_q4k_f1
     int bpr, int m_tokens, int tiles_n, int tiles_m) {
     constexpr int WN = Cfg::WN, TI = Cfg::TI, TJ = Cfg::TJ, BN = Cfg::BN, BM = Cfg::BM;
     constexpr int NT = Cfg::NT, KS = Cfg::KS, PITCH = Cfg::PITCH, WP = Cfg::WP, WPT = Cfg::WPT;
-    constexpr int APT = Cfg::APT, AS = Cfg::ASETS;
+    constexpr int APT = Cfg::APT, AS = Cfg::ASETS, AB = Cfg::ABUF;
     constexpr uint32_t SW = Cfg::SW, SA = Cfg::SA;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     _Float16 *sW = reinterpret_cast<_Float16 *>(lds);
     _Float16 *sA = reinterpret_cast<_Float16 *>(lds + 2 * SW);
-    float *sE = reinterpret_cast<float *>(lds + 2 * SW + 2 * SA);
+    float *sE = reinterpret_cast<float *>(lds + 2 * SW + AB * SA);
 
     // work-group -> tile: work-group i runs on XCD i % 8; XCD x takes a
     // contiguous range of tiles, so the token tiles of one W tile share an L2
@@ -433,18 +454,20 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC * Cfg::NT / 256) void gemm_q4k_f1
     const uint8_t *wrow[WPT];
 #pragma unroll
     for (int k = 0; k < WPT; ++k) {
+        // piece p: row p % BN, half p / BN, so the 8 lanes of each LDS store
+        // group write 8 consecutive rows (distinct banks at an 80-half pitch)
         const int p = tid + NT * k;
         wown[k] = p < WP;
-        wr[k] = min(p >> 1, BN - 1);
-        wh[k] = p & 1;
+        wr[k] = p % BN;
+        wh[k] = (p / BN) & 1;
         wrow[k] = w + (size_t)min(n0 + wr[k], n - 1) * row_bytes;
     }
 
     // ---- per-row range: bound on |weight| over the row's blocks ------------
-    // (two threads per row, blocks wh, wh+2, ..., eight loads in flight)
+    // (each of a row's two piece threads reads all of its block headers)
     float bound[WPT];
 #pragma unroll
-    for (int k = 0; k < WPT; ++k) bound[k] = row_range_bound(wrow[k], wh[k], 2, bpr);
+    for (int k = 0; k < WPT; ++k) bound[k] = row_range_bound(wrow[k], 0, 1, bpr);
 
     // ---- step loaders (registers) ------------------------------------------
     const uint16_t *aptr[APT];
@@ -476,7 +499,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC * Cfg::NT / 256) void gemm_q4k_f1
     float srow[WPT];
 #pragma unroll
     for (int k = 0; k < WPT; ++k) {
-        const int e = range_exp(fmaxf(bound[k], __shfl_xor(bound[k], 1, 64)));
+        const int e = range_exp(bound[k]);
         srow[k] = ldexpf(1.0f, e);
         if (wown[k] && wh[k] == 0) sE[wr[k]] = ldexpf(1.0f, -e);
     }
@@ -484,7 +507,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC * Cfg::NT / 256) void gemm_q4k_f1
     // step t -> LDS buffer: activations copied, weights dequantized
     const uint32_t magic = __builtin_amdgcn_readfirstlane(0x64006400u) + (uint32_t)(tid >> 16);
     auto storeA = [&](int set, int buf) __attribute__((always_inline)) {
-        uint8_t *dA = lds + 2 * SW + buf * SA;
+        uint8_t *dA = lds + 2 * SW + (AB == 2 ? buf : 0) * SA;
 #pragma unroll
         for (int k = 0; k < APT; ++k) *reinterpret_cast<u32x4 *>(dA + alds[k]) = Ar[set][k];
     };
@@ -535,7 +558,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC * Cfg::NT / 256) void gemm_q4k_f1
         for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     auto compute = [&](int buf) __attribute__((always_inline)) {
         const _Float16 *W_ = sW + buf * (BN * PITCH);
-        const _Float16 *A_ = sA + buf * (BM * PITCH);
+        const _Float16 *A_ = sA + (AB == 2 ? buf : 0) * (BM * PITCH);
         if constexpr (Cfg::PRE) {
             half8 wa[2][TI], tb[2][TJ];
 #pragma unroll
@@ -593,6 +616,18 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC * Cfg::NT / 256) void gemm_q4k_f1
         constexpr int P = decltype(par)::value;  // t & 1
         constexpr int NS = (P + 1) & 1;           // buffer / weight set of step t+1
         constexpr int AN = AS == 2 ? NS : 0;      // activation set of step t+1
+        if constexpr (AB == 1) {
+            // one activation buffer: every wavefront is done reading step t's
+            // activations before step t+1's are written over them
+            compute(P);
+            __syncthreads();
+            storeA(AN, NS);
+            storeW(t + 1, NS, NS);
+            loadA(t + AD, AN);
+            loadW(t + 3, NS);
+            __syncthreads();
+            return;
+        }
         if (!dq_first) compute(P);
         storeA(AN, NS);
         storeW(t + 1, NS, NS);
@@ -601,11 +636,11 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC * Cfg::NT / 256) void gemm_q4k_f1
         if (dq_first) compute(P);
         __syncthreads();
     };
-    // Wavefronts w and w + 4 share a SIMD: with 8 wavefronts the first
-    // computes and then dequantizes, the second dequantizes and then
-    // computes, so one's dequant VALU work runs while the other's MFMAs
-    // occupy the matrix core.
-    if (NT / 64 <= 4 || wave < 4) {
+    // Wavefronts w, w + 4, ... share a SIMD: with 8 or more wavefronts the
+    // first half computes and then dequantizes, the second half dequantizes
+    // and then computes, so dequant VALU work runs while other wavefronts'
+    // MFMAs occupy the matrix core.
+    if (NT / 64 <= 4 || wave < NT / 128) {
         for (int t = 0; t < T; t += 2) {
             stage(t, std::integral_constant<int, 0>{}, false);
             stage(t + 1, std::integral_constant<int, 1>{}, false);  // T % 4 == 0
@@ -678,7 +713,16 @@ hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n,
         const char *v = std::getenv("MGQ_GEMM_LDS");
         return (v && *v) ? std::atoi(v) : -1;
     }();
-    if (big_env == 1 || (big_env < 0 && m_tokens >= 384))
+    // The LDS-dequant kernel computes whole 256-token tiles, one work-group
+    // per CU: it wins (M = 512 x 18944: 96-101 against 101-102 us) only when
+    // its token tiles are nearly full and its tiles make one nearly full
+    // round; otherwise (M = 256: 88 against 66 us; M = 384: half-empty token
+    // tiles; M >= 768: a second, partial round) the 128-token kernel below.
+    const long tn2 = (n + G2Cfg::BN - 1) / G2Cfg::BN, tm2 = (m_tokens + G2Cfg::BM - 1) / G2Cfg::BM;
+    const long cus2 = device_cus();
+    const bool lds_fits = 10L * m_tokens >= 9L * G2Cfg::BM * tm2 && tn2 * tm2 <= cus2 &&
+                          2 * tn2 * tm2 > cus2;
+    if (big_env == 1 || (big_env < 0 && lds_fits))
         return gemm_lds_launch(w, a, c, n, bpr, m_tokens, stream);
     // Tile height by the rows the busiest CU computes: ceil(tiles / #CUs) x
     // BN, the lower one, ties to 160 (a second resident tile on a CU adds

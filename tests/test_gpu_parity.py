@@ -357,22 +357,44 @@ def _range_weight(rng, n, bpr, kind):
     return b.ravel()
 
 
-@pytest.mark.parametrize("m", [40, 384])
+def _gemm_check(L, orc, w, a, n, bpr, m, rows=None):
+    wt, at, ct = dev(w), dev(a.view(np.uint16)), empty_f32(m * n)
+    _lib.check("gemm", L.launch_gemm_q4k_f16(ptr(wt), ptr(at), ptr(ct), n, bpr, m, None))
+    C = host(ct).reshape(m, n).astype(np.float64)
+    assert np.all(np.isfinite(C))
+    C_ref, A = orc.gemm_f16(w, a.view(np.uint16), n, bpr, rows=rows)
+    if rows is not None:
+        C = C[:, rows]
+    k = bpr * 256
+    assert np.all(np.abs(C - C_ref) <= 1e-2 * A / np.sqrt(k))
+    assert np.linalg.norm(C - C_ref) <= 1e-3 * np.linalg.norm(C_ref)
+
+
+# (200, 40): the 128-token kernel; (32000, 256): 200 tiles of 160 x 256, the
+# LDS-dequant kernel (rows sampled)
+@pytest.mark.parametrize("n,m", [(200, 40), (32000, 256)])
 @pytest.mark.parametrize("kind", ["tiny", "huge", "mixed", "random"])
-def test_gemm_f16_dynamic_range(L, orc, kind, m):
-    n, bpr = 200, 4
+def test_gemm_f16_dynamic_range(L, orc, kind, n, m):
+    bpr = 4 if n < 1000 else 1
     note(f"gemm range {kind} n={n} bpr={bpr} m={m}")
     rng = np.random.default_rng(0x6E11 + m)
     w = _range_weight(rng, n, bpr, kind)
     a = rng.normal(0, 1, size=(m, bpr * 256)).astype(np.float16)
-    wt, at, ct = dev(w), dev(a.view(np.uint16)), empty_f32(m * n)
-    _lib.check("gemm", L.launch_gemm_q4k_f16(ptr(wt), ptr(at), ptr(ct), n, bpr, m, None))
-    C = host(ct).reshape(m, n).astype(np.float64)
-    C_ref, A = orc.gemm_f16(w, a.view(np.uint16), n, bpr)
-    k = bpr * 256
-    assert np.all(np.isfinite(C))
-    assert np.all(np.abs(C - C_ref) <= 1e-2 * A / np.sqrt(k))
-    assert np.linalg.norm(C - C_ref) <= 1e-3 * np.linalg.norm(C_ref)
+    rows = None if n < 1000 else np.sort(rng.choice(n, size=192, replace=False)).astype(np.int32)
+    _gemm_check(L, orc, w, a, n, bpr, m, rows)
+
+
+# Shapes the LDS-dequant kernel takes (one nearly full round of 160 x 256
+# tiles): full token tiles, ragged tokens, ragged rows, several super-blocks
+@pytest.mark.parametrize("n,bpr,m", [(32000, 1, 256), (30000, 3, 250), (20000, 14, 512)])
+def test_gemm_lds_kernel_shapes(L, orc, n, bpr, m):
+    note(f"gemm lds kernel n={n} bpr={bpr} m={m}")
+    rng = np.random.default_rng(n + m)
+    w = orc.seeded_weight(n + bpr, n, bpr * 256)
+    a = orc.normal(0xF17 + m, m * bpr * 256).astype(np.float16).reshape(m, -1)
+    rows = np.sort(np.concatenate([rng.choice(n - 160, size=120, replace=False),
+                                   np.arange(n - 40, n)])).astype(np.int32)
+    _gemm_check(L, orc, w, a, n, bpr, m, np.unique(rows))
 
 
 # -------------------------------------------------------------------- chain --
