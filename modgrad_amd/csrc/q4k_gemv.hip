@@ -287,7 +287,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
                                                             const float *__restrict__ xsv,
                                                             float *__restrict__ y, int n,
                                                             int bpr, int rounds, GemvFuse fz,
-                                                            GemvSched sch) {
+                                                            GemvSched sch, int gr) {
     static_assert(Q8 ? (FUSE == 0 || FUSE == kFuseQuant) : (FUSE & kFuseQuant) == 0,
                   "fused glue runs on f32 activations; quantization only in Q8 mode");
     static_assert(!(FUSE & kFmtQ5K) || FUSE == kFmtQ5K, "Q5_K weights: plain f32 matvec only");
@@ -304,7 +304,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     float *aux = reinterpret_cast<float *>(lds + Lo.aux);
     const size_t row_bytes = (size_t)bpr * BB;
     const int stages = (bpr + C - 1) / C;
-    const int groups = (n + R - 1) / R;
+    // a row group is gr <= R rows (the tile's rows past gr re-read row gr - 1)
+    const int groups = (n + gr - 1) / gr;
     const int my_groups = sched_count(sch, (int)blockIdx.x, (int)gridDim.x, groups);
     const int Q = my_groups * VM * stages;        // stages this work-group streams
     constexpr int PIECES = R * BP * C;            // 16-byte pieces per stage
@@ -336,13 +337,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         q = std::min(q, Q - 1);
         const int vg = q / stages;  // pass index: row group vg / VM, matrix vg % VM
         const uint32_t r0 =
-            (uint32_t)sched_group(sch, (int)blockIdx.x, (int)gridDim.x, vg / VM) * R;
+            (uint32_t)sched_group(sch, (int)blockIdx.x, (int)gridDim.x, vg / VM) * (uint32_t)gr;
+        const uint32_t glast = (uint32_t)gr - 1u;
         const uint8_t *wm = (VM == 2 && (vg & 1)) ? fz.w2 : w;
         const uint32_t tcol = (uint32_t)((q % stages) * C * BB);
         const uint32_t rlast = (uint32_t)(n - 1), rb = (uint32_t)row_bytes;
 #pragma unroll
         for (int k = 0; k < IPW; ++k) {
-            const uint32_t rr = std::min(r0 + prow[k], rlast);
+            const uint32_t rr = std::min(r0 + std::min(prow[k], glast), rlast);
             const uint32_t col = std::min(tcol + pcol[k], plast[k]);
             const uint64_t off = (uint64_t)rr * rb + col;  // one v_mad_u64_u32
             dst[k] = ld_u32x4(wm + off);
@@ -751,8 +753,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     }
     const float *yb = reinterpret_cast<const float *>(lds + Lo.ybuf);
     for (int i = tid; i < my_groups * R; i += NW * 64) {
-        const int r = sched_group(sch, (int)blockIdx.x, (int)gridDim.x, i / R) * R + (i % R);
-        if (r < n) {
+        const int ri = i % R;
+        const int r = sched_group(sch, (int)blockIdx.x, (int)gridDim.x, i / R) * gr + ri;
+        if (ri < gr && r < n) {
             if constexpr (VM == 2) {
                 // pass 2j = gate rows of group j, 2j+1 = up rows
                 const int gi = (i / R) * 2 * R + (i % R);
@@ -799,11 +802,12 @@ static hipError_t lds_attr_all() {
 
 template <int R, int C, int NW, int PF, bool DB, int XIT, bool Q8, int FUSE>
 static hipError_t launch_xit(const uint8_t *w, const GemvAct &a, const GemvFuse &fz, float *y,
-                             int n, int bpr, hipStream_t stream, bool persistent) {
+                             int n, int bpr, hipStream_t stream, bool persistent, int gr) {
     auto kern = gemv_mfma_kernel<R, C, NW, PF, DB, XIT, Q8, FUSE>;
     const hipError_t attr = lds_attr<R, C, NW, PF, DB, XIT, Q8, FUSE>();
     if (attr != hipSuccess) return attr;
-    const long groups = (n + R - 1) / R;
+    if (gr <= 0 || gr > R) gr = R;
+    const long groups = (n + gr - 1) / gr;
     long grid = groups, rounds = 1;
     GemvSched sch{(int)groups, 0};
     if (persistent) {
@@ -822,7 +826,7 @@ static hipError_t launch_xit(const uint8_t *w, const GemvAct &a, const GemvFuse 
     const MfmaLayout Lo = mfma_layout(bpr, R, C, NW, (int)rounds, DB, Q8, FUSE);
     if (Lo.total > 160 * 1024) return hipErrorNotSupported;
     kern<<<(unsigned)grid, NW * 64, Lo.total, stream>>>(w, a.x, a.xq, a.xd, a.xsum, y, n, bpr,
-                                                        (int)rounds, fz, sch);
+                                                        (int)rounds, fz, sch, gr);
     return hipGetLastError();
 }
 
@@ -831,10 +835,10 @@ static hipError_t launch_xit(const uint8_t *w, const GemvAct &a, const GemvFuse 
 // 16-byte items, bpr*20 of them).
 template <int R, int C, int NW, int PF, bool DB, bool Q8, int FUSE>
 static hipError_t launch_cfg(const uint8_t *w, const GemvAct &a, const GemvFuse &fz, float *y,
-                             int n, int bpr, hipStream_t stream, bool persistent) {
+                             int n, int bpr, hipStream_t stream, bool persistent, int gr = 0) {
     const int items = (Q8 && !(FUSE & kFuseQuant)) ? bpr * 20 : bpr * 32;
     const int need = (items + NW * 64 - 1) / (NW * 64);
-#define MGQ_XIT(X) launch_xit<R, C, NW, PF, DB, X, Q8, FUSE>(w, a, fz, y, n, bpr, stream, persistent)
+#define MGQ_XIT(X) launch_xit<R, C, NW, PF, DB, X, Q8, FUSE>(w, a, fz, y, n, bpr, stream, persistent, gr)
     if (need <= 1) return MGQ_XIT(1);
     if (need <= 2) return MGQ_XIT(2);
     if (need <= 4) return MGQ_XIT(4);
@@ -849,8 +853,10 @@ static hipError_t launch_cfg(const uint8_t *w, const GemvAct &a, const GemvFuse 
 // (The fused variants instantiate only the dispatched configurations 0-3.)
 template <bool Q8, int FUSE>
 static hipError_t launch_any(int cfg, const uint8_t *w, const GemvAct &a, const GemvFuse &fz,
-                             float *y, int n, int bpr, hipStream_t stream) {
+                             float *y, int n, int bpr, hipStream_t stream, int gr = 0) {
     switch (cfg) {
+        // one group of gr (17..32) rows per CU: two 16-row tiles, 14 waves
+        case 8: return launch_cfg<32, 14, 14, 1, false, Q8, FUSE>(w, a, fz, y, n, bpr, stream, false, gr);
         case 0: return launch_cfg<32, 8, 8, 1, false, Q8, FUSE>(w, a, fz, y, n, bpr, stream, true);
         case 1: return launch_cfg<16, 14, 7, 1, true, Q8, FUSE>(w, a, fz, y, n, bpr, stream, false);
         case 2: return launch_cfg<16, 16, 8, 1, true, Q8, FUSE>(w, a, fz, y, n, bpr, stream, false);
@@ -872,6 +878,7 @@ static hipError_t launch_any(int cfg, const uint8_t *w, const GemvAct &a, const 
 template <int FUSE>
 static hipError_t prepare_fuse() {
     hipError_t e = lds_attr_all<32, 8, 8, 1, false, false, FUSE>();
+    if (e == hipSuccess) e = lds_attr_all<32, 14, 14, 1, false, false, FUSE>();
     if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, false, false, FUSE>();
     if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, true, false, FUSE>();
     if (e == hipSuccess) e = lds_attr_all<16, 16, 8, 1, true, false, FUSE>();
@@ -884,6 +891,8 @@ hipError_t gemv_prepare() {
     if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, true, true>();
     if (e == hipSuccess) e = lds_attr_all<16, 16, 8, 1, true, true>();
     if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, false, true>();
+    if (e == hipSuccess) e = lds_attr_all<32, 14, 14, 1, false, true>();
+    if (e == hipSuccess) e = lds_attr_all<32, 14, 14, 1, false, true, kFuseQuant>();
     if (e == hipSuccess) e = lds_attr_all<32, 8, 8, 1, false, true, kFuseQuant>();
     if (e == hipSuccess) e = lds_attr_all<16, 14, 7, 1, true, true, kFuseQuant>();
     if (e == hipSuccess) e = lds_attr_all<16, 16, 8, 1, true, true, kFuseQuant>();
@@ -901,7 +910,7 @@ static hipError_t mfma_dispatch(const uint8_t *w, const GemvAct &a, float *y, in
                                 hipStream_t stream, const GemvFuse &fz = GemvFuse{},
                                 int work_rows = 0) {
     static const int force = env_int("MGQ_GEMV_CFG", -1);  // tuning override
-    int cfg;
+    int cfg, gr = 0;
     if (force >= 0) {
         cfg = force;
     } else {
@@ -909,11 +918,21 @@ static hipError_t mfma_dispatch(const uint8_t *w, const GemvAct &a, float *y, in
         // run of HBM), single-buffered so three work-groups share a CU,
         // persistent. Longer K: 16 blocks per stage, or persistent 32-row
         // groups of 8 blocks when the groups outnumber the CUs.
-        const bool many = ((work_rows > 0 ? work_rows : n) + 15) / 16 > device_cus();
+        const long g16 = ((work_rows > 0 ? work_rows : n) + 15) / 16, cus = device_cus();
+        const bool many = g16 > cus;
         if (bpr <= 14) cfg = 6;
         else cfg = many ? 0 : 2;
+        // Between one and 1.5 16-row groups per CU (qkv 4608 x 3584: 288),
+        // the CUs that get a second group set the time (256 groups: 5.45 us,
+        // 257: 6.21, 288: 6.73): one group of ceil(N / #CUs) rows per CU
+        // instead (288: 6.30, 384: 6.78 against 6.82). From ~416 groups on
+        // the second groups are spread evenly enough that it loses.
+        if (bpr <= 14 && work_rows == 0 && g16 > cus && 2 * g16 <= 3 * cus) {
+            gr = (int)((n + cus - 1) / cus);
+            cfg = 8;
+        }
     }
-    hipError_t e = launch_any<Q8, FUSE>(cfg, w, a, fz, y, n, bpr, stream);
+    hipError_t e = launch_any<Q8, FUSE>(cfg, w, a, fz, y, n, bpr, stream, gr);
     // LDS too small for the double-buffered stages (Q5_K's 176-byte blocks on
     // down): single-buffered 16-row stages (26.2 -> 17.9 us on Q5_K
     // 3584x18944), then persistent 32-row groups

@@ -320,6 +320,20 @@ def test_matvec_batched_single_row_is_the_matvec(L, orc):
     assert np.array_equal(Y[0], run_gemv(L, w, x, n, bpr))
 
 
+# Just past one 16-row group per CU the launcher runs one group of
+# ceil(N / #CUs) rows per CU (two 16-row tiles, rows past the group re-read
+# its last row): ragged groups, several K lengths, random bytes.
+@pytest.mark.parametrize("n,bpr", [(4112, 14), (4600, 7), (6000, 1), (5000, 14)])
+def test_matvec_one_group_per_cu_shapes(L, orc, n, bpr):
+    note(f"matvec one group per CU n={n} bpr={bpr}")
+    rng = np.random.default_rng(n * 31 + bpr)
+    w = random_q4k_bytes(rng, n * bpr)
+    x = rng.standard_normal(bpr * 256).astype(np.float32)
+    y = run_gemv(L, w, x, n, bpr)
+    y_ref, a = orc.gemv(w, x, n, bpr)
+    assert_gemv_close(y, y_ref, a)
+
+
 # --------------------------------------------------------------------- GEMM --
 # (70000, 1, 16): 547 tiles of 128 rows but 438 of 160 for 512 resident
 # slots, so the 160-row tile runs; the others, ragged tiles of either height
