@@ -369,20 +369,28 @@ __global__ __launch_bounds__(512) void gemv_batched_mfma_kernel(const uint8_t *_
             *yb = (sl == 0) ? sum : *yb + sum;
         }
     };
+    static_assert(PF >= 1 && PF <= 8, "register sets are indexed by compile-time constants up to 8");
+    // stage q0 + f with register set f (a compile-time index), for every
+    // f < PF while q0 + f < lim
+    auto steps = [&](const int q0, const int lim) __attribute__((always_inline)) {
+#define MGQ_STEP(f)                                                                         \
+        if constexpr (PF > (f))                                                             \
+            if (q0 + (f) < lim) step(q0 + (f), std::integral_constant<int, (f) % PF>{}, q0 + (f) + 1 < Q);
+        MGQ_STEP(0) MGQ_STEP(1) MGQ_STEP(2) MGQ_STEP(3)
+        MGQ_STEP(4) MGQ_STEP(5) MGQ_STEP(6) MGQ_STEP(7)
+#undef MGQ_STEP
+    };
     lstore(stg[0]);
     int q0 = 0;
     if (Q > PF) {
         gload(PF, stg[0]);
         __syncthreads();
-        for (; q0 + PF < Q; q0 += PF) {
-            step(q0, std::integral_constant<int, 0>{}, true);
-            if constexpr (PF > 1) step(q0 + 1, std::integral_constant<int, 1 % PF>{}, true);
-        }
+        // every stage of these rounds has a next one (q0 + PF < Q)
+        for (; q0 + PF < Q; q0 += PF) steps(q0, q0 + PF);
     } else {
         __syncthreads();
     }
-    if (q0 < Q) step(q0, std::integral_constant<int, 0>{}, q0 + 1 < Q);
-    if constexpr (PF > 1) if (q0 + 1 < Q) step(q0 + 1, std::integral_constant<int, 1 % PF>{}, q0 + 2 < Q);
+    steps(q0, Q);  // the last <= PF stages
     __syncthreads();
     // Y[b][r], rows fastest
     for (int i = tid; i < my_groups * R * BP; i += NW * 64) {
@@ -442,11 +450,23 @@ hipError_t gemv_batched_mfma_launch(const uint8_t *w, const float *X, float *Y, 
         X, batch, bpr, sets, ((uintptr_t)X & 15u) == 0, ws, Y, ksplit ? batch * n : 0);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    // Weight stages in flight (register sets). One batch set (B <= 8), µs
+    // per call at B = 8, gate / down, table pass included: 2 stages
+    // 18.8 / 20.8, 3: 19.7 / 21.7, 4: 19.7 / 22.8, 6: 21.2 / 24.2,
+    // 8: 22.6 / 29.1 (VGPRs 167 -> 239 for the 16-row kernel). Two sets
+    // (B <= 16) run at 256 VGPRs and stay at one stage (two: down 25.9 ->
+    // 85 us).
+#ifndef MGQ_BPF1
+#define MGQ_BPF1 2
+#endif
+#ifndef MGQ_BPF2
+#define MGQ_BPF2 1
+#endif
     if (ksplit)
-        return sets == 1 ? batched_main_launch<32, 1, 2>(w, ws, Y, n, bpr, batch, 2, stream)
-                         : batched_main_launch<32, 2, 1>(w, ws, Y, n, bpr, batch, 2, stream);
-    if (sets == 1) return batched_main_launch<16, 1, 2>(w, ws, Y, n, bpr, batch, 1, stream);
-    return batched_main_launch<16, 2, 1>(w, ws, Y, n, bpr, batch, 1, stream);
+        return sets == 1 ? batched_main_launch<32, 1, MGQ_BPF1>(w, ws, Y, n, bpr, batch, 2, stream)
+                         : batched_main_launch<32, 2, MGQ_BPF2>(w, ws, Y, n, bpr, batch, 2, stream);
+    if (sets == 1) return batched_main_launch<16, 1, MGQ_BPF1>(w, ws, Y, n, bpr, batch, 1, stream);
+    return batched_main_launch<16, 2, MGQ_BPF2>(w, ws, Y, n, bpr, batch, 1, stream);
 }
 
 }  // namespace mgq
