@@ -398,6 +398,20 @@ def test_gemm_f16_dynamic_range(L, orc, kind, n, m):
     _gemm_check(L, orc, w, a, n, bpr, m, rows)
 
 
+# The 128-token kernel at its 160-row tile height with several super-blocks
+# (the raw-W LDS refill across super-blocks) and several token tiles:
+# (70000, 3, 16) and the config-5 weight at M = 256 (rows sampled)
+@pytest.mark.parametrize("n,bpr,m", [(70000, 3, 16), (18944, 14, 256)])
+def test_gemm_160_row_tiles_multi_block(L, orc, n, bpr, m):
+    note(f"gemm 160-row tiles n={n} bpr={bpr} m={m}")
+    rng = np.random.default_rng(n + bpr + m)
+    w = orc.seeded_weight(0x160 + bpr, n, bpr * 256)
+    a = orc.normal(0xF18 + m, m * bpr * 256).astype(np.float16).reshape(m, -1)
+    rows = np.unique(np.concatenate([rng.choice(n, size=160, replace=False),
+                                     np.arange(n - 32, n)])).astype(np.int32)
+    _gemm_check(L, orc, w, a, n, bpr, m, rows)
+
+
 # Shapes the LDS-dequant kernel takes (one nearly full round of 160 x 256
 # tiles): full token tiles, ragged tokens, ragged rows, several super-blocks
 @pytest.mark.parametrize("n,bpr,m", [(32000, 1, 256), (30000, 3, 250), (20000, 14, 512)])
