@@ -357,10 +357,40 @@ def run_batched(torch, q4k, args):
             if not np.all(r <= 1e-4):
                 parity = f"FAIL {name} b={b}: max err/absdot {r.max():.3e}"
     parity = parity or f"ok (max err/absdot {worst:.2e} <= 1e-4)"
+    # per shape, and gate|up as one call: in a model gate and up read the
+    # same X, so with their rows contiguous (one 37888-row tensor, as the
+    # decode workload stores them) one operand table serves both
+    per_shape = {}
+    for name in ("gate", "down"):
+        sub = [it for it in items if it[0] == name]
+
+        def launch_one(st, sub=sub):
+            for _, w, X, Y, ws, n, bpr in sub:
+                q4k.kern.matvec_q4k_batched(w.data_ptr(), X.data_ptr(), Y.data_ptr(), n, bpr, B, st,
+                                            workspace=ws)
+        per_shape[f"{name}_us"] = round(time_captured(torch, launch_one, args.steps, args.warmup)
+                                        * 1e3 / len(sub), 3)
+    gu = []
+    for c in range(copies // 2):
+        bpr = HIDDEN // BLOCK_ELEMS
+        w = make_q4k(torch, 2 * INTER, HIDDEN, gen)
+        X = torch.randn((B, HIDDEN), device="cuda", generator=gen)
+        Y = torch.empty((B, 2 * INTER), device="cuda")
+        ws = torch.empty(q4k.kern.batched_workspace_bytes(bpr, B), dtype=torch.uint8, device="cuda")
+        gu.append((w, X, Y, ws, 2 * INTER, bpr))
+
+    def launch_gu(st):
+        for w, X, Y, ws, n, bpr in gu:
+            q4k.kern.matvec_q4k_batched(w.data_ptr(), X.data_ptr(), Y.data_ptr(), n, bpr, B, st,
+                                        workspace=ws)
+    us_gu = time_captured(torch, launch_gu, args.steps, args.warmup) * 1e3 / len(gu)
+    gu_bytes = 2 * INTER * (HIDDEN // BLOCK_ELEMS) * BLOCK_BYTES + 4 * B * (HIDDEN + 2 * INTER)
+    per_shape["gate_up_fused_37888x3584_us"] = round(us_gu, 3)
+    per_shape["gate_up_fused_gbs"] = round(gu_bytes / (us_gu * 1e-6) / 1e9, 1)
     return {"workload": f"config4: batched B={B}, gate 18944x3584 + down 3584x18944, "
                         f"{copies} rotating copies, one graph",
             "us_per_launch": round(ms * 1e3 / len(items), 3), "gbs": nbytes / (ms * 1e-3) / 1e9,
-            "bytes_per_launch": nbytes // len(items), "parity": parity,
+            "bytes_per_launch": nbytes // len(items), "parity": parity, "per_shape": per_shape,
             "kernel": "mgq::gemv_batched_mfma_kernel (+ batched_table_kernel)"}
 
 
