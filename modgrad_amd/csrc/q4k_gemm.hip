@@ -50,14 +50,11 @@ namespace mgq {
 namespace gemm {
 constexpr int BM = 128;        // tokens per work-group
 constexpr int BK = 64;         // k per step (one 32-byte qs group: 2 sub-blocks)
-#ifndef MGQ_AROW
-#define MGQ_AROW 80
-#endif
 // halves per activation LDS row: 64 + 16 pad (160 B). At this pitch the 16
 // lanes of a b128 operand read hit distinct banks (measured: 4 cycles per
 // read against 8 at a 72-half pitch, and ~60 when rows are not 16-byte
 // aligned).
-constexpr int AROW = MGQ_AROW;
+constexpr int AROW = 80;
 constexpr int SROW = 10;       // dwords per scale row (8 + 2 pad: conflict-free b64 reads)
 constexpr int NXCD = 8;        // XCDs the hardware deals work-groups across, round robin
 }  // namespace gemm
@@ -369,13 +366,10 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__r
 // register sets (2: loaded two steps ahead, like the weights; 1: one step
 // ahead). PRE: a step's MFMA operands are all read from LDS before its
 // first MFMA.
-template <int WN_, int WM_, int TI_, int TJ_, int ASETS_, bool PRE_, int PITCH_ = 80, int OCC_ = 1,
-          int ABUF_ = 2>
+template <int WN_, int WM_, int TI_, int TJ_, int ASETS_, bool PRE_, int PITCH_ = 80>
 struct G2 {
-    static constexpr int ABUF = ABUF_;            // activation LDS buffers (1: two barriers per step)
     static constexpr int WN = WN_, WM = WM_, TI = TI_, TJ = TJ_, ASETS = ASETS_;
     static constexpr bool PRE = PRE_;
-    static constexpr int OCC = OCC_;              // resident work-groups per CU
     static constexpr int BN = WN * 16 * TI;       // W rows per work-group
     static constexpr int BM = WM * 16 * TJ;       // tokens per work-group
     static constexpr int NT = 64 * WN * WM;       // threads
@@ -386,53 +380,29 @@ struct G2 {
     static constexpr int WPT = (WP + NT - 1) / NT;
     static constexpr int APT = BM * 8 / NT;       // activation pieces per thread per step
     static constexpr uint32_t SW = BN * PITCH * 2, SA = BM * PITCH * 2;
-    static constexpr uint32_t LDS = 2 * SW + ABUF * SA + BN * 4;
+    static constexpr uint32_t LDS = 2 * SW + 2 * SA + BN * 4;
     static_assert(BM * 8 % NT == 0, "whole activation pieces per thread");
 };
 
-#ifndef MGQ_GEMM_CFG
-#define MGQ_GEMM_CFG 2
-#endif
-#if MGQ_GEMM_CFG == 0
-using G2Cfg = G2<2, 4, 5, 4, 2, false>;
-#elif MGQ_GEMM_CFG == 1
-using G2Cfg = G2<2, 4, 5, 4, 1, false>;
-#elif MGQ_GEMM_CFG == 2
+// 160 W rows x 256 tokens, 8 wavefronts of 80 x 64, activations one step
+// ahead, operands preloaded. Alternatives measured on the config-5 shape and
+// not kept: two activation sets (+3-5 %), 4 wavefronts of 160 x 64 with AGPR
+// accumulators, 16 wavefronts of 80 x 32, two 4-wavefront work-groups per CU
+// with a single activation buffer (all slower).
 using G2Cfg = G2<2, 4, 5, 4, 1, true>;
-#elif MGQ_GEMM_CFG == 3
-using G2Cfg = G2<1, 4, 10, 4, 2, false>;
-#elif MGQ_GEMM_CFG == 4
-using G2Cfg = G2<1, 4, 10, 4, 2, true>;
-#elif MGQ_GEMM_CFG == 5
-using G2Cfg = G2<1, 4, 10, 4, 1, true>;
-#elif MGQ_GEMM_CFG == 6
-using G2Cfg = G2<2, 2, 5, 4, 1, true, 68, 2>;
-#elif MGQ_GEMM_CFG == 7
-using G2Cfg = G2<2, 2, 5, 4, 2, true, 68, 2>;
-#elif MGQ_GEMM_CFG == 8
-using G2Cfg = G2<2, 2, 5, 4, 1, true, 72, 2, 1>;
-#elif MGQ_GEMM_CFG == 9
-using G2Cfg = G2<2, 2, 5, 4, 2, true, 72, 2, 1>;
-#elif MGQ_GEMM_CFG == 10
-using G2Cfg = G2<2, 8, 5, 2, 1, false>;
-#elif MGQ_GEMM_CFG == 11
-using G2Cfg = G2<2, 8, 5, 2, 1, true>;
-#elif MGQ_GEMM_CFG == 12
-using G2Cfg = G2<2, 8, 5, 2, 2, false>;
-#endif
 
 template <class Cfg>
-__global__ __launch_bounds__(Cfg::NT, Cfg::OCC * Cfg::NT / 256) void gemm_q4k_f16_lds_kernel(
+__global__ __launch_bounds__(Cfg::NT, Cfg::NT / 256) void gemm_q4k_f16_lds_kernel(
     const uint8_t *__restrict__ w, const uint16_t *__restrict__ a, float *__restrict__ c, int n,
     int bpr, int m_tokens, int tiles_n, int tiles_m) {
     constexpr int WN = Cfg::WN, TI = Cfg::TI, TJ = Cfg::TJ, BN = Cfg::BN, BM = Cfg::BM;
     constexpr int NT = Cfg::NT, KS = Cfg::KS, PITCH = Cfg::PITCH, WP = Cfg::WP, WPT = Cfg::WPT;
-    constexpr int APT = Cfg::APT, AS = Cfg::ASETS, AB = Cfg::ABUF;
+    constexpr int APT = Cfg::APT, AS = Cfg::ASETS;
     constexpr uint32_t SW = Cfg::SW, SA = Cfg::SA;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     _Float16 *sW = reinterpret_cast<_Float16 *>(lds);
     _Float16 *sA = reinterpret_cast<_Float16 *>(lds + 2 * SW);
-    float *sE = reinterpret_cast<float *>(lds + 2 * SW + AB * SA);
+    float *sE = reinterpret_cast<float *>(lds + 2 * SW + 2 * SA);
 
     // work-group -> tile: work-group i runs on XCD i % 8; XCD x takes a
     // contiguous range of tiles, so the token tiles of one W tile share an L2
@@ -507,7 +477,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC * Cfg::NT / 256) void gemm_q4k_f1
     // step t -> LDS buffer: activations copied, weights dequantized
     const uint32_t magic = __builtin_amdgcn_readfirstlane(0x64006400u) + (uint32_t)(tid >> 16);
     auto storeA = [&](int set, int buf) __attribute__((always_inline)) {
-        uint8_t *dA = lds + 2 * SW + (AB == 2 ? buf : 0) * SA;
+        uint8_t *dA = lds + 2 * SW + buf * SA;
 #pragma unroll
         for (int k = 0; k < APT; ++k) *reinterpret_cast<u32x4 *>(dA + alds[k]) = Ar[set][k];
     };
@@ -558,7 +528,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC * Cfg::NT / 256) void gemm_q4k_f1
         for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     auto compute = [&](int buf) __attribute__((always_inline)) {
         const _Float16 *W_ = sW + buf * (BN * PITCH);
-        const _Float16 *A_ = sA + (AB == 2 ? buf : 0) * (BM * PITCH);
+        const _Float16 *A_ = sA + buf * (BM * PITCH);
         if constexpr (Cfg::PRE) {
             half8 wa[2][TI], tb[2][TJ];
 #pragma unroll
@@ -616,18 +586,6 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC * Cfg::NT / 256) void gemm_q4k_f1
         constexpr int P = decltype(par)::value;  // t & 1
         constexpr int NS = (P + 1) & 1;           // buffer / weight set of step t+1
         constexpr int AN = AS == 2 ? NS : 0;      // activation set of step t+1
-        if constexpr (AB == 1) {
-            // one activation buffer: every wavefront is done reading step t's
-            // activations before step t+1's are written over them
-            compute(P);
-            __syncthreads();
-            storeA(AN, NS);
-            storeW(t + 1, NS, NS);
-            loadA(t + AD, AN);
-            loadW(t + 3, NS);
-            __syncthreads();
-            return;
-        }
         if (!dq_first) compute(P);
         storeA(AN, NS);
         storeW(t + 1, NS, NS);
