@@ -604,7 +604,7 @@ def assert_dp4a_close(y, y_ref, absterm, tol=1e-5):
 
 
 @pytest.mark.parametrize("n,bpr", [(1, 1), (17, 3), (64, 14), (3584, 14), (700, 74), (4100, 17),
-                                   (30000, 14), (300, 100)])
+                                   (30000, 14), (300, 100), (4608, 14), (6000, 5)])
 def test_dp4a_matvec_matches_oracle(L, orc, n, bpr):
     # shapes that take each launch configuration of the matrix-core kernel's
     # Q8 mode (few/many row groups, one/several stages, fallback to
@@ -707,7 +707,9 @@ def test_dp4a_nonfinite_rows_are_zero(L, orc):
                                    # Q6_K K-chunked stages: chunk remainders, odd bpr (2-byte
                                    # aligned rows), a partial last group, 2 rounds, 8 items/thread
                                    (16, 15), (48, 29), (520, 43), (9600, 16), (3584, 74),
-                                   (232, 101)])
+                                   (232, 101),
+                                   # one row group per CU (Q5_K: 17..24-row groups)
+                                   (4608, 14), (6000, 7)])
 def test_kquant_matvec_matches_oracle(L, orc, fmt, n, bpr):
     from tests.gpu_util import random_kquant_bytes
     note(f"{'q5k' if fmt == 176 else 'q6k'} n={n} bpr={bpr}")
