@@ -104,9 +104,7 @@ def time_graph(torch, q4k, wl: Workload, steps: int, warmup: int, mode: str = "a
                        for _, w, x, y, n, k in wl.launches], CHAIN_MODES[mode])
     impl = "persistent" if chain.mode() == CHAIN_MODES["persistent"] else "graph"
     stream = torch.cuda.current_stream()
-    for i in range(warmup):
-        chain.launch(stream)
-    torch.cuda.synchronize()
+    _settle(torch, lambda: chain.launch(stream), stream, warmup)
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record(stream)
     for i in range(steps):
@@ -216,6 +214,27 @@ def cpu_baseline(torch, wl: Workload, target_s: float, threads: int, launches: i
             "tokens_per_s_equiv_1thread": round(gbs1 * 1e9 / wl.bytes_per_pass, 4)}
 
 
+WARM_MS = 100.0  # least untimed run time before a timed region (ms)
+
+
+def _settle(torch, run_once, stream, warmup: int) -> None:
+    """`warmup` untimed runs, then more up to ~WARM_MS in all, so that clocks
+    and caches are at steady state when the timed region starts (after a
+    short warm-up the first timed launches of a heavy kernel run ~10 % slow)."""
+    for _ in range(warmup):
+        run_once()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    run_once()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    extra = int(min(2000, max(0.0, WARM_MS / max(t0.elapsed_time(t1), 1e-3) - warmup)))
+    for _ in range(extra):
+        run_once()
+    torch.cuda.synchronize()
+
+
 def time_captured(torch, launch, steps: int, warmup: int) -> float:
     """ms per replay of a HIP graph captured (through torch) from `launch`,
     a callable that enqueues one pass on the stream it is given."""
@@ -226,10 +245,8 @@ def time_captured(torch, launch, steps: int, warmup: int) -> float:
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
         launch(torch.cuda.current_stream())
-    for _ in range(warmup):
-        g.replay()
-    torch.cuda.synchronize()
     cur = torch.cuda.current_stream()
+    _settle(torch, g.replay, cur, warmup)
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record(cur)
     for _ in range(steps):
@@ -254,9 +271,7 @@ def time_op_chain(torch, q4k, ops, steps: int, warmup: int) -> float:
     by the library, mgq_chain_create_ops), timed like time_captured."""
     chain = q4k.Chain.from_ops(ops)
     stream = torch.cuda.current_stream()
-    for _ in range(max(1, warmup)):
-        chain.launch(stream)
-    torch.cuda.synchronize()
+    _settle(torch, lambda: chain.launch(stream), stream, max(1, warmup))
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record(stream)
     for _ in range(steps):
@@ -769,6 +784,7 @@ def run_side_workload(torch, q4k, args) -> int:
           "decode7b_glue": run_decode_glue, "decode7b_q4km": run_decode_q4km}[args.workload]
     r = fn(torch, q4k, args)
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "warmup_min_ms": WARM_MS,
            # ms per graph replay of the headline measurement (dp4a and glue time
            # their two-launch / unfused baseline first)
            "pass_ms_spread": SPREADS[1 if args.workload in ("decode7b_dp4a", "decode7b_glue")
@@ -868,6 +884,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_min_ms": WARM_MS,
         "ms_per_step": round(ms, 5),
         "step_ms_spread": spread,
         "higher_is_better": True,

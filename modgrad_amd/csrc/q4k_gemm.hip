@@ -6,12 +6,13 @@
 // 2^e (row_range_exp: keeps every |weight| of the row below 2^15, so f16
 // neither overflows nor goes subnormal), with d*sc*2^e and dmin*m*2^e
 // rounded to f16 and the weight computed and rounded in f16; C is scaled
-// back by 2^-e exactly.
+// back by 2^-e exactly. (gemm_q4k_f16_lds_kernel applies one more fixed
+// power of two, 2^-20, to the weights and takes it back in C: see there.)
 //
 // Two kernels: gemm_q4k_f16_lds_kernel (below), which dequantizes each W
 // element once per work-group into an f16 LDS tile, where its 160 x 256
-// tiles make one full round (config 5: M = 512, N = 18944); otherwise
-// gemm_q4k_f16_kernel, whose 128-token tiles keep every CU busy.
+// tiles fill their rounds (config 5: M = 512, N = 18944; M = 1024);
+// otherwise gemm_q4k_f16_kernel, whose 128-token tiles keep every CU busy.
 //
 // gemm_q4k_f16_kernel -- work-group tile: BN W rows x 128 tokens (BN = 128 or 160, whichever gives
 // the busiest CU fewer rows to compute), 4 wavefronts of BN/2 x 64 outputs (BN/32 x 4
@@ -75,6 +76,15 @@ __device__ __forceinline__ uint32_t dq2(uint32_t v, uint32_t mask, uint32_t magi
                                         h2_t nm1) {
     const h2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
     const h2_t q = __builtin_bit_cast(h2_t, and_or(v, mask, magic)) - k1024;
+    return __builtin_bit_cast(uint32_t, q * d1 + nm1);
+}
+
+// Two f16 weights (bytes 0 and 2 of v, nibble selected by mask) as a pair:
+// the masked nibble is the f16 subnormal q * 2^-24 (or 16q * 2^-24), exact,
+// and one fused multiply-add with d1 = D (the multiplier times 2^24) gives
+// q * d1 * 2^-24 + nm1 rounded once.
+__device__ __forceinline__ uint32_t dqs2(uint32_t v, uint32_t mask, h2_t d1, h2_t nm1) {
+    const h2_t q = __builtin_bit_cast(h2_t, v & mask);
     return __builtin_bit_cast(uint32_t, q * d1 + nm1);
 }
 
@@ -344,60 +354,51 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__r
 // (tokens), each 80 rows x 64 tokens = 5 x 4 v_mfma_f32_16x16x32_f16 tiles
 // (W rows the A operand, tokens the B operand, so a lane's 4 accumulators
 // are 4 consecutive W rows of one token: one 16-byte store into C [M][N]).
-// One work-group per CU (120 KiB of LDS); at M = 512 and N = 18944 the 238
+// One work-group per CU (134 KiB of LDS); at M = 512 and N = 18944 the 238
 // tiles are one round on the 256 CUs.
 //
 // K step = 64 (one 32-byte qs group: sub-blocks 2G and 2G+1 of a
-// super-block). Per step the work-group loads 160 x 16-byte qs pieces x 2
-// and 256 tokens x 128 B of activations into registers, two steps ahead of
-// the one being computed; a step's registers are written to a double-
-// buffered LDS stage (the activations as they are, the weights dequantized
-// to f16 in natural k order by the thread that loaded them), one barrier per
-// step.
+// super-block). Per step the work-group loads 160 x 2 16-byte qs pieces and
+// 256 tokens x 128 B of activations into registers (weights three steps
+// ahead, activations two); a step's registers are written to a double-
+// buffered LDS stage (activations as they are, weights dequantized to f16
+// in natural k order), one barrier per step. Every wavefront runs the same
+// instruction stream: each dequantizes 40 of the step's 320 pieces (lanes
+// 40..63 repeat lanes 16..39: same data to the same address), and its MFMAs
+// are interleaved with that VALU work, its LDS stores and its global loads
+// (sched_group_barrier), so the matrix core and the VALU stay busy together.
 //
-// Range. Each W row gets a power-of-two scale 2^e chosen from its block
-// headers so that every dequantized |weight| of the row is below 2^15: the
-// f16 weights neither overflow (d*sc*q up to ~6e7) nor fall into f16
-// subnormals for small d; C is multiplied by 2^-e (exact) at the end. The
-// weight itself is q*(d*sc*2^e) + (-dmin*m*2^e) with both factors rounded
-// to f16 once and one f16 fused multiply-add.
-// Tile shape as template parameters: WN x WM wavefronts, each TI x TJ
-// 16x16 MFMA tiles (16*TI W rows x 16*TJ tokens). ASETS = activation
-// register sets (2: loaded two steps ahead, like the weights; 1: one step
-// ahead). PRE: a step's MFMA operands are all read from LDS before its
-// first MFMA.
-template <int WN_, int WM_, int TI_, int TJ_, int ASETS_, bool PRE_, int PITCH_ = 80>
-struct G2 {
-    static constexpr int WN = WN_, WM = WM_, TI = TI_, TJ = TJ_, ASETS = ASETS_;
-    static constexpr bool PRE = PRE_;
-    static constexpr int BN = WN * 16 * TI;       // W rows per work-group
-    static constexpr int BM = WM * 16 * TJ;       // tokens per work-group
-    static constexpr int NT = 64 * WN * WM;       // threads
+// Range. Each W row gets a power-of-two exponent e from its block headers
+// such that every dequantized |weight| * 2^e < 2^15 (row_range_bound). The
+// nibble is masked in place as the f16 subnormal q * 2^-24 (or 16q * 2^-24
+// for the high nibble), exact, and one v_pk_fma_f16 with the sub-block pair
+// (d*sc*2^(e+4), -dmin*m*2^(e-20)) gives (q*d*sc - dmin*m) * 2^(e-20),
+// rounded once; |d*sc| * 2^(e+4) < 2^15 * 63*16/945 stays below the f16
+// maximum, and weights above 2^-9 of the row's largest stay normal. C is
+// multiplied by 2^(20-e) (exact) at the end.
+struct G2Cfg {
+    static constexpr int WN = 2, WM = 4, TI = 5, TJ = 4;
+    static constexpr int BN = WN * 16 * TI;       // 160 W rows per work-group
+    static constexpr int BM = WM * 16 * TJ;       // 256 tokens per work-group
+    static constexpr int NT = 64 * WN * WM;       // 512 threads
     static constexpr int KS = 64;                 // k per step
-    static constexpr int PITCH = PITCH_;          // halves per LDS row (64 + pad)
-    static_assert(PITCH % 8 == 0, "16-byte aligned LDS rows (b128 accesses)");
+    static constexpr int PITCH = 80;              // halves per LDS row (64 + pad)
     static constexpr int WP = BN * 2;             // 16-byte qs pieces per step
-    static constexpr int WPT = (WP + NT - 1) / NT;
+    static constexpr int WPW = WP / (NT / 64);    // pieces per wavefront (40)
     static constexpr int APT = BM * 8 / NT;       // activation pieces per thread per step
     static constexpr uint32_t SW = BN * PITCH * 2, SA = BM * PITCH * 2;
     static constexpr uint32_t LDS = 2 * SW + 2 * SA + BN * 4;
+    static_assert(PITCH % 8 == 0, "16-byte aligned LDS rows (b128 accesses)");
+    static_assert(WP % (NT / 64) == 0 && 2 * WPW >= 64 && WPW <= 64, "piece split");
     static_assert(BM * 8 % NT == 0, "whole activation pieces per thread");
 };
 
-// 160 W rows x 256 tokens, 8 wavefronts of 80 x 64, activations one step
-// ahead, operands preloaded. Alternatives measured on the config-5 shape and
-// not kept: two activation sets (+3-5 %), 4 wavefronts of 160 x 64 with AGPR
-// accumulators, 16 wavefronts of 80 x 32, two 4-wavefront work-groups per CU
-// with a single activation buffer (all slower).
-using G2Cfg = G2<2, 4, 5, 4, 1, true>;
-
-template <class Cfg>
-__global__ __launch_bounds__(Cfg::NT, Cfg::NT / 256) void gemm_q4k_f16_lds_kernel(
+__global__ __launch_bounds__(G2Cfg::NT, 1) void gemm_q4k_f16_lds_kernel(
     const uint8_t *__restrict__ w, const uint16_t *__restrict__ a, float *__restrict__ c, int n,
     int bpr, int m_tokens, int tiles_n, int tiles_m) {
+    using Cfg = G2Cfg;
     constexpr int WN = Cfg::WN, TI = Cfg::TI, TJ = Cfg::TJ, BN = Cfg::BN, BM = Cfg::BM;
-    constexpr int NT = Cfg::NT, KS = Cfg::KS, PITCH = Cfg::PITCH, WP = Cfg::WP, WPT = Cfg::WPT;
-    constexpr int APT = Cfg::APT, AS = Cfg::ASETS;
+    constexpr int KS = Cfg::KS, PITCH = Cfg::PITCH, WPW = Cfg::WPW, APT = Cfg::APT;
     constexpr uint32_t SW = Cfg::SW, SA = Cfg::SA;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     _Float16 *sW = reinterpret_cast<_Float16 *>(lds);
@@ -417,105 +418,84 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::NT / 256) void gemm_q4k_f16_lds_kerne
     const int T = bpr * 4;  // K steps
     const size_t row_bytes = (size_t)bpr * kBlockBytes;
 
-    // this thread's qs pieces: W row wr (clamped past n), bytes 16*wh.. of the
-    // step's 32-byte qs group
-    bool wown[WPT];
-    int wr[WPT], wh[WPT];
-    const uint8_t *wrow[WPT];
-#pragma unroll
-    for (int k = 0; k < WPT; ++k) {
-        // piece p: row p % BN, half p / BN, so the 8 lanes of each LDS store
-        // group write 8 consecutive rows (distinct banks at an 80-half pitch)
-        const int p = tid + NT * k;
-        wown[k] = p < WP;
-        wr[k] = p % BN;
-        wh[k] = (p / BN) & 1;
-        wrow[k] = w + (size_t)min(n0 + wr[k], n - 1) * row_bytes;
-    }
-
-    // ---- per-row range: bound on |weight| over the row's blocks ------------
-    // (each of a row's two piece threads reads all of its block headers)
-    float bound[WPT];
-#pragma unroll
-    for (int k = 0; k < WPT; ++k) bound[k] = row_range_bound(wrow[k], 0, 1, bpr);
+    // this lane's qs piece p: W row wr = p % BN (clamped past n), bytes
+    // 16*wh.. (wh = p / BN) of each step's 32-byte qs group; the 8 lanes of
+    // an LDS store group write 8 consecutive rows (distinct banks at an
+    // 80-half pitch)
+    const int p = wave * WPW + (lane < WPW ? lane : lane - (64 - WPW));
+    const int wr = p % BN, wh = p / BN;
+    const uint8_t *wrow = w + (size_t)min(n0 + wr, n - 1) * row_bytes;
 
     // ---- step loaders (registers) ------------------------------------------
     const uint16_t *aptr[APT];
     uint32_t alds[APT];
 #pragma unroll
     for (int k = 0; k < APT; ++k) {
-        const int p = tid + NT * k, tok = p >> 3, part = p & 7;
+        const int pa = tid + Cfg::NT * k, tok = pa >> 3, part = pa & 7;
         aptr[k] = a + (size_t)min(m0 + tok, m_tokens - 1) * K + 8 * part;
         alds[k] = (uint32_t)((tok * PITCH + 8 * part) * 2);
     }
-    u32x4 Ar[AS][APT], Wq[2][WPT], Wh[2][WPT];
-    auto loadA = [&](int t, int set) __attribute__((always_inline)) {
+    u32x4 Ar[APT], Wq[2], Hd;
+    auto loadA = [&](int t) __attribute__((always_inline)) {
         t = min(t, T - 1);
 #pragma unroll
-        for (int k = 0; k < APT; ++k) Ar[set][k] = ld_u32x4(aptr[k] + (size_t)t * KS);
+        for (int k = 0; k < APT; ++k) Ar[k] = ld_u32x4(aptr[k] + (size_t)t * KS);
     };
     auto loadW = [&](int t, int set) __attribute__((always_inline)) {
         t = min(t, T - 1);
-        const int b = t >> 2, G = t & 3;
-#pragma unroll
-        for (int k = 0; k < WPT; ++k) {
-            const uint8_t *blk = wrow[k] + (size_t)b * kBlockBytes;
-            Wq[set][k] = ld_u32x4(blk + 16 + 32 * G + 16 * wh[k]);
-            Wh[set][k] = ld_u32x4(blk);
-        }
+        Wq[set] = ld_u32x4(wrow + (size_t)(t >> 2) * kBlockBytes + 16 + 32 * (t & 3) + 16 * wh);
     };
-
-    // row scales (need the header loads above, issued before any step load)
-    float srow[WPT];
-#pragma unroll
-    for (int k = 0; k < WPT; ++k) {
-        const int e = range_exp(bound[k]);
-        srow[k] = ldexpf(1.0f, e);
-        if (wown[k] && wh[k] == 0) sE[wr[k]] = ldexpf(1.0f, -e);
-    }
+    // header of the super-block that step t opens (once per 4 steps)
+    auto loadH = [&](int t) __attribute__((always_inline)) {
+        Hd = ld_u32x4(wrow + (size_t)(min(t, T - 1) >> 2) * kBlockBytes);
+    };
 
     // step t -> LDS buffer: activations copied, weights dequantized
-    const uint32_t magic = __builtin_amdgcn_readfirstlane(0x64006400u) + (uint32_t)(tid >> 16);
-    auto storeA = [&](int set, int buf) __attribute__((always_inline)) {
+    auto storeA = [&](int buf) __attribute__((always_inline)) {
         uint8_t *dA = lds + 2 * SW + buf * SA;
 #pragma unroll
-        for (int k = 0; k < APT; ++k) *reinterpret_cast<u32x4 *>(dA + alds[k]) = Ar[set][k];
+        for (int k = 0; k < APT; ++k) *reinterpret_cast<u32x4 *>(dA + alds[k]) = Ar[k];
     };
-    auto storeW = [&](int t, int set, int buf) __attribute__((always_inline)) {
-        t = min(t, T - 1);
-        const int G = t & 3;
+    // the block's 8 sub-block pairs (d*sc*2^(e+4), -dmin*m*2^(e-20)) as f16,
+    // decoded once per super-block from its header (sub-block index
+    // constant: no branches); d*sc and dmin*m are exact in f32 and the
+    // factors are powers of two, so each is rounded to f16 once
+    float sD, sN;  // 2^(e+4), 2^(e-20): set in the prologue from the row range
+    uint32_t scl[8];
+    auto decode = [&]() __attribute__((always_inline)) {
+        const float d = half_bits_finite(Hd[0]) * sD;
+        const float nm = -(half_bits_finite(Hd[0] >> 16) * sN);
 #pragma unroll
-        for (int k = 0; k < WPT; ++k) {
-            if (!wown[k]) continue;
-            const u32x4 h = Wh[set][k];
-            const float d = half_bits_finite(h[0]), dmin = half_bits_finite(h[0] >> 16);
-            uint32_t sc0, mn0, sc1, mn1;
-            scale_min(2 * G, h[1], h[2], h[3], sc0, mn0);
-            scale_min(2 * G + 1, h[1], h[2], h[3], sc1, mn1);
-            const float sr = srow[k];
-            const _Float16 dl = (_Float16)(d * (float)sc0 * sr);
-            const _Float16 nl = (_Float16)(-(dmin * (float)mn0 * sr));
-            const _Float16 dh = (_Float16)(d * (float)sc1 * sr * 0.0625f);  // high nibbles arrive as 16*q
-            const _Float16 nh = (_Float16)(-(dmin * (float)mn1 * sr));
-            const h2_t dl2 = {dl, dl}, nl2 = {nl, nl}, dh2 = {dh, dh}, nh2 = {nh, nh};
-            u32x4 lo[2], hi[2];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const uint32_t v = Wq[set][k][u];
-                const uint32_t p0 = __builtin_amdgcn_perm(v, v, 0x0C010C00u);  // bytes 0, 1 -> 0, 2
-                const uint32_t p1 = __builtin_amdgcn_perm(v, v, 0x0C030C02u);  // bytes 2, 3 -> 0, 2
-                lo[u >> 1][2 * (u & 1)] = dq2(p0, 0x000F000Fu, magic, dl2, nl2);
-                lo[u >> 1][2 * (u & 1) + 1] = dq2(p1, 0x000F000Fu, magic, dl2, nl2);
-                hi[u >> 1][2 * (u & 1)] = dq2(p0, 0x00F000F0u, magic, dh2, nh2);
-                hi[u >> 1][2 * (u & 1) + 1] = dq2(p1, 0x00F000F0u, magic, dh2, nh2);
-            }
-            // low nibbles: k = 16*wh + 0..15 of the step; high nibbles: 32 + that
-            uint8_t *dW = lds + buf * SW + (size_t)(wr[k] * PITCH + 16 * wh[k]) * 2;
-            *reinterpret_cast<u32x4 *>(dW) = lo[0];
-            *reinterpret_cast<u32x4 *>(dW + 16) = lo[1];
-            *reinterpret_cast<u32x4 *>(dW + 64) = hi[0];
-            *reinterpret_cast<u32x4 *>(dW + 80) = hi[1];
+        for (int j = 0; j < 8; ++j) {
+            uint32_t sc, mn;
+            scale_min(j, Hd[1], Hd[2], Hd[3], sc, mn);
+            const _Float16 d1 = (_Float16)(d * (float)sc * ((j & 1) ? 0.0625f : 1.0f));  // high nibbles arrive as 16*q
+            const _Float16 n1 = (_Float16)(nm * (float)mn);
+            scl[j] = __builtin_bit_cast(uint32_t, (h2_t){d1, n1});
         }
+    };
+    auto storeW = [&](auto gc, int set, int buf) __attribute__((always_inline)) {
+        constexpr int G = decltype(gc)::value;  // qs group of the step: sub-blocks 2G, 2G+1
+        const h2_t sl = __builtin_bit_cast(h2_t, scl[2 * G]);
+        const h2_t sh = __builtin_bit_cast(h2_t, scl[2 * G + 1]);
+        const h2_t dl2 = {sl[0], sl[0]}, nl2 = {sl[1], sl[1]}, dh2 = {sh[0], sh[0]}, nh2 = {sh[1], sh[1]};
+        u32x4 lo[2], hi[2];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t v = Wq[set][u];
+            const uint32_t p0 = __builtin_amdgcn_perm(v, v, 0x0C010C00u);  // bytes 0, 1 -> 0, 2
+            const uint32_t p1 = __builtin_amdgcn_perm(v, v, 0x0C030C02u);  // bytes 2, 3 -> 0, 2
+            lo[u >> 1][2 * (u & 1)] = dqs2(p0, 0x000F000Fu, dl2, nl2);
+            lo[u >> 1][2 * (u & 1) + 1] = dqs2(p1, 0x000F000Fu, dl2, nl2);
+            hi[u >> 1][2 * (u & 1)] = dqs2(p0, 0x00F000F0u, dh2, nh2);
+            hi[u >> 1][2 * (u & 1) + 1] = dqs2(p1, 0x00F000F0u, dh2, nh2);
+        }
+        // low nibbles: k = 16*wh + 0..15 of the step; high nibbles: 32 + that
+        uint8_t *dW = lds + buf * SW + (size_t)(wr * PITCH + 16 * wh) * 2;
+        *reinterpret_cast<u32x4 *>(dW) = lo[0];
+        *reinterpret_cast<u32x4 *>(dW + 16) = lo[1];
+        *reinterpret_cast<u32x4 *>(dW + 64) = hi[0];
+        *reinterpret_cast<u32x4 *>(dW + 80) = hi[1];
     };
 
     // ---- compute roles -----------------------------------------------------
@@ -526,88 +506,85 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::NT / 256) void gemm_q4k_f16_lds_kerne
     for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // a step's operands are all read from LDS before its first MFMA
     auto compute = [&](int buf) __attribute__((always_inline)) {
         const _Float16 *W_ = sW + buf * (BN * PITCH);
         const _Float16 *A_ = sA + buf * (BM * PITCH);
-        if constexpr (Cfg::PRE) {
-            half8 wa[2][TI], tb[2][TJ];
+        half8 wa[2][TI], tb[2][TJ];
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < 2; ++h) {
 #pragma unroll
-                for (int i = 0; i < TI; ++i)
-                    wa[h][i] = *reinterpret_cast<const half8 *>(&W_[(wn + 16 * i + l16) * PITCH + 32 * h + 8 * q]);
+            for (int i = 0; i < TI; ++i)
+                wa[h][i] = *reinterpret_cast<const half8 *>(&W_[(wn + 16 * i + l16) * PITCH + 32 * h + 8 * q]);
 #pragma unroll
-                for (int j = 0; j < TJ; ++j)
-                    tb[h][j] = *reinterpret_cast<const half8 *>(&A_[(wm + 16 * j + l16) * PITCH + 32 * h + 8 * q]);
-            }
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int i = 0; i < TI; ++i)
-#pragma unroll
-                    for (int j = 0; j < TJ; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[h][i], tb[h][j], acc[i][j], 0, 0, 0);
-        } else {
-#pragma unroll
-            for (int kk = 0; kk < KS; kk += 32) {
-                half8 wa[TI], tb[TJ];
-#pragma unroll
-                for (int i = 0; i < TI; ++i)
-                    wa[i] = *reinterpret_cast<const half8 *>(&W_[(wn + 16 * i + l16) * PITCH + kk + 8 * q]);
-#pragma unroll
-                for (int j = 0; j < TJ; ++j)
-                    tb[j] = *reinterpret_cast<const half8 *>(&A_[(wm + 16 * j + l16) * PITCH + kk + 8 * q]);
-#pragma unroll
-                for (int i = 0; i < TI; ++i)
-#pragma unroll
-                    for (int j = 0; j < TJ; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[i], tb[j], acc[i][j], 0, 0, 0);
-            }
+            for (int j = 0; j < TJ; ++j)
+                tb[h][j] = *reinterpret_cast<const half8 *>(&A_[(wm + 16 * j + l16) * PITCH + 32 * h + 8 * q]);
         }
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[h][i], tb[h][j], acc[i][j], 0, 0, 0);
     };
 
     // ---- pipeline ----------------------------------------------------------
     // Step t computes buffer t & 1, then writes step t+1 into the other
     // buffer and refills the registers it came from: weights with step t+3
-    // (two sets), activations with step t+3 (two sets) or t+2 (one set).
-    // Loads past the last step re-read it (clamped), so every load is
-    // unconditional and the load counter waits only for the data it needs.
-    constexpr int AD = AS == 2 ? 3 : 2;  // activation prefetch distance
-    loadA(0, 0);
+    // (two sets), activations with step t+2. The header of the block step
+    // t+3 opens is loaded at t = 1 mod 4 and decoded at t = 3 mod 4, just
+    // before that block's first step is stored. Loads past the last step
+    // re-read it (clamped), so every load is unconditional and the load
+    // counter waits only for the data it needs.
+    loadH(0);
+    loadA(0);
     loadW(0, 0);
-    if constexpr (AS == 2) loadA(1, 1);
     loadW(1, 1);
-    storeA(0, 0);
-    storeW(0, 0, 0);
-    loadA(AD - 1, 0);
+    // per-row range (each of a row's piece lanes reads all of its block
+    // headers) while the first steps' loads fly
+    {
+        const int e = range_exp(row_range_bound(wrow, 0, 1, bpr));
+        sD = ldexpf(1.0f, e + 4);
+        sN = ldexpf(1.0f, e - 20);
+        if (wh == 0) sE[wr] = ldexpf(1.0f, 20 - e);
+    }
+    decode();
+    storeA(0);
+    storeW(std::integral_constant<int, 0>{}, 0, 0);
+    loadA(1);
     loadW(2, 0);
     __syncthreads();
-    auto stage = [&](int t, auto par, bool dq_first) __attribute__((always_inline)) {
-        constexpr int P = decltype(par)::value;  // t & 1
-        constexpr int NS = (P + 1) & 1;           // buffer / weight set of step t+1
-        constexpr int AN = AS == 2 ? NS : 0;      // activation set of step t+1
-        if (!dq_first) compute(P);
-        storeA(AN, NS);
-        storeW(t + 1, NS, NS);
-        loadA(t + AD, AN);
+    auto stage = [&](int t, auto ph) __attribute__((always_inline)) {
+        constexpr int PH = decltype(ph)::value;  // t & 3
+        constexpr int P = PH & 1;                 // buffer of step t
+        constexpr int NS = P ^ 1;                 // buffer / weight set of step t+1
+        compute(P);
+        storeA(NS);
+        if constexpr (PH == 3) decode();
+        storeW(std::integral_constant<int, (PH + 1) & 3>{}, NS, NS);
+        loadA(t + 2);
         loadW(t + 3, NS);
-        if (dq_first) compute(P);
+        if constexpr (PH == 1) loadH(t + 3);
+        // operand reads first, then each MFMA followed by a share of the
+        // dequant VALU work, the LDS stores and the global loads
+        constexpr int NM = 2 * TI * TJ;
+        __builtin_amdgcn_sched_group_barrier(0x0100, 2 * (TI + TJ), 0);  // DS reads
+        __builtin_amdgcn_sched_group_barrier(0x0002, 6, 0);              // VALU
+#pragma unroll
+        for (int i = 0; i < NM; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);               // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x0002, PH == 3 ? 4 : 2, 0);  // VALU
+            if (i % 4 == 3) __builtin_amdgcn_sched_group_barrier(0x0200, 1, 0);  // DS write
+            if (i % 6 == 5) __builtin_amdgcn_sched_group_barrier(0x0020, 1, 0);  // VMEM read
+        }
         __syncthreads();
     };
-    // Wavefronts w, w + 4, ... share a SIMD: with 8 or more wavefronts the
-    // first half computes and then dequantizes, the second half dequantizes
-    // and then computes, so dequant VALU work runs while other wavefronts'
-    // MFMAs occupy the matrix core.
-    if (NT / 64 <= 4 || wave < NT / 128) {
-        for (int t = 0; t < T; t += 2) {
-            stage(t, std::integral_constant<int, 0>{}, false);
-            stage(t + 1, std::integral_constant<int, 1>{}, false);  // T % 4 == 0
-        }
-    } else {
-        for (int t = 0; t < T; t += 2) {
-            stage(t, std::integral_constant<int, 0>{}, true);
-            stage(t + 1, std::integral_constant<int, 1>{}, true);
-        }
+    for (int t = 0; t < T; t += 4) {  // T = 4 * bpr
+        stage(t, std::integral_constant<int, 0>{});
+        stage(t + 1, std::integral_constant<int, 1>{});
+        stage(t + 2, std::integral_constant<int, 2>{});
+        stage(t + 3, std::integral_constant<int, 3>{});
     }
 
     // ---- epilogue: lane holds W rows wn+16i+4q+v of token wm+16j+l16 --------
@@ -637,7 +614,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::NT / 256) void gemm_q4k_f16_lds_kerne
 static std::atomic<int> g_gemm_lds_state[64];
 
 hipError_t gemm_prepare() {
-    return allow_full_lds((const void *)gemm_q4k_f16_lds_kernel<G2Cfg>, g_gemm_lds_state);
+    return allow_full_lds((const void *)gemm_q4k_f16_lds_kernel, g_gemm_lds_state);
 }
 
 static hipError_t gemm_lds_launch(const uint8_t *w, const uint16_t *a, float *c, int n, int bpr,
@@ -648,7 +625,7 @@ static hipError_t gemm_lds_launch(const uint8_t *w, const uint16_t *a, float *c,
     const long ntiles = (long)tn * tm;
     const long grid = (ntiles + gemm::NXCD - 1) / gemm::NXCD * gemm::NXCD;
     if (grid > 0x7FFFFFFFL) return hipErrorInvalidValue;
-    gemm_q4k_f16_lds_kernel<G2Cfg><<<(unsigned)grid, G2Cfg::NT, G2Cfg::LDS, stream>>>(
+    gemm_q4k_f16_lds_kernel<<<(unsigned)grid, G2Cfg::NT, G2Cfg::LDS, stream>>>(
         w, a, c, n, bpr, m_tokens, tn, tm);
     return hipGetLastError();
 }
@@ -672,14 +649,16 @@ hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n,
         return (v && *v) ? std::atoi(v) : -1;
     }();
     // The LDS-dequant kernel computes whole 256-token tiles, one work-group
-    // per CU: it wins (M = 512 x 18944: 96-101 against 101-102 us) only when
-    // its token tiles are nearly full and its tiles make one nearly full
-    // round; otherwise (M = 256: 88 against 66 us; M = 384: half-empty token
-    // tiles; M >= 768: a second, partial round) the 128-token kernel below.
+    // per CU. Measured on 18944 x 3584 (us, warm; LDS kernel against the
+    // 128-token kernel below): M = 256 76 / 61, 384 82 / 80, 512 83 / 94,
+    // 640 150 / 120, 768 154 / 137, 1024 159 / 176. It wins when its token
+    // tiles are at least 90 % full and its tiles fill their rounds: one round
+    // more than half full, or several rounds at least 85 % full.
     const long tn2 = (n + G2Cfg::BN - 1) / G2Cfg::BN, tm2 = (m_tokens + G2Cfg::BM - 1) / G2Cfg::BM;
-    const long cus2 = device_cus();
-    const bool lds_fits = 10L * m_tokens >= 9L * G2Cfg::BM * tm2 && tn2 * tm2 <= cus2 &&
-                          2 * tn2 * tm2 > cus2;
+    const long cus2 = device_cus(), tiles2 = tn2 * tm2;
+    const long rounds2 = (tiles2 + cus2 - 1) / cus2;
+    const bool lds_fits = 10L * m_tokens >= 9L * G2Cfg::BM * tm2 &&
+                          (rounds2 == 1 ? 2 * tiles2 > cus2 : 20 * tiles2 >= 17 * rounds2 * cus2);
     if (big_env == 1 || (big_env < 0 && lds_fits))
         return gemm_lds_launch(w, a, c, n, bpr, m_tokens, stream);
     // Tile height by the rows the busiest CU computes: ceil(tiles / #CUs) x

@@ -412,9 +412,12 @@ def test_gemm_160_row_tiles_multi_block(L, orc, n, bpr, m):
     _gemm_check(L, orc, w, a, n, bpr, m, rows)
 
 
-# Shapes the LDS-dequant kernel takes (one nearly full round of 160 x 256
-# tiles): full token tiles, ragged tokens, ragged rows, several super-blocks
-@pytest.mark.parametrize("n,bpr,m", [(32000, 1, 256), (30000, 3, 250), (20000, 14, 512)])
+# Shapes the LDS-dequant kernel takes (one round of 160 x 256 tiles more than
+# half full, or several rounds at least 85 % full): full token tiles, ragged
+# tokens, ragged rows, several super-blocks; two rounds (476 tiles) with full
+# and with ragged token tiles
+@pytest.mark.parametrize("n,bpr,m", [(32000, 1, 256), (30000, 3, 250), (20000, 14, 512),
+                                     (18944, 2, 1024), (18944, 2, 1000)])
 def test_gemm_lds_kernel_shapes(L, orc, n, bpr, m):
     note(f"gemm lds kernel n={n} bpr={bpr} m={m}")
     rng = np.random.default_rng(n + m)
