@@ -214,6 +214,56 @@ def cpu_baseline(torch, wl: Workload, target_s: float, threads: int, launches: i
             "tokens_per_s_equiv_1thread": round(gbs1 * 1e9 / wl.bytes_per_pass, 4)}
 
 
+def cpu_jobs_baseline(jobs, units_per_pass: float, unit: str, sample: str, threads: int,
+                      target_s: float, target_1t_s: float = 3.0, digits: int = 2):
+    """The reference CPU GEMV restated (oracle: kfd::llm::matvec, llm.rs:468-534,
+    rows in parallel as its rayon pool does, llm.rs:506-511) on a side
+    workload's sample: `jobs` = [(w, x, y, n, bpr)], one pass runs each once
+    and is worth `units_per_pass` of the workload's metric (GB as the GPU line
+    counts them, or TFLOP); timed on `threads` threads and on one thread."""
+    from oracle import oracle as orc
+
+    def timed(nthreads: int, budget: float):
+        for w, x, y, n, bpr in jobs:  # warm-up
+            orc.cpu_matvec(w, x, y, n, bpr, nthreads)
+        reps, t_total = 0, 0.0
+        while t_total < budget:
+            t = time.perf_counter()
+            for w, x, y, n, bpr in jobs:
+                orc.cpu_matvec(w, x, y, n, bpr, nthreads)
+            t_total += time.perf_counter() - t
+            reps += 1
+        return units_per_pass * reps / t_total, reps, t_total
+
+    v, reps, t_total = timed(threads, target_s)
+    v1, reps1, t1 = timed(1, target_1t_s) if threads > 1 else (v, reps, t_total)
+    return {"value": round(v, digits), "unit": unit, "cores": threads, "kind": "port",
+            "sample": f"{sample}, x {reps} passes, {t_total:.1f} s on {threads} threads; "
+                      f"1 thread: x {reps1} passes, {t1:.1f} s; "
+                      f"AVX-512={'yes' if orc.cpu_has_avx512() else 'no'}",
+            "value_1thread": round(v1, digits + 1), "cpu_model": cpu_model(),
+            "host_logical_cpus": os.cpu_count()}
+
+
+def cpu_flat_baseline(w, x, n: int, k: int, launch_gb: float, target_s: float = 3.0):
+    """Config 1's flattened layout has no CPU path in the reference (the
+    LinearResidentQuantized forward is GPU-only, neuron.rs:897-1108); the
+    oracle's flat-layout dequant-dot (one thread, f64) stands in, in the
+    GPU line's bytes per launch."""
+    from oracle import oracle as orc
+    orc.gemv_flat(w, x, n, k)
+    reps, t_total = 0, 0.0
+    while t_total < target_s:
+        t = time.perf_counter()
+        orc.gemv_flat(w, x, n, k)
+        t_total += time.perf_counter() - t
+        reps += 1
+    return {"value": round(launch_gb * reps / t_total, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle flat-layout dequant-dot (f64) on one 4864x896 launch, x {reps} passes, "
+                      f"{t_total:.1f} s on 1 thread (the reference has no CPU path for this layout)",
+            "cpu_model": cpu_model(), "host_logical_cpus": os.cpu_count()}
+
+
 WARM_MS = 100.0  # least untimed run time before a timed region (ms)
 
 
@@ -332,7 +382,8 @@ def run_config1(torch, q4k, args):
     return {"workload": "config1: 4864x896 flattened Q4_K (LinearResidentQuantized layout), "
                         f"{copies} rotating copies, one graph", "us_per_launch": round(us, 3),
             "gbs": gbs, "bytes_per_launch": nbytes // copies, "parity": parity,
-            "kernel": "mgq::gemv_flat_kernel<2>"}
+            "kernel": "mgq::gemv_flat_kernel<2>",
+            "cpu_flat": (w_host, x_host, n, k, nbytes / copies / 1e9)}
 
 
 def run_batched(torch, q4k, args):
@@ -402,11 +453,22 @@ def run_batched(torch, q4k, args):
     gu_bytes = 2 * INTER * (HIDDEN // BLOCK_ELEMS) * BLOCK_BYTES + 4 * B * (HIDDEN + 2 * INTER)
     per_shape["gate_up_fused_37888x3584_us"] = round(us_gu, 3)
     per_shape["gate_up_fused_gbs"] = round(gu_bytes / (us_gu * 1e-6) / 1e9, 1)
+    # CPU: the reference's CPU GEMV has no batch, so a batched call is B
+    # matvecs over the same weights; one pass = the last gate and down calls,
+    # worth their bytes as the GPU line counts them
+    jobs, pass_bytes = [], 0
+    for name, w, X, Y, ws, n, bpr in items[-2:]:
+        wh, Xh = w.cpu().numpy(), X.cpu().numpy()
+        jobs += [(wh, np.ascontiguousarray(Xh[b]), np.empty(n, np.float32), n, bpr) for b in range(B)]
+        pass_bytes += n * bpr * BLOCK_BYTES + 4 * B * (bpr * BLOCK_ELEMS + n)
     return {"workload": f"config4: batched B={B}, gate 18944x3584 + down 3584x18944, "
                         f"{copies} rotating copies, one graph",
             "us_per_launch": round(ms * 1e3 / len(items), 3), "gbs": nbytes / (ms * 1e-3) / 1e9,
             "bytes_per_launch": nbytes // len(items), "parity": parity, "per_shape": per_shape,
-            "kernel": "mgq::gemv_batched_mfma_kernel (+ batched_table_kernel)"}
+            "kernel": "mgq::gemv_batched_mfma_kernel (+ batched_table_kernel)",
+            "cpu": (jobs, pass_bytes / 1e9, "GB/s",
+                    f"one gate and one down call at B={B} as {len(jobs)} CPU matvecs "
+                    f"({pass_bytes / 1e6:.1f} MB per pass as the GPU line counts it)", 2)}
 
 
 def run_prefill(torch, q4k, args):
@@ -437,9 +499,17 @@ def run_prefill(torch, q4k, args):
     frob = float(np.linalg.norm(Cg - C_ref) / max(np.linalg.norm(C_ref), 1e-300))
     parity = (f"ok (frobenius rel {frob:.2e} <= 1e-3, per-element <= 1e-2*sum|w||a|/sqrt(K))"
               if elem_ok and frob <= 1e-3 else f"FAIL: frobenius rel {frob:.3e}, elementwise {elem_ok}")
+    # CPU: the reference's prefill is a per-token matvec loop
+    # (gemma4_rocm.rs:26-34); on the CPU that is one GEMV per token, timed on
+    # 16 of the 512 tokens (f32 activations: the f16 values, exactly)
+    wh = ws[-1].cpu().numpy()
+    toks = 16
+    jobs = [(wh, A[t].float().cpu().numpy(), np.empty(n, np.float32), n, bpr) for t in range(toks)]
     return {"workload": f"config5: prefill 18944x3584 Q4_K x f16 [512x3584], {copies} weight copies",
             "us_per_launch": round(s * 1e6, 3), "tflops": tflops, "parity": parity,
-            "kernel": "mgq::gemm_q4k_f16_lds_kernel"}
+            "kernel": "mgq::gemm_q4k_f16_lds_kernel",
+            "cpu": (jobs, 2.0 * n * k * toks / 1e12, "TFLOP/s",
+                    f"{toks} of the 512 tokens, one CPU matvec each (2*N*K flops per token)", 5)}
 
 
 def run_decode_dp4a(torch, q4k, args):
@@ -811,6 +881,14 @@ def run_side_workload(torch, q4k, args) -> int:
             out[key] = round(r[key], 4)
     if "per_shape" in r:
         out["per_shape"] = r["per_shape"]
+    if not args.no_cpu and "cpu" in r:
+        jobs, units, unit, sample, digits = r["cpu"]
+        threads = cpu_threads()
+        secs = min(args.cpu_seconds, 5.0)
+        log(f"cpu baseline ({threads} threads, ~{secs:.0f} s, then 1 thread ~3 s)")
+        out["cpu_baseline"] = cpu_jobs_baseline(jobs, units, unit, sample, threads, secs, digits=digits)
+    elif not args.no_cpu and "cpu_flat" in r:
+        out["cpu_baseline"] = cpu_flat_baseline(*r["cpu_flat"])
     log(f"{r['workload']}: {r['us_per_launch']} us per launch; parity {r['parity']}")
     print(json.dumps(out), flush=True)
     return 0
