@@ -665,10 +665,11 @@ def run_decode_q4km(torch, q4k, args):
     """A Q4_K_M 7B-class decode step from one weight arena (the GGUF loader's
     layout): Q4_K everywhere except attn_v and ffn_down on the Q4_K_M
     'more bits' layers (Q6_K) and the Q6_K output matrix, as llama.cpp's
-    Q4_K_M recipe assigns them. Per layer: RMSNorm fused into q|k (and v when
-    v is Q4_K; otherwise one rms_norm launch feeds q|k and the Q6_K v), o,
-    RMSNorm + gate/up + GeGLU fused, down (Q4_K or Q6_K); then rms_norm +
-    the Q6_K lm_head. Seeded random weights, one captured graph."""
+    Q4_K_M recipe assigns them. Per layer: RMSNorm fused into q|k and into v
+    (Q4_K or Q6_K; an rms_norm launch only where the fused Q6_K kernel cannot
+    take the tensor), o, RMSNorm + gate/up + GeGLU fused, down (Q4_K or
+    Q6_K); then RMSNorm fused into the Q6_K lm_head. Seeded random weights,
+    one captured graph."""
     from oracle import oracle as orc
     from modgrad_amd.arena import WeightArena
     from modgrad_amd.gguf import GgmlType
@@ -714,7 +715,7 @@ def run_decode_q4km(torch, q4k, args):
     for l in range(LAYERS):
         p = f"blk.{l}."
         h0, h1 = hs[2 * l].data_ptr(), hs[2 * l + 1].data_ptr()
-        if A.dtype[p + "attn_v.weight"] == Q4:
+        if A.norm_fusable(p + "attn_v.weight"):
             ops.append(A.op_qmatvec_rmsnorm(p + "attn_qk.weight", h0, p + "attn_norm.weight", eps,
                                             qk.data_ptr()))
             ops.append(A.op_qmatvec_rmsnorm(p + "attn_v.weight", h0, p + "attn_norm.weight", eps,
@@ -728,15 +729,24 @@ def run_decode_q4km(torch, q4k, args):
         ops.append(A.op_qmatvec_glu(p + "ffn_gate.weight", p + "ffn_up.weight", h1, glu.data_ptr(),
                                     norm=p + "ffn_norm.weight", eps=eps))
         ops.append(A.op_qmatvec(p + "ffn_down.weight", glu.data_ptr(), dn.data_ptr()))
-    ops.append(q4k.op_rms_norm(hs[-1].data_ptr(), A.ptr("output_norm.weight"), xn.data_ptr(), 1,
-                               HIDDEN, eps))
-    ops.append(A.op_qmatvec("output.weight", xn.data_ptr(), logits.data_ptr()))
+    if A.norm_fusable("output.weight"):
+        ops.append(A.op_qmatvec_rmsnorm("output.weight", hs[-1].data_ptr(), "output_norm.weight",
+                                        eps, logits.data_ptr()))
+    else:
+        ops.append(q4k.op_rms_norm(hs[-1].data_ptr(), A.ptr("output_norm.weight"), xn.data_ptr(),
+                                   1, HIDDEN, eps))
+        ops.append(A.op_qmatvec("output.weight", xn.data_ptr(), logits.data_ptr()))
     launches = [len(ops)]
     ms = time_op_chain(torch, q4k, ops, args.steps, args.warmup)
     # parity: the last layer's Q6_K or Q4_K down (its GLU input as produced)
     # and the Q6_K lm_head, sampled rows against the oracle
     worst, fail = 0.0, None
-    checks = [(f"blk.{LAYERS - 1}.ffn_down.weight", glu, dn), ("output.weight", xn, logits)]
+    # lm_head's input: the oracle's rms_norm of the last hidden state (the
+    # fused kernel never writes the normalized vector)
+    xn_ref = orc.rms_norm(hs[-1].cpu().numpy(), arena.tensor("output_norm.weight").view(torch.float32)
+                          .cpu().numpy(), 1, HIDDEN, eps).astype(np.float32)
+    checks = [(f"blk.{LAYERS - 1}.ffn_down.weight", glu.cpu().numpy(), dn),
+              ("output.weight", xn_ref, logits)]
     rng = np.random.default_rng(9)
     for name, xin, yout in checks:
         nrow, kin = arena.shape(name)
@@ -745,9 +755,9 @@ def run_decode_q4km(torch, q4k, args):
         idx = np.sort(rng.choice(nrow, size=256, replace=False))
         wv = arena.tensor(name).view(nrow, -1)[torch.from_numpy(idx).cuda()].cpu().numpy().ravel()
         if t == Q4:
-            y_ref, a = orc.gemv(wv, xin.cpu().numpy(), idx.size, kin // 256)
+            y_ref, a = orc.gemv(wv, xin, idx.size, kin // 256)
         else:
-            y_ref, a = orc.gemv_kquant(bb, wv, xin.cpu().numpy(), idx.size, kin // 256)
+            y_ref, a = orc.gemv_kquant(bb, wv, xin, idx.size, kin // 256)
         r = np.abs(yout.cpu().numpy()[idx].astype(np.float64) - y_ref) / a
         worst = max(worst, float(r.max()))
         if not np.all(r <= 1e-4):

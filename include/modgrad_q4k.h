@@ -239,6 +239,21 @@ hipError_t launch_matvec_q4k_rmsnorm_ex(const unsigned char *w_q4, const float *
                                         const float *norm_w, float eps, float *y, int out_dim,
                                         int blocks_per_row, hipStream_t stream);
 
+/* Fused RMSNorm -> Q6_K matvec: y = W * rms_norm(x, norm_w, eps), replacing
+ * the reference decode's launch_rms_norm + launch_matvec_q6k pair where a
+ * Q4_K_M model's Q6_K tensors follow a norm (attn_v on its 'more bits'
+ * layers, the output matrix; rocm_gemma.rs:439-440 with the dtype dispatch
+ * of rocm_gemma.rs:291-309). No counterpart in the reference as one call.
+ * Computed as rstd * (W * (x .* norm_w)) on the matrix-core kernel, whose
+ * activation staging multiplies by norm_w and reduces sum(x^2). Same per-row
+ * bound as launch_matvec_q6k against the f64 matvec of the normalized
+ * vector. Runs on the whole-row kernel only: hipErrorNotSupported unless w
+ * is 16-byte aligned, out_dim * blocks_per_row * 210 is a multiple of 16 and
+ * blocks_per_row <= 14 (K <= 3584); callers then keep the two launches. */
+hipError_t launch_matvec_q6k_rmsnorm_ex(const unsigned char *w_q6, const float *x,
+                                        const float *norm_w, float eps, float *y, int out_dim,
+                                        int blocks_per_row, hipStream_t stream);
+
 /* Fused gate/up matvec + GLU: y[i] = act(g[i]) * u[i] with g = W_gate * xn,
  * u = W_up * xn, xn = rms_norm(x, norm_w, eps) when norm_w is not null (else
  * xn = x). Replaces the reference FFN's launch_rms_norm + two
@@ -307,7 +322,9 @@ hipError_t mgq_chain_destroy(void *chain);
  *                        MGQ_LAYOUT_FLAT, in_dim = K), Q5_K or Q6_K
  *                        (in_dim % 256 == 0); out_dim rows.
  *   MGQ_OP_MATVEC_NORM   y = W rms_norm(x, norm_w, eps); Q4_K, rows layout
- *                        (launch_matvec_q4k_rmsnorm_ex).
+ *                        (launch_matvec_q4k_rmsnorm_ex), or Q6_K where
+ *                        launch_matvec_q6k_rmsnorm_ex runs (else
+ *                        hipErrorNotSupported at creation).
  *   MGQ_OP_MATVEC_GLU    y = act(W xn) .* (W2 xn), xn = rms_norm(x, norm_w,
  *                        eps) when norm_w is not null, else x; Q4_K, rows
  *                        layout (launch_matvec_q4k_glu_ex).

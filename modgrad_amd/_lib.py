@@ -51,6 +51,7 @@ SIGNATURES = {
     "launch_scale": (I, [P, F, I]),
     "launch_scale_ex": (I, [P, F, I, P]),
     "launch_matvec_q4k_rmsnorm_ex": (I, [P, P, P, F, P, I, I, P]),
+    "launch_matvec_q6k_rmsnorm_ex": (I, [P, P, P, F, P, I, I, P]),
     "launch_matvec_q4k_glu_ex": (I, [P, P, P, P, F, I, P, I, I, P]),
     "mgq_chain_create": (I, [P, I, P]),
     "mgq_chain_create_ex": (I, [P, I, I, P]),

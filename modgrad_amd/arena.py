@@ -26,7 +26,8 @@ import numpy as np
 
 from . import _lib
 from .gguf import GgmlType, GgufFile, data_size
-from .q4k import BackendError, _stream_ptr, kern, op_matvec, op_matvec_glu, op_matvec_norm
+from .q4k import (BackendError, _stream_ptr, kern, op_matvec, op_matvec_glu, op_matvec_norm,
+                  q6k_norm_fits)
 
 ALIGN = 256
 
@@ -138,12 +139,25 @@ class WeightArena:
         else:
             raise BackendError("Unsupported", f"{name}: no matvec for {t.name}")
 
+    def norm_fusable(self, name: str) -> bool:
+        """Whether y = W rms_norm(x) runs as one launch for this tensor: Q4_K
+        always, Q6_K where the fused kernel takes it (q4k.q6k_norm_fits)."""
+        n, k = self.shape(name)
+        t = self.dtype[name]
+        if t == GgmlType.Q4_K:
+            return True
+        return t == GgmlType.Q6_K and k % 256 == 0 and q6k_norm_fits(self.ptr(name), n, k // 256)
+
     def qmatvec_rmsnorm(self, name: str, x: int, norm: str, eps: float, y: int,
                         stream=None) -> None:
-        """y = W rms_norm(x, norm, eps) in one launch (Q4_K weights)."""
+        """y = W rms_norm(x, norm, eps) in one launch (Q4_K weights, or Q6_K
+        where norm_fusable)."""
         n, k = self.shape(name)
-        self._need(name, GgmlType.Q4_K)
         self._need(norm, GgmlType.F32)
+        if self.dtype[name] == GgmlType.Q6_K and self.norm_fusable(name):
+            kern.matvec_q6k_rmsnorm(self.ptr(name), x, self.ptr(norm), eps, y, n, k // 256, stream)
+            return
+        self._need(name, GgmlType.Q4_K)
         kern.matvec_q4k_rmsnorm(self.ptr(name), x, self.ptr(norm), eps, y, n, k // 256, stream)
 
     def qmatvec_glu(self, gate: str, up: str, x: int, y: int, norm: str | None = None,
@@ -175,8 +189,10 @@ class WeightArena:
     def op_qmatvec_rmsnorm(self, name: str, x: int, norm: str, eps: float,
                            y: int) -> "_lib.OpDesc":
         n, k = self.shape(name)
-        self._need(name, GgmlType.Q4_K)
         self._need(norm, GgmlType.F32)
+        if self.dtype[name] == GgmlType.Q6_K and self.norm_fusable(name):
+            return op_matvec_norm(self.ptr(name), x, self.ptr(norm), eps, y, n, k, _lib.DTYPE_Q6_K)
+        self._need(name, GgmlType.Q4_K)
         return op_matvec_norm(self.ptr(name), x, self.ptr(norm), eps, y, n, k)
 
     def op_qmatvec_glu(self, gate: str, up: str, x: int, y: int, norm: str | None = None,

@@ -268,6 +268,12 @@ hipError_t mgq_chain_create_ex(const mgq_gemv_desc *descs, int n, int mode, void
 
 static bool bad_f32(const float *p) { return !p || misaligned4(p); }
 
+// The fused RMSNorm -> Q6_K matvec runs on the whole-row matrix-core kernel
+// only: 16-byte aligned w, a tensor of whole 16-byte chunks, K <= 14 blocks.
+static bool q6k_norm_fits(const unsigned char *w, int out_dim, int bpr) {
+    return ((uintptr_t)w & 15u) == 0 && ((int64_t)out_dim * bpr * 210) % 16 == 0 && bpr <= 14;
+}
+
 // Host-side checks of one op descriptor (the launchers check again).
 static hipError_t op_check(const mgq_op_desc &o) {
     switch (o.op) {
@@ -284,6 +290,13 @@ static hipError_t op_check(const mgq_op_desc &o) {
         if (o.dtype != MGQ_DTYPE_Q5_K && o.dtype != MGQ_DTYPE_Q6_K) return hipErrorInvalidValue;
         return o.in_dim % 256 ? hipErrorInvalidValue : hipSuccess;
     case MGQ_OP_MATVEC_NORM:
+        if (o.dtype == MGQ_DTYPE_Q6_K) {
+            if (!o.w || bad_f32(o.x) || bad_f32(o.y) || bad_f32(o.norm_w) || o.out_dim <= 0 ||
+                o.in_dim <= 0 || o.in_dim % 256)
+                return hipErrorInvalidValue;
+            return q6k_norm_fits(o.w, o.out_dim, o.in_dim / 256) ? hipSuccess : hipErrorNotSupported;
+        }
+        [[fallthrough]];
     case MGQ_OP_MATVEC_GLU: {
         if (o.dtype != MGQ_DTYPE_Q4_K || !o.w || bad_f32(o.x) || bad_f32(o.y)) return hipErrorInvalidValue;
         if (o.out_dim <= 0 || o.in_dim <= 0 || o.in_dim % 256) return hipErrorInvalidValue;
@@ -314,6 +327,9 @@ static hipError_t op_launch(const mgq_op_desc &o, hipStream_t s) {
             return launch_matvec_q5k_ex(o.w, o.x, o.y, o.out_dim, o.in_dim / 256, s);
         return launch_matvec_q6k_ex(o.w, o.x, o.y, o.out_dim, o.in_dim / 256, s);
     case MGQ_OP_MATVEC_NORM:
+        if (o.dtype == MGQ_DTYPE_Q6_K)
+            return launch_matvec_q6k_rmsnorm_ex(o.w, o.x, o.norm_w, o.eps, o.y, o.out_dim,
+                                                o.in_dim / 256, s);
         return launch_matvec_q4k_rmsnorm_ex(o.w, o.x, o.norm_w, o.eps, o.y, o.out_dim,
                                             o.in_dim / 256, s);
     case MGQ_OP_MATVEC_GLU:
@@ -425,6 +441,15 @@ hipError_t launch_matvec_q4k_rmsnorm_ex(const unsigned char *w_q4, const float *
         return hipErrorInvalidValue;
     return mgq::gemv_fused_launch(w_q4, nullptr, x, norm_w, eps, MGQ_ACT_GELU_TANH, y, out_dim,
                                   blocks_per_row, stream);
+}
+
+hipError_t launch_matvec_q6k_rmsnorm_ex(const unsigned char *w_q6, const float *x,
+                                        const float *norm_w, float eps, float *y, int out_dim,
+                                        int blocks_per_row, hipStream_t stream) {
+    const hipError_t e = check_kquant(w_q6, x, y, out_dim, blocks_per_row);
+    if (e != hipSuccess) return e;
+    if (!norm_w || misaligned4(norm_w)) return hipErrorInvalidValue;
+    return mgq::gemv_q6k_mfma_norm_launch(w_q6, x, norm_w, eps, y, out_dim, blocks_per_row, stream);
 }
 
 hipError_t launch_matvec_q4k_glu_ex(const unsigned char *w_gate, const unsigned char *w_up,

@@ -174,6 +174,10 @@ hipError_t gemv_q5k_mfma_launch(const uint8_t *w, const float *x, float *y, int 
 // misaligned w or x, or a tensor that does not end on a 16-byte boundary.
 hipError_t gemv_q6k_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                                 hipStream_t stream);
+// Fused RMSNorm -> Q6_K matvec on the matrix cores (whole-row stages only:
+// K <= 14 blocks); hipErrorNotSupported outside them or for misaligned w.
+hipError_t gemv_q6k_mfma_norm_launch(const uint8_t *w, const float *x, const float *nw, float eps,
+                                     float *y, int n, int bpr, hipStream_t stream);
 
 // Q5_K / Q6_K matvecs (f32 activations) and Q6_K on Q8_1 activations.
 hipError_t gemv_q5k_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,

@@ -61,7 +61,7 @@ constexpr int SLOTC = (15 + SEG * BB + 15) / 16;            // 16-byte chunks pe
 constexpr int kQ6mMaxBpr = q6m::MAX_BPR;
 
 struct Q6mLayout {
-    uint32_t meta, stage, aux, ybuf;
+    uint32_t meta, stage, aux, ybuf, normp;
     size_t total;
 };
 
@@ -76,7 +76,8 @@ __host__ __device__ inline Q6mLayout q6m_layout(int bpr, int rounds, bool chunke
     // + 16: the 3-dword window around the last bytes of row 15 may end past them
     L.aux = L.stage + (chunked ? (uint32_t)(R * SLOTC * 16) : (uint32_t)(R * bpr * BB)) + 16;
     L.ybuf = L.aux + (uint32_t)nw * R * 4;
-    L.total = (size_t)L.ybuf + (size_t)R * rounds * 4;
+    L.normp = L.ybuf + (uint32_t)R * rounds * 4;  // fused RMSNorm: one sum(x^2) per wavefront
+    L.total = (size_t)L.normp + 16 * 4;
     return L;
 }
 
@@ -224,11 +225,18 @@ __device__ __forceinline__ void q6m_row_sums(float yacc, float *aux, float *ybuf
     }
 }
 
+// NORM: y = W * rms_norm(x, nw, eps) (the reference decode's launch_rms_norm
+// + launch_matvec_q6k pair, rocm_gemma.rs:439-440), computed as
+// rstd * (W * (x .* nw)): the table is built from x .* nw while sum(x^2) is
+// reduced, and the rows are scaled once at the end.
+template <bool NORM>
 __global__ __launch_bounds__(q6m::NT) void gemv_q6k_mfma_kernel(const uint8_t *__restrict__ w,
                                                                 const float *__restrict__ x,
                                                                 float *__restrict__ y, int n,
                                                                 int bpr, int rounds,
-                                                                GemvSched sch) {
+                                                                GemvSched sch,
+                                                                const float *__restrict__ nw,
+                                                                float eps) {
     using namespace q6m;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const Q6mLayout Lo = q6m_layout(bpr, rounds, false);
@@ -266,9 +274,26 @@ __global__ __launch_bounds__(q6m::NT) void gemv_q6k_mfma_kernel(const uint8_t *_
     // bpr <= 14 makes it at most one item per thread
     const int nitems = bpr * 32;
     const int ii = min(tid, nitems - 1);
-    const f32x4 v0 = ld_f32x4(x + (size_t)ii * 8);
-    const f32x4 v1 = ld_f32x4(x + (size_t)ii * 8 + 4);
+    f32x4 v0 = ld_f32x4(x + (size_t)ii * 8);
+    f32x4 v1 = ld_f32x4(x + (size_t)ii * 8 + 4);
+    f32x4 n0, n1;
+    if constexpr (NORM) {
+        n0 = ld_f32x4(nw + (size_t)ii * 8);
+        n1 = ld_f32x4(nw + (size_t)ii * 8 + 4);
+    }
     gload(0);
+    if constexpr (NORM) {
+        // this item's sum of x^2 (a clamped duplicate past the end adds 0),
+        // reduced per wavefront; the table holds x .* nw
+        float ssq = tid < nitems ? ((v0[0] * v0[0] + v0[1] * v0[1]) + (v0[2] * v0[2] + v0[3] * v0[3])) +
+                                       ((v1[0] * v1[0] + v1[1] * v1[1]) + (v1[2] * v1[2] + v1[3] * v1[3]))
+                                 : 0.0f;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ssq += __shfl_xor(ssq, off, 64);
+        if (lane == 0) reinterpret_cast<float *>(lds + Lo.normp)[wave] = ssq;
+        v0 *= n0;
+        v1 *= n1;
+    }
     q6m_item(lds, meta, tid, tid < nitems, v0, v1);
     lstore();
     gload(1);
@@ -289,9 +314,18 @@ __global__ __launch_bounds__(q6m::NT) void gemv_q6k_mfma_kernel(const uint8_t *_
         gload(q + 2);   // issued unconditionally, so every wait is exact
         __syncthreads();
     }
+    float rstd = 1.0f;
+    if constexpr (NORM) {
+        // rms_norm's 1/sqrt(mean(x^2) + eps) (kernels/rms_norm.hip:63-68); the
+        // partials were published by the barrier before the first group
+        const float *np = reinterpret_cast<const float *>(lds + Lo.normp);
+        float ss = 0.0f;
+        for (int wv = 0; wv < NW; ++wv) ss += np[wv];
+        rstd = rsqrtf(ss / (float)(bpr * kBlockElems) + eps);
+    }
     for (int i = tid; i < my_groups * R; i += NT) {
         const int r = sched_group(sch, (int)blockIdx.x, (int)gridDim.x, i / R) * R + (i % R);
-        if (r < n) y[r] = ybuf[i];
+        if (r < n) y[r] = NORM ? ybuf[i] * rstd : ybuf[i];
     }
 }
 
@@ -399,10 +433,10 @@ namespace {
 
 // Persistent launch of `kern` with the occupancy at `probe_lds` bytes
 // (persistent_plan: balanced, or age-skewed for pairs of work-groups per CU).
-template <typename K>
+template <typename K, typename... Extra>
 hipError_t q6m_launch(K kern, bool chunked, int nw, const uint8_t *w, const float *x, float *y,
                       int n, int bpr, int probe_bpr, int &occ, hipError_t &attr,
-                      hipStream_t stream) {
+                      hipStream_t stream, Extra... extra) {
     using namespace q6m;
     if (attr != hipSuccess) return attr;
     if (occ == 0) {
@@ -417,7 +451,7 @@ hipError_t q6m_launch(K kern, bool chunked, int nw, const uint8_t *w, const floa
     const PersistPlan p = persistent_plan((n + R - 1) / R, occ);
     const size_t lds = q6m_layout(bpr, (int)p.rounds, chunked, nw).total;
     if (lds > 160 * 1024) return hipErrorNotSupported;
-    kern<<<(unsigned)p.grid, nw * 64, lds, stream>>>(w, x, y, n, bpr, (int)p.rounds, p.sch);
+    kern<<<(unsigned)p.grid, nw * 64, lds, stream>>>(w, x, y, n, bpr, (int)p.rounds, p.sch, extra...);
     return hipGetLastError();
 }
 
@@ -444,10 +478,10 @@ hipError_t gemv_q6k_mfma_launch(const uint8_t *w, const float *x, float *y, int 
         return hipErrorNotSupported;
     if (bpr <= MAX_BPR) {
         static std::atomic<int> lds_state[64];
-        hipError_t attr = allow_full_lds((const void *)gemv_q6k_mfma_kernel, lds_state);
+        hipError_t attr = allow_full_lds((const void *)gemv_q6k_mfma_kernel<false>, lds_state);
         static int occ = 0;
-        return q6m_launch(gemv_q6k_mfma_kernel, false, NW, w, x, y, n, bpr, MAX_BPR, occ, attr,
-                          stream);
+        return q6m_launch(gemv_q6k_mfma_kernel<false>, false, NW, w, x, y, n, bpr, MAX_BPR, occ, attr,
+                          stream, (const float *)nullptr, 0.0f);
     }
     constexpr int LNW = LONG_NW, LNT = LNW * 64;
     const int need = (bpr * 32 + LNT - 1) / LNT;  // table items per thread
@@ -457,6 +491,21 @@ hipError_t gemv_q6k_mfma_launch(const uint8_t *w, const float *x, float *y, int 
     if (need <= 6) return q6m_long_launch<LNW, 6>(w, x, y, n, bpr, stream);
     if (need <= 8) return q6m_long_launch<LNW, 8>(w, x, y, n, bpr, stream);
     return hipErrorNotSupported;
+}
+
+hipError_t gemv_q6k_mfma_norm_launch(const uint8_t *w, const float *x, const float *nw, float eps,
+                                     float *y, int n, int bpr, hipStream_t stream) {
+    using namespace q6m;
+    // the whole-row kernel only: 16-byte aligned w, a tensor size that is a
+    // multiple of 16, K <= MAX_BPR blocks (the shapes a norm feeds: q|k|v,
+    // the output matrix)
+    if (((uintptr_t)w & 15u) || (((long)n * bpr * BB) % 16) || bpr > MAX_BPR)
+        return hipErrorNotSupported;
+    static std::atomic<int> lds_state[64];
+    hipError_t attr = allow_full_lds((const void *)gemv_q6k_mfma_kernel<true>, lds_state);
+    static int occ = 0;
+    return q6m_launch(gemv_q6k_mfma_kernel<true>, false, NW, w, x, y, n, bpr, MAX_BPR, occ, attr,
+                      stream, nw, eps);
 }
 
 }  // namespace mgq

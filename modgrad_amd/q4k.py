@@ -281,6 +281,15 @@ class kern:
                                                       _stream_ptr(stream)), "matvec_q4k_rmsnorm")
 
     @staticmethod
+    def matvec_q6k_rmsnorm(w: int, x: int, norm_w: int, eps: float, y: int, out_dim: int,
+                           bpr: int, stream=None) -> None:
+        """y = W * rms_norm(x, norm_w, eps) for Q6_K W in one launch (the
+        reference's rms_norm + matvec_q6k pair); BackendError("Unsupported")
+        outside q6k_norm_fits."""
+        _chk(_lib.load().launch_matvec_q6k_rmsnorm_ex(w, x, norm_w, eps, y, out_dim, bpr,
+                                                      _stream_ptr(stream)), "matvec_q6k_rmsnorm")
+
+    @staticmethod
     def matvec_q4k_glu(w_gate: int, w_up: int, x: int, y: int, out_dim: int, bpr: int,
                        norm_w: int | None = None, eps: float = 0.0,
                        act: int = _lib.ACT_GELU_TANH, stream=None) -> None:
@@ -351,10 +360,17 @@ def op_matvec(dtype: int, w: int, x: int, y: int, out_dim: int, in_dim: int,
 
 
 def op_matvec_norm(w: int, x: int, norm_w: int, eps: float, y: int, out_dim: int,
-                   in_dim: int) -> "_lib.OpDesc":
-    """y = W rms_norm(x) (Q4_K, one fused kernel)."""
-    return _lib.OpDesc(op=_lib.OP_MATVEC_NORM, dtype=_lib.DTYPE_Q4_K, w=w, x=x, norm_w=norm_w,
+                   in_dim: int, dtype: int = _lib.DTYPE_Q4_K) -> "_lib.OpDesc":
+    """y = W rms_norm(x) in one fused kernel: Q4_K, or Q6_K where
+    q6k_norm_fits(w, out_dim, in_dim // 256)."""
+    return _lib.OpDesc(op=_lib.OP_MATVEC_NORM, dtype=dtype, w=w, x=x, norm_w=norm_w,
                        eps=eps, y=y, out_dim=out_dim, in_dim=in_dim)
+
+
+def q6k_norm_fits(w: int, out_dim: int, bpr: int) -> bool:
+    """Whether the fused RMSNorm -> Q6_K matvec takes this tensor: 16-byte
+    aligned, whole 16-byte chunks (210-byte blocks), K <= 14 blocks."""
+    return w % 16 == 0 and (out_dim * bpr * 210) % 16 == 0 and bpr <= 14
 
 
 def op_matvec_glu(w_gate: int, w_up: int, x: int, y: int, out_dim: int, in_dim: int,

@@ -9,6 +9,7 @@ import pytest
 
 from modgrad_amd import _lib
 
+NOT_SUPPORTED = 801  # hipErrorNotSupported
 INVALID = _lib.hipErrorInvalidValue
 FAKE = 0x10000  # never dereferenced: every call below fails validation first
 
@@ -241,6 +242,20 @@ def test_op_chain_rejects_bad_descriptors_before_any_device_call(L):
         d.update(change)
         arr = (_lib.OpDesc * 2)(_lib.OpDesc(**good), _lib.OpDesc(**d))
         assert L.mgq_chain_create_ops(arr, 2, ctypes.byref(h)) == INVALID, change
+        assert h.value is None
+    # the fused RMSNorm Q6_K matvec: no norm weights is invalid; a tensor its
+    # whole-row kernel cannot take (K > 14 blocks, w not 16-byte aligned, a
+    # size that is not whole 16-byte chunks) is hipErrorNotSupported, still
+    # before any device call
+    q6n = dict(op=_lib.OP_MATVEC_NORM, dtype=_lib.DTYPE_Q6_K, norm_w=FAKE)
+    for change, code in [(dict(norm_w=None), INVALID), (dict(in_dim=300), INVALID),
+                         (dict(in_dim=15 * 256), NOT_SUPPORTED), (dict(w=FAKE + 2), NOT_SUPPORTED),
+                         (dict(out_dim=3), NOT_SUPPORTED)]:
+        d = dict(good)
+        d.update(q6n)
+        d.update(change)
+        arr = (_lib.OpDesc * 2)(_lib.OpDesc(**good), _lib.OpDesc(**d))
+        assert L.mgq_chain_create_ops(arr, 2, ctypes.byref(h)) == code, change
         assert h.value is None
     arr = (_lib.OpDesc * 1)(_lib.OpDesc(**good))
     assert L.mgq_chain_create_ops(arr, 0, ctypes.byref(h)) == INVALID

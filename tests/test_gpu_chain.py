@@ -148,8 +148,9 @@ def test_op_chain_mixed_dtypes_and_glue(L, orc):
     Q5_K matvecs on its output, the fused RMSNorm Q4_K matvec, the fused
     gate/up GLU matvec on that, a Q4_K down matvec on the GLU output, the
     standalone GLU, a residual add and a flat-layout Q4_K matvec reading the
-    residual sum. Every output is checked against the oracle applied to the
-    inputs the GPU actually produced, on three replays."""
+    residual sum, and the fused RMSNorm Q6_K matvec. Every output is checked
+    against the oracle applied to the inputs the GPU actually produced, on
+    three replays."""
     from modgrad_amd import q4k
     from tests.gpu_util import random_kquant_bytes
     note("op chain: Q4_K/Q5_K/Q6_K matvecs, fused norm/GLU matvecs, glue")
@@ -168,7 +169,7 @@ def test_op_chain_mixed_dtypes_and_glue(L, orc):
     dv = {k: dev(v) for k, v in dict(h0=h0, nw1=nw1, nw2=nw2, w6=w6, w5=w5, w4=w4, wg=wg,
                                           wu=wu, wd=wd, wf=wf).items()}
     out = {k: empty_f32(n) for k, n in dict(xn=H, q=KV, v=KV, y3=H, g=I, d=H, z=KV,
-                                            yf=8).items()}
+                                            yf=8, q6n=KV).items()}
     P = lambda k: ptr(dv[k]) if k in dv else ptr(out[k])
     Q4, Q5, Q6 = _lib.DTYPE_Q4_K, _lib.DTYPE_Q5_K, _lib.DTYPE_Q6_K
     ops = [
@@ -181,6 +182,7 @@ def test_op_chain_mixed_dtypes_and_glue(L, orc):
         q4k.op_glu(P("q"), P("v"), P("z"), KV, _lib.ACT_GELU_TANH),
         q4k.op_residual_add(P("d"), P("y3"), H),
         q4k.op_matvec(Q4, P("wf"), P("d"), P("yf"), 8, 96, _lib.LAYOUT_FLAT),
+        q4k.op_matvec_norm(P("w6"), P("h0"), P("nw1"), eps, P("q6n"), KV, H, Q6),
     ]
     ch = q4k.Chain.from_ops(ops)
     assert ch.mode() == _lib.CHAIN_GRAPH
@@ -212,6 +214,8 @@ def test_op_chain_mixed_dtypes_and_glue(L, orc):
         assert np.all(np.abs(r["z"].astype(np.float64) - zref) <= 2e-6 * np.abs(r["q"] * r["v"]) + 1e-30)
         y, A = orc.gemv_flat(wf, r["d"][:96], 8, 96)
         assert_gemv_close(r["yf"], y, A)
+        y, A = orc.gemv_kquant(210, w6, xn_ref, KV, H // 256)
+        assert_gemv_close(r["q6n"], y, A)
         if first is None:
             first = r
         else:

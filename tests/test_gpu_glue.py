@@ -7,7 +7,7 @@ Bounds:
   glu       |out - ref| <= 2e-6 |gate * up| (tanhf/expf of the device
             library vs the host's)
   fused     the matvec bound, 1e-4 * sum|w||xn| per row, xn the oracle's
-            normalized vector; for the GLU the bound propagates through
+            normalized vector (Q4_K and Q6_K); for the GLU the bound propagates through
             act (|act'| <= 1.13 for gelu_tanh, <= 1.1 for silu).
 """
 import sys
@@ -139,6 +139,72 @@ def test_matvec_glu_matches_unfused_chain(L, orc, n, bpr, act, norm):
     err = np.abs(y - ref)
     bad = np.nonzero(~(err <= bound))[0]
     assert bad.size == 0, (bad[:5].tolist(), err[bad[:5]].tolist(), bound[bad[:5]].tolist())
+
+
+# Q6_K tensors a norm feeds: attn_v 512x3584, a 1000-row K = 2048 shape, one
+# block, ragged row groups (4104 rows); n * bpr a multiple of 8 (whole
+# 16-byte chunks), as the fused kernel requires
+Q6_NORM_SHAPES = [(512, 14), (1000, 8), (48, 1), (4104, 14)]
+
+
+@pytest.mark.parametrize("n,bpr", Q6_NORM_SHAPES)
+def test_matvec_q6k_rmsnorm_matches_norm_then_matvec(L, orc, n, bpr):
+    from tests.gpu_util import random_kquant_bytes
+    note(f"matvec_q6k_rmsnorm n={n} bpr={bpr}")
+    k = bpr * 256
+    w = random_kquant_bytes(np.random.default_rng(0x66 + n + bpr), n * bpr, 210)
+    x = orc.normal(1200 + n, k, 1.7)
+    nw = orc.normal(1300 + n, k, 0.5) + np.float32(1.0)
+    eps = 1e-6
+    wt, xt, nt, yt = dev(w), dev(x), dev(nw), empty_f32(n)
+    _lib.check("q6k rmsnorm matvec", L.launch_matvec_q6k_rmsnorm_ex(ptr(wt), ptr(xt), ptr(nt), eps,
+                                                                    ptr(yt), n, bpr, None))
+    y = host(yt)
+    xn = orc.rms_norm(x, nw, 1, k, eps)
+    y_ref, A = orc.gemv_kquant(210, w, xn, n, bpr)
+    assert_gemv_close(y, y_ref, A)
+
+
+def test_matvec_q6k_rmsnorm_output_matrix(L, orc):
+    """The Q4_K_M output matrix, 152064 x 3584 Q6_K, at full size (rows
+    sampled, including the last ones)."""
+    import torch
+    note("matvec_q6k_rmsnorm 152064x3584")
+    n, bpr = 152064, 14
+    k = bpr * 256
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x6F)
+    wt = torch.randint(0, 256, (n * bpr, 210), dtype=torch.uint8, device="cuda", generator=gen)
+    dd = (torch.rand((n * bpr,), device="cuda", generator=gen) * 2e-3 + 1e-4).to(torch.float16)
+    wt[:, 208:210] = dd.view(torch.uint8).view(-1, 2)
+    x = orc.normal(1400, k, 1.1)
+    nw = orc.normal(1500, k, 0.4) + np.float32(1.0)
+    xt, nt, yt = dev(x), dev(nw), empty_f32(n)
+    _lib.check("q6k rmsnorm lm_head", L.launch_matvec_q6k_rmsnorm_ex(wt.data_ptr(), ptr(xt), ptr(nt),
+                                                                     1e-6, ptr(yt), n, bpr, None))
+    idx = np.unique(np.concatenate([np.random.default_rng(3).choice(n, 200, replace=False),
+                                    np.arange(n - 24, n)]))
+    wr = wt.view(n, bpr * 210)[torch.from_numpy(idx).cuda()].cpu().numpy().ravel()
+    xn = orc.rms_norm(x, nw, 1, k, 1e-6)
+    y_ref, A = orc.gemv_kquant(210, wr, xn, idx.size, bpr)
+    assert_gemv_close(host(yt)[idx], y_ref, A)
+
+
+def test_matvec_q6k_rmsnorm_rejects_what_its_kernel_cannot_take(L, orc):
+    """hipErrorNotSupported (no launch) for a weight that is not 16-byte
+    aligned, K > 14 blocks, or a tensor that is not whole 16-byte chunks;
+    hipErrorInvalidValue without norm weights."""
+    from tests.gpu_util import random_kquant_bytes
+    note("matvec_q6k_rmsnorm argument checks")
+    n, bpr = 64, 16
+    w = random_kquant_bytes(np.random.default_rng(5), n * bpr + 1, 210)
+    x = orc.normal(1, bpr * 256)
+    wt, xt, nt, yt = dev(w), dev(x), dev(np.ones(bpr * 256, np.float32)), empty_f32(n)
+    f = L.launch_matvec_q6k_rmsnorm_ex
+    assert f(ptr(wt) + 2, ptr(xt), ptr(nt), 1e-6, ptr(yt), n, 8, None) == 801
+    assert f(ptr(wt), ptr(xt), ptr(nt), 1e-6, ptr(yt), n, 15, None) == 801
+    assert f(ptr(wt), ptr(xt), ptr(nt), 1e-6, ptr(yt), 3, 1, None) == 801
+    assert f(ptr(wt), ptr(xt), None, 1e-6, ptr(yt), n, 8, None) == _lib.hipErrorInvalidValue
 
 
 def test_fused_matvecs_are_deterministic(L, orc):
