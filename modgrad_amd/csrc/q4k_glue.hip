@@ -13,6 +13,11 @@ namespace mgq {
 // order (thread t sums c = t, t+256, ...; then a pairwise tree t += t+128,
 // t+64, ..., 1), so it matches the reference bit for bit; the tree's last six
 // levels run inside one wavefront (DPP row shifts via shfl_down).
+// Elements per thread whose loads are all issued before the first is used
+// (hidden <= 4096 is one such chunk: one memory latency per pass instead of
+// one per element).
+constexpr int kNormPT = 16;
+
 __global__ __launch_bounds__(256) void rms_norm_kernel(const float *__restrict__ x,
                                                        const float *__restrict__ w,
                                                        float *__restrict__ y, int hidden,
@@ -21,8 +26,27 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float *__restrict__
     const int tid = threadIdx.x;
     const float *xr = x + (size_t)blockIdx.x * hidden;
     float *yr = y + (size_t)blockIdx.x * hidden;
+    // sum of squares in the order c = tid, tid + 256, ... (one fmaf each;
+    // elements past the end load as 0 and leave the sum unchanged)
+    float xv[kNormPT], wv[kNormPT];
     float s = 0.0f;
-    for (int c = tid; c < hidden; c += 256) s += xr[c] * xr[c];
+    const bool one = hidden <= 256 * kNormPT;  // uniform: x stays in registers
+    for (int c0 = 0; c0 < hidden; c0 += 256 * kNormPT) {
+#pragma unroll
+        for (int i = 0; i < kNormPT; ++i) {
+            const int c = c0 + tid + 256 * i;
+            xv[i] = c < hidden ? xr[c] : 0.0f;
+        }
+        if (one) {
+#pragma unroll
+            for (int i = 0; i < kNormPT; ++i) {
+                const int c = tid + 256 * i;
+                wv[i] = c < hidden ? w[c] : 0.0f;  // in flight during the reduction
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kNormPT; ++i) s = fmaf(xv[i], xv[i], s);
+    }
     part[tid] = s;
     __syncthreads();
     if (tid < 128) part[tid] += part[tid + 128];
@@ -35,7 +59,27 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float *__restrict__
     }
     __syncthreads();
     const float rstd = rsqrtf(part[0] / (float)hidden + eps);
-    for (int c = tid; c < hidden; c += 256) yr[c] = xr[c] * rstd * w[c];
+    if (one) {
+#pragma unroll
+        for (int i = 0; i < kNormPT; ++i) {
+            const int c = tid + 256 * i;
+            if (c < hidden) yr[c] = xv[i] * rstd * wv[i];
+        }
+        return;
+    }
+    for (int c0 = 0; c0 < hidden; c0 += 256 * kNormPT) {
+#pragma unroll
+        for (int i = 0; i < kNormPT; ++i) {
+            const int c = c0 + tid + 256 * i;
+            xv[i] = c < hidden ? xr[c] : 0.0f;
+            wv[i] = c < hidden ? w[c] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < kNormPT; ++i) {
+            const int c = c0 + tid + 256 * i;
+            if (c < hidden) yr[c] = xv[i] * rstd * wv[i];
+        }
+    }
 }
 
 hipError_t rms_norm_launch(const float *x, const float *w, float *y, int rows, int hidden,
