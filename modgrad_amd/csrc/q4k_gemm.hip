@@ -368,14 +368,20 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__r
 // are interleaved with that VALU work, its LDS stores and its global loads
 // (sched_group_barrier), so the matrix core and the VALU stay busy together.
 //
-// Range. Each W row gets a power-of-two exponent e from its block headers
-// such that every dequantized |weight| * 2^e < 2^15 (row_range_bound). The
-// nibble is masked in place as the f16 subnormal q * 2^-24 (or 16q * 2^-24
-// for the high nibble), exact, and one v_pk_fma_f16 with the sub-block pair
-// (d*sc*2^(e+4), -dmin*m*2^(e-20)) gives (q*d*sc - dmin*m) * 2^(e-20),
-// rounded once; |d*sc| * 2^(e+4) < 2^15 * 63*16/945 stays below the f16
-// maximum, and weights above 2^-9 of the row's largest stay normal. C is
-// multiplied by 2^(20-e) (exact) at the end.
+// Range. Each W row carries a running power-of-two exponent: block b of the
+// row is dequantized at the e that keeps every |weight| of blocks 0..b
+// times 2^e below 2^15 (range_exp of the running maximum of
+// 945|d| + 63|dmin|), so e never grows from one block to the next except
+// past an all-zero prefix. The nibble is masked in place as the f16
+// subnormal q * 2^-24 (or 16q * 2^-24 for the high nibble), exact, and one
+// v_pk_fma_f16 with the sub-block pair (d*sc*2^(e+4), -dmin*m*2^(e-20))
+// gives (q*d*sc - dmin*m) * 2^(e-20), rounded once; |d*sc| * 2^(e+4) <
+// 2^15 * 63*16/945 stays below the f16 maximum, and weights above 2^-9 of
+// the largest seen so far stay normal. When a block changes e, the row's
+// sums so far are multiplied by 2^(e_new - e_old) (exact, a power of two)
+// between the two blocks' MFMAs, and C is multiplied by 2^(20-e) of the
+// last block at the end. No pass over the row's headers precedes the
+// first MFMA.
 struct G2Cfg {
     static constexpr int WN = 2, WM = 4, TI = 5, TJ = 4;
     static constexpr int BN = WN * 16 * TI;       // 160 W rows per work-group
@@ -387,7 +393,7 @@ struct G2Cfg {
     static constexpr int WPW = WP / (NT / 64);    // pieces per wavefront (40)
     static constexpr int APT = BM * 8 / NT;       // activation pieces per thread per step
     static constexpr uint32_t SW = BN * PITCH * 2, SA = BM * PITCH * 2;
-    static constexpr uint32_t LDS = 2 * SW + 2 * SA + BN * 4;
+    static constexpr uint32_t LDS = 2 * SW + 2 * SA + 2 * BN * 4;
     static_assert(PITCH % 8 == 0, "16-byte aligned LDS rows (b128 accesses)");
     static_assert(WP % (NT / 64) == 0 && 2 * WPW >= 64 && WPW <= 64, "piece split");
     static_assert(BM * 8 % NT == 0, "whole activation pieces per thread");
@@ -403,7 +409,8 @@ __global__ __launch_bounds__(G2Cfg::NT, 1) void gemm_q4k_f16_lds_kernel(
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     _Float16 *sW = reinterpret_cast<_Float16 *>(lds);
     _Float16 *sA = reinterpret_cast<_Float16 *>(lds + 2 * SW);
-    float *sE = reinterpret_cast<float *>(lds + 2 * SW + 2 * SA);
+    float *sE = reinterpret_cast<float *>(lds + 2 * SW + 2 * SA);  // per row: 2^(20-e), C's scale
+    float *sF = sE + BN;  // per row: 2^(e_new - e_old) of the block being opened
 
     // work-group -> tile: work-group i runs on XCD i % 8; XCD x takes a
     // contiguous range of tiles, so the token tiles of one W tile share an L2
@@ -427,19 +434,22 @@ __global__ __launch_bounds__(G2Cfg::NT, 1) void gemm_q4k_f16_lds_kernel(
     const uint8_t *wrow = w + (size_t)min(n0 + wr, n - 1) * row_bytes;
 
     // ---- step loaders (registers) ------------------------------------------
-    const uint16_t *aptr[APT];
-    uint32_t alds[APT];
+    // activation piece k of this thread: token tid/8 + 64k of the tile
+    // (clamped past m_tokens), 16 bytes at 8*(tid%8) of the step's 64 values;
+    // 32-bit byte offsets from the step's base (the launcher keeps
+    // m_tokens * K * 2 below 2^32), so the loads take a scalar base
+    uint32_t aoff[APT];
 #pragma unroll
     for (int k = 0; k < APT; ++k) {
-        const int pa = tid + Cfg::NT * k, tok = pa >> 3, part = pa & 7;
-        aptr[k] = a + (size_t)min(m0 + tok, m_tokens - 1) * K + 8 * part;
-        alds[k] = (uint32_t)((tok * PITCH + 8 * part) * 2);
+        const int tok = (tid >> 3) + (Cfg::NT / 8) * k;
+        aoff[k] = (uint32_t)(((size_t)min(m0 + tok, m_tokens - 1) * K + 8 * (tid & 7)) * 2);
     }
+    const uint32_t alds0 = (uint32_t)(((tid >> 3) * PITCH + 8 * (tid & 7)) * 2);
     u32x4 Ar[APT], Wq[2], Hd;
     auto loadA = [&](int t) __attribute__((always_inline)) {
-        t = min(t, T - 1);
+        const uint8_t *base = reinterpret_cast<const uint8_t *>(a) + (size_t)min(t, T - 1) * KS * 2;
 #pragma unroll
-        for (int k = 0; k < APT; ++k) Ar[k] = ld_u32x4(aptr[k] + (size_t)t * KS);
+        for (int k = 0; k < APT; ++k) Ar[k] = ld_u32x4(base + aoff[k]);
     };
     auto loadW = [&](int t, int set) __attribute__((always_inline)) {
         t = min(t, T - 1);
@@ -452,19 +462,31 @@ __global__ __launch_bounds__(G2Cfg::NT, 1) void gemm_q4k_f16_lds_kernel(
 
     // step t -> LDS buffer: activations copied, weights dequantized
     auto storeA = [&](int buf) __attribute__((always_inline)) {
-        uint8_t *dA = lds + 2 * SW + buf * SA;
+        uint8_t *dA = lds + 2 * SW + buf * SA + alds0;
 #pragma unroll
-        for (int k = 0; k < APT; ++k) *reinterpret_cast<u32x4 *>(dA + alds[k]) = Ar[k];
+        for (int k = 0; k < APT; ++k)
+            *reinterpret_cast<u32x4 *>(dA + k * (Cfg::NT / 8) * PITCH * 2) = Ar[k];
     };
     // the block's 8 sub-block pairs (d*sc*2^(e+4), -dmin*m*2^(e-20)) as f16,
     // decoded once per super-block from its header (sub-block index
     // constant: no branches); d*sc and dmin*m are exact in f32 and the
-    // factors are powers of two, so each is rounded to f16 once
-    float sD, sN;  // 2^(e+4), 2^(e-20): set in the prologue from the row range
+    // factors are powers of two, so each is rounded to f16 once. The row's
+    // exponent e follows the running bound; the lane of each row's first
+    // piece publishes the rescale of the sums so far and C's scale.
+    float bnd = 0.0f;  // max of 945|d| + 63|dmin| over the row's blocks so far
+    int erow = 0;
     uint32_t scl[8];
     auto decode = [&]() __attribute__((always_inline)) {
-        const float d = half_bits_finite(Hd[0]) * sD;
-        const float nm = -(half_bits_finite(Hd[0] >> 16) * sN);
+        const float dh = half_bits_finite(Hd[0]), mh = half_bits_finite(Hd[0] >> 16);
+        bnd = fmaxf(bnd, fabsf(dh) * 945.0f + fabsf(mh) * 63.0f);
+        const int e = range_exp(bnd);
+        if (wh == 0) {
+            sF[wr] = ldexpf(1.0f, e - erow);
+            sE[wr] = ldexpf(1.0f, 20 - e);
+        }
+        erow = e;
+        const float d = dh * ldexpf(1.0f, e + 4);
+        const float nm = -(mh * ldexpf(1.0f, e - 20));
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             uint32_t sc, mn;
@@ -506,79 +528,114 @@ __global__ __launch_bounds__(G2Cfg::NT, 1) void gemm_q4k_f16_lds_kernel(
     for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // a step's operands are all read from LDS before its first MFMA
-    auto compute = [&](int buf) __attribute__((always_inline)) {
+    // operands of one k half (32 of the step's 64): W rows first, then tokens,
+    // in the order the MFMAs below consume them
+    half8 wa[2][TI], tb[2][TJ];
+    auto readOps = [&](int buf, auto hc) __attribute__((always_inline)) {
+        constexpr int h = decltype(hc)::value;
         const _Float16 *W_ = sW + buf * (BN * PITCH);
         const _Float16 *A_ = sA + buf * (BM * PITCH);
-        half8 wa[2][TI], tb[2][TJ];
+        wa[h][0] = *reinterpret_cast<const half8 *>(&W_[(wn + l16) * PITCH + 32 * h + 8 * q]);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int j = 0; j < TJ; ++j)
+            tb[h][j] = *reinterpret_cast<const half8 *>(&A_[(wm + 16 * j + l16) * PITCH + 32 * h + 8 * q]);
 #pragma unroll
-            for (int i = 0; i < TI; ++i)
-                wa[h][i] = *reinterpret_cast<const half8 *>(&W_[(wn + 16 * i + l16) * PITCH + 32 * h + 8 * q]);
+        for (int i = 1; i < TI; ++i)
+            wa[h][i] = *reinterpret_cast<const half8 *>(&W_[(wn + 16 * i + l16) * PITCH + 32 * h + 8 * q]);
+    };
+    auto mfmaHalf = [&](auto hc) __attribute__((always_inline)) {
+        constexpr int h = decltype(hc)::value;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
 #pragma unroll
             for (int j = 0; j < TJ; ++j)
-                tb[h][j] = *reinterpret_cast<const half8 *>(&A_[(wm + 16 * j + l16) * PITCH + 32 * h + 8 * q]);
-        }
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int i = 0; i < TI; ++i)
-#pragma unroll
-                for (int j = 0; j < TJ; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[h][i], tb[h][j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[h][i], tb[h][j], acc[i][j], 0, 0, 0);
     };
+    using H0 = std::integral_constant<int, 0>;
+    using H1 = std::integral_constant<int, 1>;
 
     // ---- pipeline ----------------------------------------------------------
-    // Step t computes buffer t & 1, then writes step t+1 into the other
-    // buffer and refills the registers it came from: weights with step t+3
-    // (two sets), activations with step t+2. The header of the block step
-    // t+3 opens is loaded at t = 1 mod 4 and decoded at t = 3 mod 4, just
-    // before that block's first step is stored. Loads past the last step
-    // re-read it (clamped), so every load is unconditional and the load
+    // Weights are loaded two steps before their dequantized store (two
+    // register sets), activations one step before theirs. The header of the
+    // block that step t+4 opens is loaded at t = 0 mod 4 and decoded at
+    // t = 2 mod 4, just before that block's first store. Loads past the last
+    // step re-read it (clamped), so every load is unconditional and the load
     // counter waits only for the data it needs.
     loadH(0);
     loadA(0);
     loadW(0, 0);
     loadW(1, 1);
-    // per-row range (each of a row's piece lanes reads all of its block
-    // headers) while the first steps' loads fly
-    {
-        const int e = range_exp(row_range_bound(wrow, 0, 1, bpr));
-        sD = ldexpf(1.0f, e + 4);
-        sN = ldexpf(1.0f, e - 20);
-        if (wh == 0) sE[wr] = ldexpf(1.0f, 20 - e);
-    }
     decode();
     storeA(0);
-    storeW(std::integral_constant<int, 0>{}, 0, 0);
     loadA(1);
+    storeW(std::integral_constant<int, 0>{}, 0, 0);
     loadW(2, 0);
+    storeW(std::integral_constant<int, 1>{}, 1, 1);
+    loadW(3, 1);
     __syncthreads();
+    readOps(0, H0{});
+    // One barrier per step, between its two k halves; step t's operands sit
+    // in LDS buffer t & 1. Before the barrier: the first half's MFMAs
+    // (operands read after the previous barrier), the second half's operand
+    // reads from the same buffer, step t+1's activation stores into the
+    // other buffer and the loads that refill those registers (one step
+    // before their use). After it: the second half's MFMAs, the first-half
+    // operand reads of step t+1, and step t+2's dequantized weights into
+    // buffer t & 1, whose last reads came before the barrier (with the
+    // weight loads for step t+4). Every read of a buffer comes before the
+    // barrier that precedes its next store, so LDS latency hides under the
+    // MFMAs, and the LDS stores and dequant work split across both halves.
     auto stage = [&](int t, auto ph) __attribute__((always_inline)) {
         constexpr int PH = decltype(ph)::value;  // t & 3
-        constexpr int P = PH & 1;                 // buffer of step t
-        constexpr int NS = P ^ 1;                 // buffer / weight set of step t+1
-        compute(P);
+        constexpr int P = PH & 1;                 // buffer of step t (and t+2)
+        constexpr int NS = P ^ 1;                 // buffer of step t+1
+        constexpr int NM = TI * TJ;               // MFMAs per half
+        readOps(P, H1{});
+        mfmaHalf(H0{});
         storeA(NS);
-        if constexpr (PH == 3) decode();
-        storeW(std::integral_constant<int, (PH + 1) & 3>{}, NS, NS);
         loadA(t + 2);
-        loadW(t + 3, NS);
-        if constexpr (PH == 1) loadH(t + 3);
-        // operand reads first, then each MFMA followed by a share of the
-        // dequant VALU work, the LDS stores and the global loads
-        constexpr int NM = 2 * TI * TJ;
-        __builtin_amdgcn_sched_group_barrier(0x0100, 2 * (TI + TJ), 0);  // DS reads
-        __builtin_amdgcn_sched_group_barrier(0x0002, 6, 0);              // VALU
+        if constexpr (PH == 0) loadH(t + 4);
 #pragma unroll
         for (int i = 0; i < NM; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);               // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x0002, PH == 3 ? 4 : 2, 0);  // VALU
-            if (i % 4 == 3) __builtin_amdgcn_sched_group_barrier(0x0200, 1, 0);  // DS write
-            if (i % 6 == 5) __builtin_amdgcn_sched_group_barrier(0x0020, 1, 0);  // VMEM read
+            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);                       // MFMA
+            if (i < TI + TJ) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);        // DS read
+            if (i >= 10 && i % 2 == 0 && i < 18) __builtin_amdgcn_sched_group_barrier(0x0200, 1, 0);  // DS write
+            if (i >= 11 && i % 2 == 1) __builtin_amdgcn_sched_group_barrier(0x0020, 1, 0);  // VMEM read
+            __builtin_amdgcn_sched_group_barrier(0x0002, 1, 0);                       // VALU
         }
+        __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        readOps(NS, H0{});
+        mfmaHalf(H1{});
+        // step t+2's weights open the next block at t = 2 mod 4: its scales
+        // replace this block's, whose last step (t+1) was stored one step ago
+        if constexpr (PH == 2) decode();
+        storeW(std::integral_constant<int, (PH + 2) & 3>{}, P, P);
+        loadW(t + 4, P);
+        // the block ends with this half: rescale the sums by the factors the
+        // next block's decode published (one step ago, before the barrier)
+        f32x4 fr[TI];
+        if constexpr (PH == 3) {
+#pragma unroll
+            for (int i = 0; i < TI; ++i) fr[i] = *reinterpret_cast<const f32x4 *>(&sF[wn + 16 * i + 4 * q]);
+        }
+#pragma unroll
+        for (int i = 0; i < NM; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);                 // MFMA
+            if (i < TI + TJ + (PH == 3 ? TI : 0)) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);  // DS read
+            __builtin_amdgcn_sched_group_barrier(0x0002, PH == 2 ? 7 : 3, 0);     // VALU
+            if (i >= 10 && i % 2 == 1 && i < 18) __builtin_amdgcn_sched_group_barrier(0x0200, 1, 0);  // DS write
+            if (i == 18) __builtin_amdgcn_sched_group_barrier(0x0020, 1, 0);        // VMEM read
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (PH == 3) {
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j) acc[i][j] *= fr[i];
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
     for (int t = 0; t < T; t += 4) {  // T = 4 * bpr
         stage(t, std::integral_constant<int, 0>{});
@@ -659,7 +716,9 @@ hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n,
     const long rounds2 = (tiles2 + cus2 - 1) / cus2;
     const bool lds_fits = 10L * m_tokens >= 9L * G2Cfg::BM * tm2 &&
                           (rounds2 == 1 ? 2 * tiles2 > cus2 : 20 * tiles2 >= 17 * rounds2 * cus2);
-    if (big_env == 1 || (big_env < 0 && lds_fits))
+    // the LDS kernel addresses A with 32-bit byte offsets
+    const bool a32 = (uint64_t)m_tokens * (uint64_t)bpr * kBlockElems * 2 <= 0xFFFFFFFFull;
+    if (a32 && (big_env == 1 || (big_env < 0 && lds_fits)))
         return gemm_lds_launch(w, a, c, n, bpr, m_tokens, stream);
     // Tile height by the rows the busiest CU computes: ceil(tiles / #CUs) x
     // BN, the lower one, ties to 160 (a second resident tile on a CU adds

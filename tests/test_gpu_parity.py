@@ -354,8 +354,9 @@ def test_gemm_f16_small(L, orc, n, bpr, m):
 
 # Random-byte blocks across the f16 range of d/dmin: tiny (f16 subnormal d,
 # weights ~1e-4), huge (weights up to ~6e7, past f16's 65504), ten decades
-# mixed inside one row, and raw random header bytes (Inf/NaN d read as 0).
-# M = 40 runs the 128-token-tile kernel, M = 384 the LDS-dequant kernel.
+# mixed inside one row, eight decades rising along every row (each block
+# larger than the one before), and raw random header bytes (Inf/NaN d read
+# as 0).
 def _range_weight(rng, n, bpr, kind):
     nb = n * bpr
     if kind == "random":
@@ -365,6 +366,9 @@ def _range_weight(rng, n, bpr, kind):
         d = rng.uniform(1e-8, 3e-6, size=(nb, 2))
     elif kind == "huge":
         d = rng.uniform(1e2, 6e4, size=(nb, 2))
+    elif kind == "rising":
+        j = np.tile(np.arange(bpr), n)[:, None] + rng.uniform(0, 1, size=(nb, 2))
+        d = 10.0 ** (-7 + 8 * j / bpr)
     else:  # mixed
         d = 10.0 ** rng.uniform(-7, 1, size=(nb, 2))
     b[:, 0:4] = d.astype(np.float16).view(np.uint8).reshape(nb, 4)
@@ -385,11 +389,13 @@ def _gemm_check(L, orc, w, a, n, bpr, m, rows=None):
 
 
 # (200, 40): the 128-token kernel; (32000, 256): 200 tiles of 160 x 256, the
-# LDS-dequant kernel (rows sampled)
-@pytest.mark.parametrize("n,m", [(200, 40), (32000, 256)])
-@pytest.mark.parametrize("kind", ["tiny", "huge", "mixed", "random"])
+# LDS-dequant kernel, one block per row; (20000, 512): the LDS-dequant kernel
+# with 14 blocks per row, where a row's scale follows its blocks (rows
+# sampled on the large shapes)
+@pytest.mark.parametrize("n,m", [(200, 40), (32000, 256), (20000, 512)])
+@pytest.mark.parametrize("kind", ["tiny", "huge", "mixed", "rising", "random"])
 def test_gemm_f16_dynamic_range(L, orc, kind, n, m):
-    bpr = 4 if n < 1000 else 1
+    bpr = {200: 4, 32000: 1, 20000: 14}[n]
     note(f"gemm range {kind} n={n} bpr={bpr} m={m}")
     rng = np.random.default_rng(0x6E11 + m)
     w = _range_weight(rng, n, bpr, kind)
