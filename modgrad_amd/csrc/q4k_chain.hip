@@ -115,8 +115,7 @@ typedef __attribute__((address_space(1))) u32x4_a1 g_u32x4_a1;
 // Activation reads: 16-byte buffer loads with the device-scope coherence bit
 // (sc1) over a resource covering exactly the vector, so reads past its end
 // return zeros without touching memory.
-constexpr int kBufSc1 = 16;            // cache-policy bit sc1 of buffer instructions
-constexpr int kBufWord3 = 0x00020000;  // raw buffer: 32-bit data format
+constexpr int kBufSc1 = 16;  // cache-policy bit sc1 of buffer instructions
 __device__ __forceinline__ u32x4 ld_w16(const uint8_t *p) { return *(const g_u32x4_a1 *)p; }
 __device__ __forceinline__ void st_sc1(float *p, float v) {
     __hip_atomic_store((g_f32 *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -315,7 +314,7 @@ __global__ __launch_bounds__(pc::NT) void chain_kernel(const ChainTask *__restri
         const ChainTask &t = task(d);
         const int bpr = t.bpr, nitems = bpr * 32;
         const __amdgpu_buffer_rsrc_t xr =
-            __builtin_amdgcn_make_buffer_rsrc((void *)t.x, 0, nitems * 32, kBufWord3);
+            __builtin_amdgcn_make_buffer_rsrc((void *)t.x, 0, nitems * 32, kRawBufWord3);
         // eight dword loads per item, which the compiler merges into two
         // 16-byte loads (the 128-bit builtin's vector result does not survive
         // element extraction on this compiler)

@@ -71,6 +71,10 @@ typedef float f32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 __device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) {
     return *reinterpret_cast<const u32_a1 *>(p);
 }
+// Word 3 of a raw buffer resource (stride 0, 32-bit data format): offsets
+// are in bytes, and a read at or past num_records returns zeros.
+constexpr int kRawBufWord3 = 0x00020000;
+
 __device__ __forceinline__ u32x4 ld_u32x4(const void *p) {
     return *reinterpret_cast<const u32x4_a1 *>(p);
 }

@@ -368,20 +368,24 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__r
 // are interleaved with that VALU work, its LDS stores and its global loads
 // (sched_group_barrier), so the matrix core and the VALU stay busy together.
 //
-// Range. Each W row carries a running power-of-two exponent: block b of the
-// row is dequantized at the e that keeps every |weight| of blocks 0..b
-// times 2^e below 2^15 (range_exp of the running maximum of
-// 945|d| + 63|dmin|), so e never grows from one block to the next except
-// past an all-zero prefix. The nibble is masked in place as the f16
+// Range. Each W row carries a running power-of-two exponent e. Any e at or
+// below tight = range_exp(running max of 945|d| + 63|dmin| over the row's
+// blocks so far) keeps every |weight| * 2^e below 2^15. A row starts at
+// tight - kRangeHeadroom of its first nonzero block and keeps e while the
+// later blocks' tight stays at or above it; a block that overruns it (more
+// than 2^kRangeHeadroom above the first block's bound) lowers e to its
+// tight - kRangeHeadroom. The nibble is masked in place as the f16
 // subnormal q * 2^-24 (or 16q * 2^-24 for the high nibble), exact, and one
 // v_pk_fma_f16 with the sub-block pair (d*sc*2^(e+4), -dmin*m*2^(e-20))
 // gives (q*d*sc - dmin*m) * 2^(e-20), rounded once; |d*sc| * 2^(e+4) <
-// 2^15 * 63*16/945 stays below the f16 maximum, and weights above 2^-9 of
-// the largest seen so far stay normal. When a block changes e, the row's
-// sums so far are multiplied by 2^(e_new - e_old) (exact, a power of two)
-// between the two blocks' MFMAs, and C is multiplied by 2^(20-e) of the
-// last block at the end. No pass over the row's headers precedes the
+// 2^15 * 63*16/945 stays below the f16 maximum, and weights above
+// 2^-(9 - kRangeHeadroom) of the largest seen so far stay normal f16. When
+// a block changes some row's e (a flag in LDS says so), the work-group's
+// sums so far are multiplied by 2^(e_new - e_old) per row (exact, a power
+// of two) between the two blocks' MFMAs; C is multiplied by 2^(20-e) of
+// the last block at the end. No pass over the row's headers precedes the
 // first MFMA.
+constexpr int kRangeHeadroom = 4;
 struct G2Cfg {
     static constexpr int WN = 2, WM = 4, TI = 5, TJ = 4;
     static constexpr int BN = WN * 16 * TI;       // 160 W rows per work-group
@@ -390,12 +394,12 @@ struct G2Cfg {
     static constexpr int KS = 64;                 // k per step
     static constexpr int PITCH = 80;              // halves per LDS row (64 + pad)
     static constexpr int WP = BN * 2;             // 16-byte qs pieces per step
-    static constexpr int WPW = WP / (NT / 64);    // pieces per wavefront (40)
+    static constexpr int WWAVES = WP / 64;        // wavefronts that dequantize W (5)
     static constexpr int APT = BM * 8 / NT;       // activation pieces per thread per step
     static constexpr uint32_t SW = BN * PITCH * 2, SA = BM * PITCH * 2;
-    static constexpr uint32_t LDS = 2 * SW + 2 * SA + 2 * BN * 4;
+    static constexpr uint32_t LDS = 2 * SW + 2 * SA + 2 * BN * 4 + 16;
     static_assert(PITCH % 8 == 0, "16-byte aligned LDS rows (b128 accesses)");
-    static_assert(WP % (NT / 64) == 0 && 2 * WPW >= 64 && WPW <= 64, "piece split");
+    static_assert(WP % 64 == 0 && WWAVES <= NT / 64, "whole wavefronts of W pieces");
     static_assert(BM * 8 % NT == 0, "whole activation pieces per thread");
 };
 
@@ -404,13 +408,14 @@ __global__ __launch_bounds__(G2Cfg::NT, 1) void gemm_q4k_f16_lds_kernel(
     int bpr, int m_tokens, int tiles_n, int tiles_m) {
     using Cfg = G2Cfg;
     constexpr int WN = Cfg::WN, TI = Cfg::TI, TJ = Cfg::TJ, BN = Cfg::BN, BM = Cfg::BM;
-    constexpr int KS = Cfg::KS, PITCH = Cfg::PITCH, WPW = Cfg::WPW, APT = Cfg::APT;
+    constexpr int KS = Cfg::KS, PITCH = Cfg::PITCH, APT = Cfg::APT;
     constexpr uint32_t SW = Cfg::SW, SA = Cfg::SA;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     _Float16 *sW = reinterpret_cast<_Float16 *>(lds);
     _Float16 *sA = reinterpret_cast<_Float16 *>(lds + 2 * SW);
     float *sE = reinterpret_cast<float *>(lds + 2 * SW + 2 * SA);  // per row: 2^(20-e), C's scale
     float *sF = sE + BN;  // per row: 2^(e_new - e_old) of the block being opened
+    int *sFlag = reinterpret_cast<int *>(sF + BN);  // [1]: some row's e changed; [0]: dummy
 
     // work-group -> tile: work-group i runs on XCD i % 8; XCD x takes a
     // contiguous range of tiles, so the token tiles of one W tile share an L2
@@ -425,39 +430,49 @@ __global__ __launch_bounds__(G2Cfg::NT, 1) void gemm_q4k_f16_lds_kernel(
     const int T = bpr * 4;  // K steps
     const size_t row_bytes = (size_t)bpr * kBlockBytes;
 
-    // this lane's qs piece p: W row wr = p % BN (clamped past n), bytes
-    // 16*wh.. (wh = p / BN) of each step's 32-byte qs group; the 8 lanes of
-    // an LDS store group write 8 consecutive rows (distinct banks at an
-    // 80-half pitch)
-    const int p = wave * WPW + (lane < WPW ? lane : lane - (64 - WPW));
+    // W dequantization: the first WWAVES wavefronts, one qs piece per lane
+    // (an LDS store instruction costs the same whatever its active lanes, so
+    // whole wavefronts take the 320 pieces of a step). Piece p: W row
+    // wr = p % BN (clamped past n), bytes 16*wh.. (wh = p / BN) of each
+    // step's 32-byte qs group; the 8 lanes of an LDS store group write 8
+    // consecutive rows (distinct banks at an 80-half pitch)
+    const bool isW = __builtin_amdgcn_readfirstlane(wave) < Cfg::WWAVES;
+    const int p = (isW ? wave : 0) * 64 + lane;
     const int wr = p % BN, wh = p / BN;
-    const uint8_t *wrow = w + (size_t)min(n0 + wr, n - 1) * row_bytes;
+    // Global loads are raw buffer loads: a 32-bit per-lane byte offset plus
+    // a per-step scalar offset (the launcher keeps W and A below 2^32 bytes),
+    // so no per-load address arithmetic. Offsets: the lane's row header and
+    // its qs piece.
+    const __amdgpu_buffer_rsrc_t wbuf = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)w, 0, (int)(uint32_t)((uint64_t)n * row_bytes), kRawBufWord3);
+    const __amdgpu_buffer_rsrc_t abuf = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)a, 0, (int)(uint32_t)((uint64_t)m_tokens * K * 2), kRawBufWord3);
+    const uint32_t hoff = (uint32_t)((size_t)min(n0 + wr, n - 1) * row_bytes);
 
     // ---- step loaders (registers) ------------------------------------------
-    // activation piece k of this thread: token tid/8 + 64k of the tile
-    // (clamped past m_tokens), 16 bytes at 8*(tid%8) of the step's 64 values;
-    // 32-bit byte offsets from the step's base (the launcher keeps
-    // m_tokens * K * 2 below 2^32), so the loads take a scalar base
-    uint32_t aoff[APT];
-#pragma unroll
-    for (int k = 0; k < APT; ++k) {
-        const int tok = (tid >> 3) + (Cfg::NT / 8) * k;
-        aoff[k] = (uint32_t)(((size_t)min(m0 + tok, m_tokens - 1) * K + 8 * (tid & 7)) * 2);
-    }
+    // activation piece k of this thread: token tid/8 + 64k of the tile, 16
+    // bytes at 8*(tid%8) of the step's 64 values. The per-lane offset stays
+    // below 2^32 (the launcher checks (m_tokens + BM) * K * 2), and token
+    // rows past m_tokens fall past num_records, so they read as zeros; the
+    // per-step scalar offset stays inside a token row.
+    const uint32_t aoff0 = (uint32_t)(((size_t)(m0 + (tid >> 3)) * K + 8 * (tid & 7)) * 2);
+    const uint32_t astride = (uint32_t)(Cfg::NT / 8) * (uint32_t)K * 2;
     const uint32_t alds0 = (uint32_t)(((tid >> 3) * PITCH + 8 * (tid & 7)) * 2);
     u32x4 Ar[APT], Wq[2], Hd;
-    auto loadA = [&](int t) __attribute__((always_inline)) {
-        const uint8_t *base = reinterpret_cast<const uint8_t *>(a) + (size_t)min(t, T - 1) * KS * 2;
+    auto loadA_to = [&](u32x4(&dst)[APT], int t) __attribute__((always_inline)) {
+        const int so = min(t, T - 1) * KS * 2;
 #pragma unroll
-        for (int k = 0; k < APT; ++k) Ar[k] = ld_u32x4(base + aoff[k]);
+        for (int k = 0; k < APT; ++k)
+            dst[k] = __builtin_amdgcn_raw_buffer_load_b128(abuf, aoff0 + k * astride, so, 0);
     };
+    auto loadA = [&](int t) __attribute__((always_inline)) { loadA_to(Ar, t); };
     auto loadW = [&](int t, int set) __attribute__((always_inline)) {
         t = min(t, T - 1);
-        Wq[set] = ld_u32x4(wrow + (size_t)(t >> 2) * kBlockBytes + 16 + 32 * (t & 3) + 16 * wh);
+        Wq[set] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, hoff + 16 * wh, (t >> 2) * kBlockBytes + 32 * (t & 3) + 16, 0);
     };
     // header of the super-block that step t opens (once per 4 steps)
     auto loadH = [&](int t) __attribute__((always_inline)) {
-        Hd = ld_u32x4(wrow + (size_t)(min(t, T - 1) >> 2) * kBlockBytes);
+        Hd = __builtin_amdgcn_raw_buffer_load_b128(wbuf, hoff, (min(t, T - 1) >> 2) * kBlockBytes, 0);
     };
 
     // step t -> LDS buffer: activations copied, weights dequantized
@@ -471,19 +486,23 @@ __global__ __launch_bounds__(G2Cfg::NT, 1) void gemm_q4k_f16_lds_kernel(
     // decoded once per super-block from its header (sub-block index
     // constant: no branches); d*sc and dmin*m are exact in f32 and the
     // factors are powers of two, so each is rounded to f16 once. The row's
-    // exponent e follows the running bound; the lane of each row's first
-    // piece publishes the rescale of the sums so far and C's scale.
+    // exponent follows the running bound; every piece lane of the row
+    // publishes the same rescale of the sums so far and C's scale (no
+    // branch), and a lane whose row changed e sets the flag (the others
+    // write the dummy slot).
     float bnd = 0.0f;  // max of 945|d| + 63|dmin| over the row's blocks so far
     int erow = 0;
     uint32_t scl[8];
     auto decode = [&]() __attribute__((always_inline)) {
         const float dh = half_bits_finite(Hd[0]), mh = half_bits_finite(Hd[0] >> 16);
+        const bool fresh = bnd == 0.0f;  // no nonzero block before this one
         bnd = fmaxf(bnd, fabsf(dh) * 945.0f + fabsf(mh) * 63.0f);
-        const int e = range_exp(bnd);
-        if (wh == 0) {
-            sF[wr] = ldexpf(1.0f, e - erow);
-            sE[wr] = ldexpf(1.0f, 20 - e);
-        }
+        const int tight = range_exp(bnd);
+        const int e = (fresh || tight < erow) ? tight - kRangeHeadroom : erow;
+        float *se = sE + wr;  // sF[wr] = se[BN]: one address for both
+        se[BN] = ldexpf(1.0f, e - erow);
+        se[0] = ldexpf(1.0f, 20 - e);
+        sFlag[e != erow ? 1 : 0] = 1;
         erow = e;
         const float d = dh * ldexpf(1.0f, e + 4);
         const float nm = -(mh * ldexpf(1.0f, e - 20));
@@ -524,32 +543,35 @@ __global__ __launch_bounds__(G2Cfg::NT, 1) void gemm_q4k_f16_lds_kernel(
     const int wn = (wave % WN) * (16 * TI), wm = (wave / WN) * (16 * TJ);
     const int l16 = lane & 15, q = lane >> 4;
     f32x4 acc[TI][TJ];
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // operands of one k half (32 of the step's 64): W rows first, then tokens,
-    // in the order the MFMAs below consume them
-    half8 wa[2][TI], tb[2][TJ];
-    auto readOps = [&](int buf, auto hc) __attribute__((always_inline)) {
+    // Operand registers: the token operands of both k halves (32 of the
+    // step's 64 k each), and one set of W operands: wa[i] is reread for the
+    // next half right after the four MFMAs that use it, so a half's MFMAs run
+    // while the next half's operands arrive without holding two W sets.
+    half8 wa[TI], tb[2][TJ];
+    auto readA = [&](int buf, auto hc) __attribute__((always_inline)) {
         constexpr int h = decltype(hc)::value;
-        const _Float16 *W_ = sW + buf * (BN * PITCH);
         const _Float16 *A_ = sA + buf * (BM * PITCH);
-        wa[h][0] = *reinterpret_cast<const half8 *>(&W_[(wn + l16) * PITCH + 32 * h + 8 * q]);
 #pragma unroll
         for (int j = 0; j < TJ; ++j)
             tb[h][j] = *reinterpret_cast<const half8 *>(&A_[(wm + 16 * j + l16) * PITCH + 32 * h + 8 * q]);
-#pragma unroll
-        for (int i = 1; i < TI; ++i)
-            wa[h][i] = *reinterpret_cast<const half8 *>(&W_[(wn + 16 * i + l16) * PITCH + 32 * h + 8 * q]);
     };
-    auto mfmaHalf = [&](auto hc) __attribute__((always_inline)) {
+    auto readW = [&](int buf, auto hc, int i) __attribute__((always_inline)) {
         constexpr int h = decltype(hc)::value;
+        const _Float16 *W_ = sW + buf * (BN * PITCH);
+        wa[i] = *reinterpret_cast<const half8 *>(&W_[(wn + 16 * i + l16) * PITCH + 32 * h + 8 * q]);
+    };
+    // MFMAs of half hc; the token operands of half rc from buffer rbuf first,
+    // then the W operands of that half, each after its last use here
+    auto halfStep = [&](auto hc, int rbuf, auto rc) __attribute__((always_inline)) {
+        constexpr int h = decltype(hc)::value;
+        readA(rbuf, rc);
 #pragma unroll
-        for (int i = 0; i < TI; ++i)
+        for (int i = 0; i < TI; ++i) {
 #pragma unroll
             for (int j = 0; j < TJ; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[h][i], tb[h][j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[i], tb[h][j], acc[i][j], 0, 0, 0);
+            readW(rbuf, rc, i);
+        }
     };
     using H0 = std::integral_constant<int, 0>;
     using H1 = std::integral_constant<int, 1>;
@@ -561,19 +583,32 @@ __global__ __launch_bounds__(G2Cfg::NT, 1) void gemm_q4k_f16_lds_kernel(
     // t = 2 mod 4, just before that block's first store. Loads past the last
     // step re-read it (clamped), so every load is unconditional and the load
     // counter waits only for the data it needs.
-    loadH(0);
+    // prologue: steps 0 and 1 of both operands in flight at once (the
+    // accumulators are not live yet)
+    u32x4 A1[APT];
     loadA(0);
-    loadW(0, 0);
-    loadW(1, 1);
-    decode();
+    loadA_to(A1, 1);
+    if (isW) {
+        loadH(0);
+        loadW(0, 0);
+        loadW(1, 1);
+        decode();
+        storeW(std::integral_constant<int, 0>{}, 0, 0);
+        loadW(2, 0);
+        storeW(std::integral_constant<int, 1>{}, 1, 1);
+        loadW(3, 1);
+    }
     storeA(0);
-    loadA(1);
-    storeW(std::integral_constant<int, 0>{}, 0, 0);
-    loadW(2, 0);
-    storeW(std::integral_constant<int, 1>{}, 1, 1);
-    loadW(3, 1);
+#pragma unroll
+    for (int k = 0; k < APT; ++k) Ar[k] = A1[k];
     __syncthreads();
-    readOps(0, H0{});
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    readA(0, H0{});
+#pragma unroll
+    for (int i = 0; i < TI; ++i) readW(0, H0{}, i);
     // One barrier per step, between its two k halves; step t's operands sit
     // in LDS buffer t & 1. Before the barrier: the first half's MFMAs
     // (operands read after the previous barrier), the second half's operand
@@ -590,15 +625,14 @@ __global__ __launch_bounds__(G2Cfg::NT, 1) void gemm_q4k_f16_lds_kernel(
         constexpr int P = PH & 1;                 // buffer of step t (and t+2)
         constexpr int NS = P ^ 1;                 // buffer of step t+1
         constexpr int NM = TI * TJ;               // MFMAs per half
-        readOps(P, H1{});
-        mfmaHalf(H0{});
+        halfStep(H0{}, P, H1{});
         storeA(NS);
         loadA(t + 2);
-        if constexpr (PH == 0) loadH(t + 4);
 #pragma unroll
         for (int i = 0; i < NM; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);                       // MFMA
-            if (i < TI + TJ) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);        // DS read
+            if (i < TJ) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);             // DS read (tokens)
+            if (i % TJ == TJ - 1) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);   // DS read (W)
             if (i >= 10 && i % 2 == 0 && i < 18) __builtin_amdgcn_sched_group_barrier(0x0200, 1, 0);  // DS write
             if (i >= 11 && i % 2 == 1) __builtin_amdgcn_sched_group_barrier(0x0020, 1, 0);  // VMEM read
             __builtin_amdgcn_sched_group_barrier(0x0002, 1, 0);                       // VALU
@@ -606,34 +640,37 @@ __global__ __launch_bounds__(G2Cfg::NT, 1) void gemm_q4k_f16_lds_kernel(
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
-        readOps(NS, H0{});
-        mfmaHalf(H1{});
-        // step t+2's weights open the next block at t = 2 mod 4: its scales
-        // replace this block's, whose last step (t+1) was stored one step ago
-        if constexpr (PH == 2) decode();
-        storeW(std::integral_constant<int, (PH + 2) & 3>{}, P, P);
-        loadW(t + 4, P);
-        // the block ends with this half: rescale the sums by the factors the
-        // next block's decode published (one step ago, before the barrier)
-        f32x4 fr[TI];
-        if constexpr (PH == 3) {
-#pragma unroll
-            for (int i = 0; i < TI; ++i) fr[i] = *reinterpret_cast<const f32x4 *>(&sF[wn + 16 * i + 4 * q]);
-        }
+        halfStep(H1{}, NS, H0{});
+        // the block ends with this half: the next block's decode (one step
+        // ago, before the barrier) flagged whether some row's e changed
+        int changed = 0;
+        if constexpr (PH == 3) changed = sFlag[1];
 #pragma unroll
         for (int i = 0; i < NM; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);                 // MFMA
-            if (i < TI + TJ + (PH == 3 ? TI : 0)) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);  // DS read
-            __builtin_amdgcn_sched_group_barrier(0x0002, PH == 2 ? 7 : 3, 0);     // VALU
-            if (i >= 10 && i % 2 == 1 && i < 18) __builtin_amdgcn_sched_group_barrier(0x0200, 1, 0);  // DS write
-            if (i == 18) __builtin_amdgcn_sched_group_barrier(0x0020, 1, 0);        // VMEM read
+            if (i < TJ + (PH == 3 ? 1 : 0)) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);  // DS read (tokens)
+            if (i % TJ == TJ - 1) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);  // DS read (W)
         }
         __builtin_amdgcn_sched_barrier(0);
+        if (isW) {
+            // step t+2's weights open the next block at t = 2 mod 4: its
+            // scales replace this block's, whose last step (t+1) was stored
+            // one step ago
+            if constexpr (PH == 2) decode();
+            storeW(std::integral_constant<int, (PH + 2) & 3>{}, P, P);
+            loadW(t + 4, P);
+            if constexpr (PH == 0) loadH(t + 4);
+        }
+        if constexpr (PH == 1) sFlag[1] = 0;  // read at step 3 mod 4, set at 2 mod 4
         if constexpr (PH == 3) {
+            if (__builtin_amdgcn_readfirstlane(changed)) {  // rare: rescale the sums so far
 #pragma unroll
-            for (int i = 0; i < TI; ++i)
+                for (int i = 0; i < TI; ++i) {
+                    const f32x4 fr = *reinterpret_cast<const f32x4 *>(&sF[wn + 16 * i + 4 * q]);
 #pragma unroll
-                for (int j = 0; j < TJ; ++j) acc[i][j] *= fr[i];
+                    for (int j = 0; j < TJ; ++j) acc[i][j] *= fr;
+                }
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -716,8 +753,10 @@ hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n,
     const long rounds2 = (tiles2 + cus2 - 1) / cus2;
     const bool lds_fits = 10L * m_tokens >= 9L * G2Cfg::BM * tm2 &&
                           (rounds2 == 1 ? 2 * tiles2 > cus2 : 20 * tiles2 >= 17 * rounds2 * cus2);
-    // the LDS kernel addresses A with 32-bit byte offsets
-    const bool a32 = (uint64_t)m_tokens * (uint64_t)bpr * kBlockElems * 2 <= 0xFFFFFFFFull;
+    // the LDS kernel addresses A (including a tile's token rows past
+    // m_tokens) and W with 32-bit byte offsets
+    const bool a32 = ((uint64_t)m_tokens + G2Cfg::BM) * (uint64_t)bpr * kBlockElems * 2 <= 0xFFFFFFFFull &&
+                     (uint64_t)n * (uint64_t)bpr * kBlockBytes <= 0xFFFFFFFFull;
     if (a32 && (big_env == 1 || (big_env < 0 && lds_fits)))
         return gemm_lds_launch(w, a, c, n, bpr, m_tokens, stream);
     // Tile height by the rows the busiest CU computes: ceil(tiles / #CUs) x
