@@ -3,11 +3,13 @@
 // No counterpart in the reference (its prefill is a per-token GEMV loop,
 // crates/modgrad-gemma/examples/gemma4_rocm.rs:26-34); each weight is the
 // canonical dequantized value (gguf.rs:364-404) times a per-row power of two
-// 2^e (row_range_exp: keeps every |weight| of the row below 2^15, so f16
-// neither overflows nor goes subnormal), with d*sc*2^e and dmin*m*2^e
-// rounded to f16 and the weight computed and rounded in f16; C is scaled
-// back by 2^-e exactly. (gemm_q4k_f16_lds_kernel applies one more fixed
-// power of two, 2^-20, to the weights and takes it back in C: see there.)
+// 2^e that keeps every |weight| of the row below 2^15, so f16 neither
+// overflows nor goes subnormal (gemm_q4k_f16_kernel: row_range_exp over all
+// of the row's blocks; gemm_q4k_f16_lds_kernel: a running exponent, see
+// there), with d*sc*2^e and dmin*m*2^e rounded to f16 and the weight
+// computed and rounded in f16; C is scaled back by 2^-e exactly.
+// (gemm_q4k_f16_lds_kernel applies one more fixed power of two, 2^-20, to
+// the weights and takes it back in C.)
 //
 // Two kernels: gemm_q4k_f16_lds_kernel (below), which dequantizes each W
 // element once per work-group into an f16 LDS tile, where its 160 x 256
@@ -359,14 +361,16 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint8_t *__r
 //
 // K step = 64 (one 32-byte qs group: sub-blocks 2G and 2G+1 of a
 // super-block). Per step the work-group loads 160 x 2 16-byte qs pieces and
-// 256 tokens x 128 B of activations into registers (weights three steps
-// ahead, activations two); a step's registers are written to a double-
+// 256 tokens x 128 B of activations into registers (weights two steps
+// before their store, activations one); they are written to a double-
 // buffered LDS stage (activations as they are, weights dequantized to f16
-// in natural k order), one barrier per step. Every wavefront runs the same
-// instruction stream: each dequantizes 40 of the step's 320 pieces (lanes
-// 40..63 repeat lanes 16..39: same data to the same address), and its MFMAs
-// are interleaved with that VALU work, its LDS stores and its global loads
-// (sched_group_barrier), so the matrix core and the VALU stay busy together.
+// in natural k order). The 320 pieces are exactly five wavefronts of one
+// piece per lane, so the first five wavefronts dequantize and no LDS store
+// repeats another (a store instruction costs the same whatever its active
+// lanes); all eight copy activations and compute. The barrier of each step
+// sits between its two k halves (see the pipeline below), and
+// sched_group_barrier interleaves each half's MFMAs with its LDS operand
+// reads, stores and loads.
 //
 // Range. Each W row carries a running power-of-two exponent e. Any e at or
 // below tight = range_exp(running max of 945|d| + 63|dmin| over the row's
