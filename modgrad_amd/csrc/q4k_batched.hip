@@ -76,12 +76,16 @@ __device__ __forceinline__ int split_exponent(float amax) {
     return e;
 }
 
-// grid (bpr, sets), 256 threads: thread = (batch b' = tid/32, 8-float chunk)
+// grid (bpr, sets), 256 threads: thread = (batch b' = tid/32, 8-float chunk
+// ch of block j). Every A-operand entry of the 8 k-slot groups holds one
+// aligned 8-float chunk of the block (its values in k-slot order
+// 0,2,1,3,4,6,5,7): entry (c, g) takes chunk 16(c>>2) + 8(g>>1) + 4(c&1) +
+// 2(g&1) + ((c>>1)&1) (bt_pair_offset), so the thread that loaded chunk ch
+// writes its two entries (xh and xl rows of its batch) from registers.
 __global__ __launch_bounds__(256) void batched_table_kernel(const float *__restrict__ X, int batch,
                                                             int bpr, int sets, bool x_aligned16,
                                                             uint8_t *__restrict__ ws,
                                                             float *__restrict__ yzero, int ytotal) {
-    __shared__ float xs[8][256];
     // Y = 0 ahead of a K-split main kernel (it adds its partials atomically)
     {
         const int nthr = (int)(gridDim.x * gridDim.y) * 256;
@@ -89,7 +93,6 @@ __global__ __launch_bounds__(256) void batched_table_kernel(const float *__restr
              i += nthr)
             yzero[i] = 0.0f;
     }
-    __shared__ float xsum[8][8];
     const int j = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
     const int bl = tid >> 5, ch = tid & 31, b = s * 8 + bl;
     const size_t K = (size_t)bpr * kBlockElems;
@@ -121,49 +124,50 @@ __global__ __launch_bounds__(256) void batched_table_kernel(const float *__restr
 #pragma unroll
     for (int off = 1; off < 32; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
     const int e = split_exponent(amax);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) xs[bl][ch * 8 + i] = ldexpf(v[i], e);
-    if ((ch & 3) == 0) xsum[bl][ch >> 2] = sum;
     float *meta = reinterpret_cast<float *>(ws + batched_ws(bpr, sets).meta);
     const size_t js = (size_t)j * sets + s;
     if (ch == 0) meta[(js * 8 + bl) * 2] = ldexpf(1.0f, 20 - e);
-    __syncthreads();
 
-    // k-slot groups: entry (c, lane), lane = (m = 2b' + part, g); slot q
-    // holds qs byte o + {0,2,1,3,4,6,5,7}[q] with o = bt_pair_offset(c/2, g),
-    // i.e. block position 64*(o/32) + 32*(c%2) + o%32 + ...
+    // the two entries of chunk ch: k-slot group c, lanes (m = 2b' + part, g)
     uint8_t *atab = ws + js * kBatchOps * 1024;
-    for (int E = tid; E < 8 * 64; E += 256) {
-        const int c = E >> 6, lane = E & 63, m = lane & 15, g = lane >> 4;
-        const int bb = m >> 1, part = m & 1;
-        const int o = bt_pair_offset(c >> 1, g);
-        const int pos0 = 64 * (o >> 5) + 32 * (c & 1) + (o & 31);
+    {
+        const int c = (((ch >> 4) & 1) << 2) | ((ch & 1) << 1) | ((ch >> 2) & 1);
+        const int g = (((ch >> 3) & 1) << 1) | ((ch >> 1) & 1);
         constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
-        half8 out;
+        half8 hi, lo;
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            const float xv = xs[bb][pos0 + perm[q]];
+            const float xv = ldexpf(v[perm[q]], e);
             const _Float16 h = (_Float16)xv;
-            out[q] = part ? (_Float16)(xv - (float)h) : h;
+            hi[q] = h;
+            lo[q] = (_Float16)(xv - (float)h);
         }
-        *reinterpret_cast<half8 *>(atab + (size_t)c * 1024 + lane * 16) = out;
+        uint8_t *dst = atab + (size_t)c * 1024 + (size_t)(2 * bl + 16 * g) * 16;
+        *reinterpret_cast<half8 *>(dst) = hi;
+        *reinterpret_cast<half8 *>(dst + 16) = lo;
     }
-    // sub-block sums: lanes (m, g = 0) hold xsum[b'][0..7], other lanes zero
-    if (tid < 64) {
-        const int lane = tid, m = lane & 15, g = lane >> 4, bb = m >> 1, part = m & 1;
+    // sub-block-sum operand: lanes (m = 2b' + part, g = 0) hold the 8 sums of
+    // batch b', lanes with g != 0 zero; thread ch < 8 of batch b' writes
+    // lane (2b' + (ch & 1)) + 16 (ch >> 1). Sum q sits in lanes 4q..4q+3 of
+    // the batch's 32.
+    float sq[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) sq[q] = __shfl(sum, (tid & 32) + 4 * q, 64);
+    if (ch < 8) {
+        const int part = ch & 1, g = ch >> 1;
         float smax = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) smax = fmaxf(smax, fabsf(xsum[bb][q]));
+        for (int q = 0; q < 8; ++q) smax = fmaxf(smax, fabsf(sq[q]));
         const int es = split_exponent(smax);
         half8 out;
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            const float xv = ldexpf(xsum[bb][q], es);
+            const float xv = ldexpf(sq[q], es);
             const _Float16 h = (_Float16)xv;
             out[q] = g != 0 ? (_Float16)0.0f : (part ? (_Float16)(xv - (float)h) : h);
         }
-        *reinterpret_cast<half8 *>(atab + (size_t)8 * 1024 + lane * 16) = out;
-        if (g == 0 && part == 0) meta[(js * 8 + bb) * 2 + 1] = ldexpf(1.0f, -es);
+        *reinterpret_cast<half8 *>(atab + (size_t)8 * 1024 + (size_t)(2 * bl + part + 16 * g) * 16) = out;
+        if (g == 0 && part == 0) meta[(js * 8 + bl) * 2 + 1] = ldexpf(1.0f, -es);
     }
 }
 
