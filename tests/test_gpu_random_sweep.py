@@ -5,7 +5,8 @@ purpose; this sweep draws them at random (a fixed seed, so the same cases run
 every time) to reach the combinations nobody picked: ragged row groups and
 stages, the persistent schedules at odd group counts, weights at every byte
 offset, activations 4 bytes past 16-byte alignment, and batch sizes between
-the powers of two. Gates are the BASELINE ones (per row |y - y_f64| <=
+the powers of two; and the same for the Q5_K / Q6_K matvecs and the
+RMSNorm / GLU-fused Q4_K matvecs. Gates are the BASELINE ones (per row |y - y_f64| <=
 1e-4 * sum_k |w_rk||x_k|; the f16 GEMM at the tolerance of its own tests).
 """
 import numpy as np
@@ -140,3 +141,78 @@ def test_random_flat_layout(L, orc, n, k):
                L.launch_matvec_q4k_ex(ptr(wt), ptr(xt), ptr(yt), n, k, _lib.LAYOUT_FLAT, None))
     y_ref, a = orc.gemv_flat(w, x, n, k)
     assert_gemv_close(host(yt), y_ref, a)
+
+
+def _more_cases():
+    rng = np.random.default_rng(0x5EED2027)
+    kq, glu = [], []
+    while len(kq) < 24:  # Q5_K / Q6_K: both kernel families, K up to 100 blocks
+        fmt = 176 if len(kq) % 2 else 210
+        n = int(np.exp(rng.uniform(0, np.log(30000)))) if len(kq) % 3 else int(rng.integers(4000, 30001))
+        bpr = int(rng.integers(1, 101)) if len(kq) % 4 else int(rng.integers(1, 15))
+        if n * bpr <= 200_000:
+            kq.append((fmt, n, bpr))
+    while len(glu) < 12:  # fused RMSNorm and/or GLU on the Q4_K matvec
+        n = int(np.exp(rng.uniform(0, np.log(20000))))
+        bpr = int(rng.integers(1, 30))
+        if n * bpr <= 150_000:
+            g, nm = int(rng.integers(0, 2)), int(rng.integers(0, 2))
+            glu.append((n, bpr, g, nm if g else 1, int(rng.integers(0, 2))))
+    return kq, glu
+
+
+KQUANT, GLU = _more_cases()
+
+
+@pytest.mark.parametrize("fmt,n,bpr", KQUANT)
+def test_random_kquant_matvec(L, orc, fmt, n, bpr):
+    from tests.gpu_util import random_kquant_bytes
+    note(f"sweep {'q5k' if fmt == 176 else 'q6k'} n={n} bpr={bpr}")
+    rng = np.random.default_rng(fmt * 7919 + n * 3 + bpr)
+    w = random_kquant_bytes(rng, n * bpr, fmt)
+    x = rng.standard_normal(bpr * 256).astype(np.float32)
+    wt, xt, yt = dev(w), dev(x), empty_f32(n)
+    fn = L.launch_matvec_q5k if fmt == 176 else L.launch_matvec_q6k
+    _lib.check("kquant", fn(ptr(wt), ptr(xt), ptr(yt), n, bpr))
+    y_ref, a = orc.gemv_kquant(fmt, w, x, n, bpr)
+    assert_gemv_close(host(yt), y_ref, a)
+
+
+@pytest.mark.parametrize("n,bpr,glu,norm,act", GLU)
+def test_random_fused_matvec(L, orc, n, bpr, glu, norm, act):
+    """RMSNorm-fused matvec, or the gate/up matvec with its GLU (with or
+    without the norm), against norm -> matvec(s) -> activation in the oracle."""
+    note(f"sweep fused n={n} bpr={bpr} glu={glu} norm={norm} act={act}")
+    rng = np.random.default_rng(n * 5 + bpr * 11 + 2 * glu + norm)
+    k = bpr * 256
+    wg = random_q4k_bytes(rng, n * bpr)
+    wu = random_q4k_bytes(rng, n * bpr)
+    x = (1.3 * rng.standard_normal(k)).astype(np.float32)
+    nw = (0.5 * rng.standard_normal(k) + 1.0).astype(np.float32)
+    eps = 1e-5
+    wgt, wut, xt, nt, yt = dev(wg), dev(wu), dev(x), dev(nw), empty_f32(n)
+    xn = orc.rms_norm(x, nw, 1, k, eps) if norm else x
+    if not glu:
+        _lib.check("norm matvec", L.launch_matvec_q4k_rmsnorm_ex(ptr(wgt), ptr(xt), ptr(nt), eps,
+                                                                 ptr(yt), n, bpr, None))
+        y_ref, A = orc.gemv(wg, xn, n, bpr)
+        assert_gemv_close(host(yt), y_ref, A)
+        return
+    _lib.check("glu matvec", L.launch_matvec_q4k_glu_ex(ptr(wgt), ptr(wut), ptr(xt),
+                                                        ptr(nt) if norm else None, eps, act,
+                                                        ptr(yt), n, bpr, None))
+    y = host(yt).astype(np.float64)
+    g, Ag = orc.gemv(wg, xn, n, bpr)
+    u, Au = orc.gemv(wu, xn, n, bpr)
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    if act == 0:
+        a = 0.5 * g64 * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (g64 + 0.044715 * g64 ** 3)))
+    else:
+        a = g64 / (1.0 + np.exp(-g64))
+    ref = a * u64
+    # the glue tests' bound: the activation's slope (at most 1.13) carries the
+    # gate's matvec error, |a| the up matvec's
+    bound = 1e-4 * (1.13 * Ag * np.abs(u64) + np.abs(a) * Au) + 1e-5 * np.abs(ref) + 1e-30
+    err = np.abs(y - ref)
+    bad = np.nonzero(~(err <= bound))[0]
+    assert bad.size == 0, (bad[:5].tolist(), err[bad[:5]].tolist(), bound[bad[:5]].tolist())
