@@ -6,7 +6,8 @@ every time) to reach the combinations nobody picked: ragged row groups and
 stages, the persistent schedules at odd group counts, weights at every byte
 offset, activations 4 bytes past 16-byte alignment, and batch sizes between
 the powers of two; and the same for the Q5_K / Q6_K matvecs and the
-RMSNorm / GLU-fused Q4_K matvecs. Gates are the BASELINE ones (per row |y - y_f64| <=
+RMSNorm / GLU-fused Q4_K matvecs, and the Q8_1 quantizer + dp4a matvec.
+Gates are the BASELINE ones (per row |y - y_f64| <=
 1e-4 * sum_k |w_rk||x_k|; the f16 GEMM at the tolerance of its own tests).
 """
 import numpy as np
@@ -216,3 +217,42 @@ def test_random_fused_matvec(L, orc, n, bpr, glu, norm, act):
     err = np.abs(y - ref)
     bad = np.nonzero(~(err <= bound))[0]
     assert bad.size == 0, (bad[:5].tolist(), err[bad[:5]].tolist(), bound[bad[:5]].tolist())
+
+
+def _dp4a_cases():
+    rng = np.random.default_rng(0x5EED2028)
+    out = []
+    while len(out) < 16:  # Q8_1 activations, weights at any byte offset
+        n = int(np.exp(rng.uniform(0, np.log(40000)))) if len(out) % 2 else int(rng.integers(4000, 40001))
+        bpr = int(rng.integers(1, 81)) if len(out) % 3 else int(rng.integers(1, 15))
+        if n * bpr <= 250_000:
+            out.append((n, bpr, int(rng.integers(0, 16))))
+    return out
+
+
+DP4A = _dp4a_cases()
+
+
+@pytest.mark.parametrize("n,bpr,woff", DP4A)
+def test_random_dp4a_matvec(L, orc, n, bpr, woff):
+    """quantize_q8_1 bit-exact, then the dp4a matvec against the oracle's f64
+    evaluation of the same formula (the dp4a tests' bound)."""
+    note(f"sweep dp4a n={n} bpr={bpr} w+{woff}")
+    rng = np.random.default_rng(n * 13 + bpr * 5 + woff)
+    w = random_q4k_bytes(rng, n * bpr)
+    x = rng.standard_normal(bpr * 256).astype(np.float32)
+    nsub = x.size // 32
+    xt = dev(x)
+    xq, xd, xs = filled_u8(nsub * 32 + 64, 0x5A), empty_f32(nsub + 4), empty_f32(nsub + 4)
+    _lib.check("quantize_q8_1", L.launch_quantize_q8_1(ptr(xt), ptr(xq), ptr(xd), ptr(xs), x.size))
+    q, d, s = host(xq)[:nsub * 32].view(np.int8), host(xd)[:nsub], host(xs)[:nsub]
+    rq, rd, rs = orc.quantize_q8_1(x)
+    assert np.array_equal(q, rq) and np.array_equal(d.view(np.uint32), rd.view(np.uint32))
+    assert np.array_equal(s, rs)
+    wt, yt = dev(np.concatenate([np.zeros(woff, np.uint8), w])), empty_f32(n)
+    _lib.check("dp4a", L.launch_matvec_q4k_dp4a(ptr(wt) + woff, ptr(xq), ptr(xd), ptr(xs), ptr(yt),
+                                                n, bpr))
+    y_ref, absterm = orc.gemv_dp4a(w, q, d, s, n, bpr)
+    err = np.abs(host(yt).astype(np.float64) - y_ref)
+    bad = np.nonzero(~(err <= 1e-5 * absterm + 1e-30))[0]
+    assert bad.size == 0, (bad[:5].tolist(), err[bad[:5]].tolist(), absterm[bad[:5]].tolist())
