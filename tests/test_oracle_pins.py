@@ -184,6 +184,30 @@ def test_quantize_constant_closed_form(orc):
     assert q.tobytes() == want
 
 
+def test_quantize_ties_round_half_away_from_zero(orc):
+    # gguf.rs:549-559 rounds scales and nibbles with f32::round, which takes
+    # an exact half away from zero; rint (half to even) differs at every even
+    # k + 0.5. Sub-block 0 (legacy positions 0..31) has max 945/1024, so its
+    # local d is 63*2^-10, the super-block d is 2^-10 (f16 0x1400), its scale
+    # 63 and d1 = 63*2^-10; x = t*d1 then quantizes from exactly t. Sub-block
+    # 1 (positions 128..159) has local d = 41*2^-11, i.e. scale exactly 20.5.
+    d1 = 63.0 / 1024.0
+    ties = [0.5, 1.5, 2.5, 4.5, 6.5, 14.5]
+    x = np.zeros(256, np.float32)
+    x[0] = np.float32(945.0 / 1024.0)
+    for i, t in enumerate(ties):
+        x[1 + i] = np.float32(t * d1)
+        assert float(x[1 + i]) / d1 == t  # exact in f32
+    x[128] = np.float32(615.0 / 2048.0)
+    q = orc.quantize(x)
+    assert q[0:4].tobytes() == struct.pack("<HH", 0x1400, 0)
+    nib = q[16:48] & 15
+    assert nib[0] == 15
+    assert list(nib[1:1 + len(ties)]) == [1, 2, 3, 5, 7, 15]  # half to even: 0, 2, 2, 4, 6, 14
+    assert orc.get_scale_min_k4(0, q[4:16].tobytes()) == (63, 0)
+    assert orc.get_scale_min_k4(1, q[4:16].tobytes()) == (21, 0)  # half to even: 20
+
+
 def test_quantize_uses_legacy_subblock_order(orc):
     # Sub-block is (legacy positions OFFS[is]..+32) holds the constant 0.1*(is+1):
     # its scale must then grow with is like 63*(is+1)/8. A quantizer using the
