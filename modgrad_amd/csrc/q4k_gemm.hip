@@ -761,7 +761,10 @@ hipError_t gemm_f16_launch(const uint8_t *w, const uint16_t *a, float *c, int n,
     // m_tokens) and W with 32-bit byte offsets
     const bool a32 = ((uint64_t)m_tokens + G2Cfg::BM) * (uint64_t)bpr * kBlockElems * 2 <= 0xFFFFFFFFull &&
                      (uint64_t)n * (uint64_t)bpr * kBlockBytes <= 0xFFFFFFFFull;
-    if (a32 && (big_env == 1 || (big_env < 0 && lds_fits)))
+    // its buffer_load_b128 reads assume 16-byte aligned W and A; the
+    // 128/160-token kernel below reads both through alignment-1 global loads
+    const bool aligned16 = (((uintptr_t)w | (uintptr_t)a) & 15u) == 0;
+    if (a32 && aligned16 && (big_env == 1 || (big_env < 0 && lds_fits)))
         return gemm_lds_launch(w, a, c, n, bpr, m_tokens, stream);
     // Tile height by the rows the busiest CU computes: ceil(tiles / #CUs) x
     // BN, the lower one, ties to 160 (a second resident tile on a CU adds

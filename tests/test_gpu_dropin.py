@@ -213,6 +213,28 @@ def test_gemm_operands_at_offsets(L, orc, woff, aoff):
     assert np.linalg.norm(C - C_ref) <= 1e-3 * np.linalg.norm(C_ref)
 
 
+@pytest.mark.parametrize("n,bpr,m,woff,aoff", [(32000, 1, 256, 1, 2), (32000, 1, 256, 12, 6),
+                                                (20000, 14, 512, 1, 2), (20000, 14, 512, 12, 6),
+                                                (20000, 14, 512, 0, 8)])
+def test_gemm_prefill_shapes_at_offsets(L, orc, n, bpr, m, woff, aoff):
+    # Shapes that take the LDS-dequant kernel when W and A are 16-byte
+    # aligned; misaligned operands must still give the oracle's result.
+    note(f"gemm prefill-sized n={n} bpr={bpr} m={m}, w offset {woff}, A offset {aoff}")
+    rng = np.random.default_rng(n + 7 * m + woff + 131 * aoff)
+    w = random_q4k_bytes(rng, n * bpr)
+    a = rng.standard_normal((m, bpr * 256)).astype(np.float16)
+    wt, wp = at_offset(w, woff)
+    at, ap = at_offset(a.view(np.uint16), aoff)
+    ct = empty_f32(m * n)
+    _lib.check("gemm", L.launch_gemm_q4k_f16(wp, ap, ptr(ct), n, bpr, m, None))
+    rows = np.sort(rng.choice(n, size=256, replace=False))
+    C = host(ct).reshape(m, n)[:, rows]
+    C_ref, A = orc.gemm_f16(w, a.view(np.uint16), n, bpr, rows=rows)
+    k = bpr * 256
+    assert np.all(np.abs(C - C_ref) <= 1e-2 * A / np.sqrt(k))
+    assert np.linalg.norm(C - C_ref) <= 1e-3 * np.linalg.norm(C_ref)
+
+
 @pytest.mark.parametrize("fmt,off", [(176, 1), (176, 4), (210, 2), (210, 3)])
 def test_kquant_weights_at_offsets(L, orc, fmt, off):
     # Q5_K on the Q4_K matrix-core kernel's Q5_K mode, Q6_K on the staged
