@@ -34,6 +34,43 @@ def test_noalloc_rejects_shapes_beyond_the_scratch():
     assert fn(FAKE, FAKE + 2, FAKE, 16, 14, 8, None) == _lib.hipErrorInvalidValue
 
 
+@pytest.mark.gpu
+def test_noalloc_under_graph_capture(orc):
+    # The process's first noalloc call (no mgq_prepare before it; this test
+    # runs before the ones that call it) is made inside a torch.cuda.graph
+    # capture, so the scratch lookup happens mid-capture. The graph then
+    # holds the fixed scratch address: three replays with new X contents,
+    # each followed by eager work of the program (the workspace entry point
+    # on the same X), must give the workspace entry point's bits.
+    import torch
+    L = _lib.load()
+    n, bpr, batch = 1000, 14, 8
+    w = orc.seeded_weight(41, n, bpr * 256)
+    wt = dev(w)
+    Xt = torch.zeros(batch * bpr * 256, dtype=torch.float32, device="cuda")
+    Y_g, Y_ws = empty_f32(batch * n), empty_f32(batch * n)
+    nws = L.mgq_batched_workspace_bytes(bpr, batch)
+    ws = filled_u8(nws, 0x55)
+    note(f"noalloc captured in a graph: n={n} bpr={bpr} B={batch}")
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    with torch.cuda.graph(g, stream=side):
+        rc = L.launch_matvec_q4k_batched_noalloc(ptr(wt), ptr(Xt), ptr(Y_g), n, bpr, batch,
+                                                 torch.cuda.current_stream().cuda_stream)
+    _lib.check("batched_noalloc (captured)", rc)
+    for rep in range(3):
+        X = orc.normal(4100 + rep, batch * bpr * 256)
+        Xt.copy_(torch.from_numpy(X))
+        Y_g.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        _lib.check("batched", L.launch_matvec_q4k_batched(ptr(wt), ptr(Xt), ptr(Y_ws), n, bpr,
+                                                          batch, ptr(ws), nws, None))
+        a, b = host(Y_ws), host(Y_g)
+        assert np.all(np.isfinite(a))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"replay {rep}"
+
+
 def run_pair(L, orc, n, bpr, batch, seed):
     w = orc.seeded_weight(seed, n, bpr * 256)
     X = orc.normal(seed + 1, batch * bpr * 256).reshape(batch, -1)
