@@ -422,10 +422,7 @@ static hipError_t batched_main_launch(const uint8_t *w, const uint8_t *ws, float
     constexpr int BP = 8 * SETS;
     constexpr size_t base = (size_t)R * ((9 * 8) | 1) * 16 + 2 * (size_t)8 * R * BP * 4;
     const long groups = (n + R - 1) / R;
-    int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)kern, 512,
-                                                     base + 8 * R * BP * 4) != hipSuccess || occ <= 0)
-        occ = 1;
+    const int occ = occupancy_cached((const void *)kern, 512, base + 8 * R * BP * 4, 1);
     const long maxgrid = (long)device_cus() * occ;
     const long rounds = (groups + maxgrid - 1) / maxgrid;
     const long grid = (groups + rounds - 1) / rounds;

@@ -813,10 +813,9 @@ static hipError_t launch_xit(const uint8_t *w, const GemvAct &a, const GemvFuse 
     if (persistent) {
         static const int occ_env = env_int("MGQ_GEMV_OCC", 0);
         const size_t base = mfma_layout(bpr, R, C, NW, 8, DB, Q8, FUSE).total;
-        int occ = 0;  // resident work-groups per CU (registers and LDS)
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)kern, NW * 64,
-                                                         base) != hipSuccess || occ <= 0)
-            occ = (int)std::min<size_t>(4, (160 * 1024) / base);
+        // resident work-groups per CU (registers and LDS)
+        int occ = occupancy_cached((const void *)kern, NW * 64, base,
+                                   (int)std::min<size_t>(4, (160 * 1024) / base));
         if (occ_env > 0) occ = occ_env;
         const PersistPlan p = persistent_plan(groups, occ);
         grid = p.grid;
@@ -901,6 +900,7 @@ hipError_t gemv_prepare() {
     if (e == hipSuccess) e = prepare_fuse<kFuseNorm>();
     if (e == hipSuccess) e = prepare_fuse<kFuseGlu>();
     if (e == hipSuccess) e = prepare_fuse<kFuseNorm | kFuseGlu>();
+    if (e == hipSuccess) e = q6k_prepare();
     return e;
 }
 

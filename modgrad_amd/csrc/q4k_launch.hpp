@@ -9,6 +9,9 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdlib>
+#include <map>
+#include <mutex>
+#include <tuple>
 
 namespace mgq {
 
@@ -27,6 +30,30 @@ inline int device_cus() {
     return cus[dev];
 }
 
+// Resident work-groups per CU of `kern` at `threads` threads and `lds` bytes
+// of dynamic LDS on the current device, from the runtime's occupancy query,
+// or `dflt` when the query fails. Cached per (kernel, device, threads, lds):
+// the runtime is asked once per shape class, not on every launch (the
+// reference's engine launches every matvec eagerly, 113+ per token).
+inline int occupancy_cached(const void *kern, int threads, size_t lds, int dflt) {
+    static std::mutex mu;
+    static std::map<std::tuple<const void *, int, int, size_t>, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return dflt;
+    const auto key = std::make_tuple(kern, dev, threads, lds);
+    {
+        std::lock_guard<std::mutex> g(mu);
+        const auto it = cache.find(key);
+        if (it != cache.end()) return it->second;
+    }
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, threads, lds) != hipSuccess || occ <= 0)
+        occ = dflt;
+    std::lock_guard<std::mutex> g(mu);
+    cache.emplace(key, occ);
+    return occ;
+}
+
 // Allows `kern` the whole 160 KiB of gfx950 LDS. The attribute belongs to the
 // current device, so it is set once per (kernel, device); `state` is the
 // call site's per-device record (0 = not yet set, else hipError_t + 1).
@@ -39,6 +66,22 @@ inline hipError_t allow_full_lds(const void *kern, std::atomic<int> (&state)[64]
         state[dev].store(s, std::memory_order_release);
     }
     return (hipError_t)(s - 1);
+}
+
+// allow_full_lds for kernels told apart by address only (instances of one
+// signature): the per-device state is kept per kernel in a map.
+inline hipError_t allow_full_lds_by_addr(const void *kern) {
+    static std::mutex mu;
+    static std::map<std::pair<const void *, int>, hipError_t> done;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> g(mu);
+    const auto key = std::make_pair(kern, dev);
+    const auto it = done.find(key);
+    if (it != done.end()) return it->second;
+    const hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    done.emplace(key, e);
+    return e;
 }
 
 // Row-group schedule of a persistent launch (G = gridDim.x work-groups). In
@@ -125,8 +168,11 @@ hipError_t gemv_flat_launch(const uint8_t *w, const float *x, float *y, int n, i
 hipError_t gemv_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                             hipStream_t stream);
 
-// One-time kernel attribute setup (dynamic LDS limit); safe to call often.
+// One-time kernel attribute setup (dynamic LDS limit) of the GEMV kernels,
+// the Q6_K kernels included; safe to call often.
 hipError_t gemv_prepare();
+// The Q6_K matrix-core kernels' LDS attributes and occupancy (q4k_q6k_mfma.hip).
+hipError_t q6k_prepare();
 
 // Looks up the current device's address of the no-allocation entry point's
 // fixed scratch array (once per device).

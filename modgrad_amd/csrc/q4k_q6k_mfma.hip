@@ -430,24 +430,27 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_mfma_long_kernel(const uint8
 
 namespace {
 
+// LDS attribute and occupancy of `kern` for rows of up to `probe_bpr` blocks
+// on the current device (both cached: only the first call per device asks
+// the runtime).
+template <typename K>
+hipError_t q6m_setup(K kern, bool chunked, int nw, int probe_bpr, int *occ) {
+    using namespace q6m;
+    const hipError_t attr = allow_full_lds_by_addr((const void *)kern);
+    if (attr != hipSuccess) return attr;
+    *occ = occupancy_cached((const void *)kern, nw * 64, q6m_layout(probe_bpr, 32, chunked, nw).total, 1);
+    return hipSuccess;
+}
 
-// Persistent launch of `kern` with the occupancy at `probe_lds` bytes
+// Persistent launch of `kern` with the occupancy at `probe_bpr` blocks per row
 // (persistent_plan: balanced, or age-skewed for pairs of work-groups per CU).
 template <typename K, typename... Extra>
 hipError_t q6m_launch(K kern, bool chunked, int nw, const uint8_t *w, const float *x, float *y,
-                      int n, int bpr, int probe_bpr, int &occ, hipError_t &attr,
-                      hipStream_t stream, Extra... extra) {
+                      int n, int bpr, int probe_bpr, hipStream_t stream, Extra... extra) {
     using namespace q6m;
+    int occ = 1;
+    const hipError_t attr = q6m_setup(kern, chunked, nw, probe_bpr, &occ);
     if (attr != hipSuccess) return attr;
-    if (occ == 0) {
-        int o = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, (const void *)kern, nw * 64,
-                                                         q6m_layout(probe_bpr, 32, chunked, nw).total) !=
-                hipSuccess ||
-            o <= 0)
-            o = 1;
-        occ = o;
-    }
     const PersistPlan p = persistent_plan((n + R - 1) / R, occ);
     const size_t lds = q6m_layout(bpr, (int)p.rounds, chunked, nw).total;
     if (lds > 160 * 1024) return hipErrorNotSupported;
@@ -455,19 +458,41 @@ hipError_t q6m_launch(K kern, bool chunked, int nw, const uint8_t *w, const floa
     return hipGetLastError();
 }
 
+// rows of the long (K-chunked) kernel with XI table items per thread: at most
+template <int NW, int XI>
+constexpr int q6m_long_probe() { return std::min(XI * NW * 64 / 32, 100); }
+
 template <int NW, int XI>
 hipError_t q6m_long_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                            hipStream_t stream) {
-    static std::atomic<int> lds_state[64];
-    hipError_t attr = allow_full_lds((const void *)gemv_q6k_mfma_long_kernel<NW, XI>, lds_state);
-    static int occ = 0;
     // occupancy at the largest row this instance serves
-    const int probe = std::min(XI * NW * 64 / 32, 100);
-    return q6m_launch(gemv_q6k_mfma_long_kernel<NW, XI>, true, NW, w, x, y, n, bpr, probe, occ,
-                      attr, stream);
+    return q6m_launch(gemv_q6k_mfma_long_kernel<NW, XI>, true, NW, w, x, y, n, bpr,
+                      q6m_long_probe<NW, XI>(), stream);
+}
+
+template <int NW, int XI>
+hipError_t q6m_long_setup() {
+    int occ = 0;
+    return q6m_setup(gemv_q6k_mfma_long_kernel<NW, XI>, true, NW, q6m_long_probe<NW, XI>(), &occ);
 }
 
 }  // namespace
+
+// Sets every Q6_K matrix-core kernel's LDS attribute and caches its occupancy
+// on the current device, so that no launcher makes those runtime calls later
+// (e.g. inside a stream capture).
+hipError_t q6k_prepare() {
+    using namespace q6m;
+    int occ = 0;
+    hipError_t e = q6m_setup(gemv_q6k_mfma_kernel<false>, false, NW, MAX_BPR, &occ);
+    if (e == hipSuccess) e = q6m_setup(gemv_q6k_mfma_kernel<true>, false, NW, MAX_BPR, &occ);
+    if (e == hipSuccess) e = q6m_long_setup<LONG_NW, 1>();
+    if (e == hipSuccess) e = q6m_long_setup<LONG_NW, 2>();
+    if (e == hipSuccess) e = q6m_long_setup<LONG_NW, 4>();
+    if (e == hipSuccess) e = q6m_long_setup<LONG_NW, 6>();
+    if (e == hipSuccess) e = q6m_long_setup<LONG_NW, 8>();
+    return e;
+}
 
 hipError_t gemv_q6k_mfma_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
                                 hipStream_t stream) {
@@ -476,13 +501,9 @@ hipError_t gemv_q6k_mfma_launch(const uint8_t *w, const float *x, float *y, int 
     // a tensor size that is a multiple of 16 (x needs only float alignment)
     if (((uintptr_t)w & 15u) || (((long)n * bpr * BB) % 16))
         return hipErrorNotSupported;
-    if (bpr <= MAX_BPR) {
-        static std::atomic<int> lds_state[64];
-        hipError_t attr = allow_full_lds((const void *)gemv_q6k_mfma_kernel<false>, lds_state);
-        static int occ = 0;
-        return q6m_launch(gemv_q6k_mfma_kernel<false>, false, NW, w, x, y, n, bpr, MAX_BPR, occ, attr,
-                          stream, (const float *)nullptr, 0.0f);
-    }
+    if (bpr <= MAX_BPR)
+        return q6m_launch(gemv_q6k_mfma_kernel<false>, false, NW, w, x, y, n, bpr, MAX_BPR, stream,
+                          (const float *)nullptr, 0.0f);
     constexpr int LNW = LONG_NW, LNT = LNW * 64;
     const int need = (bpr * 32 + LNT - 1) / LNT;  // table items per thread
     if (need <= 1) return q6m_long_launch<LNW, 1>(w, x, y, n, bpr, stream);
@@ -501,11 +522,8 @@ hipError_t gemv_q6k_mfma_norm_launch(const uint8_t *w, const float *x, const flo
     // the output matrix)
     if (((uintptr_t)w & 15u) || (((long)n * bpr * BB) % 16) || bpr > MAX_BPR)
         return hipErrorNotSupported;
-    static std::atomic<int> lds_state[64];
-    hipError_t attr = allow_full_lds((const void *)gemv_q6k_mfma_kernel<true>, lds_state);
-    static int occ = 0;
-    return q6m_launch(gemv_q6k_mfma_kernel<true>, false, NW, w, x, y, n, bpr, MAX_BPR, occ, attr,
-                      stream, nw, eps);
+    return q6m_launch(gemv_q6k_mfma_kernel<true>, false, NW, w, x, y, n, bpr, MAX_BPR, stream, nw,
+                      eps);
 }
 
 }  // namespace mgq
