@@ -93,7 +93,7 @@ class Workload:
         self.weight_bytes = sum(w.numel() for _, w, _, _, _, _ in self.launches)
 
 
-CHAIN_MODES = {"auto": 0, "graph": 1, "persistent": 2}
+CHAIN_MODES = {"auto": 0, "graph": 1, "persistent": 2, "eager": 3}
 
 
 def time_graph(torch, q4k, wl: Workload, steps: int, warmup: int, mode: str = "auto"):
@@ -128,6 +128,67 @@ def time_graph(torch, q4k, wl: Workload, steps: int, warmup: int, mode: str = "a
     if faults:
         raise RuntimeError("the persistent chain reported a timed-out grid-wide wait")
     return ms, spread, impl
+
+
+def time_eager(torch, q4k, wl: Workload, steps: int, warmup: int):
+    """The reference engine's calling pattern (rocm_gemma.rs:312-345,
+    rocm.rs:951-953): every matvec launched by launch_matvec_q4k_ex on the
+    null stream (an MGQ_CHAIN_EAGER chain enqueues them one by one, with no
+    Python between them), then one device synchronize per step. Returns ms per
+    step (host wall clock, the synchronize included), its spread, and the host
+    microseconds per launch call (the enqueue loop alone)."""
+    chain = q4k.Chain([(w.data_ptr(), x.data_ptr(), y.data_ptr(), n, k // BLOCK_ELEMS)
+                       for _, w, x, y, n, k in wl.launches], CHAIN_MODES["eager"])
+    assert chain.mode() == CHAIN_MODES["eager"]
+    t_end = time.perf_counter() + WARM_MS * 1e-3
+    for i in range(max(1, warmup)):
+        chain.launch(None)
+        torch.cuda.synchronize()
+    while time.perf_counter() < t_end:
+        chain.launch(None)
+        torch.cuda.synchronize()
+    host, per = [], []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        a = time.perf_counter()
+        chain.launch(None)
+        b = time.perf_counter()
+        torch.cuda.synchronize()
+        host.append(b - a)
+        per.append(time.perf_counter() - a)
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    chain.close()
+    host_us = float(np.median(host)) * 1e6 / len(wl.launches)
+    return ms, _spread(np.array(per) * 1e3), host_us
+
+
+def shape_times(torch, q4k, wl: Workload, reps: int = 20) -> dict:
+    """us per launch of each launch shape of the step, measured after the
+    timed region: the step's launches of one shape (their own weights and
+    activations) as one graph chain, replayed `reps` times between events."""
+    groups = {}
+    for i, (name, _, _, _, n, k) in enumerate(wl.launches):
+        groups.setdefault(name.split(".")[-1].split("#")[0], []).append(i)
+    stream = torch.cuda.current_stream()
+    out = {}
+    for shape, idx in groups.items():
+        chain = q4k.Chain([(wl.launches[i][1].data_ptr(), wl.launches[i][2].data_ptr(),
+                            wl.launches[i][3].data_ptr(), wl.launches[i][4],
+                            wl.launches[i][5] // BLOCK_ELEMS) for i in idx], CHAIN_MODES["graph"])
+        for _ in range(3):
+            chain.launch(stream)
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for _ in range(reps):
+            chain.launch(stream)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        n, k = wl.launches[idx[0]][4], wl.launches[idx[0]][5]
+        us = t0.elapsed_time(t1) * 1e3 / (reps * len(idx))
+        out[shape] = {"shape": f"{n}x{k}", "launches": len(idx), "us_per_launch": round(us, 3),
+                      "hbm_frac": round(gemv_bytes(n, k) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        chain.close()
+    return out
 
 
 def check_parity(torch, wl: Workload, rows: int = 256) -> str:
@@ -527,19 +588,17 @@ def run_decode_dp4a(torch, q4k, args):
         q8.append((torch.empty(k, dtype=torch.int8, device="cuda"),
                    torch.empty(nsub, device="cuda"), torch.empty(nsub, device="cuda")))
 
-    def two_launch(st):
-        for (name, w, x, y, n, k), (xq, xd, xs) in zip(wl.launches, q8):
-            q4k.kern.quantize_q8_1(x.data_ptr(), xq.data_ptr(), xd.data_ptr(), xs.data_ptr(), k, st)
-            q4k.kern.matvec_q4k_dp4a(w.data_ptr(), xq.data_ptr(), xd.data_ptr(), xs.data_ptr(),
-                                     y.data_ptr(), n, k // BLOCK_ELEMS, st)
-
-    def fused(st):
-        for name, w, x, y, n, k in wl.launches:
-            q4k.kern.quantize_matvec_q4k_dp4a(w.data_ptr(), x.data_ptr(), y.data_ptr(), n,
-                                              k // BLOCK_ELEMS, st)
-
-    ms_two = time_captured(torch, two_launch, args.steps, args.warmup)
-    ms = time_captured(torch, fused, args.steps, args.warmup)
+    # both recorded by the library as op chains (mgq_chain_create_ops), the
+    # way a Rust host keeping the reference's default arm would record them
+    two_launch, fused = [], []
+    for (name, w, x, y, n, k), (xq, xd, xs) in zip(wl.launches, q8):
+        two_launch += [q4k.op_quantize_q8_1(x.data_ptr(), xq.data_ptr(), xd.data_ptr(),
+                                            xs.data_ptr(), k),
+                       q4k.op_matvec_dp4a(12, w.data_ptr(), xq.data_ptr(), xd.data_ptr(),
+                                          xs.data_ptr(), y.data_ptr(), n, k)]
+        fused.append(q4k.op_quantize_matvec_dp4a(w.data_ptr(), x.data_ptr(), y.data_ptr(), n, k))
+    ms_two = time_op_chain(torch, q4k, two_launch, args.steps, args.warmup)
+    ms = time_op_chain(torch, q4k, fused, args.steps, args.warmup)
     worst = 0.0
     for name, w, x, y, n, k in (wl.launches[0], wl.launches[3], wl.launches[-1]):
         bpr = k // BLOCK_ELEMS
@@ -554,7 +613,7 @@ def run_decode_dp4a(torch, q4k, args):
     return {"workload": "decode7b_dp4a: the decode7b step on Q8_1 activations, each matvec as "
                         "launch_quantize_matvec_q4k_dp4a_ex (113 launches; the reference's "
                         "quantize_q8_1 + matvec_q4k_dp4a pair, 226 launches, timed beside it), "
-                        "one graph each",
+                        "each step one op chain (mgq_chain_create_ops)",
             "us_per_launch": round(ms * 1e3 / len(wl.launches), 3), "gbs": nbytes / (ms * 1e-3) / 1e9,
             "bytes_per_launch": nbytes // len(wl.launches), "parity": parity,
             "kernel": "mgq::gemv_mfma_kernel<..., Q8, kFuseQuant>",
@@ -916,6 +975,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--no-shapes", action="store_true",
+                    help="decode7b/layer/gateup: skip the per-shape times after the timed region")
     ap.add_argument("--chain", default="auto", choices=sorted(CHAIN_MODES),
                     help="decode7b/layer/gateup: the chain's implementation")
     args = ap.parse_args()
@@ -948,8 +1009,20 @@ def main() -> int:
     torch.cuda.synchronize()
     log(f"{len(wl.launches)} launches, {wl.weight_bytes / 1e9:.3f} GB weights resident")
 
-    ms, spread, impl = time_graph(torch, q4k, wl, args.steps, args.warmup, args.chain)
-    log(f"timed {args.steps} steps ({impl} chain): {ms:.4f} ms/step; per-step events {spread}")
+    host_us = None
+    if args.chain == "eager":
+        ms, spread, host_us = time_eager(torch, q4k, wl, args.steps, args.warmup)
+        impl = "eager"
+        log(f"timed {args.steps} steps (eager, null stream, one device synchronize per step): "
+            f"{ms:.4f} ms/step; host {host_us:.3f} us per launch call; per-step {spread}")
+    else:
+        ms, spread, impl = time_graph(torch, q4k, wl, args.steps, args.warmup, args.chain)
+        log(f"timed {args.steps} steps ({impl} chain): {ms:.4f} ms/step; per-step events {spread}")
+    shapes = None
+    if impl == "graph" and not args.no_shapes:
+        shapes = shape_times(torch, q4k, wl)
+        log("per shape (graph of that shape's launches, after the timed region): " +
+            ", ".join(f"{k} {v['us_per_launch']} us" for k, v in shapes.items()))
     parity = "skipped" if args.no_parity else check_parity(torch, wl)
     log(f"parity: {parity}")
     nl = len(wl.launches)
@@ -982,6 +1055,8 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": desc, "matvecs_per_step": nl, "chain": impl,
                    "launches_per_step": 1 if impl == "persistent" else nl,
+                   "stream": "null stream, one hipDeviceSynchronize per step" if impl == "eager"
+                   else "one graph launch per step",
                    "bytes_per_step": wl.bytes_per_pass, "weights": "q4_k (144 B / 256 weights)",
                    "batch": 1},
         "tokens_per_s": round(1000.0 / ms, 2) if args.workload == "decode7b" else None,
@@ -992,6 +1067,10 @@ def main() -> int:
                      "traffic": profiled_traffic(args.workload, impl), "kernel": kernel,
                      "avg_launch_us": round(avg_s * 1e6, 3), "avg_launch_bytes": int(avg_b)},
     }
+    if host_us is not None:
+        out["host_us_per_launch_call"] = round(host_us, 3)
+    if shapes is not None:
+        out["per_shape"] = shapes
     if not args.no_cpu:
         threads = cpu_threads()
         log(f"cpu baseline ({threads} threads, ~{args.cpu_seconds:.0f} s, then 1 thread ~5 s)")

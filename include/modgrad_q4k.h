@@ -281,11 +281,12 @@ typedef struct mgq_gemv_desc {
  * y must not alias its own x or any weights. The chain keeps the
  * descriptors' pointers: buffers must outlive it.
  *
- * Two implementations:
+ * Three implementations:
  *   MGQ_CHAIN_PERSISTENT  one cooperative launch for the whole chain: a
  *       persistent kernel streams the next matvec's weights while it waits
- *       for the previous matvec's output (grid-wide completion counters, no
- *       fences). Row-aligned Q4_K with blocks_per_row <= 84. A launch is not
+ *       for the previous matvec's output (grid-wide completion counters
+ *       behind agent-scope release/acquire fences). Row-aligned Q4_K with
+ *       blocks_per_row <= 84. A launch is not
  *       capturable into a HIP graph, and launches of one chain must be
  *       ordered (one stream, or synchronized): the chain owns its counters.
  *       Measured on MI355X it is slower than the graph (one 15-wave
@@ -293,18 +294,24 @@ typedef struct mgq_gemv_desc {
  *       rate), so it is opt-in.
  *   MGQ_CHAIN_GRAPH       the n launch_matvec_q4k_ex launches recorded into
  *       a HIP graph (stream capture on a private stream).
+ *   MGQ_CHAIN_EAGER       nothing recorded: every mgq_chain_launch enqueues
+ *       the n launch_matvec_q4k_ex launches one after another on its
+ *       stream, as the reference engine launches its kernels
+ *       (rocm_gemma.rs:312-345); for callers that cannot keep a graph, and
+ *       to measure that calling pattern.
  * MGQ_CHAIN_AUTO takes the graph (environment MGQ_CHAIN=persistent selects
  * the persistent kernel where it can run). MGQ_CHAIN_PERSISTENT returns
  * hipErrorNotSupported when it cannot run. */
 #define MGQ_CHAIN_AUTO 0
 #define MGQ_CHAIN_GRAPH 1
 #define MGQ_CHAIN_PERSISTENT 2
+#define MGQ_CHAIN_EAGER 3
 hipError_t mgq_chain_create_ex(const mgq_gemv_desc *descs, int n, int mode, void **chain_out);
 /* mgq_chain_create_ex with MGQ_CHAIN_AUTO. */
 hipError_t mgq_chain_create(const mgq_gemv_desc *descs, int n, void **chain_out);
 /* Launches the chain on `stream`; ordered after prior work on that stream. */
 hipError_t mgq_chain_launch(void *chain, hipStream_t stream);
-/* The chain's implementation (MGQ_CHAIN_GRAPH / MGQ_CHAIN_PERSISTENT) and,
+/* The chain's implementation (MGQ_CHAIN_GRAPH / _PERSISTENT / _EAGER) and,
  * for the persistent kernel, its fault word: nonzero when a grid-wide wait
  * gave up (bounded at seconds) in some launch, i.e. results are not to be
  * trusted. Reading it synchronizes with the device. Either pointer may be
@@ -332,6 +339,16 @@ hipError_t mgq_chain_destroy(void *chain);
  *                        in_dim (launch_rms_norm_ex).
  *   MGQ_OP_GLU           y = act(x) .* x2 over out_dim (launch_glu_ex).
  *   MGQ_OP_RESIDUAL_ADD  y += x over out_dim (launch_residual_add_ex).
+ * The reference engine's default dp4a arm (rocm_gemma.rs:283,298-306;
+ * rocm.rs:477-479,490-491):
+ *   MGQ_OP_QUANTIZE_Q8_1 x (in_dim f32, in_dim % 32 == 0) -> Q8_1 xq, xd, xsum
+ *                        (launch_quantize_q8_1_ex).
+ *   MGQ_OP_MATVEC_DP4A   y = W . Q8_1(xq, xd, xsum); dtype Q4_K
+ *                        (launch_matvec_q4k_dp4a_ex) or Q6_K
+ *                        (launch_matvec_q6k_dp4a_ex), in_dim = K.
+ *   MGQ_OP_QUANTIZE_MATVEC_DP4A  the two above in one launch for Q4_K
+ *                        (launch_quantize_matvec_q4k_dp4a_ex: y from x, same
+ *                        bits; xq/xd/xsum unused).
  * No counterpart in the reference's C ABI: its chain is Rust code that
  * launches these kernels one by one; this records them into one graph. */
 #define MGQ_OP_MATVEC 0
@@ -340,6 +357,9 @@ hipError_t mgq_chain_destroy(void *chain);
 #define MGQ_OP_RMS_NORM 3
 #define MGQ_OP_GLU 4
 #define MGQ_OP_RESIDUAL_ADD 5
+#define MGQ_OP_QUANTIZE_Q8_1 6
+#define MGQ_OP_MATVEC_DP4A 7
+#define MGQ_OP_QUANTIZE_MATVEC_DP4A 8
 /* GGML tensor types (gguf.rs:9-40) of the quantized weights */
 #define MGQ_DTYPE_Q4_K 12
 #define MGQ_DTYPE_Q5_K 13
@@ -359,6 +379,9 @@ typedef struct mgq_op_desc {
     int in_dim;               /* matvec K / RMSNorm row length */
     int rows;                 /* MGQ_OP_RMS_NORM: rows */
     float eps;                /* RMSNorm epsilon */
+    signed char *xq;          /* Q8_1 ops: int8 activations [in_dim] */
+    float *xd;                /* Q8_1 ops: scale per 32 activations [in_dim/32] */
+    float *xsum;              /* Q8_1 ops: sum per 32 activations [in_dim/32] */
 } mgq_op_desc;
 
 /* A chain of mgq_op_desc kernels recorded into one HIP graph (the chain's
@@ -373,10 +396,13 @@ hipError_t mgq_chain_create_ops(const mgq_op_desc *ops, int n, void **chain_out)
 /* Prepares the current device: sets the GEMV kernels' LDS attributes, which
  * belong to a device (every launcher also does this on its first use on a
  * device), and looks up the device address of the fixed scratch array of
- * launch_matvec_q4k_batched_noalloc. Allocates nothing. Apart from that array
- * (used by that entry point only) the library keeps no device memory and no
- * mutable device state, so launches on different streams may run
- * concurrently. Safe to call more than once. */
+ * launch_matvec_q4k_batched_noalloc. Allocates nothing. Device memory the
+ * library holds: that fixed array (used by that entry point only), and the
+ * task table and completion counters that mgq_chain_create_ex allocates for
+ * a persistent chain (MGQ_CHAIN_PERSISTENT), freed by mgq_chain_destroy.
+ * Every other launcher allocates nothing and keeps no mutable device state,
+ * so its launches on different streams may run concurrently. Safe to call
+ * more than once. */
 hipError_t mgq_prepare(void);
 
 /* Library version string, e.g. "modgrad_q4k 0.1.0 gfx950". */

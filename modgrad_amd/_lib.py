@@ -70,12 +70,16 @@ LAYOUT_FLAT = 1
 CHAIN_AUTO = 0
 CHAIN_GRAPH = 1
 CHAIN_PERSISTENT = 2
+CHAIN_EAGER = 3
 OP_MATVEC = 0
 OP_MATVEC_NORM = 1
 OP_MATVEC_GLU = 2
 OP_RMS_NORM = 3
 OP_GLU = 4
 OP_RESIDUAL_ADD = 5
+OP_QUANTIZE_Q8_1 = 6
+OP_MATVEC_DP4A = 7
+OP_QUANTIZE_MATVEC_DP4A = 8
 DTYPE_Q4_K = 12
 DTYPE_Q5_K = 13
 DTYPE_Q6_K = 14
@@ -90,7 +94,7 @@ class OpDesc(ctypes.Structure):
     """mgq_op_desc (one kernel of an op chain)."""
     _fields_ = [("op", I), ("dtype", I), ("layout", I), ("act", I), ("w", P), ("w2", P),
                 ("x", P), ("x2", P), ("norm_w", P), ("y", P), ("out_dim", I), ("in_dim", I),
-                ("rows", I), ("eps", F)]
+                ("rows", I), ("eps", F), ("xq", P), ("xd", P), ("xsum", P)]
 
 
 class HipError(RuntimeError):

@@ -184,6 +184,7 @@ struct mgq_chain {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     mgq::PersistentChain *pers = nullptr;
+    std::vector<mgq_gemv_desc> eager;  // MGQ_CHAIN_EAGER: launched one by one
 };
 
 }  // extern "C"
@@ -230,7 +231,8 @@ static bool env_chain_persistent() {
 
 hipError_t mgq_chain_create_ex(const mgq_gemv_desc *descs, int n, int mode, void **chain_out) {
     if (!chain_out || !descs || n <= 0) return hipErrorInvalidValue;
-    if (mode != MGQ_CHAIN_AUTO && mode != MGQ_CHAIN_GRAPH && mode != MGQ_CHAIN_PERSISTENT)
+    if (mode != MGQ_CHAIN_AUTO && mode != MGQ_CHAIN_GRAPH && mode != MGQ_CHAIN_PERSISTENT &&
+        mode != MGQ_CHAIN_EAGER)
         return hipErrorInvalidValue;
     *chain_out = nullptr;
     for (int i = 0; i < n; ++i) {
@@ -242,6 +244,18 @@ hipError_t mgq_chain_create_ex(const mgq_gemv_desc *descs, int n, int mode, void
     }
     hipError_t e = mgq::gemv_prepare();  // not allowed to happen mid-capture
     if (e != hipSuccess) return e;
+    if (mode == MGQ_CHAIN_EAGER) {
+        auto *ch = new (std::nothrow) mgq_chain;
+        if (!ch) return hipErrorOutOfMemory;
+        try {
+            ch->eager.assign(descs, descs + n);
+        } catch (...) {
+            delete ch;
+            return hipErrorOutOfMemory;
+        }
+        *chain_out = ch;
+        return hipSuccess;
+    }
     if (mode == MGQ_CHAIN_PERSISTENT || (mode == MGQ_CHAIN_AUTO && env_chain_persistent())) {
         mgq::PersistentChain *p = nullptr;
         e = mgq::chain_persistent_create(descs, n, &p);
@@ -313,6 +327,21 @@ static hipError_t op_check(const mgq_op_desc &o) {
         return (o.act == MGQ_ACT_GELU_TANH || o.act == MGQ_ACT_SILU) ? hipSuccess : hipErrorInvalidValue;
     case MGQ_OP_RESIDUAL_ADD:
         return (bad_f32(o.x) || bad_f32(o.y) || o.out_dim <= 0) ? hipErrorInvalidValue : hipSuccess;
+    case MGQ_OP_QUANTIZE_Q8_1:
+        if (bad_f32(o.x) || !o.xq || bad_f32(o.xd) || bad_f32(o.xsum) || o.in_dim < 32 || o.in_dim % 32)
+            return hipErrorInvalidValue;
+        return hipSuccess;
+    case MGQ_OP_MATVEC_DP4A:
+        if (!o.w || !o.xq || bad_f32(o.xd) || bad_f32(o.y) || o.out_dim <= 0 || o.in_dim <= 0 ||
+            o.in_dim % 256)
+            return hipErrorInvalidValue;
+        if (o.dtype == MGQ_DTYPE_Q4_K) return bad_f32(o.xsum) ? hipErrorInvalidValue : hipSuccess;
+        return o.dtype == MGQ_DTYPE_Q6_K ? hipSuccess : hipErrorInvalidValue;
+    case MGQ_OP_QUANTIZE_MATVEC_DP4A:
+        if (o.dtype != MGQ_DTYPE_Q4_K || !o.w || bad_f32(o.x) || bad_f32(o.y) || o.out_dim <= 0 ||
+            o.in_dim <= 0 || o.in_dim % 256)
+            return hipErrorInvalidValue;
+        return hipSuccess;
     default:
         return hipErrorInvalidValue;
     }
@@ -339,6 +368,14 @@ static hipError_t op_launch(const mgq_op_desc &o, hipStream_t s) {
         return launch_rms_norm_ex(o.x, o.norm_w, o.y, o.rows, o.in_dim, o.eps, s);
     case MGQ_OP_GLU:
         return launch_glu_ex(o.x, o.x2, o.y, o.out_dim, o.act, s);
+    case MGQ_OP_QUANTIZE_Q8_1:
+        return launch_quantize_q8_1_ex(o.x, o.xq, o.xd, o.xsum, o.in_dim, s);
+    case MGQ_OP_MATVEC_DP4A:
+        if (o.dtype == MGQ_DTYPE_Q4_K)
+            return launch_matvec_q4k_dp4a_ex(o.w, o.xq, o.xd, o.xsum, o.y, o.out_dim, o.in_dim / 256, s);
+        return launch_matvec_q6k_dp4a_ex(o.w, o.xq, o.xd, o.xsum, o.y, o.out_dim, o.in_dim / 256, s);
+    case MGQ_OP_QUANTIZE_MATVEC_DP4A:
+        return launch_quantize_matvec_q4k_dp4a_ex(o.w, o.x, o.y, o.out_dim, o.in_dim / 256, s);
     default:
         return launch_residual_add_ex(o.y, o.x, o.out_dim, s);
     }
@@ -364,13 +401,21 @@ hipError_t mgq_chain_launch(void *chain, hipStream_t stream) {
     if (!chain) return hipErrorInvalidValue;
     auto *ch = static_cast<mgq_chain *>(chain);
     if (ch->pers) return mgq::chain_persistent_launch(ch->pers, stream);
+    if (!ch->exec) {  // eager: the reference's one-launch-per-matvec pattern
+        for (const mgq_gemv_desc &d : ch->eager) {
+            const hipError_t e = launch_matvec_q4k_ex(d.w_q4, d.x, d.y, d.out_dim,
+                                                      d.blocks_per_row * 256, MGQ_LAYOUT_ROWS, stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     return hipGraphLaunch(ch->exec, stream);
 }
 
 hipError_t mgq_chain_info(void *chain, int *mode, unsigned *faults) {
     if (!chain) return hipErrorInvalidValue;
     auto *ch = static_cast<mgq_chain *>(chain);
-    if (mode) *mode = ch->pers ? MGQ_CHAIN_PERSISTENT : MGQ_CHAIN_GRAPH;
+    if (mode) *mode = ch->pers ? MGQ_CHAIN_PERSISTENT : ch->exec ? MGQ_CHAIN_GRAPH : MGQ_CHAIN_EAGER;
     if (faults) {
         *faults = 0;
         if (ch->pers) return mgq::chain_persistent_faults(ch->pers, faults);

@@ -16,11 +16,13 @@
 // descriptor < d, exactly the ordering of launching them one after another
 // on a stream. A descriptor's y must not alias its own x or any weights.
 //
-// Completion signalling (no fences, no whole-cache operations): y values are
-// written with agent-scope atomic stores (write-through to the coherence
-// point: a probe on MI355X saw no stale value across XCDs after them), a
-// work-group's control wave waits for its stores to complete and then adds 1
-// to its shard of the finished descriptor's counter: descriptor d has 16
+// Completion signalling by the HSA memory model: y values are written with
+// agent-scope atomic stores, then the work-group's control wave issues an
+// agent-scope release fence (its stores complete and reach the device
+// coherence point) and adds 1 to its shard of the finished descriptor's
+// counter (relaxed, so the fence heads the release sequence); a waiter that
+// has read every shard at its target issues an agent-scope acquire fence
+// before its work-group reads any y. Descriptor d has 16
 // device-scope counters, work-group b adds to counter b % 16, so no counter
 // takes more than 16 adds per launch. A work-group with no rows in a
 // descriptor signals it as soon as it moves past it. Every work-group
@@ -28,8 +30,8 @@
 // means every work-group is done with d and everything before it; waiters
 // poll those 16 counters with agent-scope loads. Counters only grow (64-bit;
 // the launch index is folded into the targets) and are never reset.
-// Measured on MI355X: ~1.5 us per grid-wide wait, against 3.5-8 us for one
-// shared counter or one flag per work-group.
+// Sharding measured on MI355X (before the fences): ~1.5 us per grid-wide
+// wait, against 3.5-8 us for one shared counter or one flag per work-group.
 //
 // Work-group layout (one per CU): 14 compute waves + 1 control wave. The
 // compute waves run the matrix-core GEMV of gemv_mfma_kernel (16-row groups,
@@ -187,7 +189,10 @@ __global__ __launch_bounds__(pc::NT) void chain_kernel(const ChainTask *__restri
                     if (row < t.n) st_sc1(t.y + row, ybuf[i]);
                 }
             }
-            __builtin_amdgcn_s_waitcnt(0);  // every y store of this wave is complete
+            // release at agent scope: every y store of this wave (and anything
+            // else this work-group wrote before) is visible device-wide before
+            // any counter add below is
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
             // one lane per task to signal, in parallel (a work-group skips
             // ahead over tasks where it has no rows)
             for (int t = signaled + lane; t < upto; t += 64)
@@ -211,7 +216,14 @@ __global__ __launch_bounds__(pc::NT) void chain_kernel(const ChainTask *__restri
                                            __HIP_MEMORY_SCOPE_AGENT) >= target;
                 else if (lane == NCTR)
                     bad = __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
-                if (__all(ok)) break;
+                if (__all(ok)) {
+                    // acquire at agent scope: the counters read above were
+                    // made by adds that followed their work-group's release,
+                    // so every y they cover is visible to this work-group's
+                    // reads after the barrier that follows this wait
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+                    break;
+                }
                 if (__any(bad)) break;
                 if (++spins > spin_limit) {
                     if (lane == 0) atomicOr(err, 1u);
@@ -485,7 +497,7 @@ static hipError_t chain_attr() {
     return allow_full_lds((const void *)chain_kernel<kChainPF>, state);
 }
 
-// 0 if the descriptors fit the persistent chain (row-aligned Q4_K, K <= 80
+// 0 if the descriptors fit the persistent chain (row-aligned Q4_K, K <= 84
 // blocks, LDS within 160 KiB, cooperative launch on this device), else the
 // reason as a hipError_t.
 hipError_t chain_persistent_create(const mgq_gemv_desc *descs, int n, PersistentChain **out) {

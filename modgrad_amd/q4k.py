@@ -396,12 +396,32 @@ def op_residual_add(h: int, x: int, n: int) -> "_lib.OpDesc":
     return _lib.OpDesc(op=_lib.OP_RESIDUAL_ADD, x=x, y=h, out_dim=n)
 
 
+def op_quantize_q8_1(x: int, xq: int, xd: int, xsum: int, n: int) -> "_lib.OpDesc":
+    """x (n f32) -> Q8_1 xq, xd, xsum (launch_quantize_q8_1, rocm.rs:477)."""
+    return _lib.OpDesc(op=_lib.OP_QUANTIZE_Q8_1, x=x, xq=xq, xd=xd, xsum=xsum, in_dim=n)
+
+
+def op_matvec_dp4a(dtype: int, w: int, xq: int, xd: int, xsum: int, y: int, out_dim: int,
+                   in_dim: int) -> "_lib.OpDesc":
+    """y = W . Q8_1(xq, xd, xsum) for Q4_K or Q6_K weights
+    (launch_matvec_q4k_dp4a / launch_matvec_q6k_dp4a, rocm.rs:478-491)."""
+    return _lib.OpDesc(op=_lib.OP_MATVEC_DP4A, dtype=dtype, w=w, xq=xq, xd=xd, xsum=xsum, y=y,
+                       out_dim=out_dim, in_dim=in_dim)
+
+
+def op_quantize_matvec_dp4a(w: int, x: int, y: int, out_dim: int, in_dim: int) -> "_lib.OpDesc":
+    """op_quantize_q8_1 then op_matvec_dp4a (Q4_K) in one launch, same bits."""
+    return _lib.OpDesc(op=_lib.OP_QUANTIZE_MATVEC_DP4A, dtype=_lib.DTYPE_Q4_K, w=w, x=x, y=y,
+                       out_dim=out_dim, in_dim=in_dim)
+
+
 class Chain:
     """A decode step's row-aligned matvecs as one launchable chain
-    (mgq_chain_create_ex): a persistent kernel (mode CHAIN_PERSISTENT) or a
-    HIP graph (CHAIN_GRAPH); CHAIN_AUTO picks the persistent kernel when it
-    applies. Each launch runs the matvecs in order, each seeing the earlier
-    ones' outputs."""
+    (mgq_chain_create_ex): a persistent kernel (mode CHAIN_PERSISTENT), a
+    HIP graph (CHAIN_GRAPH) or the launches enqueued one by one at every
+    launch (CHAIN_EAGER); CHAIN_AUTO takes the graph unless the
+    environment variable MGQ_CHAIN=persistent is set. Each launch runs the
+    matvecs in order, each seeing the earlier ones' outputs."""
 
     def __init__(self, descs, mode: int = _lib.CHAIN_AUTO):
         if descs is None:  # from_ops

@@ -236,7 +236,18 @@ def test_op_chain_rejects_bad_descriptors_before_any_device_call(L):
            dict(op=_lib.OP_MATVEC_GLU, dtype=_lib.DTYPE_Q6_K, w2=FAKE),
            dict(op=_lib.OP_RMS_NORM, norm_w=FAKE, rows=0),
            dict(op=_lib.OP_GLU, x2=None),
-           dict(op=_lib.OP_RESIDUAL_ADD, out_dim=-1)]
+           dict(op=_lib.OP_RESIDUAL_ADD, out_dim=-1),
+           # the dp4a arm: Q8_1 buffers required, K a multiple of 32 / 256,
+           # Q4_K or Q6_K weights (Q4_K only when fused with the quantizer)
+           dict(op=_lib.OP_QUANTIZE_Q8_1, xq=None, xd=FAKE, xsum=FAKE),
+           dict(op=_lib.OP_QUANTIZE_Q8_1, xq=FAKE, xd=FAKE + 2, xsum=FAKE),
+           dict(op=_lib.OP_QUANTIZE_Q8_1, xq=FAKE, xd=FAKE, xsum=FAKE, in_dim=48),
+           dict(op=_lib.OP_MATVEC_DP4A, xq=FAKE, xd=FAKE, xsum=None),
+           dict(op=_lib.OP_MATVEC_DP4A, xq=FAKE, xd=FAKE, xsum=FAKE, dtype=_lib.DTYPE_Q5_K),
+           dict(op=_lib.OP_MATVEC_DP4A, xq=FAKE, xd=FAKE, xsum=FAKE, in_dim=288),
+           dict(op=_lib.OP_MATVEC_DP4A, xq=None, xd=FAKE, xsum=FAKE, dtype=_lib.DTYPE_Q6_K),
+           dict(op=_lib.OP_QUANTIZE_MATVEC_DP4A, dtype=_lib.DTYPE_Q6_K),
+           dict(op=_lib.OP_QUANTIZE_MATVEC_DP4A, x=None)]
     for change in bad:
         d = dict(good)
         d.update(change)

@@ -1,4 +1,4 @@
-"""GPU tests of the decode-step chain (mgq_chain_create_ex), both
+"""GPU tests of the decode-step chain (mgq_chain_create_ex), its three
 implementations, through the C ABI against the oracle.
 
 - The persistent kernel and the graph of launch_matvec_q4k launches both meet
@@ -86,7 +86,7 @@ def test_persistent_and_graph_chains_match_oracle(L, orc, k):
     graph.close()
 
 
-@pytest.mark.parametrize("mode", [_lib.CHAIN_PERSISTENT, _lib.CHAIN_GRAPH])
+@pytest.mark.parametrize("mode", [_lib.CHAIN_PERSISTENT, _lib.CHAIN_GRAPH, _lib.CHAIN_EAGER])
 def test_chain_with_real_dependencies(L, orc, mode):
     # x_{d+1} = y_d: dims 3584 -> 512 -> 256 -> 4608 -> 3584 -> 18944 -> 3584
     dims = [3584, 512, 256, 4608, 3584, 18944, 3584]
@@ -114,6 +114,31 @@ def test_chain_with_real_dependencies(L, orc, mode):
     if mode == _lib.CHAIN_PERSISTENT:
         assert ch.faults() == 0
     ch.close()
+
+
+@pytest.mark.parametrize("k", range(len(SHAPES)))
+def test_eager_chain_equals_graph_chain(L, orc, k):
+    # MGQ_CHAIN_EAGER enqueues the same launch_matvec_q4k_ex launches the
+    # graph records, so both give the same bits, on the null stream too
+    shapes = SHAPES[k]
+    note(f"chain eager vs graph {shapes}")
+    bufs, descs, refs = independent(orc, shapes, 300 + k)
+    eager = make_chain(descs, _lib.CHAIN_EAGER)
+    assert eager.mode() == _lib.CHAIN_EAGER
+    graph = make_chain(descs, _lib.CHAIN_GRAPH)
+    got = []
+    for ch in (graph, eager, eager):
+        for _, _, yt in bufs:
+            yt.fill_(float("nan"))
+        ch.launch()
+        got.append([host(yt).copy() for _, _, yt in bufs])
+    for (y_ref, a), y in zip(refs, got[1]):
+        assert_gemv_close(y, y_ref, a)
+    for run in got[1:]:
+        for y0, y in zip(got[0], run):
+            assert np.array_equal(y0.view(np.uint32), y.view(np.uint32))
+    eager.close()
+    graph.close()
 
 
 def test_persistent_chain_rejects_long_rows(L, orc):
@@ -216,6 +241,91 @@ def test_op_chain_mixed_dtypes_and_glue(L, orc):
         assert_gemv_close(r["yf"], y, A)
         y, A = orc.gemv_kquant(210, w6, xn_ref, KV, H // 256)
         assert_gemv_close(r["q6n"], y, A)
+        if first is None:
+            first = r
+        else:
+            for k in r:
+                assert np.array_equal(r[k].view(np.uint32), first[k].view(np.uint32)), k
+    ch.close()
+
+
+def _dp4a_close(y, y_ref, absterm):
+    # the dp4a formula in f64 (the oracle) against the kernel's f32 sums
+    err = np.abs(y.astype(np.float64) - y_ref)
+    assert np.all(err <= 1e-5 * absterm + 1e-30), float(np.max(err / np.maximum(absterm, 1e-300)))
+
+
+def test_op_chain_dp4a_arm(L, orc):
+    """The reference engine's default Q8_1/dp4a arm (rocm_gemma.rs:283,
+    298-306; rocm.rs:477-479, 490-491) recorded by mgq_chain_create_ops:
+    RMSNorm, quantize_q8_1, the Q4_K and Q6_K dp4a matvecs on its Q8_1
+    activations, the fused quantize + Q4_K dp4a matvec, a GLU, a second
+    quantize and dp4a matvec on the GLU output, and a residual add. Every
+    output is checked against the oracle on the GPU's own inputs (Q8_1 bit for
+    bit, matvecs against the f64 dp4a formula), the Q4_K result also against
+    the reference's RMS-relative < 0.02 gate on f32 activations, on three
+    replays with identical bits."""
+    from modgrad_amd import q4k
+    from tests.gpu_util import random_kquant_bytes
+    import torch
+    note("op chain: the dp4a arm (quantize_q8_1, Q4_K/Q6_K dp4a, fused quantize+dp4a)")
+    rng = np.random.default_rng(0xD4A)
+    H, KV, eps = 1024, 512, 1e-5
+    h0 = (rng.standard_normal(H) * 1.5).astype(np.float32)
+    nw = (rng.standard_normal(H) * 0.3 + 1.0).astype(np.float32)
+    wq = orc.seeded_weight(31, KV, H)
+    wv = random_kquant_bytes(rng, KV * H // 256, 210)
+    wo = orc.seeded_weight(32, H, H)
+    wd = orc.seeded_weight(33, H, KV)
+    dv = {k: dev(v) for k, v in dict(h0=h0, nw=nw, wq=wq, wv=wv, wo=wo, wd=wd).items()}
+    out = {k: empty_f32(n) for k, n in dict(xn=H, q=KV, v=KV, o=H, z=KV, d=H).items()}
+    q8 = {k: (torch.empty(n, dtype=torch.int8, device="cuda"), empty_f32(n // 32), empty_f32(n // 32))
+          for k, n in dict(a=H, b=KV).items()}
+    P = lambda k: ptr(dv[k]) if k in dv else ptr(out[k])
+    Q = lambda k: tuple(ptr(t) for t in q8[k])
+    Q4, Q6 = _lib.DTYPE_Q4_K, _lib.DTYPE_Q6_K
+    ops = [
+        q4k.op_rms_norm(P("h0"), P("nw"), P("xn"), 1, H, eps),
+        q4k.op_quantize_q8_1(P("xn"), *Q("a"), H),
+        q4k.op_matvec_dp4a(Q4, P("wq"), *Q("a"), P("q"), KV, H),
+        q4k.op_matvec_dp4a(Q6, P("wv"), *Q("a"), P("v"), KV, H),
+        q4k.op_quantize_matvec_dp4a(P("wo"), P("xn"), P("o"), H, H),
+        q4k.op_glu(P("q"), P("v"), P("z"), KV, _lib.ACT_SILU),
+        q4k.op_quantize_q8_1(P("z"), *Q("b"), KV),
+        q4k.op_matvec_dp4a(Q4, P("wd"), *Q("b"), P("d"), H, KV),
+        q4k.op_residual_add(P("d"), P("o"), H),
+    ]
+    ch = q4k.Chain.from_ops(ops)
+    assert ch.mode() == _lib.CHAIN_GRAPH
+    first = None
+    for rep in range(3):
+        for t in out.values():
+            t.fill_(float("nan"))
+        ch.launch()
+        r = {k: host(t) for k, t in out.items()}
+        r8 = {k: tuple(host(t) for t in v) for k, v in q8.items()}
+        qa, da, sa = orc.quantize_q8_1(r["xn"])
+        assert np.array_equal(r8["a"][0], qa) and np.array_equal(r8["a"][1].view(np.uint32), da.view(np.uint32))
+        assert np.array_equal(r8["a"][2].view(np.uint32), sa.view(np.uint32))
+        y, A = orc.gemv_dp4a(wq, qa, da, sa, KV, H // 256)
+        _dp4a_close(r["q"], y, A)
+        yf, _ = orc.gemv(wq, r["xn"], KV, H // 256)
+        rms = np.sqrt(np.sum((r["q"].astype(np.float64) - yf) ** 2) / np.sum(yf.astype(np.float64) ** 2))
+        assert rms < 0.02  # the reference's dp4a acceptance gate (rocm_dp4a_check.rs:63)
+        y, A = orc.gemv_q6k_dp4a(wv, qa, da, KV, H // 256)
+        _dp4a_close(r["v"], y, A)
+        y, A = orc.gemv_dp4a(wo, qa, da, sa, H, H // 256)
+        o_ref = y
+        qb, db, sb = orc.quantize_q8_1(r["z"])
+        assert np.array_equal(r8["b"][0], qb) and np.array_equal(r8["b"][1].view(np.uint32), db.view(np.uint32))
+        y, A = orc.gemv_dp4a(wd, qb, db, sb, H, KV // 256)
+        # d = Wd . Q8(z), then d += o (one f32 add per element)
+        res = r["d"].astype(np.float64) - r["o"]
+        assert np.all(np.abs(res - y) <= 1e-5 * A + 2 ** -23 * np.abs(r["d"]) + 1e-30)
+        # o came from the fused quantize+dp4a launch: the dp4a formula on Q8(xn)
+        o_gpu = r["o"].astype(np.float64)
+        _, Ao = orc.gemv_dp4a(wo, qa, da, sa, H, H // 256)
+        assert np.all(np.abs(o_gpu - o_ref) <= 1e-5 * Ao + 1e-30)
         if first is None:
             first = r
         else:
