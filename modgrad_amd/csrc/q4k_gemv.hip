@@ -291,6 +291,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     static_assert(Q8 ? (FUSE == 0 || FUSE == kFuseQuant) : (FUSE & kFuseQuant) == 0,
                   "fused glue runs on f32 activations; quantization only in Q8 mode");
     static_assert(!(FUSE & kFmtQ5K) || FUSE == kFmtQ5K, "Q5_K weights: plain f32 matvec only");
+    static_assert(R == 32 || C % 2 == 0, "R = 16: a unit is a pair of blocks, so C must be even");
     constexpr bool Q5 = (FUSE & kFmtQ5K) != 0;
     constexpr int BP = block_pieces(FUSE);  // 16-byte pieces per block
     constexpr int BB = BP * 16;              // block bytes
@@ -304,10 +305,6 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     float *aux = reinterpret_cast<float *>(lds + Lo.aux);
     const size_t row_bytes = (size_t)bpr * BB;
     const int stages = (bpr + C - 1) / C;
-    // a row group is gr <= R rows (the tile's rows past gr re-read row gr - 1)
-    const int groups = (n + gr - 1) / gr;
-    const int my_groups = sched_count(sch, (int)blockIdx.x, (int)gridDim.x, groups);
-    const int Q = my_groups * VM * stages;        // stages this work-group streams
     constexpr int PIECES = R * BP * C;            // 16-byte pieces per stage
     constexpr int IPW = ((PIECES + 63) / 64 + NW - 1) / NW;  // wave loads per wavefront
     constexpr int I = IPW * NW;                   // wave loads per stage (padded)
@@ -333,14 +330,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         pcol[k] = (uint32_t)(cb * BB + 16 * pc);          // byte column within the stage
         plast[k] = (uint32_t)((bpr - 1) * BB + 16 * pc);  // same piece of the last block
     }
-    auto gload = [&](int q, u32x4(&dst)[IPW]) {
-        q = std::min(q, Q - 1);
-        const int vg = q / stages;  // pass index: row group vg / VM, matrix vg % VM
-        const uint32_t r0 =
-            (uint32_t)sched_group(sch, (int)blockIdx.x, (int)gridDim.x, vg / VM) * (uint32_t)gr;
+    // Stage (pass vg, column tcol) of the rows from r0: matrix wm, the tile
+    // rows past the group (gr <= R rows) re-read its last row.
+    auto gload_at = [&](uint32_t r0, uint32_t tcol, const uint8_t *wm, u32x4(&dst)[IPW]) {
         const uint32_t glast = (uint32_t)gr - 1u;
-        const uint8_t *wm = (VM == 2 && (vg & 1)) ? fz.w2 : w;
-        const uint32_t tcol = (uint32_t)((q % stages) * C * BB);
         const uint32_t rlast = (uint32_t)(n - 1), rb = (uint32_t)row_bytes;
 #pragma unroll
         for (int k = 0; k < IPW; ++k) {
@@ -349,6 +342,23 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
             const uint64_t off = (uint64_t)rr * rb + col;  // one v_mad_u64_u32
             dst[k] = ld_u32x4(wm + off);
         }
+    };
+    // The first stage: row group 0 of every schedule is blockIdx.x (and a
+    // work-group owns at least one), pass 0 reads w from column 0. It needs
+    // no schedule arithmetic, so its loads go out before the divisions that
+    // the schedule takes (plan(), right after them).
+    auto gload_first = [&](u32x4(&dst)[IPW]) {
+        gload_at((uint32_t)blockIdx.x * (uint32_t)gr, 0u, w, dst);
+    };
+    // The schedule, computed while the first loads are in flight (before the
+    // activation table is built, so it never delays the next stage's loads).
+    int groups = 0, my_groups = 0, Q = 0;  // row groups; this work-group's; its stages
+    auto plan = [&]() {
+        // a row group is gr <= R rows (the tile's rows past gr re-read row gr - 1)
+        groups = (n + gr - 1) / gr;
+        my_groups = sched_count(sch, (int)blockIdx.x, (int)gridDim.x, groups);
+        Q = my_groups * VM * stages;
+        __asm__ volatile("" : : "s"(Q), "s"(my_groups));  // materialized here
     };
     auto lstore = [&](int buf, const u32x4(&src)[IPW]) {
 #pragma unroll
@@ -376,8 +386,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         xv0[it] = ld_f32x4(x + (size_t)i * 8);
         xv1[it] = ld_f32x4(x + (size_t)i * 8 + 4);
     }
-#pragma unroll
-    for (int f = 0; f < PF; ++f) gload(f, stg[f]);
+    gload_first(stg[0]);
+    plan();
 #pragma unroll
     for (int it = 0; it < XIT; ++it) {
         if (it >= its) break;
@@ -430,8 +440,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
                                               : reinterpret_cast<const uint8_t *>(xsv + (size_t)(i - nq - 2 * bpr) * 4);
         cv[it] = ld_u32x4(src);
     }
-#pragma unroll
-    for (int f = 0; f < PF; ++f) gload(f, stg[f]);
+    gload_first(stg[0]);
+    plan();
 #pragma unroll
     for (int it = 0; it < XIT; ++it) {
         const int i = tid + it * NW * 64;
@@ -461,8 +471,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         }
     }
     float ssq = 0.0f;  // kFuseNorm: this lane's sum of x^2
-#pragma unroll
-    for (int f = 0; f < PF; ++f) gload(f, stg[f]);
+    gload_first(stg[0]);
+    plan();
 
     for (int b = tid; b < bpr; b += NW * 64)  // the blocks' zero slots
         *reinterpret_cast<u32x4 *>(lds + (size_t)b * Lo.tab_stride + 1024) = u32x4{0u, 0u, 0u, 0u};
@@ -526,6 +536,16 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         if (lane == 0) reinterpret_cast<float *>(lds + Lo.normp)[wave] = ssq;
     }
   }
+    auto gload = [&](int q, u32x4(&dst)[IPW]) {
+        q = std::min(q, Q - 1);
+        const int vg = q / stages;  // pass index: row group vg / VM, matrix vg % VM
+        const uint32_t r0 =
+            (uint32_t)sched_group(sch, (int)blockIdx.x, (int)gridDim.x, vg / VM) * (uint32_t)gr;
+        const uint8_t *wm = (VM == 2 && (vg & 1)) ? fz.w2 : w;
+        gload_at(r0, (uint32_t)((q % stages) * C * BB), wm, dst);
+    };
+#pragma unroll
+    for (int f = 1; f < PF; ++f) gload(f, stg[f]);
     // (the barrier before the first stage is computed also orders the table)
     lstore(0, stg[0]);
 
@@ -847,7 +867,7 @@ static hipError_t launch_cfg(const uint8_t *w, const GemvAct &a, const GemvFuse 
 }
 
 // Launch configurations (rows per work-group, blocks per stage, wavefronts,
-// stages in flight, LDS double buffer, persistent). 1, 3, 4, 5 and 7 are
+// stages in flight, LDS double buffer, persistent). 1, 3, 4 and 5 are
 // tuning alternatives kept for the sweep (MGQ_GEMV_CFG).
 // (The fused variants instantiate only the dispatched configurations 0-3.)
 template <bool Q8, int FUSE>
@@ -867,8 +887,6 @@ static hipError_t launch_any(int cfg, const uint8_t *w, const GemvAct &a, const 
                     return launch_cfg<16, 14, 7, 2, true, Q8, 0>(w, a, fz, y, n, bpr, stream, true);
                 if (cfg == 5)
                     return launch_cfg<32, 14, 7, 1, true, Q8, 0>(w, a, fz, y, n, bpr, stream, true);
-                if (cfg == 7)
-                    return launch_cfg<16, 7, 7, 1, true, Q8, 0>(w, a, fz, y, n, bpr, stream, true);
             }
             return hipErrorInvalidValue;
     }
