@@ -203,17 +203,15 @@ __global__ __launch_bounds__(512) void gemv_batched_mfma_kernel(const uint8_t *_
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const size_t row_bytes = (size_t)bpr * kBlockBytes;
-    // K split: work-group id = kp * G + bx; K part kp takes slices
-    // [sl0, sl0 + slices) of all of them (kparts <= slices overall)
-    const int G = (int)gridDim.x / kparts;
-    const int kp = (int)blockIdx.x / G, bx = (int)blockIdx.x - kp * G;
+    // K split (kparts = 1 or 2): work-group id = kp * G + bx; K part kp takes
+    // slices [sl0, sl0 + slices) of all of them (kparts <= slices overall).
+    // Shifts only: the first stage's loads go out before any division.
+    const int G = (int)gridDim.x >> (kparts - 1);
+    const int kp = (int)blockIdx.x >= G ? 1 : 0, bx = (int)blockIdx.x - kp * G;
     const int all_slices = (bpr + C - 1) / C;
-    const int spk = (all_slices + kparts - 1) / kparts;
+    const int spk = (all_slices + kparts - 1) >> (kparts - 1);
     const int sl0 = kp * spk;
     const int slices = std::min(all_slices, sl0 + spk) - sl0;
-    const int groups = (n + R - 1) / R;
-    const int my_groups = (groups - bx + G - 1) / G;
-    const int Q = my_groups * slices;  // stage q = (slice q / my_groups, group q % my_groups)
 
     u32x4 stg[PF][IPW];
     uint32_t prow[IPW], pcol[IPW], plast[IPW], plds[IPW];
@@ -227,11 +225,8 @@ __global__ __launch_bounds__(512) void gemv_batched_mfma_kernel(const uint8_t *_
         pcol[k] = (uint32_t)(cb * kBlockBytes + 16 * pc);
         plast[k] = (uint32_t)((bpr - 1) * kBlockBytes + 16 * pc);
     }
-    auto gload = [&](int q, u32x4(&dst)[IPW]) {
-        q = std::min(q, Q - 1);
-        const int sl = q / my_groups, t = q - sl * my_groups;
-        const uint32_t r0 = ((uint32_t)bx + (uint32_t)t * (uint32_t)G) * R;
-        const uint32_t tcol = (uint32_t)((sl0 + sl) * C * kBlockBytes);
+    // stage of the R rows from r0 at byte column tcol
+    auto gload_at = [&](uint32_t r0, uint32_t tcol, u32x4(&dst)[IPW]) {
         const uint32_t rlast = (uint32_t)(n - 1), rb = (uint32_t)row_bytes;
 #pragma unroll
         for (int k = 0; k < IPW; ++k) {
@@ -239,6 +234,18 @@ __global__ __launch_bounds__(512) void gemv_batched_mfma_kernel(const uint8_t *_
             const uint32_t col = std::min(tcol + pcol[k], plast[k]);
             dst[k] = ld_u32x4(w + (uint64_t)rr * rb + col);
         }
+    };
+    // stage 0 = (slice 0, group 0 = bx); every work-group has at least one
+    // group in its K part
+    gload_at((uint32_t)bx * R, (uint32_t)(sl0 * C * kBlockBytes), stg[0]);
+    const int groups = (n + R - 1) / R;
+    const int my_groups = (groups - bx + G - 1) / G;
+    const int Q = my_groups * slices;  // stage q = (slice q / my_groups, group q % my_groups)
+    auto gload = [&](int q, u32x4(&dst)[IPW]) {
+        q = std::min(q, Q - 1);
+        const int sl = q / my_groups, t = q - sl * my_groups;
+        gload_at(((uint32_t)bx + (uint32_t)t * (uint32_t)G) * R,
+                 (uint32_t)((sl0 + sl) * C * kBlockBytes), dst);
     };
     auto lstore = [&](const u32x4(&src)[IPW]) {
 #pragma unroll
@@ -269,7 +276,7 @@ __global__ __launch_bounds__(512) void gemv_batched_mfma_kernel(const uint8_t *_
     };
     load_a(0, anext, mnext);
 #pragma unroll
-    for (int f = 0; f < PF; ++f) gload(f, stg[f]);
+    for (int f = 1; f < PF; ++f) gload(f, stg[f]);
 
     auto step = [&](const int q, auto fc, const bool more) {
         constexpr int F = decltype(fc)::value;
