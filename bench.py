@@ -320,6 +320,8 @@ def cpu_flat_baseline(w, x, n: int, k: int, launch_gb: float, target_s: float = 
         t_total += time.perf_counter() - t
         reps += 1
     return {"value": round(launch_gb * reps / t_total, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "stand_in": "no reference CPU path exists for the flattened layout; this is the oracle's "
+                        "f64 flat-layout dequant-dot, not a restatement of a reference CPU kernel",
             "sample": f"oracle flat-layout dequant-dot (f64) on one 4864x896 launch, x {reps} passes, "
                       f"{t_total:.1f} s on 1 thread (the reference has no CPU path for this layout)",
             "cpu_model": cpu_model(), "host_logical_cpus": os.cpu_count()}
