@@ -1,7 +1,7 @@
 // Host-side check of the persistent launch schedule (q4k_launch.hpp): for
-// every shape, each row group is assigned to exactly one (work-group, round)
-// and no work-group takes more rounds than the launch sizes its result
-// buffer for. Built with hipcc and run by tests/test_native_sched.py; with no
+// every shape, each row group is assigned to exactly one (work-group, round),
+// work-group b's first row group is b, and no work-group takes more rounds
+// than the launch sizes its result buffer for. Built with hipcc and run by tests/test_native_sched.py; with no
 // device visible, device_cus() reports 256.
 #include "../../modgrad_amd/csrc/q4k_launch.hpp"
 
@@ -16,6 +16,13 @@ int main() {
             const int G = (int)p.grid;
             std::vector<int> hits(groups, 0);
             for (int b = 0; b < G; ++b) {
+                // the GEMV issues its first stage before computing the
+                // schedule, assuming work-group b's first row group is b
+                if (mgq::sched_group(p.sch, b, G, 0) != b) {
+                    std::printf("FAIL groups=%ld occ=%d b=%d first group %d\n", groups, occ, b,
+                                mgq::sched_group(p.sch, b, G, 0));
+                    return 1;
+                }
                 const int c = mgq::sched_count(p.sch, b, G, (int)groups);
                 if (c > p.rounds || c < 1) {
                     std::printf("FAIL groups=%ld occ=%d b=%d count=%d rounds=%ld\n", groups, occ, b,

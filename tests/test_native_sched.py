@@ -1,8 +1,9 @@
 """The persistent launch schedule of the matrix-core GEMV and Q6_K kernels
 (modgrad_amd/csrc/q4k_launch.hpp: persistent_plan, sched_count, sched_group),
 compiled for the host and checked over ~3,600 shapes: every row group is
-streamed by exactly one (work-group, round), and no work-group takes more
-rounds than its result buffer holds."""
+streamed by exactly one (work-group, round), work-group b starts with row
+group b (the GEMV issues that stage's loads before computing the schedule),
+and no work-group takes more rounds than its result buffer holds."""
 import os
 import shutil
 import subprocess
