@@ -918,6 +918,41 @@ def profiled_traffic(workload: str, impl: str = "graph"):
     return None
 
 
+def other_configs(torch, q4k, steps: int) -> dict:
+    """BASELINE configs 1, 2, 4 (B = 8) and 5 measured after the headline's
+    timed region, each as its own --workload line measures it (graph
+    replays over rotating weight copies, oracle parity on sampled rows) but
+    with fewer replays and no CPU baseline, so that the default line records
+    every config."""
+    ns = argparse.Namespace(steps=steps, warmup=2, batch=8)
+    out = {}
+    r = run_config1(torch, q4k, ns)
+    out["config1"] = {"workload": r["workload"], "kernel": r["kernel"],
+                      "us_per_launch": r["us_per_launch"], "gbs": round(r["gbs"], 1),
+                      "hbm_frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "parity": r["parity"]}
+    del r
+    wl = Workload(torch, layer_shapes(), copies=10)
+    out["config2"] = {"workload": "layer: q,k,v,o,gate,up,down of one 7B layer, unfused, "
+                                  "10 rotating weight copies, one graph per shape",
+                      "kernel": "mgq::gemv_mfma_kernel", "per_shape": shape_times(torch, q4k, wl),
+                      "parity": check_parity(torch, wl)}
+    del wl
+    r = run_batched(torch, q4k, ns)
+    out["config4"] = {"workload": r["workload"], "kernel": r["kernel"],
+                      "us_per_launch": r["us_per_launch"], "gbs": round(r["gbs"], 1),
+                      "hbm_frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "per_shape": r["per_shape"],
+                      "parity": r["parity"]}
+    del r
+    r = run_prefill(torch, q4k, ns)
+    out["config5"] = {"workload": r["workload"], "kernel": r["kernel"],
+                      "us_per_launch": r["us_per_launch"], "tflops": round(r["tflops"], 1),
+                      "mfma_frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
+                      "parity": r["parity"]}
+    del r
+    torch.cuda.empty_cache()
+    return out
+
+
 def run_side_workload(torch, q4k, args) -> int:
     """BASELINE configs 1, 4 and 5: one JSON line each, same field layout."""
     fn = {"config1": run_config1, "batched": run_batched, "prefill": run_prefill,
@@ -978,7 +1013,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
     ap.add_argument("--no-shapes", action="store_true",
-                    help="decode7b/layer/gateup: skip the per-shape times after the timed region")
+                    help="decode7b/layer/gateup: skip the per-shape times (and, for decode7b, "
+                         "BASELINE configs 1, 2, 4, 5) measured after the timed region")
     ap.add_argument("--chain", default="auto", choices=sorted(CHAIN_MODES),
                     help="decode7b/layer/gateup: the chain's implementation")
     args = ap.parse_args()
@@ -1027,6 +1063,13 @@ def main() -> int:
             ", ".join(f"{k} {v['us_per_launch']} us" for k, v in shapes.items()))
     parity = "skipped" if args.no_parity else check_parity(torch, wl)
     log(f"parity: {parity}")
+    configs = None
+    if args.workload == "decode7b" and not args.no_shapes:
+        configs = other_configs(torch, q4k, steps=20)
+        for key, c in configs.items():
+            log(f"{key}: " + (", ".join(f"{k} {v['us_per_launch']} us" for k, v in
+                                        c["per_shape"].items()) if key == "config2"
+                              else f"{c['us_per_launch']} us per launch") + f"; parity {c['parity']}")
     nl = len(wl.launches)
     if impl == "persistent":
         # one cooperative launch per step runs all the matvecs: the kernel's
@@ -1073,6 +1116,8 @@ def main() -> int:
         out["host_us_per_launch_call"] = round(host_us, 3)
     if shapes is not None:
         out["per_shape"] = shapes
+    if configs is not None:
+        out["other_configs"] = configs
     if not args.no_cpu:
         threads = cpu_threads()
         log(f"cpu baseline ({threads} threads, ~{args.cpu_seconds:.0f} s, then 1 thread ~5 s)")
