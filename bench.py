@@ -60,6 +60,23 @@ def decode_step_shapes():
     return shapes
 
 
+def shard_step_shapes(g: int):
+    """One GPU's share of the decode step when it is sharded over g GPUs (the
+    plan for more than one GPU): q/k/v, gate|up and lm_head split by rows,
+    o and down by K at super-block boundaries (the largest share, when the
+    blocks do not divide evenly); every GPU then holds a slice of every
+    matvec and runs the same 113 launches at these shapes."""
+    qkv = NQ * HEAD + 2 * NKV * HEAD
+    bo = -(-(NQ * HEAD // BLOCK_ELEMS) // g) * BLOCK_ELEMS
+    bd = -(-(INTER // BLOCK_ELEMS) // g) * BLOCK_ELEMS
+    shapes = []
+    for l in range(LAYERS):
+        shapes += [(f"L{l}.qkv", -(-qkv // g), HIDDEN), (f"L{l}.o", HIDDEN, bo),
+                   (f"L{l}.gate_up", -(-2 * INTER // g), HIDDEN), (f"L{l}.down", HIDDEN, bd)]
+    shapes.append(("lm_head", -(-VOCAB // g), HIDDEN))
+    return shapes
+
+
 def layer_shapes():
     """the 7 per-layer matvecs, unfused."""
     return [("q", HIDDEN, HIDDEN), ("k", NKV * HEAD, HIDDEN), ("v", NKV * HEAD, HIDDEN),
@@ -1007,7 +1024,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="decode7b",
                     choices=["decode7b", "layer", "gateup", "config1", "batched", "prefill",
-                             "decode7b_dp4a", "q5k", "q6k", "decode7b_glue", "decode7b_q4km"])
+                             "decode7b_dp4a", "q5k", "q6k", "decode7b_glue", "decode7b_q4km",
+                             "shard"])
+    ap.add_argument("--shards", type=int, default=8,
+                    help="--workload shard: one GPU's share of the decode step over this many GPUs")
     ap.add_argument("--batch", type=int, default=8, help="batch for --workload batched (1..16)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -1037,6 +1057,15 @@ def main() -> int:
         wl = Workload(torch, decode_step_shapes())
         desc = ("decode7b: 28 x (qkv 4608x3584, o 3584x3584, gate|up 37888x3584, down 3584x18944) "
                 "+ lm_head 152064x3584, batch 1, one HIP graph per step")
+    elif args.workload == "shard":
+        g = max(1, args.shards)
+        wl = Workload(torch, shard_step_shapes(g))
+        qkv = NQ * HEAD + 2 * NKV * HEAD
+        desc = (f"shard: one GPU's share of decode7b over {g} GPUs (rows: qkv {-(-qkv // g)}x3584, "
+                f"gate|up {-(-2 * INTER // g)}x3584, lm_head {-(-VOCAB // g)}x3584; K: o 3584x"
+                f"{-(-14 // g) * 256}, down 3584x{-(-74 // g) * 256}), 113 launches, one HIP graph "
+                "per step; collectives not included")
+        args.no_cpu = True
     elif args.workload == "layer":
         # 7 unfused launches x 10 rotating copies (1.3 GB) so the 256 MB MALL cannot hold them
         wl = Workload(torch, layer_shapes(), copies=10)
