@@ -34,7 +34,12 @@
 //        of the one being computed.
 //    Per 32 rows x 1 block a wave issues 16 MFMAs and about 220 VALU ops.
 //
-// 3. gemv_batched_kernel -- vector-ALU batched GEMV (up to 16 activation rows).
+// 3. gemv_wave_kernel -- the same arithmetic with every wavefront staging
+//    its own unit through its own LDS slot, so stages need no work-group
+//    barrier; used for plain f32 matvecs whose work-groups stream several
+//    stages (gate|up, lm_head, down).
+//
+// 4. gemv_batched_kernel -- vector-ALU batched GEMV (up to 16 activation rows).
 #include "q4k_device.hpp"
 #include "q4k_launch.hpp"
 
@@ -795,6 +800,296 @@ static int env_int(const char *name, int dflt) {
 }
 
 
+// ---------------------------------------------------------- wave-private ---
+// gemv_wave_kernel: the matrix-core GEMV with every wavefront streaming its
+// own unit (f32 activations, Q4_K). The stage of a row group is UNITS = NW
+// units (R = 16: blocks 2u, 2u+1 of the 16 rows; R = 32: block u of both
+// 16-row tiles); wavefront u loads exactly the 288 16-byte pieces of unit u
+// (18- or 9-piece runs of its rows, 16 bytes per lane), stores them to its own
+// LDS slot and computes from it, so no work-group barrier sits between
+// stages: a wavefront starts on its unit as soon as its own pieces land. Its
+// row sums of each row group go to LDS (one slot per group and wavefront)
+// and are reduced across wavefronts once, after the stream, in the same
+// order as gemv_mfma_kernel (identical results).
+struct WaveLayout {
+    uint32_t meta, slots, aux;
+    size_t total;
+};
+template <int R, int NW>
+__host__ __device__ constexpr uint32_t wave_slot_pitch() { return R == 32 ? 9u : 19u; }  // pieces per row
+template <int R, int NW>
+__host__ __device__ inline WaveLayout wave_layout(int bpr, int rounds) {
+    WaveLayout L;
+    L.meta = (uint32_t)bpr * 1040u;
+    L.slots = L.meta + (uint32_t)bpr * 64u;
+    L.aux = L.slots + (uint32_t)NW * R * wave_slot_pitch<R, NW>() * 16u;
+    L.total = (size_t)L.aux + (size_t)rounds * NW * R * 4;
+    return L;
+}
+
+template <int R, int C, int NW, int XIT>
+__global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__restrict__ w,
+                                                            const float *__restrict__ x,
+                                                            float *__restrict__ y, int n, int bpr,
+                                                            int rounds, GemvSched sch, int gr) {
+    constexpr int UNITS = (R == 32) ? C : C / 2;
+    static_assert(UNITS == NW, "one unit per wavefront and stage");
+    static_assert(R == 32 || C % 2 == 0, "R = 16: a unit is a pair of blocks");
+    constexpr int BP = 9, BB = 144;
+    constexpr int RUN = (R == 32) ? BP : 2 * BP;         // pieces of one row in a unit
+    constexpr int UP = R * RUN;                          // pieces per unit (288)
+    constexpr int IPW = (UP + 63) / 64;                  // wave loads per unit
+    constexpr uint32_t SP = wave_slot_pitch<R, NW>();    // LDS pieces per slot row
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const WaveLayout Lo = wave_layout<R, NW>(bpr, rounds);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    float *meta = reinterpret_cast<float *>(lds + Lo.meta);
+    float *aux = reinterpret_cast<float *>(lds + Lo.aux);
+    const size_t row_bytes = (size_t)bpr * BB;
+    const int stages = (bpr + C - 1) / C;
+    // this wavefront's unit: blocks cb0 (and cb0 + 1 when R = 16) of each stage
+    const int cb0 = (R == 32) ? wave : 2 * wave;
+    uint8_t *slot = lds + Lo.slots + (uint32_t)wave * (R * SP * 16u);
+
+    // piece p of the unit: row p / RUN, piece p % RUN of the row's run (R = 16:
+    // block cb0 + (p % RUN) / 9), clamped past the unit's 288
+    uint32_t prow[IPW], pcol[IPW], plds[IPW], ppc[IPW];
+#pragma unroll
+    for (int k = 0; k < IPW; ++k) {
+        const int p = std::min(k * 64 + lane, UP - 1);
+        const int row = p / RUN, rem = p - row * RUN;
+        prow[k] = (uint32_t)row;
+        pcol[k] = (uint32_t)(cb0 * BB + 16 * rem);       // byte column within the stage
+        ppc[k] = (uint32_t)(16 * (rem % BP));             // the piece within its block
+        plds[k] = (uint32_t)((row * SP + rem) * 16);
+    }
+    u32x4 stg[IPW];
+    // unit pieces of stage column tcol of the rows from r0 (the tile rows past
+    // the group re-read its last row; blocks past the row end re-read the last)
+    auto gload_at = [&](uint32_t r0, uint32_t tcol) {
+        const uint32_t glast = (uint32_t)gr - 1u, rlast = (uint32_t)(n - 1);
+        const uint32_t rb = (uint32_t)row_bytes, lastb = (uint32_t)((bpr - 1) * BB);
+#pragma unroll
+        for (int k = 0; k < IPW; ++k) {
+            const uint32_t rr = std::min(r0 + std::min(prow[k], glast), rlast);
+            const uint32_t c0 = tcol + pcol[k];
+            const uint32_t col = std::min(c0 - ppc[k], lastb) + ppc[k];
+            stg[k] = ld_u32x4(w + ((uint64_t)rr * rb + col));
+        }
+    };
+    auto lstore = [&]() {
+#pragma unroll
+        for (int k = 0; k < IPW; ++k) *reinterpret_cast<u32x4 *>(slot + plds[k]) = stg[k];
+    };
+
+    // ---- prologue: x loads, the first unit, then the activation table -------
+    const int nitems = bpr * 32;
+    const int its = (nitems + NW * 64 - 1) / (NW * 64);
+    f32x4 xv0[XIT], xv1[XIT];
+#pragma unroll
+    for (int it = 0; it < XIT; ++it) {
+        if (it >= its) break;
+        const int i = std::min(tid + it * NW * 64, nitems - 1);
+        xv0[it] = ld_f32x4(x + (size_t)i * 8);
+        xv1[it] = ld_f32x4(x + (size_t)i * 8 + 4);
+    }
+    gload_at((uint32_t)blockIdx.x * (uint32_t)gr, 0u);
+    const int groups = (n + gr - 1) / gr;
+    const int my_groups = sched_count(sch, (int)blockIdx.x, (int)gridDim.x, groups);
+    const int Q = my_groups * stages;
+    __asm__ volatile("" : : "s"(Q), "s"(my_groups));
+
+    for (int b = tid; b < bpr; b += NW * 64)
+        *reinterpret_cast<u32x4 *>(lds + (size_t)b * 1040 + 1024) = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int it = 0; it < XIT; ++it) {
+        if (it >= its) break;
+        const int i = tid + it * NW * 64;
+        const f32x4 v0 = xv0[it], v1 = xv1[it];
+        float amax = fmaxf(fmaxf(fmaxf(fabsf(v0[0]), fabsf(v0[1])), fmaxf(fabsf(v0[2]), fabsf(v0[3]))),
+                           fmaxf(fmaxf(fabsf(v1[0]), fabsf(v1[1])), fmaxf(fabsf(v1[2]), fabsf(v1[3]))));
+        float sum = ((v0[0] + v0[1]) + (v0[2] + v0[3])) + ((v1[0] + v1[1]) + (v1[2] + v1[3]));
+        amax = fmaxf(amax, quad_xor<1>(amax));
+        amax = fmaxf(amax, quad_xor<2>(amax));
+        sum += quad_xor<1>(sum);
+        sum += quad_xor<2>(sum);
+        if (i >= nitems) continue;
+        int e = 0;
+        if (amax > 0.0f && amax <= 3.402823466e38f) {
+            int ex;
+            frexpf(amax, &ex);
+            e = std::min(std::max(14 - ex, -90), 140);
+        }
+        const int b = i >> 5, sb = (i >> 2) & 7, j = i & 3;
+        if (j == 0) {
+            meta[b * 16 + sb] = ldexpf(1.0f, ((sb & 1) ? 20 : 24) - e);
+            meta[b * 16 + 8 + sb] = sum;
+        }
+        const int G = sb >> 1;
+        const int c = 2 * (2 * (G >> 1) + (j & 1)) + (sb & 1), h = 2 * (G & 1) + (j >> 1);
+        const float xs[8] = {v0[0], v0[2], v0[1], v0[3], v1[0], v1[2], v1[1], v1[3]};
+        u32x4 hh, hl;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float a0 = ldexpf(xs[2 * q], e), a1 = ldexpf(xs[2 * q + 1], e);
+            const auto hp = __builtin_amdgcn_cvt_pkrtz(a0, a1);
+            const auto lp = __builtin_amdgcn_cvt_pkrtz(a0 - (float)hp[0], a1 - (float)hp[1]);
+            hh[q] = __builtin_bit_cast(uint32_t, hp);
+            hl[q] = __builtin_bit_cast(uint32_t, lp);
+        }
+        uint8_t *ent = lds + (size_t)b * 1040 + (size_t)((c * 4 + h) * 32);
+        *reinterpret_cast<u32x4 *>(ent) = hh;
+        *reinterpret_cast<u32x4 *>(ent + 16) = hl;
+    }
+    __syncthreads();  // the table is complete; from here no wavefront waits for another
+
+    // ---- per-lane constants (as in gemv_mfma_kernel) ------------------------
+    const int n16 = lane & 15, g = lane >> 4, jq = g >> 1, sh = 16 * (g & 1);
+    const uint32_t lmask = jq ? 0x0F0F0F0Fu : 0x3F3F3F3Fu, hmask = jq ? 0x30303030u : 0u;
+    uint32_t aoff[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const int o = pair_byte_offset(c >> 1, g);
+        const int sb = 2 * (o >> 5) + (c & 1);
+        const bool hit = (n16 >> 1) == sb;
+        aoff[c] = hit ? (uint32_t)((c * 4 + g) * 32 + (n16 & 1) * 16) : 1024u;
+    }
+    auto decode = [&](const u32x4 &hd, int b, float s0, float s1) -> float {
+        const float d = half_bits_finite(hd[0]), dmin = half_bits_finite(hd[0] >> 16);
+        const uint32_t scs = jq ? hd[3] : hd[1], mns = jq ? (hd[3] >> 4) : hd[2];
+        const uint32_t scq = ((scs & lmask) | ((hd[1] >> 2) & hmask)) >> sh;
+        const uint32_t mnq = ((mns & lmask) | ((hd[2] >> 2) & hmask)) >> sh;
+        const float *mb = meta + b * 16 + 2 * g;
+        const float t1 = (float)(scq & 0xFFu) * (s0 * mb[0]) + (float)((scq >> 8) & 0xFFu) * (s1 * mb[1]);
+        const float t2 = (float)(mnq & 0xFFu) * mb[8] + (float)((mnq >> 8) & 0xFFu) * mb[9];
+        return d * t1 - dmin * t2;
+    };
+    auto piece = [&](int row, int cbl, int pc) -> const u32x4 & {
+        return *reinterpret_cast<const u32x4 *>(slot + (row * SP + cbl * BP + pc) * 16);
+    };
+
+    float yaccA = 0.0f, yaccB = 0.0f;
+    for (int q = 0; q < Q; ++q) {
+        const int t = q % stages;
+        lstore();
+        __asm__ volatile("" ::: "memory");  // the unit's reads follow its stores (in-order LDS)
+        {
+            // the next unit (past the last one: the last again, a cache hit),
+            // unconditional so the load-counter waits stay exact
+            const int q1 = std::min(q + 1, Q - 1);
+            const uint32_t r0 =
+                (uint32_t)sched_group(sch, (int)blockIdx.x, (int)gridDim.x, q1 / stages) * (uint32_t)gr;
+            gload_at(r0, (uint32_t)((q1 % stages) * C * BB));
+        }
+        const int bA = t * C + cb0, bB = (R == 32) ? bA : bA + 1;
+        if (bA < bpr) {
+            const bool hasB = bB < bpr;
+            const int bBc = hasB ? bB : bA;
+            const int rowB = (R == 32) ? 16 : 0, cbB = (R == 32) ? 0 : 1;
+            const u32x4 qa0 = piece(n16, 0, 1 + g), qa1 = piece(n16, 0, 5 + g);
+            const u32x4 qb0 = piece(rowB + n16, cbB, 1 + g), qb1 = piece(rowB + n16, cbB, 5 + g);
+            const u32x4 hdA = piece(n16, 0, 0), hdB = piece(rowB + n16, cbB, 0);
+            f32x4 accA = {0.f, 0.f, 0.f, 0.f}, accB = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const half8 aA = *reinterpret_cast<const half8 *>(lds + (uint32_t)bA * 1040u + aoff[c]);
+                const half8 aB = (R == 32) ? aA
+                    : *reinterpret_cast<const half8 *>(lds + (uint32_t)bBc * 1040u + aoff[c]);
+                const int p = c >> 1;
+                const uint32_t mask = (c & 1) ? 0x00F000F0u : 0x000F000Fu;
+                const uint32_t wa0 = p < 2 ? qa0[2 * p] : qa1[2 * p - 4];
+                const uint32_t wa1 = p < 2 ? qa0[2 * p + 1] : qa1[2 * p - 3];
+                const uint32_t wb0 = p < 2 ? qb0[2 * p] : qb1[2 * p - 4];
+                const uint32_t wb1 = p < 2 ? qb0[2 * p + 1] : qb1[2 * p - 3];
+                const u32x4 ba = u32x4{wa0 & mask, (wa0 >> 8) & mask, wa1 & mask, (wa1 >> 8) & mask};
+                const u32x4 bb = u32x4{wb0 & mask, (wb0 >> 8) & mask, wb1 & mask, (wb1 >> 8) & mask};
+                accA = __builtin_amdgcn_mfma_f32_16x16x32_f16(aA, __builtin_bit_cast(half8, ba), accA, 0, 0, 0);
+                accB = __builtin_amdgcn_mfma_f32_16x16x32_f16(aB, __builtin_bit_cast(half8, bb), accB, 0, 0, 0);
+            }
+            const float cA = decode(hdA, bA, accA[0] + accA[1], accA[2] + accA[3]);
+            const float cB = decode(hdB, bBc, accB[0] + accB[1], accB[2] + accB[3]);
+            if (R == 32) {
+                yaccA += cA;
+                yaccB += cB;
+            } else {
+                yaccA += hasB ? cA + cB : cA;
+            }
+        }
+        if (t == stages - 1) {
+            // this wavefront's sums of the group's rows, to its own slot
+            yaccA += __shfl_xor(yaccA, 16, 64);
+            yaccA += __shfl_xor(yaccA, 32, 64);
+            yaccB += __shfl_xor(yaccB, 16, 64);
+            yaccB += __shfl_xor(yaccB, 32, 64);
+            float *ag = aux + ((size_t)(q / stages) * NW + wave) * R;
+            if (lane < 16) {
+                ag[lane] = yaccA;
+                if (R == 32) ag[16 + lane] = yaccB;
+            }
+            yaccA = 0.0f;
+            yaccB = 0.0f;
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < my_groups * R; i += NW * 64) {
+        const int gi = i / R, ri = i % R;
+        const int r = sched_group(sch, (int)blockIdx.x, (int)gridDim.x, gi) * gr + ri;
+        if (ri < gr && r < n) {
+            const float *ag = aux + (size_t)gi * NW * R + ri;
+            float sum = 0.0f;
+            for (int wv = 0; wv < NW; ++wv) sum += ag[wv * R];
+            y[r] = sum;
+        }
+    }
+}
+
+template <int R, int C, int NW, int XIT>
+static hipError_t launch_wave_xit(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                                  hipStream_t stream, bool persistent, int gr) {
+    auto kern = gemv_wave_kernel<R, C, NW, XIT>;
+    const hipError_t attr = allow_full_lds_by_addr((const void *)kern);
+    if (attr != hipSuccess) return attr;
+    if (gr <= 0 || gr > R) gr = R;
+    const long groups = (n + gr - 1) / gr;
+    long grid = groups, rounds = 1;
+    GemvSched sch{(int)groups, 0};
+    if (persistent) {
+        const size_t base = wave_layout<R, NW>(bpr, 8).total;
+        const int occ = occupancy_cached((const void *)kern, NW * 64, base,
+                                         (int)std::min<size_t>(4, (160 * 1024) / base));
+        const PersistPlan p = persistent_plan(groups, occ);
+        grid = p.grid;
+        rounds = p.rounds;
+        sch = p.sch;
+    }
+    const WaveLayout Lo = wave_layout<R, NW>(bpr, (int)rounds);
+    if (Lo.total > 160 * 1024) return hipErrorNotSupported;
+    kern<<<(unsigned)grid, NW * 64, Lo.total, stream>>>(w, x, y, n, bpr, (int)rounds, sch, gr);
+    return hipGetLastError();
+}
+
+// the kernels' LDS limit, set outside any stream capture
+template <int R, int C, int NW>
+static hipError_t wave_prepare() {
+    hipError_t e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<R, C, NW, 1>);
+    if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<R, C, NW, 2>);
+    if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<R, C, NW, 4>);
+    if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<R, C, NW, 8>);
+    return e;
+}
+
+template <int R, int C, int NW>
+static hipError_t launch_wave(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                              hipStream_t stream, bool persistent, int gr = 0) {
+    const int need = (bpr * 32 + NW * 64 - 1) / (NW * 64);
+    if (need <= 1) return launch_wave_xit<R, C, NW, 1>(w, x, y, n, bpr, stream, persistent, gr);
+    if (need <= 2) return launch_wave_xit<R, C, NW, 2>(w, x, y, n, bpr, stream, persistent, gr);
+    if (need <= 4) return launch_wave_xit<R, C, NW, 4>(w, x, y, n, bpr, stream, persistent, gr);
+    if (need <= 8) return launch_wave_xit<R, C, NW, 8>(w, x, y, n, bpr, stream, persistent, gr);
+    return hipErrorNotSupported;
+}
+
 // Activation operands of one launch: f32 x, or (Q8) int8 xq with its
 // per-sub-block scale xd and sum xsum.
 struct GemvAct {
@@ -919,6 +1214,8 @@ hipError_t gemv_prepare() {
     if (e == hipSuccess) e = prepare_fuse<kFuseGlu>();
     if (e == hipSuccess) e = prepare_fuse<kFuseNorm | kFuseGlu>();
     if (e == hipSuccess) e = q6k_prepare();
+    if (e == hipSuccess) e = wave_prepare<16, 14, 7>();
+    if (e == hipSuccess) e = wave_prepare<16, 16, 8>();
     return e;
 }
 
@@ -950,7 +1247,22 @@ static hipError_t mfma_dispatch(const uint8_t *w, const GemvAct &a, float *y, in
             cfg = 8;
         }
     }
-    hipError_t e = launch_any<Q8, FUSE>(cfg, w, a, fz, y, n, bpr, stream, gr);
+    hipError_t e = hipErrorNotSupported;
+    if constexpr (!Q8 && FUSE == 0) {
+        // Plain f32 matvecs whose work-groups stream more than one stage:
+        // the wave-private kernel (no barrier between stages). Decode step,
+        // alternating on one box: 1182-1183 -> 1140-1141 us (gate|up -0.8,
+        // down -0.55 us per launch). One-stage launches (o, qkv: 256 groups
+        // or fewer) measured 0.1-0.3 us slower on it and keep the staged
+        // kernel. MGQ_GEMV_WAVE=0 turns it off.
+        static const int wave_env = env_int("MGQ_GEMV_WAVE", 1);
+        const bool multi = (long)(n + 15) / 16 > 2 * device_cus();
+        if (wave_env && force < 0) {
+            if (cfg == 6 && multi) e = launch_wave<16, 14, 7>(w, a.x, y, n, bpr, stream, true);
+            else if (cfg == 2) e = launch_wave<16, 16, 8>(w, a.x, y, n, bpr, stream, false);
+        }
+    }
+    if (e == hipErrorNotSupported) e = launch_any<Q8, FUSE>(cfg, w, a, fz, y, n, bpr, stream, gr);
     // LDS too small for the double-buffered stages (Q5_K's 176-byte blocks on
     // down): single-buffered 16-row stages (26.2 -> 17.9 us on Q5_K
     // 3584x18944), then persistent 32-row groups
