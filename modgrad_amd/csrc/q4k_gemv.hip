@@ -1215,7 +1215,7 @@ hipError_t gemv_prepare() {
     if (e == hipSuccess) e = prepare_fuse<kFuseNorm | kFuseGlu>();
     if (e == hipSuccess) e = q6k_prepare();
     if (e == hipSuccess) e = wave_prepare<16, 14, 7>();
-    if (e == hipSuccess) e = wave_prepare<16, 16, 8>();
+    if (e == hipSuccess) e = wave_prepare<16, 20, 10>();
     return e;
 }
 
@@ -1252,14 +1252,16 @@ static hipError_t mfma_dispatch(const uint8_t *w, const GemvAct &a, float *y, in
         // Plain f32 matvecs whose work-groups stream more than one stage:
         // the wave-private kernel (no barrier between stages). Decode step,
         // alternating on one box: 1182-1183 -> 1140-1141 us (gate|up -0.8,
-        // down -0.55 us per launch). One-stage launches (o, qkv: 256 groups
-        // or fewer) measured 0.1-0.3 us slower on it and keep the staged
-        // kernel. MGQ_GEMV_WAVE=0 turns it off.
+        // down -0.55 us per launch), and 20-block stages over 10 wavefronts
+        // for the long rows: 1146 -> 1137-1138 us (down 12.3 -> 12.0 us;
+        // 16 / 26 / 28 / 32 blocks: 12.3 / 12.0 / 12.45 / 12.75 us). One-stage
+        // launches (o, qkv: 256 groups or fewer) measured 0.1-0.3 us slower
+        // on it and keep the staged kernel. MGQ_GEMV_WAVE=0 turns it off.
         static const int wave_env = env_int("MGQ_GEMV_WAVE", 1);
         const bool multi = (long)(n + 15) / 16 > 2 * device_cus();
         if (wave_env && force < 0) {
             if (cfg == 6 && multi) e = launch_wave<16, 14, 7>(w, a.x, y, n, bpr, stream, true);
-            else if (cfg == 2) e = launch_wave<16, 16, 8>(w, a.x, y, n, bpr, stream, false);
+            else if (cfg == 2) e = launch_wave<16, 20, 10>(w, a.x, y, n, bpr, stream, false);
         }
     }
     if (e == hipErrorNotSupported) e = launch_any<Q8, FUSE>(cfg, w, a, fz, y, n, bpr, stream, gr);
