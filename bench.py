@@ -848,7 +848,7 @@ def run_decode_q4km(torch, q4k, args):
                         f"{launches[0]} launches), one mgq_chain_create_ops graph",
             "us_per_launch": round(ms * 1e3 / launches[0], 3), "gbs": qbytes / (ms * 1e-3) / 1e9,
             "bytes_per_launch": qbytes // launches[0], "parity": parity,
-            "kernel": "mgq::gemv_mfma_kernel + mgq::gemv_q6k_mfma_kernel / _long_kernel",
+            "kernel": "mgq::gemv_wave_kernel / gemv_mfma_kernel + mgq::gemv_q6k_mfma_kernel / _long_kernel",
             "tokens_per_s": 1000.0 / ms, "ms_per_step": ms}
 
 
@@ -951,7 +951,8 @@ def other_configs(torch, q4k, steps: int) -> dict:
     wl = Workload(torch, layer_shapes(), copies=10)
     out["config2"] = {"workload": "layer: q,k,v,o,gate,up,down of one 7B layer, unfused, "
                                   "10 rotating weight copies, one graph per shape",
-                      "kernel": "mgq::gemv_mfma_kernel", "per_shape": shape_times(torch, q4k, wl),
+                      "kernel": "mgq::gemv_wave_kernel (gate, up, down) + mgq::gemv_mfma_kernel",
+                      "per_shape": shape_times(torch, q4k, wl),
                       "parity": check_parity(torch, wl)}
     del wl
     r = run_batched(torch, q4k, ns)
@@ -1105,9 +1106,11 @@ def main() -> int:
         # launch is the step, its bytes the step's
         kernel, avg_s, avg_b = "mgq::chain_kernel<2>", ms * 1e-3, wl.bytes_per_pass
     else:
-        # back-to-back GEMV launches (one graph per step): the kernel's average
-        # launch duration is the step time over its launches
-        kernel, avg_s, avg_b = "mgq::gemv_mfma_kernel", ms * 1e-3 / nl, wl.bytes_per_pass / nl
+        # back-to-back GEMV launches (one graph per step): the kernels' average
+        # launch duration is the step time over its launches (gate|up, down and
+        # lm_head on the wave-private kernel, qkv and o on the staged one)
+        kernel, avg_s, avg_b = ("mgq::gemv_wave_kernel + mgq::gemv_mfma_kernel", ms * 1e-3 / nl,
+                                wl.bytes_per_pass / nl)
     achieved = avg_b / avg_s / 1e9
     log(f"kernel {kernel} avg {avg_s * 1e6:.3f} us per launch, {achieved:.1f} GB/s")
 
