@@ -545,7 +545,7 @@ def run_batched(torch, q4k, args):
                         f"{copies} rotating copies, one graph",
             "us_per_launch": round(ms * 1e3 / len(items), 3), "gbs": nbytes / (ms * 1e-3) / 1e9,
             "bytes_per_launch": nbytes // len(items), "parity": parity, "per_shape": per_shape,
-            "kernel": "mgq::gemv_batched_mfma_kernel (+ batched_table_kernel)",
+            "kernel": "mgq::gemv_batched_wave_kernel (+ batched_table_kernel)",
             "cpu": (jobs, pass_bytes / 1e9, "GB/s",
                     f"one gate and one down call at B={B} as {len(jobs)} CPU matvecs "
                     f"({pass_bytes / 1e6:.1f} MB per pass as the GPU line counts it)", 2)}

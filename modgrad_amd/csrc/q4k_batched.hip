@@ -3,7 +3,7 @@
 // reference; the oracle is its f64 dequant-dot (rocm_matvec_check.rs:38-47)
 // applied row by row.
 //
-// Two kernels:
+// Three kernels:
 //
 // 1. batched_table_kernel turns X into matrix-core A operands, once per call,
 //    in a caller-provided workspace. Batch b of a set of 8 occupies MFMA rows
@@ -13,10 +13,13 @@
 //    operand per (block, set) carries the 8 sub-block sums of x (same split)
 //    for the dmin*m term.
 //
-// 2. gemv_batched_mfma_kernel streams the weights exactly as the GEMV does
-//    (fully coalesced 16-byte loads -> registers -> LDS stage of 16 rows x 8
-//    blocks) and keeps the batch on the MFMA M dimension, so one weight
-//    operand serves 8 batch rows per v_mfma_f32_16x16x32_f16:
+// 2. gemv_batched_wave_kernel (the default) and 3. gemv_batched_mfma_kernel
+//    (the stage kernel: shapes whose per-wavefront row sums do not fit LDS)
+//    keep the batch on the MFMA M dimension, so one weight operand serves 8
+//    batch rows per v_mfma_f32_16x16x32_f16. The wave kernel has every
+//    wavefront stage its own units (R rows x 1-2 blocks) with no barrier
+//    between them; the stage kernel streams 16 rows x 8 blocks per stage
+//    through LDS as the GEMV's stage kernel does. Both:
 //      * B operand = sc*q: the nibble masked in place is the f16 subnormal
 //        q*2^-24 (low) or 16q*2^-24 (high); one packed f16 multiply by 16*sc
 //        (low) or sc (high) makes it q*sc*2^-20 exactly (q*sc <= 945 fits the
@@ -24,10 +27,10 @@
 //        accumulator and only d is applied afterwards.
 //      * min term: one more MFMA per block with the sub-block sums of x
 //        (A) against m[0..7] of each row (B).
-//      * Stages run K-slice-major (all of a work-group's row groups for
-//        blocks 8s..8s+7, then s+1), so wave w keeps the A operands of block
-//        8s+w in registers for the whole slice; per-stage partial sums are
-//        reduced across waves into an LDS row buffer.
+//      * Work runs K-slice-major (all of a work-group's row groups for one
+//        slice of blocks, then the next), so a wavefront keeps the A
+//        operands of its blocks of the slice in registers for the whole
+//        slice.
 //      * Shapes with few row groups and a long K split K in two: the table
 //        kernel zeroes Y and each half adds its partials atomically (two
 //        addends onto 0 round the same in either order).
@@ -37,6 +40,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <type_traits>
+#include <utility>
 
 namespace mgq {
 
@@ -76,12 +80,29 @@ __device__ __forceinline__ int split_exponent(float amax) {
     return e;
 }
 
-// grid (bpr, sets), 256 threads: thread = (batch b' = tid/32, 8-float chunk
-// ch of block j). Every A-operand entry of the 8 k-slot groups holds one
-// aligned 8-float chunk of the block (its values in k-slot order
-// 0,2,1,3,4,6,5,7): entry (c, g) takes chunk 16(c>>2) + 8(g>>1) + 4(c&1) +
-// 2(g&1) + ((c>>1)&1) (bt_pair_offset), so the thread that loaded chunk ch
-// writes its two entries (xh and xl rows of its batch) from registers.
+// max over the 16 lanes of each DPP row (quad xor 1, quad xor 2, half-row
+// mirror, row mirror: every lane ends with the row's max)
+__device__ __forceinline__ float row_max16(float v) {
+    v = fmaxf(v, quad_xor<1>(v));
+    v = fmaxf(v, quad_xor<2>(v));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                       0x141, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                       0x140, 0xF, 0xF, false)));
+    return v;
+}
+
+// grid (ceil(bpr / 2), sets), 256 threads = 2 blocks x 8 batches x 16
+// threads: one 16-lane DPP row per batch; thread h of batch b' holds the
+// 8-float chunks 2h and 2h+1 of block j (sub-block h / 2). Every A-operand
+// entry of the 8 k-slot groups holds one aligned 8-float chunk of the block
+// (its values in k-slot order 0,2,1,3,4,6,5,7): entry (c, g) takes chunk
+// 16(c>>2) + 8(g>>1) + 4(c&1) + 2(g&1) + ((c>>1)&1) (bt_pair_offset), so the
+// thread that loaded a chunk writes its two entries (xh and xl rows of its
+// batch) from registers. The block max takes four DPP steps inside the row
+// and the sub-block sum ((c0 + c1) + (c2 + c3) over its chunk sums) one; a
+// layout of 32 lanes per batch needed five and two dependent lane shuffles
+// (same table, ~0.1 us per call less).
 __global__ __launch_bounds__(256) void batched_table_kernel(const float *__restrict__ X, int batch,
                                                             int bpr, int sets, bool x_aligned16,
                                                             uint8_t *__restrict__ ws,
@@ -93,68 +114,69 @@ __global__ __launch_bounds__(256) void batched_table_kernel(const float *__restr
              i += nthr)
             yzero[i] = 0.0f;
     }
-    const int j = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
-    const int bl = tid >> 5, ch = tid & 31, b = s * 8 + bl;
+    const int tid = threadIdx.x, s = blockIdx.y;
+    const int j = (int)blockIdx.x * 2 + (tid >> 7);
+    if (j >= bpr) return;  // both wavefronts of the missing block
+    const int bl = (tid >> 4) & 7, h = tid & 15, b = s * 8 + bl;
     const size_t K = (size_t)bpr * kBlockElems;
-    float v[8];
+    float v[16];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    for (int i = 0; i < 16; ++i) v[i] = 0.0f;
     if (b < batch) {
-        const float *xp = X + (size_t)b * K + (size_t)j * kBlockElems + ch * 8;
+        const float *xp = X + (size_t)b * K + (size_t)j * kBlockElems + h * 16;
         if (x_aligned16) {
-            const f32x4 a = ld_f32x4(xp);
-            const f32x4 c = ld_f32x4(xp + 4);
-            v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
-            v[4] = c[0]; v[5] = c[1]; v[6] = c[2]; v[7] = c[3];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const f32x4 a = ld_f32x4(xp + 4 * q);
+                v[4 * q] = a[0]; v[4 * q + 1] = a[1]; v[4 * q + 2] = a[2]; v[4 * q + 3] = a[3];
+            }
         } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = xp[i];
+            for (int i = 0; i < 16; ++i) v[i] = xp[i];
         }
     }
-    float amax = 0.0f, sum = 0.0f;
+    float amax = 0.0f, c0 = 0.0f, c1 = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        amax = fmaxf(amax, fabsf(v[i]));
-        sum += v[i];
+        amax = fmaxf(amax, fmaxf(fabsf(v[i]), fabsf(v[8 + i])));
+        c0 += v[i];
+        c1 += v[8 + i];
     }
-    // sub-block sums: the 4 chunks of sub-block ch/4 are lanes ch^1, ch^2
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
-    // block max over the 32 chunks of batch b'
-#pragma unroll
-    for (int off = 1; off < 32; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-    const int e = split_exponent(amax);
+    // sub-block sum ((c0 + c1) + (c2 + c3)) of its four chunks, in both lanes
+    float sum = c0 + c1;
+    sum += quad_xor<1>(sum);
+    const int e = split_exponent(row_max16(amax));
     float *meta = reinterpret_cast<float *>(ws + batched_ws(bpr, sets).meta);
     const size_t js = (size_t)j * sets + s;
-    if (ch == 0) meta[(js * 8 + bl) * 2] = ldexpf(1.0f, 20 - e);
+    if (h == 0) meta[(js * 8 + bl) * 2] = ldexpf(1.0f, 20 - e);
 
-    // the two entries of chunk ch: k-slot group c, lanes (m = 2b' + part, g)
     uint8_t *atab = ws + js * kBatchOps * 1024;
-    {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int ch = 2 * h + t;
         const int c = (((ch >> 4) & 1) << 2) | ((ch & 1) << 1) | ((ch >> 2) & 1);
         const int g = (((ch >> 3) & 1) << 1) | ((ch >> 1) & 1);
         constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
         half8 hi, lo;
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            const float xv = ldexpf(v[perm[q]], e);
-            const _Float16 h = (_Float16)xv;
-            hi[q] = h;
-            lo[q] = (_Float16)(xv - (float)h);
+            const float xv = ldexpf(v[8 * t + perm[q]], e);
+            const _Float16 hh = (_Float16)xv;
+            hi[q] = hh;
+            lo[q] = (_Float16)(xv - (float)hh);
         }
         uint8_t *dst = atab + (size_t)c * 1024 + (size_t)(2 * bl + 16 * g) * 16;
         *reinterpret_cast<half8 *>(dst) = hi;
         *reinterpret_cast<half8 *>(dst + 16) = lo;
     }
     // sub-block-sum operand: lanes (m = 2b' + part, g = 0) hold the 8 sums of
-    // batch b', lanes with g != 0 zero; thread ch < 8 of batch b' writes
-    // lane (2b' + (ch & 1)) + 16 (ch >> 1). Sum q sits in lanes 4q..4q+3 of
-    // the batch's 32.
+    // batch b', lanes with g != 0 zero; thread h < 8 of batch b' writes lane
+    // (2b' + (h & 1)) + 16 (h >> 1). Sum q is in lanes 2q, 2q+1 of the row.
     float sq[8];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) sq[q] = __shfl(sum, (tid & 32) + 4 * q, 64);
-    if (ch < 8) {
-        const int part = ch & 1, g = ch >> 1;
+    for (int q = 0; q < 8; ++q) sq[q] = __shfl(sum, (tid & 48) + 2 * q, 64);
+    if (h < 8) {
+        const int part = h & 1, g = h >> 1;
         float smax = 0.0f;
 #pragma unroll
         for (int q = 0; q < 8; ++q) smax = fmaxf(smax, fabsf(sq[q]));
@@ -163,8 +185,8 @@ __global__ __launch_bounds__(256) void batched_table_kernel(const float *__restr
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             const float xv = ldexpf(sq[q], es);
-            const _Float16 h = (_Float16)xv;
-            out[q] = g != 0 ? (_Float16)0.0f : (part ? (_Float16)(xv - (float)h) : h);
+            const _Float16 hh = (_Float16)xv;
+            out[q] = g != 0 ? (_Float16)0.0f : (part ? (_Float16)(xv - (float)hh) : hh);
         }
         *reinterpret_cast<half8 *>(atab + (size_t)8 * 1024 + (size_t)(2 * bl + part + 16 * g) * 16) = out;
         if (g == 0 && part == 0) meta[(js * 8 + bl) * 2 + 1] = ldexpf(1.0f, -es);
@@ -418,6 +440,244 @@ __global__ __launch_bounds__(512) void gemv_batched_mfma_kernel(const uint8_t *_
     }
 }
 
+// Wave-private batched kernel. A unit is R rows x CB blocks; wavefront w takes
+// blocks CB*w .. CB*w + CB-1 of each K slice of NW*CB blocks, for each of the
+// work-group's gpw row groups in turn (slice-major: the blocks' A operands
+// stay in registers for gpw units). It loads the unit's pieces with 16-byte
+// loads (runs of 9*CB pieces per row), stores them to its own LDS slot and
+// computes from it, so no work-group barrier sits between units. Its sums of
+// each (group, row, batch) accumulate over its slices in its own LDS rows; the
+// work-group adds the wavefronts' rows in wavefront order once, after the
+// stream. Every work-group takes exactly gpw groups (groups past the end
+// re-read the last row and are not written), so every wavefront runs the
+// same unit sequence. One unit is in flight per wavefront (its next unit's
+// weights load while it computes; measured faster than two or three). A
+// slice's A operands go into `areg` right after the previous slice's last
+// unit is computed, behind the next unit's weights, which are already in
+// flight: one register set.
+template <int R, int SETS, int NW, int CB>
+__global__ __launch_bounds__(NW * 64) void gemv_batched_wave_kernel(const uint8_t *__restrict__ w,
+                                                                    const uint8_t *__restrict__ ws,
+                                                                    float *__restrict__ Y, int n,
+                                                                    int bpr, int batch, int gpw,
+                                                                    int kparts) {
+    static_assert(CB == 1 || CB == 2, "one or two blocks per unit");
+    constexpr int PC = 9, BB = 144, TILES = R / 16, BP = 8 * SETS, RUN = PC * CB;
+    constexpr int UP = R * RUN, IPU = (UP + 63) / 64;
+    constexpr int SP = RUN | 1;  // LDS pieces per slot row (odd)
+    constexpr uint32_t SLOT = (uint32_t)R * SP * 16u;
+    constexpr int SW = NW * CB;  // blocks per K slice
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    uint8_t *slot = lds + (uint32_t)wave * SLOT;
+    float *acc_all = reinterpret_cast<float *>(lds + NW * SLOT);
+    const size_t row_bytes = (size_t)bpr * BB;
+
+    // K split (kparts = 1 or 2): work-group id = kp * G + bx; K part kp takes
+    // blocks [kb0, kb1), ceil(bpr / 2) of them for part 0
+    const int G = (int)gridDim.x >> (kparts - 1);
+    const int kp = (int)blockIdx.x >= G ? 1 : 0, bx = (int)blockIdx.x - kp * G;
+    const int kspan = (bpr + kparts - 1) >> (kparts - 1);
+    const int kb0 = kp * kspan, kb1 = std::min(bpr, kb0 + kspan);
+    const int wb0 = kb0 + wave * CB;  // this wavefront's first block in slice 0
+
+    // piece p of a unit: row p / RUN, piece p % RUN of the row's run
+    uint32_t prow[IPU], pcol[IPU], plds[IPU];
+#pragma unroll
+    for (int k = 0; k < IPU; ++k) {
+        const int p = std::min(k * 64 + lane, UP - 1);
+        const int row = p / RUN, rem = p - row * RUN;
+        prow[k] = (uint32_t)row;
+        pcol[k] = (uint32_t)(16 * rem);
+        plds[k] = (uint32_t)((row * SP + rem) * 16);
+    }
+    const uint32_t lastcol = (uint32_t)((bpr - 1) * BB);
+    // unit (slice sl, group index i): rows clamped to the last row, blocks
+    // past the row end to the last block (same piece)
+    u32x4 stg[IPU];
+    auto gload = [&](int sl, int i) __attribute__((always_inline)) {
+        const uint32_t r0 = (uint32_t)(bx + i * G) * (uint32_t)R, rlast = (uint32_t)(n - 1);
+        const uint32_t c0 = (uint32_t)((wb0 + sl * SW) * BB);
+#pragma unroll
+        for (int k = 0; k < IPU; ++k) {
+            const uint32_t rr = std::min(r0 + prow[k], rlast);
+            const uint32_t pc16 = pcol[k] % (16u * PC);
+            const uint32_t col = std::min(c0 + pcol[k] - pc16, lastcol) + pc16;
+            stg[k] = ld_u32x4(w + ((uint64_t)rr * row_bytes + col));
+        }
+    };
+    gload(0, 0);  // the first unit before any schedule arithmetic
+    const int slices = (kb1 - kb0 + SW - 1) / SW;
+    const int U = slices * gpw;
+    const int groups = (n + R - 1) / R;
+
+    const BatchedWs Lw = batched_ws(bpr, SETS);
+    const int n16 = lane & 15, g = lane >> 4, hsel = g >> 1;
+    u32x4 areg[CB][SETS][kBatchOps];
+    f32x4 mreg[CB][SETS];  // (corr, corr_min) of batches 2g, 2g+1 of each set
+    auto load_a = [&](int sl) __attribute__((always_inline)) {
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+            const int jb = std::min(wb0 + sl * SW + cb, bpr - 1);
+#pragma unroll
+            for (int s = 0; s < SETS; ++s) {
+                const uint8_t *base = ws + ((size_t)jb * SETS + s) * kBatchOps * 1024 + lane * 16;
+#pragma unroll
+                for (int c = 0; c < kBatchOps; ++c)
+                    areg[cb][s][c] = *reinterpret_cast<const u32x4 *>(base + c * 1024);
+                mreg[cb][s] = *reinterpret_cast<const f32x4 *>(ws + Lw.meta + (((size_t)jb * SETS + s) * 8 + 2 * g) * 8);
+            }
+        }
+    };
+    load_a(0);
+    // load position (slice, group index) of the next unit to load
+    int lsl = 0, li = 0;
+    auto advance = [&](int &sl, int &i) __attribute__((always_inline)) {
+        if (++i == gpw) {
+            i = 0;
+            ++sl;
+        }
+    };
+    advance(lsl, li);
+    const uint32_t sel0 = 0x04000400u | (uint32_t)(2 * hsel) | ((uint32_t)(2 * hsel) << 16);
+    const uint32_t sel1 = sel0 + 0x00010001u;
+    auto piece = [&](int row, int cb, int pc) -> const u32x4 & {
+        return *reinterpret_cast<const u32x4 *>(slot + (row * SP + cb * PC + pc) * 16);
+    };
+    int csl = 0, ci = 0;  // compute position
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int k = 0; k < IPU; ++k) *reinterpret_cast<u32x4 *>(slot + plds[k]) = stg[k];
+        __asm__ volatile("" ::: "memory");  // the unit's reads follow its stores (in-order LDS)
+        // the next unit (past the last one: the last again, a cache hit)
+        const bool new_slice = li == 0 && lsl < slices;
+        const int next_sl = lsl;
+        if (lsl < slices)
+            gload(lsl, li);
+        else
+            gload(slices - 1, gpw - 1);
+        advance(lsl, li);
+
+        const int jb0 = wb0 + csl * SW;
+        float yv[TILES][SETS][2];
+#pragma unroll
+        for (int T = 0; T < TILES; ++T)
+#pragma unroll
+            for (int s = 0; s < SETS; ++s) yv[T][s][0] = yv[T][s][1] = 0.0f;
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+            if (jb0 + cb >= kb1) break;
+#pragma unroll
+            for (int T = 0; T < TILES; ++T) {
+                const int row = T * 16 + n16;
+                const u32x4 hd = piece(row, cb, 0), qa0 = piece(row, cb, 1 + g), qa1 = piece(row, cb, 5 + g);
+                const float d = half_bits_finite(hd[0]), dmin = half_bits_finite(hd[0] >> 16);
+                const uint32_t sc_lo = scales4(0, hd[1], hd[3]), sc_hi = scales4(1, hd[1], hd[3]);
+                typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+                const h2 sixteen = {(_Float16)16.0f, (_Float16)16.0f};
+                uint32_t sf[2][2];
+                sf[0][0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, byte_to_h2(sc_lo, sel0)) * sixteen);
+                sf[0][1] = byte_to_h2(sc_lo, sel1);
+                sf[1][0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, byte_to_h2(sc_hi, sel0)) * sixteen);
+                sf[1][1] = byte_to_h2(sc_hi, sel1);
+                const uint32_t mn_lo = mins4(0, hd[2], hd[3]), mn_hi = mins4(1, hd[2], hd[3]);
+                const u32x4 bm = {byte_to_h2(mn_lo, 0x04010400u), byte_to_h2(mn_lo, 0x04030402u),
+                                  byte_to_h2(mn_hi, 0x04010400u), byte_to_h2(mn_hi, 0x04030402u)};
+                f32x4 acc[SETS], accm[SETS];
+#pragma unroll
+                for (int s = 0; s < SETS; ++s) {
+                    acc[s] = (f32x4){0.f, 0.f, 0.f, 0.f};
+                    accm[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        __builtin_bit_cast(half8, areg[cb][s][8]), __builtin_bit_cast(half8, bm),
+                        (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                }
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const int p = c >> 1, kind = c & 1;
+                    const uint32_t mask = kind ? 0x00F000F0u : 0x000F000Fu;
+                    const uint32_t w0 = p < 2 ? qa0[2 * p] : qa1[2 * p - 4];
+                    const uint32_t w1 = p < 2 ? qa0[2 * p + 1] : qa1[2 * p - 3];
+                    const h2 f = __builtin_bit_cast(h2, sf[p >> 1][kind]);
+                    const u32x4 bq = {
+                        __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, w0 & mask) * f),
+                        __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, (w0 >> 8) & mask) * f),
+                        __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, w1 & mask) * f),
+                        __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, (w1 >> 8) & mask) * f)};
+#pragma unroll
+                    for (int s = 0; s < SETS; ++s)
+                        acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(half8, areg[cb][s][c]), __builtin_bit_cast(half8, bq), acc[s],
+                            0, 0, 0);
+                }
+#pragma unroll
+                for (int s = 0; s < SETS; ++s) {
+                    const f32x4 mr = mreg[cb][s];
+                    yv[T][s][0] += d * ((acc[s][0] + acc[s][1]) * mr[0]) -
+                                   dmin * ((accm[s][0] + accm[s][1]) * mr[1]);
+                    yv[T][s][1] += d * ((acc[s][2] + acc[s][3]) * mr[2]) -
+                                   dmin * ((accm[s][2] + accm[s][3]) * mr[3]);
+                }
+            }
+        }
+        // the next unit starts a slice: its operands, now that these are read
+        if (new_slice) load_a(next_sl);
+        // this wavefront's rows: acc[wave][group index][row][batch]
+        float *ap = acc_all + ((size_t)wave * gpw + ci) * R * BP;
+#pragma unroll
+        for (int T = 0; T < TILES; ++T)
+#pragma unroll
+            for (int s = 0; s < SETS; ++s) {
+                float *p2 = ap + (T * 16 + n16) * BP + s * 8 + 2 * g;
+                if (csl == 0) {
+                    p2[0] = yv[T][s][0];
+                    p2[1] = yv[T][s][1];
+                } else if (jb0 < kb1) {
+                    p2[0] += yv[T][s][0];
+                    p2[1] += yv[T][s][1];
+                }
+            }
+        advance(csl, ci);
+    }
+    __syncthreads();
+    // Y[b][r], rows fastest; the wavefronts' sums added in wavefront order
+    for (int i = tid; i < gpw * R * BP; i += NW * 64) {
+        const int t = i / (R * BP), rem = i - t * R * BP, b = rem / R, r = rem - b * R;
+        const int grp = bx + t * G, row = grp * R + r;
+        if (grp < groups && row < n && b < batch) {
+            float v = 0.0f;
+            for (int wv = 0; wv < NW; ++wv) v += acc_all[(((size_t)wv * gpw + t) * R + r) * BP + b];
+            // two K parts: 0 + a + b rounds the same in either order
+            if (kparts > 1)
+                atomicAdd(&Y[(size_t)b * n + row], v);
+            else
+                Y[(size_t)b * n + row] = v;
+        }
+    }
+}
+
+// Resident work-groups per CU from the occupancy query (at the LDS of one
+// per CU), each taking gpw = ceil(groups / resident slots) row groups.
+template <int R, int SETS, int NW, int CB>
+static hipError_t batched_wave_launch(const uint8_t *w, const uint8_t *ws, float *Y, int n, int bpr,
+                                      int batch, int kparts, hipStream_t stream) {
+    constexpr int BP = 8 * SETS;
+    constexpr size_t slots = (size_t)NW * R * ((9 * CB) | 1) * 16;
+    auto kern = gemv_batched_wave_kernel<R, SETS, NW, CB>;
+    const long groups = (n + R - 1) / R;
+    const long cus = device_cus();
+    const long gpw1 = (groups * kparts + cus - 1) / cus;
+    const int occ = occupancy_cached((const void *)kern, NW * 64, slots + (size_t)NW * gpw1 * R * BP * 4, 1);
+    const long slots_total = cus * std::max(1, occ) / kparts;
+    const long gpw = (groups + slots_total - 1) / slots_total;
+    const long grid = (groups + gpw - 1) / gpw;
+    const size_t lds = slots + (size_t)NW * gpw * R * BP * 4;
+    if (lds > 160 * 1024) return hipErrorNotSupported;
+    const hipError_t attr = allow_full_lds_by_addr((const void *)kern);
+    if (attr != hipSuccess) return attr;
+    kern<<<(unsigned)(grid * kparts), NW * 64, lds, stream>>>(w, ws, Y, n, bpr, batch, (int)gpw, kparts);
+    return hipGetLastError();
+}
 
 template <int R, int SETS, int PF>
 static hipError_t batched_main_launch(const uint8_t *w, const uint8_t *ws, float *Y, int n, int bpr,
@@ -454,10 +714,34 @@ hipError_t gemv_batched_mfma_launch(const uint8_t *w, const float *X, float *Y, 
     // rounds of 32 rows on 198 work-groups against 5 of 16 on 237; 14.6
     // against 16.6 us at B = 8, and slower at B = 4 and 16 too).
     const bool ksplit = (n + 15) / 16 <= device_cus() && (bpr + 7) / 8 >= 4;
-    batched_table_kernel<<<dim3((unsigned)bpr, (unsigned)sets), 256, 0, stream>>>(
+    batched_table_kernel<<<dim3((unsigned)((bpr + 1) / 2), (unsigned)sets), 256, 0, stream>>>(
         X, batch, bpr, sets, ((uintptr_t)X & 15u) == 0, ws, Y, ksplit ? batch * n : 0);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    // Main kernel: the wave-private kernel, with units of two blocks (a
+    // 14-block slice over 7 wavefronts: gate's whole row) for one batch set
+    // and of one block for two (the operands of two blocks and two sets do
+    // not fit the registers). µs per call at B = 8 with the table pass,
+    // against the stage kernel: gate 15.8-16.8 / 17.9-18.8, gate|up fused
+    // 23.5-23.7 / 27.4-27.5, down 19.9-20.9 / 20.0-20.9. MGQ_BATCHED_WAVE=0
+    // selects the stage kernel (a tuning switch).
+    static const int wave_env = [] {
+        const char *v = std::getenv("MGQ_BATCHED_WAVE");
+        return (v && *v) ? std::atoi(v) : 1;
+    }();
+    if (wave_env) {
+        hipError_t ew;
+        if (ksplit)
+            ew = sets == 1 ? batched_wave_launch<32, 1, 7, 2>(w, ws, Y, n, bpr, batch, 2, stream)
+                           : batched_wave_launch<32, 2, 8, 1>(w, ws, Y, n, bpr, batch, 2, stream);
+        else
+            ew = sets == 1 ? batched_wave_launch<16, 1, 7, 2>(w, ws, Y, n, bpr, batch, 1, stream)
+                           : batched_wave_launch<16, 2, 8, 1>(w, ws, Y, n, bpr, batch, 1, stream);
+        if (ew != hipErrorNotSupported) return ew;
+    }
+    // The stage kernel: also for shapes whose per-wavefront row sums (gpw
+    // groups) would not fit LDS beside the slots (more than ~143k rows at
+    // B <= 8, ~70k at B <= 16).
     // Weight stages in flight (register sets). One batch set (B <= 8), µs
     // per call at B = 8, gate / down, table pass included: 2 stages
     // 18.8 / 20.8, 3: 19.7 / 21.7, 4: 19.7 / 22.8, 6: 21.2 / 24.2,

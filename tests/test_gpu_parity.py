@@ -310,6 +310,19 @@ def test_matvec_batched_k_split(L, orc, n, bpr, batch):
         assert_gemv_close(Y1[b], Y_ref[b], A[b])
 
 
+@pytest.mark.parametrize("n,bpr,batch", [(150000, 1, 8), (80000, 1, 16)])
+def test_matvec_batched_many_rows_stage_kernel(L, orc, n, bpr, batch):
+    # so many row groups per work-group that the wave kernel's per-wavefront
+    # row sums would not fit LDS: the stage kernel runs these
+    note(f"batched stage kernel n={n} bpr={bpr} B={batch}")
+    w = orc.seeded_weight(81 + batch, n, bpr * 256)
+    X = orc.normal(82 + batch, batch * bpr * 256).reshape(batch, -1)
+    Y = run_batched(L, w, X, n, bpr, batch)
+    Y_ref, A = orc.gemv_batched(w, X, n, bpr)
+    for b in range(batch):
+        assert_gemv_close(Y[b], Y_ref[b], A[b])
+
+
 def test_matvec_batched_single_row_is_the_matvec(L, orc):
     # batch 1 runs the matvec itself (no operand-table pass): bit-identical
     note("batched B=1 == gemv")
