@@ -460,7 +460,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_batched_wave_kernel(const uint8_
                                                                     const uint8_t *__restrict__ ws,
                                                                     float *__restrict__ Y, int n,
                                                                     int bpr, int batch, int gpw,
-                                                                    int kparts) {
+                                                                    int kparts, int gr) {
     static_assert(CB == 1 || CB == 2, "one or two blocks per unit");
     constexpr int PC = 9, BB = 144, TILES = R / 16, BP = 8 * SETS, RUN = PC * CB;
     constexpr int UP = R * RUN, IPU = (UP + 63) / 64;
@@ -493,15 +493,17 @@ __global__ __launch_bounds__(NW * 64) void gemv_batched_wave_kernel(const uint8_
         plds[k] = (uint32_t)((row * SP + rem) * 16);
     }
     const uint32_t lastcol = (uint32_t)((bpr - 1) * BB);
-    // unit (slice sl, group index i): rows clamped to the last row, blocks
-    // past the row end to the last block (same piece)
+    // unit (slice sl, group index i) of gr <= R rows: tile rows past the
+    // group re-read its last row, rows past n the last row; blocks past the
+    // row end re-read the last block (same piece)
     u32x4 stg[IPU];
     auto gload = [&](int sl, int i) __attribute__((always_inline)) {
-        const uint32_t r0 = (uint32_t)(bx + i * G) * (uint32_t)R, rlast = (uint32_t)(n - 1);
+        const uint32_t r0 = (uint32_t)(bx + i * G) * (uint32_t)gr, rlast = (uint32_t)(n - 1);
+        const uint32_t glast = (uint32_t)gr - 1u;
         const uint32_t c0 = (uint32_t)((wb0 + sl * SW) * BB);
 #pragma unroll
         for (int k = 0; k < IPU; ++k) {
-            const uint32_t rr = std::min(r0 + prow[k], rlast);
+            const uint32_t rr = std::min(r0 + std::min(prow[k], glast), rlast);
             const uint32_t pc16 = pcol[k] % (16u * PC);
             const uint32_t col = std::min(c0 + pcol[k] - pc16, lastcol) + pc16;
             stg[k] = ld_u32x4(w + ((uint64_t)rr * row_bytes + col));
@@ -510,7 +512,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_batched_wave_kernel(const uint8_
     gload(0, 0);  // the first unit before any schedule arithmetic
     const int slices = (kb1 - kb0 + SW - 1) / SW;
     const int U = slices * gpw;
-    const int groups = (n + R - 1) / R;
+    const int groups = (n + gr - 1) / gr;
 
     const BatchedWs Lw = batched_ws(bpr, SETS);
     const int n16 = lane & 15, g = lane >> 4, hsel = g >> 1;
@@ -643,8 +645,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_batched_wave_kernel(const uint8_
     // Y[b][r], rows fastest; the wavefronts' sums added in wavefront order
     for (int i = tid; i < gpw * R * BP; i += NW * 64) {
         const int t = i / (R * BP), rem = i - t * R * BP, b = rem / R, r = rem - b * R;
-        const int grp = bx + t * G, row = grp * R + r;
-        if (grp < groups && row < n && b < batch) {
+        const int grp = bx + t * G, row = grp * gr + r;
+        if (grp < groups && r < gr && row < n && b < batch) {
             float v = 0.0f;
             for (int wv = 0; wv < NW; ++wv) v += acc_all[(((size_t)wv * gpw + t) * R + r) * BP + b];
             // two K parts: 0 + a + b rounds the same in either order
@@ -664,18 +666,26 @@ static hipError_t batched_wave_launch(const uint8_t *w, const uint8_t *ws, float
     constexpr int BP = 8 * SETS;
     constexpr size_t slots = (size_t)NW * R * ((9 * CB) | 1) * 16;
     auto kern = gemv_batched_wave_kernel<R, SETS, NW, CB>;
-    const long groups = (n + R - 1) / R;
     const long cus = device_cus();
-    const long gpw1 = (groups * kparts + cus - 1) / cus;
+    const long gpw1 = ((long)(n + R - 1) / R * kparts + cus - 1) / cus;
     const int occ = occupancy_cached((const void *)kern, NW * 64, slots + (size_t)NW * gpw1 * R * BP * 4, 1);
     const long slots_total = cus * std::max(1, occ) / kparts;
+    // fewer R-row groups than resident work-groups: groups of ceil(n / slots)
+    // rows, one per work-group, so every CU works
+    static const int gr_env = [] {
+        const char *v = std::getenv("MGQ_BATCHED_GR");
+        return (v && *v) ? std::atoi(v) : 1;
+    }();
+    int gr = R;
+    if (gr_env && (n + R - 1) / R < slots_total) gr = (int)std::max<long>(1, (n + slots_total - 1) / slots_total);
+    const long groups = (n + gr - 1) / gr;
     const long gpw = (groups + slots_total - 1) / slots_total;
     const long grid = (groups + gpw - 1) / gpw;
     const size_t lds = slots + (size_t)NW * gpw * R * BP * 4;
     if (lds > 160 * 1024) return hipErrorNotSupported;
     const hipError_t attr = allow_full_lds_by_addr((const void *)kern);
     if (attr != hipSuccess) return attr;
-    kern<<<(unsigned)(grid * kparts), NW * 64, lds, stream>>>(w, ws, Y, n, bpr, batch, (int)gpw, kparts);
+    kern<<<(unsigned)(grid * kparts), NW * 64, lds, stream>>>(w, ws, Y, n, bpr, batch, (int)gpw, kparts, gr);
     return hipGetLastError();
 }
 
