@@ -827,7 +827,10 @@ __host__ __device__ inline WaveLayout wave_layout(int bpr, int rounds) {
     return L;
 }
 
-template <int R, int C, int NW, int XIT>
+// DIRECT (one unit per wavefront: a single stage, one group per work-group):
+// every lane loads the three pieces it computes with (block header, quant
+// pieces 1+g and 5+g of its row) straight into registers, with no LDS slot.
+template <int R, int C, int NW, int XIT, bool DIRECT = false>
 __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__restrict__ w,
                                                             const float *__restrict__ x,
                                                             float *__restrict__ y, int n, int bpr,
@@ -882,6 +885,26 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
 #pragma unroll
         for (int k = 0; k < IPW; ++k) *reinterpret_cast<u32x4 *>(slot + plds[k]) = stg[k];
     };
+    // DIRECT: header, pieces 1+g and 5+g of the unit's block(s) for this lane's
+    // row(s): {A: hd, q0, q1, B: hd, q0, q1} (R = 16: blocks cb0, cb0 + 1 of
+    // row n16; R = 32: block cb0 of rows n16 and 16 + n16)
+    u32x4 dreg[6];
+    auto gload_direct = [&](uint32_t r0) {
+        const int dl = lane & 15, dg = lane >> 4;
+        const uint32_t glast = (uint32_t)gr - 1u, rlast = (uint32_t)(n - 1);
+        const uint32_t rA = std::min(r0 + std::min((uint32_t)dl, glast), rlast);
+        const uint32_t rB = (R == 32) ? std::min(r0 + std::min((uint32_t)(16 + dl), glast), rlast) : rA;
+        const uint32_t bA = (uint32_t)std::min(cb0, bpr - 1);
+        const uint32_t bB = (R == 32) ? bA : (uint32_t)std::min(cb0 + 1, bpr - 1);
+        const uint8_t *pA = w + ((uint64_t)rA * row_bytes + bA * BB);
+        const uint8_t *pB = w + ((uint64_t)rB * row_bytes + bB * BB);
+        dreg[0] = ld_u32x4(pA);
+        dreg[1] = ld_u32x4(pA + 16 * (1 + dg));
+        dreg[2] = ld_u32x4(pA + 16 * (5 + dg));
+        dreg[3] = ld_u32x4(pB);
+        dreg[4] = ld_u32x4(pB + 16 * (1 + dg));
+        dreg[5] = ld_u32x4(pB + 16 * (5 + dg));
+    };
 
     // ---- prologue: x loads, the first unit, then the activation table -------
     const int nitems = bpr * 32;
@@ -894,7 +917,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
         xv0[it] = ld_f32x4(x + (size_t)i * 8);
         xv1[it] = ld_f32x4(x + (size_t)i * 8 + 4);
     }
-    gload_at((uint32_t)blockIdx.x * (uint32_t)gr, 0u);
+    if constexpr (DIRECT)
+        gload_direct((uint32_t)blockIdx.x * (uint32_t)gr);
+    else
+        gload_at((uint32_t)blockIdx.x * (uint32_t)gr, 0u);
     const int groups = (n + gr - 1) / gr;
     const int my_groups = sched_count(sch, (int)blockIdx.x, (int)gridDim.x, groups);
     const int Q = my_groups * stages;
@@ -972,9 +998,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
     float yaccA = 0.0f, yaccB = 0.0f;
     for (int q = 0; q < Q; ++q) {
         const int t = q % stages;
-        lstore();
-        __asm__ volatile("" ::: "memory");  // the unit's reads follow its stores (in-order LDS)
-        {
+        if constexpr (!DIRECT) {
+            lstore();
+            __asm__ volatile("" ::: "memory");  // the unit's reads follow its stores (in-order LDS)
             // the next unit (past the last one: the last again, a cache hit),
             // unconditional so the load-counter waits stay exact
             const int q1 = std::min(q + 1, Q - 1);
@@ -987,9 +1013,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
             const bool hasB = bB < bpr;
             const int bBc = hasB ? bB : bA;
             const int rowB = (R == 32) ? 16 : 0, cbB = (R == 32) ? 0 : 1;
-            const u32x4 qa0 = piece(n16, 0, 1 + g), qa1 = piece(n16, 0, 5 + g);
-            const u32x4 qb0 = piece(rowB + n16, cbB, 1 + g), qb1 = piece(rowB + n16, cbB, 5 + g);
-            const u32x4 hdA = piece(n16, 0, 0), hdB = piece(rowB + n16, cbB, 0);
+            const u32x4 qa0 = DIRECT ? dreg[1] : piece(n16, 0, 1 + g);
+            const u32x4 qa1 = DIRECT ? dreg[2] : piece(n16, 0, 5 + g);
+            const u32x4 qb0 = DIRECT ? dreg[4] : piece(rowB + n16, cbB, 1 + g);
+            const u32x4 qb1 = DIRECT ? dreg[5] : piece(rowB + n16, cbB, 5 + g);
+            const u32x4 hdA = DIRECT ? dreg[0] : piece(n16, 0, 0);
+            const u32x4 hdB = DIRECT ? dreg[3] : piece(rowB + n16, cbB, 0);
             f32x4 accA = {0.f, 0.f, 0.f, 0.f}, accB = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
@@ -1044,10 +1073,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
     }
 }
 
-template <int R, int C, int NW, int XIT>
+template <int R, int C, int NW, int XIT, bool DIRECT = false>
 static hipError_t launch_wave_xit(const uint8_t *w, const float *x, float *y, int n, int bpr,
                                   hipStream_t stream, bool persistent, int gr) {
-    auto kern = gemv_wave_kernel<R, C, NW, XIT>;
+    auto kern = gemv_wave_kernel<R, C, NW, XIT, DIRECT>;
+    // DIRECT: one unit per wavefront (a single stage, one group per work-group)
+    if (DIRECT && (persistent || bpr > C)) return hipErrorNotSupported;
     const hipError_t attr = allow_full_lds_by_addr((const void *)kern);
     if (attr != hipSuccess) return attr;
     if (gr <= 0 || gr > R) gr = R;
@@ -1077,6 +1108,14 @@ static hipError_t wave_prepare() {
     if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<R, C, NW, 4>);
     if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<R, C, NW, 8>);
     return e;
+}
+
+// one unit per wavefront with direct register loads (single-stage rows)
+template <int R, int C, int NW>
+static hipError_t launch_wave_direct(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                                     hipStream_t stream, int gr) {
+    if (bpr * 32 > NW * 64) return hipErrorNotSupported;
+    return launch_wave_xit<R, C, NW, 1, true>(w, x, y, n, bpr, stream, false, gr);
 }
 
 template <int R, int C, int NW>
@@ -1216,6 +1255,7 @@ hipError_t gemv_prepare() {
     if (e == hipSuccess) e = q6k_prepare();
     if (e == hipSuccess) e = wave_prepare<16, 14, 7>();
     if (e == hipSuccess) e = wave_prepare<16, 20, 10>();
+    if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<16, 14, 7, 1, true>);
     return e;
 }
 
@@ -1254,14 +1294,21 @@ static hipError_t mfma_dispatch(const uint8_t *w, const GemvAct &a, float *y, in
         // alternating on one box: 1182-1183 -> 1140-1141 us (gate|up -0.8,
         // down -0.55 us per launch), and 20-block stages over 10 wavefronts
         // for the long rows: 1146 -> 1137-1138 us (down 12.3 -> 12.0 us;
-        // 16 / 26 / 28 / 32 blocks: 12.3 / 12.0 / 12.45 / 12.75 us). One-stage
-        // launches (o, qkv: 256 groups or fewer) measured 0.1-0.3 us slower
-        // on it and keep the staged kernel. MGQ_GEMV_WAVE=0 turns it off.
+        // 16 / 26 / 28 / 32 blocks: 12.3 / 12.0 / 12.45 / 12.75 us).
+        // One-stage 16-row launches (o: one group per work-group) load each
+        // lane's pieces straight into registers (DIRECT): o 4.47 -> 4.30 us
+        // per launch in chains, decode step 1.138-1.140 -> 1.132-1.133 ms;
+        // with LDS slots they measured 0.1 us slower than the staged kernel.
+        // qkv's 32-row groups keep the staged kernel (direct: 5.59 -> 5.63).
+        // MGQ_GEMV_WAVE=0 turns the wave-private kernel off, MGQ_GEMV_DIRECT=0
+        // the direct loads.
         static const int wave_env = env_int("MGQ_GEMV_WAVE", 1);
+        static const int direct_env = env_int("MGQ_GEMV_DIRECT", 1);
         const bool multi = (long)(n + 15) / 16 > 2 * device_cus();
         if (wave_env && force < 0) {
             if (cfg == 6 && multi) e = launch_wave<16, 14, 7>(w, a.x, y, n, bpr, stream, true);
             else if (cfg == 2) e = launch_wave<16, 20, 10>(w, a.x, y, n, bpr, stream, false);
+            else if (cfg == 6 && direct_env) e = launch_wave_direct<16, 14, 7>(w, a.x, y, n, bpr, stream, 0);
         }
     }
     if (e == hipErrorNotSupported) e = launch_any<Q8, FUSE>(cfg, w, a, fz, y, n, bpr, stream, gr);
