@@ -221,7 +221,14 @@ struct MfmaLayout {
 // kFmtQ5K (f32 mode, no other bit): the weights are Q5_K, 176-byte blocks
 // of 11 16-byte pieces (header | qh[32] | qs[128]); the header and its scale
 // packing are Q4_K's, and the fifth bit of every weight comes from qh.
-constexpr int kFuseNorm = 1, kFuseGlu = 2, kFuseQuant = 4, kFmtQ5K = 8;
+// kStageWave (a staging variant, with any of the above): every wavefront
+// loads and stores only its own unit's pieces (at their places in the stage
+// buffer) and no work-group barrier sits between stages; the row sums of
+// every pass go to per-wavefront LDS rows and are reduced once, after the
+// stream, in the same order (results identical to the barrier-staged kernel
+// of the same stage width). Needs one unit per wavefront and stage, one
+// stage in flight and a single stage buffer.
+constexpr int kFuseNorm = 1, kFuseGlu = 2, kFuseQuant = 4, kFmtQ5K = 8, kStageWave = 16;
 __host__ __device__ constexpr int block_pieces(int fuse) { return (fuse & kFmtQ5K) ? 11 : 9; }
 struct GemvFuse {
     const uint8_t *w2;  // kFuseGlu: the up matrix
@@ -254,10 +261,11 @@ __host__ __device__ inline MfmaLayout mfma_layout(int bpr, int R, int C, int NW,
     L.stage_bytes = (uint32_t)(R * stage_row_pieces(C, bp) * 16);
     // two stage buffers when double-buffered and K needs more than one stage
     L.aux = L.stage + ((db && bpr > C) ? 2u : 1u) * L.stage_bytes;
-    L.ybuf = L.aux + (uint32_t)NW * 256u;
     // kFuseGlu: gate and up results of every row group (2x rounds);
     // kFuseNorm: one sum(x^2) partial per wavefront
     const int vm = (fuse & kFuseGlu) ? 2 : 1;
+    // kStageWave: 32 row sums per wavefront and pass (rounds x vm passes)
+    L.ybuf = L.aux + ((fuse & kStageWave) ? (uint32_t)(rounds * vm) * NW * 128u : (uint32_t)NW * 256u);
     L.normp = L.ybuf + (uint32_t)(R * rounds * vm * 4);
     L.total = (size_t)L.normp + ((fuse & kFuseNorm) ? 64 : 0);
     return L;
@@ -293,11 +301,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
                                                             float *__restrict__ y, int n,
                                                             int bpr, int rounds, GemvFuse fz,
                                                             GemvSched sch, int gr) {
-    static_assert(Q8 ? (FUSE == 0 || FUSE == kFuseQuant) : (FUSE & kFuseQuant) == 0,
+    constexpr int FM = FUSE & ~kStageWave;  // the mode bits
+    static_assert(Q8 ? (FM == 0 || FM == kFuseQuant) : (FM & kFuseQuant) == 0,
                   "fused glue runs on f32 activations; quantization only in Q8 mode");
-    static_assert(!(FUSE & kFmtQ5K) || FUSE == kFmtQ5K, "Q5_K weights: plain f32 matvec only");
+    static_assert(!(FM & kFmtQ5K) || FM == kFmtQ5K, "Q5_K weights: plain f32 matvec only");
     static_assert(R == 32 || C % 2 == 0, "R = 16: a unit is a pair of blocks, so C must be even");
     constexpr bool Q5 = (FUSE & kFmtQ5K) != 0;
+    constexpr bool WV = (FUSE & kStageWave) != 0;
+    static_assert(!WV || (PF == 1 && !DB), "kStageWave: one stage in flight, one stage buffer");
     constexpr int BP = block_pieces(FUSE);  // 16-byte pieces per block
     constexpr int BB = BP * 16;              // block bytes
     constexpr bool NORM = (FUSE & kFuseNorm) != 0;
@@ -311,9 +322,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     const size_t row_bytes = (size_t)bpr * BB;
     const int stages = (bpr + C - 1) / C;
     constexpr int PIECES = R * BP * C;            // 16-byte pieces per stage
-    constexpr int IPW = ((PIECES + 63) / 64 + NW - 1) / NW;  // wave loads per wavefront
-    constexpr int I = IPW * NW;                   // wave loads per stage (padded)
     constexpr int UNITS = (R == 32) ? C : C / 2;  // tile pairs per stage
+    static_assert(!WV || UNITS == NW, "kStageWave: one unit per wavefront and stage");
+    constexpr int RUN = (R == 32) ? BP : 2 * BP;  // kStageWave: pieces of one row in a unit
+    // wave loads per wavefront: a share of the stage, or (kStageWave) its unit
+    constexpr int IPW = WV ? (R * RUN + 63) / 64 : ((PIECES + 63) / 64 + NW - 1) / NW;
+    constexpr int I = IPW * NW;                   // wave loads per stage (padded)
 
     // ---- weight staging: global -> registers (PF sets) -> LDS ---------------
     // stg is only ever indexed with compile-time constants (the stage loop is
@@ -327,8 +341,17 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     uint32_t prow[IPW], pcol[IPW], plast[IPW], plds[IPW];
 #pragma unroll
     for (int k = 0; k < IPW; ++k) {
-        const int j = std::min((wave + k * NW) * 64 + lane, PIECES - 1);
-        const int row = j / (BP * C), rem = j - row * BP * C;
+        int row, rem;
+        if constexpr (WV) {
+            // piece p of this wavefront's unit: row p / RUN, from its first block
+            const int p = std::min(k * 64 + lane, R * RUN - 1);
+            row = p / RUN;
+            rem = ((R == 32) ? wave : 2 * wave) * BP + (p - row * RUN);
+        } else {
+            const int j = std::min((wave + k * NW) * 64 + lane, PIECES - 1);
+            row = j / (BP * C);
+            rem = j - row * BP * C;
+        }
         const int cb = rem / BP, pc = rem - cb * BP;
         plds[k] = (uint32_t)((row * RP + rem) * 16);    // LDS byte offset in the stage
         prow[k] = (uint32_t)row;
@@ -718,7 +741,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         // barrier of its step, while the first R threads may still be reading
         // this group's: the buffer they read is the other one, and reusing it
         // two groups later is ordered by the barrier between.
-        float *auxg = aux + ((q / stages) & 1) * (NW * 32);
+        float *auxg = aux + (WV ? (q / stages) : ((q / stages) & 1)) * (NW * 32);
         if (group_end) {
             // sum the 4 lanes (g = 0..3) of each row, then one value per row
             // and tile into aux (free after the prologue)
@@ -730,6 +753,20 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
                 auxg[wave * 32 + lane] = yaccA;
                 auxg[wave * 32 + 16 + lane] = yaccB;
             }
+        }
+        if constexpr (WV) {
+            // own unit only: its reads above come before these stores (LDS
+            // operations of one wavefront execute in order)
+            if (more) {
+                lstore(0, stg[(F + 1) % PF]);
+                __asm__ volatile("" ::: "memory");
+                gload(q + 1 + PF, stg[(F + 1) % PF]);
+            }
+            if (group_end) {
+                yaccA = 0.0f;
+                yaccB = 0.0f;
+            }
+            return;
         }
         if (more) {
             if (!dbuf) __syncthreads();  // every wave is done reading the single buffer
@@ -777,6 +814,30 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         rstd = rsqrtf(ss / (float)(bpr * kBlockElems) + fz.eps);
     }
     const float *yb = reinterpret_cast<const float *>(lds + Lo.ybuf);
+    if constexpr (WV) {
+        // pass vg's row ri: the wavefronts' sums in wavefront order (as the
+        // per-stage reduction adds them)
+        auto pass_sum = [&](int vg, int ri) -> float {
+            float sum = 0.0f;
+            for (int wv = 0; wv < NW; ++wv) sum += aux[(vg * NW + wv) * 32 + ri];
+            return sum;
+        };
+        for (int i = tid; i < my_groups * R; i += NW * 64) {
+            const int ri = i % R, gi = i / R;
+            const int r = sched_group(sch, (int)blockIdx.x, (int)gridDim.x, gi) * gr + ri;
+            if (ri < gr && r < n) {
+                if constexpr (VM == 2) {
+                    const float gv = pass_sum(2 * gi, ri) * rstd, uv = pass_sum(2 * gi + 1, ri) * rstd;
+                    y[r] = glu_act(gv, fz.act) * uv;
+                } else {
+                    const float v0 = pass_sum(gi, ri);
+                    const float v = NORM ? v0 * rstd : v0;
+                    y[r] = (Q8 && !isfinite(v)) ? 0.0f : v;
+                }
+            }
+        }
+        return;
+    }
     for (int i = tid; i < my_groups * R; i += NW * 64) {
         const int ri = i % R;
         const int r = sched_group(sch, (int)blockIdx.x, (int)gridDim.x, i / R) * gr + ri;
@@ -1226,6 +1287,14 @@ static hipError_t launch_any(int cfg, const uint8_t *w, const GemvAct &a, const 
     }
 }
 
+// the kStageWave configurations of one mode
+template <bool Q8, int FUSE>
+static hipError_t prepare_swave() {
+    hipError_t e = lds_attr_all<16, 14, 7, 1, false, Q8, FUSE | kStageWave>();
+    if (e == hipSuccess) e = lds_attr_all<16, 16, 8, 1, false, Q8, FUSE | kStageWave>();
+    return e;
+}
+
 template <int FUSE>
 static hipError_t prepare_fuse() {
     hipError_t e = lds_attr_all<32, 8, 8, 1, false, false, FUSE>();
@@ -1256,6 +1325,12 @@ hipError_t gemv_prepare() {
     if (e == hipSuccess) e = wave_prepare<16, 14, 7>();
     if (e == hipSuccess) e = wave_prepare<16, 20, 10>();
     if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<16, 14, 7, 1, true>);
+    if (e == hipSuccess) e = prepare_swave<true, 0>();
+    if (e == hipSuccess) e = prepare_swave<true, kFuseQuant>();
+    if (e == hipSuccess) e = prepare_swave<false, kFmtQ5K>();
+    if (e == hipSuccess) e = prepare_swave<false, kFuseNorm>();
+    if (e == hipSuccess) e = prepare_swave<false, kFuseGlu>();
+    if (e == hipSuccess) e = prepare_swave<false, kFuseNorm | kFuseGlu>();
     return e;
 }
 
@@ -1309,6 +1384,23 @@ static hipError_t mfma_dispatch(const uint8_t *w, const GemvAct &a, float *y, in
             if (cfg == 6 && multi) e = launch_wave<16, 14, 7>(w, a.x, y, n, bpr, stream, true);
             else if (cfg == 2) e = launch_wave<16, 20, 10>(w, a.x, y, n, bpr, stream, false);
             else if (cfg == 6 && direct_env) e = launch_wave_direct<16, 14, 7>(w, a.x, y, n, bpr, stream, 0);
+        }
+    }
+    if constexpr (Q8 || FUSE != 0) {
+        // The other modes (Q8 / dp4a, fused RMSNorm and GLU, Q5_K): the same
+        // per-wavefront staging inside the staged kernel (kStageWave), at the
+        // staged kernel's stage widths (14 blocks over 7 wavefronts, or 16
+        // over 8 for long rows). Steps, alternating on one box:
+        // decode7b_dp4a 1.206 -> 1.149-1.151 ms, decode7b_q4km 1.457 ->
+        // 1.414-1.415 ms (20-block stages over 10 wavefronts: the same).
+        // MGQ_GEMV_SWAVE=0 turns it off.
+        static const int swave_env = env_int("MGQ_GEMV_SWAVE", 1);
+        const bool multi = (long)(n + 15) / 16 > 2 * device_cus();
+        if (swave_env && force < 0 && e == hipErrorNotSupported) {
+            if (cfg == 6 && multi)
+                e = launch_cfg<16, 14, 7, 1, false, Q8, FUSE | kStageWave>(w, a, fz, y, n, bpr, stream, true);
+            else if (cfg == 2)
+                e = launch_cfg<16, 16, 8, 1, false, Q8, FUSE | kStageWave>(w, a, fz, y, n, bpr, stream, false);
         }
     }
     if (e == hipErrorNotSupported) e = launch_any<Q8, FUSE>(cfg, w, a, fz, y, n, bpr, stream, gr);
