@@ -44,6 +44,15 @@
 
 namespace mgq {
 
+// stage kernel: weight stages in flight for one / two batch sets (measurements
+// at its launcher)
+#ifndef MGQ_BPF1
+#define MGQ_BPF1 2
+#endif
+#ifndef MGQ_BPF2
+#define MGQ_BPF2 1
+#endif
+
 constexpr int kBatchOps = 9;  // A operands per (block, set): 8 k-slot groups + sub-block sums
 
 // Workspace layout (bytes): atab [bpr][sets][9][64 lanes][16 B], then meta
@@ -693,8 +702,7 @@ template <int R, int SETS, int PF>
 static hipError_t batched_main_launch(const uint8_t *w, const uint8_t *ws, float *Y, int n, int bpr,
                                       int batch, int kparts, hipStream_t stream) {
     auto kern = gemv_batched_mfma_kernel<R, SETS, PF>;
-    static std::atomic<int> lds_state[64];
-    const hipError_t attr = allow_full_lds((const void *)kern, lds_state);
+    const hipError_t attr = allow_full_lds_by_addr((const void *)kern);
     if (attr != hipSuccess) return attr;
     constexpr int BP = 8 * SETS;
     constexpr size_t base = (size_t)R * ((9 * 8) | 1) * 16 + 2 * (size_t)8 * R * BP * 4;
@@ -708,6 +716,20 @@ static hipError_t batched_main_launch(const uint8_t *w, const uint8_t *ws, float
     kern<<<(unsigned)(grid * kparts), 512, lds, stream>>>(w, ws, Y, n, bpr, batch, (int)rounds,
                                                           kparts);
     return hipGetLastError();
+}
+
+// the main kernels' LDS limit, set outside any stream capture (gemv_prepare)
+hipError_t batched_prepare() {
+    const void *kerns[] = {
+        (const void *)gemv_batched_wave_kernel<16, 1, 7, 2>, (const void *)gemv_batched_wave_kernel<16, 2, 8, 1>,
+        (const void *)gemv_batched_wave_kernel<32, 1, 7, 2>, (const void *)gemv_batched_wave_kernel<32, 2, 8, 1>,
+        (const void *)gemv_batched_mfma_kernel<16, 1, MGQ_BPF1>, (const void *)gemv_batched_mfma_kernel<16, 2, MGQ_BPF2>,
+        (const void *)gemv_batched_mfma_kernel<32, 1, MGQ_BPF1>, (const void *)gemv_batched_mfma_kernel<32, 2, MGQ_BPF2>};
+    for (const void *k : kerns) {
+        const hipError_t e = allow_full_lds_by_addr(k);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t gemv_batched_mfma_launch(const uint8_t *w, const float *X, float *Y, int n, int bpr,
@@ -758,12 +780,6 @@ hipError_t gemv_batched_mfma_launch(const uint8_t *w, const float *X, float *Y, 
     // 8: 22.6 / 29.1 (VGPRs 167 -> 239 for the 16-row kernel). Two sets
     // (B <= 16) run at 256 VGPRs and stay at one stage (two: down 25.9 ->
     // 85 us).
-#ifndef MGQ_BPF1
-#define MGQ_BPF1 2
-#endif
-#ifndef MGQ_BPF2
-#define MGQ_BPF2 1
-#endif
     if (ksplit)
         return sets == 1 ? batched_main_launch<32, 1, MGQ_BPF1>(w, ws, Y, n, bpr, batch, 2, stream)
                          : batched_main_launch<32, 2, MGQ_BPF2>(w, ws, Y, n, bpr, batch, 2, stream);

@@ -1331,6 +1331,7 @@ hipError_t gemv_prepare() {
     if (e == hipSuccess) e = prepare_swave<false, kFuseNorm>();
     if (e == hipSuccess) e = prepare_swave<false, kFuseGlu>();
     if (e == hipSuccess) e = prepare_swave<false, kFuseNorm | kFuseGlu>();
+    if (e == hipSuccess) e = batched_prepare();
     return e;
 }
 

@@ -169,10 +169,12 @@ hipError_t gemv_mfma_launch(const uint8_t *w, const float *x, float *y, int n, i
                             hipStream_t stream);
 
 // One-time kernel attribute setup (dynamic LDS limit) of the GEMV kernels,
-// the Q6_K kernels included; safe to call often.
+// the Q6_K and batched kernels included; safe to call often.
 hipError_t gemv_prepare();
 // The Q6_K matrix-core kernels' LDS attributes and occupancy (q4k_q6k_mfma.hip).
 hipError_t q6k_prepare();
+// The batched matvec kernels' LDS attributes (q4k_batched.hip).
+hipError_t batched_prepare();
 
 // Looks up the current device's address of the no-allocation entry point's
 // fixed scratch array (once per device).
