@@ -10,15 +10,20 @@
 // qh[32g' + l]) << 4, and w = d * sc[2j + l/16] * (q - 32).
 //
 // Work-group = 16 rows x all K, persistent over row groups; 7 wavefronts
-// (16 for the K-chunked kernel).
+// (16 for the long-row kernels).
 //   * Whole-row stage: a row group's 16 rows are one contiguous byte range
 //     (16 x RB, RB = 210 bpr), copied flat into LDS as whole 16-byte chunks;
 //     the next group's chunks wait in registers.
-//   * K-chunked stage (bpr > kQ6mMaxBpr): a stage is 14 blocks of each of the
-//     16 rows; row r's segment is copied as the 16-byte chunks from the
-//     16-byte boundary at or below its start into its own LDS slot, and the
-//     segment's offset in that chunk (s & 15) moves the lane's reads. Row sums
-//     carry over the chunks of a group; the table covers the whole row.
+//   * Long rows (bpr > kQ6mMaxBpr), wave-private (gemv_q6k_wave_long_kernel,
+//     the default): wavefront w stages block w, w + 16, ... of the 16 rows in
+//     its own LDS slot (each row segment as the 16-byte chunks from the
+//     16-byte boundary at or below its start; the segment's offset in that
+//     chunk (s & 15) moves the lane's reads) and computes from it with no
+//     barrier between units; the table covers the whole row.
+//   * K-chunked stage (gemv_q6k_mfma_long_kernel, rows too long for the
+//     wave-private kernel's LDS): a stage is 14 blocks of each of the 16
+//     rows, staged by the whole work-group the same way. Row sums carry over
+//     the chunks of a group.
 //   * One v_mfma_f32_16x16x32_f16 per sub-block: B = weights (lane (n, g):
 //     row n, positions 8g..8g+7 of the sub-block; the 6-bit q are f16
 //     subnormals q*2^-24, exact, or 16q*2^-24 for the high-nibble sub-blocks,
@@ -40,6 +45,7 @@
 #include "q4k_launch.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace mgq {
 
@@ -428,6 +434,149 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_mfma_long_kernel(const uint8
     }
 }
 
+// Long rows, wave-private: wavefront w takes blocks w, w + NW, ... of every
+// row group of the work-group in turn (a unit = one block of the 16 rows); it
+// copies the unit's 16 row segments (from the 16-byte boundary at or below
+// each segment's start: 14 chunks hold the 210 bytes and the offset) into its
+// own LDS slot (rows 15 chunks apart: the 16 rows' reads of one offset fall
+// in 16 different bank groups) and computes from it while its next unit
+// loads; no work-group barrier between units. Its row sums of every group go
+// to its own LDS rows, and the work-group adds them over the wavefronts once,
+// at the end.
+namespace q6w {
+constexpr int CH = 14;                        // 16-byte chunks per row segment
+constexpr int PITCH = 15;                     // chunks per slot row
+constexpr int UP = q6m::R * CH;               // chunks per unit (224)
+constexpr int IPU = (UP + 63) / 64;           // wave loads per unit (4)
+constexpr uint32_t SLOT = (uint32_t)q6m::R * PITCH * 16u;
+}  // namespace q6w
+
+__host__ __device__ inline Q6mLayout q6w_layout(int bpr, int rounds, int nw) {
+    using namespace q6m;
+    Q6mLayout L;
+    L.meta = (uint32_t)bpr * TAB;
+    L.stage = L.meta + (uint32_t)bpr * META * 4;
+    L.aux = L.stage + (uint32_t)nw * q6w::SLOT;
+    L.ybuf = L.aux + (uint32_t)rounds * nw * R * 4;  // (aux: rounds x nw x R row sums)
+    L.normp = L.ybuf;
+    L.total = (size_t)L.ybuf;
+    return L;
+}
+
+template <int NW, int XI>
+__global__ __launch_bounds__(NW * 64) void gemv_q6k_wave_long_kernel(const uint8_t *__restrict__ w,
+                                                                     const float *__restrict__ x,
+                                                                     float *__restrict__ y, int n,
+                                                                     int bpr, int rounds,
+                                                                     GemvSched sch) {
+    using q6m::R, q6m::BB, q6m::TAB;
+    using q6w::CH, q6w::PITCH, q6w::UP, q6w::IPU;
+    constexpr int NT = NW * 64;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const Q6mLayout Lo = q6w_layout(bpr, rounds, NW);
+    float *meta = reinterpret_cast<float *>(lds + Lo.meta);
+    float *aux = reinterpret_cast<float *>(lds + Lo.aux);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    uint8_t *slot = lds + Lo.stage + (uint32_t)wave * q6w::SLOT;
+    const long RB = (long)bpr * BB;
+    const u32x4 *wc = reinterpret_cast<const u32x4 *>(w);
+    const long last_chunk = (long)n * RB / 16 - 1;
+
+    // chunk p of a unit: row p / CH, chunk p % CH of its segment
+    int prow[IPU], pch[IPU];
+    uint32_t plds[IPU];
+#pragma unroll
+    for (int k = 0; k < IPU; ++k) {
+        const int p = min(k * 64 + lane, UP - 1);
+        prow[k] = p / CH;
+        pch[k] = p - prow[k] * CH;
+        plds[k] = (uint32_t)((prow[k] * PITCH + pch[k]) * 16);
+    }
+    u32x4 stg[IPU];
+    // the unit (group row0, block b): row segments clamped to the last row,
+    // chunks to the tensor end
+    auto gload = [&](int row0, int b) {
+#pragma unroll
+        for (int k = 0; k < IPU; ++k) {
+            const long s = (long)min(row0 + prow[k], n - 1) * RB + (long)b * BB;
+            stg[k] = wc[min((s >> 4) + pch[k], last_chunk)];
+        }
+    };
+    // this wavefront's blocks per group: w, w + NW, ...
+    const int nb = wave < bpr ? (bpr - wave + NW - 1) / NW : 0;
+    gload((int)blockIdx.x * R, min(wave, bpr - 1));  // group 0 of every schedule is blockIdx.x
+    const int groups = (n + R - 1) / R;
+    const int my_groups = sched_count(sch, (int)blockIdx.x, (int)gridDim.x, groups);
+    const int U = my_groups * nb;
+
+    // ---- prologue: the whole row's activation table, XI items per thread ---
+    const int nitems = bpr * 32;
+    f32x4 xv[2 * XI];
+#pragma unroll
+    for (int k = 0; k < XI; ++k) {
+        const int ii = min(tid + k * NT, nitems - 1);
+        xv[2 * k] = ld_f32x4(x + (size_t)ii * 8);
+        xv[2 * k + 1] = ld_f32x4(x + (size_t)ii * 8 + 4);
+    }
+#pragma unroll
+    for (int k = 0; k < XI; ++k)
+        q6m_item(lds, meta, tid + k * NT, tid + k * NT < nitems, xv[2 * k], xv[2 * k + 1]);
+    // a wavefront with no blocks contributes zero rows
+    if (nb == 0)
+        for (int i = lane; i < my_groups * R; i += 64) aux[((i / R) * NW + wave) * R + i % R] = 0.0f;
+    __syncthreads();  // the table is complete; from here no wavefront waits for another
+
+    const int n16 = lane & 15, g = lane >> 4;
+    const Q6mLane ln = q6m_lane(lane);
+    half8 aop[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) aop[c] = half8{};
+    float yacc = 0.0f;
+    int q = 0, k = 0;  // group index and block index (of nb) of unit u
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int i = 0; i < IPU; ++i) *reinterpret_cast<u32x4 *>(slot + plds[i]) = stg[i];
+        __asm__ volatile("" ::: "memory");  // the unit's reads follow its stores (in-order LDS)
+        {
+            // the next unit (past the last one: the last again, a cache hit),
+            // unconditional so the load-counter waits stay exact
+            int q1 = q, k1 = k + 1;
+            if (k1 == nb) {
+                k1 = 0;
+                q1 = q + 1;
+            }
+            if (q1 >= my_groups) {
+                q1 = my_groups - 1;
+                k1 = nb - 1;
+            }
+            gload(sched_group(sch, (int)blockIdx.x, (int)gridDim.x, q1) * R, wave + k1 * NW);
+        }
+        const int b = wave + k * NW;
+        const int row = min(sched_group(sch, (int)blockIdx.x, (int)gridDim.x, q) * R + n16, n - 1);
+        const uint32_t rb = (uint32_t)(n16 * PITCH * 16) + (uint32_t)(((long)row * RB + (long)b * BB) & 15);
+        yacc += q6m_block(lds, slot, rb, b, ln, aop, meta, g);
+        if (++k == nb) {
+            yacc += __shfl_xor(yacc, 16, 64);
+            yacc += __shfl_xor(yacc, 32, 64);
+            if (lane < 16) aux[(q * NW + wave) * R + lane] = yacc;
+            yacc = 0.0f;
+            k = 0;
+            ++q;
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < my_groups * R; i += NT) {
+        const int qi = i / R, ri = i % R;
+        const int r = sched_group(sch, (int)blockIdx.x, (int)gridDim.x, qi) * R + ri;
+        if (r < n) {
+            float s = 0.0f;
+            for (int wv = 0; wv < NW; ++wv) s += aux[(qi * NW + wv) * R + ri];
+            y[r] = s;
+        }
+    }
+}
+
 namespace {
 
 // LDS attribute and occupancy of `kern` for rows of up to `probe_bpr` blocks
@@ -471,6 +620,29 @@ hipError_t q6m_long_launch(const uint8_t *w, const float *x, float *y, int n, in
 }
 
 template <int NW, int XI>
+hipError_t q6w_long_setup(int *occ) {
+    const void *kern = (const void *)gemv_q6k_wave_long_kernel<NW, XI>;
+    const hipError_t attr = allow_full_lds_by_addr(kern);
+    if (attr != hipSuccess) return attr;
+    *occ = occupancy_cached(kern, NW * 64, q6w_layout(q6m_long_probe<NW, XI>(), 8, NW).total, 1);
+    return hipSuccess;
+}
+
+template <int NW, int XI>
+hipError_t q6w_long_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
+                           hipStream_t stream) {
+    int occ = 1;
+    const hipError_t attr = q6w_long_setup<NW, XI>(&occ);
+    if (attr != hipSuccess) return attr;
+    const PersistPlan p = persistent_plan((n + q6m::R - 1) / q6m::R, occ);
+    const size_t lds = q6w_layout(bpr, (int)p.rounds, NW).total;
+    if (lds > 160 * 1024) return hipErrorNotSupported;
+    gemv_q6k_wave_long_kernel<NW, XI><<<(unsigned)p.grid, NW * 64, lds, stream>>>(w, x, y, n, bpr,
+                                                                                (int)p.rounds, p.sch);
+    return hipGetLastError();
+}
+
+template <int NW, int XI>
 hipError_t q6m_long_setup() {
     int occ = 0;
     return q6m_setup(gemv_q6k_mfma_long_kernel<NW, XI>, true, NW, q6m_long_probe<NW, XI>(), &occ);
@@ -491,6 +663,11 @@ hipError_t q6k_prepare() {
     if (e == hipSuccess) e = q6m_long_setup<LONG_NW, 4>();
     if (e == hipSuccess) e = q6m_long_setup<LONG_NW, 6>();
     if (e == hipSuccess) e = q6m_long_setup<LONG_NW, 8>();
+    if (e == hipSuccess) e = q6w_long_setup<LONG_NW, 1>(&occ);
+    if (e == hipSuccess) e = q6w_long_setup<LONG_NW, 2>(&occ);
+    if (e == hipSuccess) e = q6w_long_setup<LONG_NW, 4>(&occ);
+    if (e == hipSuccess) e = q6w_long_setup<LONG_NW, 6>(&occ);
+    if (e == hipSuccess) e = q6w_long_setup<LONG_NW, 8>(&occ);
     return e;
 }
 
@@ -506,6 +683,24 @@ hipError_t gemv_q6k_mfma_launch(const uint8_t *w, const float *x, float *y, int 
                           (const float *)nullptr, 0.0f);
     constexpr int LNW = LONG_NW, LNT = LNW * 64;
     const int need = (bpr * 32 + LNT - 1) / LNT;  // table items per thread
+    // wave-private long rows (no barrier between units; all 16 wavefronts
+    // busy on 74 blocks where 14-block stages left 2 idle): Q4_K_M decode
+    // step 1.414 -> 1.364 ms, alternating on one box; the staged kernel for
+    // rows whose table and slots exceed LDS (bpr > ~80). MGQ_Q6K_WAVE=0
+    // selects the staged kernel.
+    static const int wave_env = [] {
+        const char *v = std::getenv("MGQ_Q6K_WAVE");
+        return (v && *v) ? std::atoi(v) : 1;
+    }();
+    if (wave_env) {
+        hipError_t ew = hipErrorNotSupported;
+        if (need <= 1) ew = q6w_long_launch<LNW, 1>(w, x, y, n, bpr, stream);
+        else if (need <= 2) ew = q6w_long_launch<LNW, 2>(w, x, y, n, bpr, stream);
+        else if (need <= 4) ew = q6w_long_launch<LNW, 4>(w, x, y, n, bpr, stream);
+        else if (need <= 6) ew = q6w_long_launch<LNW, 6>(w, x, y, n, bpr, stream);
+        else if (need <= 8) ew = q6w_long_launch<LNW, 8>(w, x, y, n, bpr, stream);
+        if (ew != hipErrorNotSupported) return ew;
+    }
     if (need <= 1) return q6m_long_launch<LNW, 1>(w, x, y, n, bpr, stream);
     if (need <= 2) return q6m_long_launch<LNW, 2>(w, x, y, n, bpr, stream);
     if (need <= 4) return q6m_long_launch<LNW, 4>(w, x, y, n, bpr, stream);
