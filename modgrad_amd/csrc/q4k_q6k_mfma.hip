@@ -14,8 +14,9 @@
 //   * Whole-row stage: a row group's 16 rows are one contiguous byte range
 //     (16 x RB, RB = 210 bpr), copied flat into LDS as whole 16-byte chunks;
 //     the next group's chunks wait in registers.
-//   * Long rows (bpr > kQ6mMaxBpr), wave-private (gemv_q6k_wave_long_kernel,
-//     the default): wavefront w stages block w, w + 16, ... of the 16 rows in
+//   * Long rows (bpr > kQ6mMaxBpr), and the fused-RMSNorm launches of any
+//     length (14 wavefronts), wave-private (gemv_q6k_wave_long_kernel, the
+//     default): wavefront w stages block w, w + NW, ... of the 16 rows in
 //     its own LDS slot (each row segment as the 16-byte chunks from the
 //     16-byte boundary at or below its start; the segment's offset in that
 //     chunk (s & 15) moves the lane's reads) and computes from it with no
@@ -458,17 +459,19 @@ __host__ __device__ inline Q6mLayout q6w_layout(int bpr, int rounds, int nw) {
     L.stage = L.meta + (uint32_t)bpr * META * 4;
     L.aux = L.stage + (uint32_t)nw * q6w::SLOT;
     L.ybuf = L.aux + (uint32_t)rounds * nw * R * 4;  // (aux: rounds x nw x R row sums)
-    L.normp = L.ybuf;
-    L.total = (size_t)L.ybuf;
+    L.normp = L.ybuf;                                 // fused RMSNorm: one sum(x^2) per wavefront
+    L.total = (size_t)L.normp + (size_t)nw * 4;
     return L;
 }
 
-template <int NW, int XI>
+template <int NW, int XI, bool NORM = false>
 __global__ __launch_bounds__(NW * 64) void gemv_q6k_wave_long_kernel(const uint8_t *__restrict__ w,
                                                                      const float *__restrict__ x,
                                                                      float *__restrict__ y, int n,
                                                                      int bpr, int rounds,
-                                                                     GemvSched sch) {
+                                                                     GemvSched sch,
+                                                                     const float *__restrict__ nw = nullptr,
+                                                                     float eps = 0.0f) {
     using q6m::R, q6m::BB, q6m::TAB;
     using q6w::CH, q6w::PITCH, q6w::UP, q6w::IPU;
     constexpr int NT = NW * 64;
@@ -519,6 +522,25 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_wave_long_kernel(const uint8
         xv[2 * k] = ld_f32x4(x + (size_t)ii * 8);
         xv[2 * k + 1] = ld_f32x4(x + (size_t)ii * 8 + 4);
     }
+    float *normp = reinterpret_cast<float *>(lds + Lo.normp);
+    if constexpr (NORM) {
+        // sum(x^2) of this thread's items (clamped duplicates add 0), reduced
+        // per wavefront; the table holds x .* nw (as gemv_q6k_mfma_kernel)
+        float ssq = 0.0f;
+#pragma unroll
+        for (int k = 0; k < XI; ++k) {
+            const f32x4 v0 = xv[2 * k], v1 = xv[2 * k + 1];
+            const float s = ((v0[0] * v0[0] + v0[1] * v0[1]) + (v0[2] * v0[2] + v0[3] * v0[3])) +
+                            ((v1[0] * v1[0] + v1[1] * v1[1]) + (v1[2] * v1[2] + v1[3] * v1[3]));
+            ssq += tid + k * NT < nitems ? s : 0.0f;
+            const int ii = min(tid + k * NT, nitems - 1);
+            xv[2 * k] = v0 * ld_f32x4(nw + (size_t)ii * 8);
+            xv[2 * k + 1] = v1 * ld_f32x4(nw + (size_t)ii * 8 + 4);
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ssq += __shfl_xor(ssq, off, 64);
+        if (lane == 0) normp[wave] = ssq;
+    }
 #pragma unroll
     for (int k = 0; k < XI; ++k)
         q6m_item(lds, meta, tid + k * NT, tid + k * NT < nitems, xv[2 * k], xv[2 * k + 1]);
@@ -566,13 +588,20 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_wave_long_kernel(const uint8
         }
     }
     __syncthreads();
+    float rstd = 1.0f;
+    if constexpr (NORM) {
+        // rms_norm's 1/sqrt(mean(x^2) + eps) (kernels/rms_norm.hip:63-68)
+        float ss = 0.0f;
+        for (int wv = 0; wv < NW; ++wv) ss += normp[wv];
+        rstd = rsqrtf(ss / (float)(bpr * kBlockElems) + eps);
+    }
     for (int i = tid; i < my_groups * R; i += NT) {
         const int qi = i / R, ri = i % R;
         const int r = sched_group(sch, (int)blockIdx.x, (int)gridDim.x, qi) * R + ri;
         if (r < n) {
             float s = 0.0f;
             for (int wv = 0; wv < NW; ++wv) s += aux[(qi * NW + wv) * R + ri];
-            y[r] = s;
+            y[r] = NORM ? s * rstd : s;
         }
     }
 }
@@ -619,26 +648,26 @@ hipError_t q6m_long_launch(const uint8_t *w, const float *x, float *y, int n, in
                       q6m_long_probe<NW, XI>(), stream);
 }
 
-template <int NW, int XI>
+template <int NW, int XI, bool NORM = false>
 hipError_t q6w_long_setup(int *occ) {
-    const void *kern = (const void *)gemv_q6k_wave_long_kernel<NW, XI>;
+    const void *kern = (const void *)gemv_q6k_wave_long_kernel<NW, XI, NORM>;
     const hipError_t attr = allow_full_lds_by_addr(kern);
     if (attr != hipSuccess) return attr;
     *occ = occupancy_cached(kern, NW * 64, q6w_layout(q6m_long_probe<NW, XI>(), 8, NW).total, 1);
     return hipSuccess;
 }
 
-template <int NW, int XI>
+template <int NW, int XI, bool NORM = false>
 hipError_t q6w_long_launch(const uint8_t *w, const float *x, float *y, int n, int bpr,
-                           hipStream_t stream) {
+                           hipStream_t stream, const float *nw = nullptr, float eps = 0.0f) {
     int occ = 1;
-    const hipError_t attr = q6w_long_setup<NW, XI>(&occ);
+    const hipError_t attr = q6w_long_setup<NW, XI, NORM>(&occ);
     if (attr != hipSuccess) return attr;
     const PersistPlan p = persistent_plan((n + q6m::R - 1) / q6m::R, occ);
     const size_t lds = q6w_layout(bpr, (int)p.rounds, NW).total;
     if (lds > 160 * 1024) return hipErrorNotSupported;
-    gemv_q6k_wave_long_kernel<NW, XI><<<(unsigned)p.grid, NW * 64, lds, stream>>>(w, x, y, n, bpr,
-                                                                                (int)p.rounds, p.sch);
+    gemv_q6k_wave_long_kernel<NW, XI, NORM><<<(unsigned)p.grid, NW * 64, lds, stream>>>(
+        w, x, y, n, bpr, (int)p.rounds, p.sch, nw, eps);
     return hipGetLastError();
 }
 
@@ -668,6 +697,7 @@ hipError_t q6k_prepare() {
     if (e == hipSuccess) e = q6w_long_setup<LONG_NW, 4>(&occ);
     if (e == hipSuccess) e = q6w_long_setup<LONG_NW, 6>(&occ);
     if (e == hipSuccess) e = q6w_long_setup<LONG_NW, 8>(&occ);
+    if (e == hipSuccess) e = q6w_long_setup<14, 1, true>(&occ);
     return e;
 }
 
@@ -678,6 +708,9 @@ hipError_t gemv_q6k_mfma_launch(const uint8_t *w, const float *x, float *y, int 
     // a tensor size that is a multiple of 16 (x needs only float alignment)
     if (((uintptr_t)w & 15u) || (((long)n * bpr * BB) % 16))
         return hipErrorNotSupported;
+    // (the wave-private kernel over 14 wavefronts, one block each, measured
+    // no faster on the plain lm_head: 86.0 -> 86.4-86.8 us; the whole-row
+    // kernel stays for plain rows of up to 14 blocks)
     if (bpr <= MAX_BPR)
         return q6m_launch(gemv_q6k_mfma_kernel<false>, false, NW, w, x, y, n, bpr, MAX_BPR, stream,
                           (const float *)nullptr, 0.0f);
@@ -717,6 +750,19 @@ hipError_t gemv_q6k_mfma_norm_launch(const uint8_t *w, const float *x, const flo
     // the output matrix)
     if (((uintptr_t)w & 15u) || (((long)n * bpr * BB) % 16) || bpr > MAX_BPR)
         return hipErrorNotSupported;
+    // The wave-private kernel, one block per wavefront over 14 wavefronts
+    // (no barrier between the copy and the compute): Q4_K_M decode step,
+    // whose fused-norm Q6_K launches are attn_v (512 rows) and the output
+    // matrix, 1.367 -> 1.356 ms alternating on one box. MGQ_Q6K_WHOLE_WAVE=0
+    // keeps the whole-row kernel.
+    static const int whole_env = [] {
+        const char *v = std::getenv("MGQ_Q6K_WHOLE_WAVE");
+        return (v && *v) ? std::atoi(v) : 1;
+    }();
+    if (whole_env) {
+        const hipError_t ew = q6w_long_launch<14, 1, true>(w, x, y, n, bpr, stream, nw, eps);
+        if (ew != hipErrorNotSupported) return ew;
+    }
     return q6m_launch(gemv_q6k_mfma_kernel<true>, false, NW, w, x, y, n, bpr, MAX_BPR, stream, nw,
                       eps);
 }
