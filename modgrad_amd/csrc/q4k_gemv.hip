@@ -33,11 +33,15 @@
 //        loads (64 consecutive pieces per wave instruction), PF stages ahead
 //        of the one being computed.
 //    Per 32 rows x 1 block a wave issues 16 MFMAs and about 220 VALU ops.
+//    Its kStageWave variant stages per wavefront (below) for the Q8 / dp4a,
+//    fused RMSNorm / GLU and Q5_K modes.
 //
 // 3. gemv_wave_kernel -- the same arithmetic with every wavefront staging
 //    its own unit through its own LDS slot, so stages need no work-group
 //    barrier; used for plain f32 matvecs whose work-groups stream several
-//    stages (gate|up, lm_head, down).
+//    stages (gate|up, lm_head, down). With DIRECT (one unit per wavefront:
+//    o and other single-stage 16-row launches) each lane loads the pieces it
+//    multiplies straight into registers.
 //
 // 4. gemv_batched_kernel -- vector-ALU batched GEMV (up to 16 activation rows).
 #include "q4k_device.hpp"
