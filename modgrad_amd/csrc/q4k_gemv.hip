@@ -921,30 +921,32 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
     uint8_t *slot = lds + Lo.slots + (uint32_t)wave * (R * SP * 16u);
 
     // piece p of the unit: row p / RUN, piece p % RUN of the row's run (R = 16:
-    // block cb0 + (p % RUN) / 9), clamped past the unit's 288
-    uint32_t prow[IPW], pcol[IPW], plds[IPW], ppc[IPW];
+    // block cb0 + (p % RUN) / 9), clamped past the unit's 288; poff is its
+    // byte offset from the unit's first piece in row 0
+    uint32_t poff[IPW], plds[IPW];
 #pragma unroll
     for (int k = 0; k < IPW; ++k) {
         const int p = std::min(k * 64 + lane, UP - 1);
         const int row = p / RUN, rem = p - row * RUN;
-        prow[k] = (uint32_t)row;
-        pcol[k] = (uint32_t)(cb0 * BB + 16 * rem);       // byte column within the stage
-        ppc[k] = (uint32_t)(16 * (rem % BP));             // the piece within its block
+        poff[k] = (uint32_t)row * (uint32_t)row_bytes + (uint32_t)(cb0 * BB + 16 * rem);
         plds[k] = (uint32_t)((row * SP + rem) * 16);
     }
     u32x4 stg[IPW];
-    // unit pieces of stage column tcol of the rows from r0 (the tile rows past
-    // the group re-read its last row; blocks past the row end re-read the last)
-    auto gload_at = [&](uint32_t r0, uint32_t tcol) {
-        const uint32_t glast = (uint32_t)gr - 1u, rlast = (uint32_t)(n - 1);
-        const uint32_t rb = (uint32_t)row_bytes, lastb = (uint32_t)((bpr - 1) * BB);
+    // unit pieces of stage column tcol of the rows from r0: one uniform base
+    // and a 32-bit offset per lane, so the next unit's loads go out one
+    // v_min after the current unit's slot stores. Pieces that no result
+    // uses (tile rows past the group or the matrix, blocks past the row end)
+    // read whatever bytes follow, clamped to the matrix's last piece.
+    const uint64_t wlast = (uint64_t)n * row_bytes - 16;
+    auto unit_lim = [&](uint64_t b0) { return (uint32_t)std::min<uint64_t>(wlast - b0, 0xFFFFFFF0ull); };
+    auto gload_b = [&](uint64_t b0, uint32_t lim) {
+        const uint8_t *base = w + b0;
 #pragma unroll
-        for (int k = 0; k < IPW; ++k) {
-            const uint32_t rr = std::min(r0 + std::min(prow[k], glast), rlast);
-            const uint32_t c0 = tcol + pcol[k];
-            const uint32_t col = std::min(c0 - ppc[k], lastb) + ppc[k];
-            stg[k] = ld_u32x4(w + ((uint64_t)rr * rb + col));
-        }
+        for (int k = 0; k < IPW; ++k) stg[k] = ld_u32x4(base + std::min(poff[k], lim));
+    };
+    auto gload_at = [&](uint32_t r0, uint32_t tcol) {
+        const uint64_t b0 = (uint64_t)r0 * row_bytes + tcol;
+        gload_b(b0, unit_lim(b0));
     };
     auto lstore = [&]() {
 #pragma unroll
@@ -1061,17 +1063,28 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
     };
 
     float yaccA = 0.0f, yaccB = 0.0f;
+    int t = 0, ug = 0;  // this unit's stage, and its group's index in the work-group's schedule
     for (int q = 0; q < Q; ++q) {
-        const int t = q % stages;
+        // the next unit (past the last one: the last again, a cache hit)
+        int t1 = t + 1, g1 = ug;
+        if (t1 == stages) {
+            t1 = 0;
+            ++g1;
+        }
+        if (q + 1 >= Q) {
+            t1 = t;
+            g1 = ug;
+        }
+        // its base, worked out before this unit's slot stores wait for its data
+        const uint64_t nb0 =
+            (uint64_t)((uint32_t)sched_group(sch, (int)blockIdx.x, (int)gridDim.x, g1) * (uint32_t)gr) * row_bytes +
+            (uint32_t)(t1 * C * BB);
+        const uint32_t nlim = unit_lim(nb0);
         if constexpr (!DIRECT) {
+            __asm__ volatile("" : : "s"(nlim), "s"((uint32_t)nb0), "s"((uint32_t)(nb0 >> 32)));
             lstore();
             __asm__ volatile("" ::: "memory");  // the unit's reads follow its stores (in-order LDS)
-            // the next unit (past the last one: the last again, a cache hit),
-            // unconditional so the load-counter waits stay exact
-            const int q1 = std::min(q + 1, Q - 1);
-            const uint32_t r0 =
-                (uint32_t)sched_group(sch, (int)blockIdx.x, (int)gridDim.x, q1 / stages) * (uint32_t)gr;
-            gload_at(r0, (uint32_t)((q1 % stages) * C * BB));
+            gload_b(nb0, nlim);  // unconditional, so the load-counter waits stay exact
         }
         const int bA = t * C + cb0, bB = (R == 32) ? bA : bA + 1;
         if (bA < bpr) {
@@ -1116,7 +1129,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
             yaccA += __shfl_xor(yaccA, 32, 64);
             yaccB += __shfl_xor(yaccB, 16, 64);
             yaccB += __shfl_xor(yaccB, 32, 64);
-            float *ag = aux + ((size_t)(q / stages) * NW + wave) * R;
+            float *ag = aux + ((size_t)ug * NW + wave) * R;
             if (lane < 16) {
                 ag[lane] = yaccA;
                 if (R == 32) ag[16 + lane] = yaccB;
@@ -1124,6 +1137,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
             yaccA = 0.0f;
             yaccB = 0.0f;
         }
+        t = t1;
+        ug = g1;
     }
     __syncthreads();
     for (int i = tid; i < my_groups * R; i += NW * 64) {
