@@ -342,7 +342,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     // exact and only the set being stored is waited for. The piece -> (row,
     // byte column) split of each load is stage-invariant and precomputed.
     constexpr int RP = stage_row_pieces(C, BP);   // LDS pieces per staged row
-    uint32_t prow[IPW], pcol[IPW], plast[IPW], plds[IPW];
+    // kStageWave: the wavefront's unit starts at block cbu of each stage
+    const int cbu = (R == 32) ? wave : 2 * wave;
+    uint32_t poff[IPW], pcol[IPW], plast[IPW], plds[IPW];
 #pragma unroll
     for (int k = 0; k < IPW; ++k) {
         int row, rem;
@@ -350,7 +352,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
             // piece p of this wavefront's unit: row p / RUN, from its first block
             const int p = std::min(k * 64 + lane, R * RUN - 1);
             row = p / RUN;
-            rem = ((R == 32) ? wave : 2 * wave) * BP + (p - row * RUN);
+            rem = cbu * BP + (p - row * RUN);
         } else {
             const int j = std::min((wave + k * NW) * 64 + lane, PIECES - 1);
             row = j / (BP * C);
@@ -358,22 +360,39 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         }
         const int cb = rem / BP, pc = rem - cb * BP;
         plds[k] = (uint32_t)((row * RP + rem) * 16);    // LDS byte offset in the stage
-        prow[k] = (uint32_t)row;
+        // the tile rows past the group (gr <= R rows) re-read its last row
+        poff[k] = (uint32_t)std::min(row, gr - 1) * (uint32_t)row_bytes;
+        if constexpr (WV) poff[k] += (uint32_t)(16 * (rem - cbu * BP));  // within the unit
         pcol[k] = (uint32_t)(cb * BB + 16 * pc);          // byte column within the stage
         plast[k] = (uint32_t)((bpr - 1) * BB + 16 * pc);  // same piece of the last block
     }
-    // Stage (pass vg, column tcol) of the rows from r0: matrix wm, the tile
-    // rows past the group (gr <= R rows) re-read its last row.
-    auto gload_at = [&](uint32_t r0, uint32_t tcol, const uint8_t *wm, u32x4(&dst)[IPW]) {
-        const uint32_t glast = (uint32_t)gr - 1u;
-        const uint32_t rlast = (uint32_t)(n - 1), rb = (uint32_t)row_bytes;
+    // Stage (pass vg, column tcol) of the rows from r0 in matrix wm: a
+    // uniform base and one 32-bit offset per lane. Pieces past the row end
+    // re-read the row's last block (kStageWave: a unit wholly past it, the
+    // row's last blocks); rows past the matrix read its last piece.
+    const uint64_t wlast = (uint64_t)n * row_bytes - 16;
+    const uint32_t lastcol = (uint32_t)std::max(bpr - (R == 32 ? 1 : 2), 0) * BB;
+    struct UnitAddr {
+        const uint8_t *base;
+        uint32_t lim, tcol;
+    };
+    auto uaddr = [&](uint32_t r0, uint32_t tcol, const uint8_t *wm) -> UnitAddr {
+        uint64_t b0 = (uint64_t)r0 * row_bytes;
+        if constexpr (WV) {
+            const uint32_t c = tcol + (uint32_t)(cbu * BB);
+            b0 += c < (uint32_t)row_bytes ? c : lastcol;
+        }
+        return UnitAddr{wm + b0, (uint32_t)std::min<uint64_t>(wlast - b0, 0xFFFFFFF0ull), tcol};
+    };
+    auto gload_u = [&](const UnitAddr &a, u32x4(&dst)[IPW]) {
 #pragma unroll
         for (int k = 0; k < IPW; ++k) {
-            const uint32_t rr = std::min(r0 + std::min(prow[k], glast), rlast);
-            const uint32_t col = std::min(tcol + pcol[k], plast[k]);
-            const uint64_t off = (uint64_t)rr * rb + col;  // one v_mad_u64_u32
-            dst[k] = ld_u32x4(wm + off);
+            const uint32_t o = WV ? poff[k] : poff[k] + std::min(a.tcol + pcol[k], plast[k]);
+            dst[k] = ld_u32x4(a.base + std::min(o, a.lim));
         }
+    };
+    auto gload_at = [&](uint32_t r0, uint32_t tcol, const uint8_t *wm, u32x4(&dst)[IPW]) {
+        gload_u(uaddr(r0, tcol, wm), dst);
     };
     // The first stage: row group 0 of every schedule is blockIdx.x (and a
     // work-group owns at least one), pass 0 reads w from column 0. It needs
@@ -568,14 +587,16 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         if (lane == 0) reinterpret_cast<float *>(lds + Lo.normp)[wave] = ssq;
     }
   }
-    auto gload = [&](int q, u32x4(&dst)[IPW]) {
+    // the base of stage q (past the last one: the last again, a cache hit)
+    auto qaddr = [&](int q) -> UnitAddr {
         q = std::min(q, Q - 1);
         const int vg = q / stages;  // pass index: row group vg / VM, matrix vg % VM
         const uint32_t r0 =
             (uint32_t)sched_group(sch, (int)blockIdx.x, (int)gridDim.x, vg / VM) * (uint32_t)gr;
         const uint8_t *wm = (VM == 2 && (vg & 1)) ? fz.w2 : w;
-        gload_at(r0, (uint32_t)((q % stages) * C * BB), wm, dst);
+        return uaddr(r0, (uint32_t)((q % stages) * C * BB), wm);
     };
+    auto gload = [&](int q, u32x4(&dst)[IPW]) { gload_u(qaddr(q), dst); };
 #pragma unroll
     for (int f = 1; f < PF; ++f) gload(f, stg[f]);
     // (the barrier before the first stage is computed also orders the table)
@@ -660,6 +681,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     auto step = [&](const int q, auto fc, const bool more) {
         constexpr int F = decltype(fc)::value;
         const int t = q % stages;
+        // the refill's base, worked out before the stage's loads are waited for
+        const UnitAddr na = qaddr(q + 1 + PF);
         const uint8_t *sbuf = lds + Lo.stage + (dbuf ? (q & 1) * Lo.stage_bytes : 0u);
         for (int u = wave; u < UNITS; u += NW) {
             // tile A = (rows rowA.., block cbA), tile B = (rows rowB.., block cbB)
@@ -764,7 +787,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
             if (more) {
                 lstore(0, stg[(F + 1) % PF]);
                 __asm__ volatile("" ::: "memory");
-                gload(q + 1 + PF, stg[(F + 1) % PF]);
+                gload_u(na, stg[(F + 1) % PF]);
             }
             if (group_end) {
                 yaccA = 0.0f;
@@ -775,7 +798,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         if (more) {
             if (!dbuf) __syncthreads();  // every wave is done reading the single buffer
             lstore(dbuf ? ((q + 1) & 1) : 0, stg[(F + 1) % PF]);
-            gload(q + 1 + PF, stg[(F + 1) % PF]);
+            gload_u(na, stg[(F + 1) % PF]);
         }
         __syncthreads();
         if (group_end) {
@@ -922,22 +945,29 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
 
     // piece p of the unit: row p / RUN, piece p % RUN of the row's run (R = 16:
     // block cb0 + (p % RUN) / 9), clamped past the unit's 288; poff is its
-    // byte offset from the unit's first piece in row 0
+    // byte offset from the unit's first piece in row 0 (tile rows past the
+    // group re-read its last row)
     uint32_t poff[IPW], plds[IPW];
 #pragma unroll
     for (int k = 0; k < IPW; ++k) {
         const int p = std::min(k * 64 + lane, UP - 1);
         const int row = p / RUN, rem = p - row * RUN;
-        poff[k] = (uint32_t)row * (uint32_t)row_bytes + (uint32_t)(cb0 * BB + 16 * rem);
+        poff[k] = (uint32_t)std::min(row, gr - 1) * (uint32_t)row_bytes + (uint32_t)(16 * rem);
         plds[k] = (uint32_t)((row * SP + rem) * 16);
     }
     u32x4 stg[IPW];
     // unit pieces of stage column tcol of the rows from r0: one uniform base
     // and a 32-bit offset per lane, so the next unit's loads go out one
-    // v_min after the current unit's slot stores. Pieces that no result
-    // uses (tile rows past the group or the matrix, blocks past the row end)
-    // read whatever bytes follow, clamped to the matrix's last piece.
+    // v_min after the current unit's slot stores. A unit wholly past the row
+    // end re-reads the row's last blocks (cache hits); the second block of a
+    // unit that starts at an odd row's last block, and rows past the matrix,
+    // read what follows (no result uses them), clamped to the last piece.
     const uint64_t wlast = (uint64_t)n * row_bytes - 16;
+    const uint32_t lastcol = (uint32_t)std::max(bpr - (R == 32 ? 1 : 2), 0) * BB;
+    auto unit_b0 = [&](uint32_t r0, uint32_t tcol) {
+        const uint32_t c = tcol + (uint32_t)(cb0 * BB);
+        return (uint64_t)r0 * row_bytes + (c < (uint32_t)row_bytes ? c : lastcol);
+    };
     auto unit_lim = [&](uint64_t b0) { return (uint32_t)std::min<uint64_t>(wlast - b0, 0xFFFFFFF0ull); };
     auto gload_b = [&](uint64_t b0, uint32_t lim) {
         const uint8_t *base = w + b0;
@@ -945,7 +975,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
         for (int k = 0; k < IPW; ++k) stg[k] = ld_u32x4(base + std::min(poff[k], lim));
     };
     auto gload_at = [&](uint32_t r0, uint32_t tcol) {
-        const uint64_t b0 = (uint64_t)r0 * row_bytes + tcol;
+        const uint64_t b0 = unit_b0(r0, tcol);
         gload_b(b0, unit_lim(b0));
     };
     auto lstore = [&]() {
@@ -1077,8 +1107,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
         }
         // its base, worked out before this unit's slot stores wait for its data
         const uint64_t nb0 =
-            (uint64_t)((uint32_t)sched_group(sch, (int)blockIdx.x, (int)gridDim.x, g1) * (uint32_t)gr) * row_bytes +
-            (uint32_t)(t1 * C * BB);
+            unit_b0((uint32_t)sched_group(sch, (int)blockIdx.x, (int)gridDim.x, g1) * (uint32_t)gr,
+                    (uint32_t)(t1 * C * BB));
         const uint32_t nlim = unit_lim(nb0);
         if constexpr (!DIRECT) {
             __asm__ volatile("" : : "s"(nlim), "s"((uint32_t)nb0), "s"((uint32_t)(nb0 >> 32)));
