@@ -491,37 +491,46 @@ __global__ __launch_bounds__(NW * 64) void gemv_batched_wave_kernel(const uint8_
     const int kb0 = kp * kspan, kb1 = std::min(bpr, kb0 + kspan);
     const int wb0 = kb0 + wave * CB;  // this wavefront's first block in slice 0
 
-    // piece p of a unit: row p / RUN, piece p % RUN of the row's run
-    uint32_t prow[IPU], pcol[IPU], plds[IPU];
+    // piece p of a unit: row p / RUN, piece p % RUN of the row's run; poff is
+    // its byte offset from the unit's first piece (tile rows past the group
+    // of gr <= R rows re-read its last row)
+    uint32_t poff[IPU], plds[IPU];
 #pragma unroll
     for (int k = 0; k < IPU; ++k) {
         const int p = std::min(k * 64 + lane, UP - 1);
         const int row = p / RUN, rem = p - row * RUN;
-        prow[k] = (uint32_t)row;
-        pcol[k] = (uint32_t)(16 * rem);
+        poff[k] = (uint32_t)std::min(row, gr - 1) * (uint32_t)row_bytes + (uint32_t)(16 * rem);
         plds[k] = (uint32_t)((row * SP + rem) * 16);
     }
-    const uint32_t lastcol = (uint32_t)((bpr - 1) * BB);
-    // unit (slice sl, group index i) of gr <= R rows: tile rows past the
-    // group re-read its last row, rows past n the last row; blocks past the
-    // row end re-read the last block (same piece)
-    u32x4 stg[IPU];
-    auto gload = [&](int sl, int i) __attribute__((always_inline)) {
-        const uint32_t r0 = (uint32_t)(bx + i * G) * (uint32_t)gr, rlast = (uint32_t)(n - 1);
-        const uint32_t glast = (uint32_t)gr - 1u;
-        const uint32_t c0 = (uint32_t)((wb0 + sl * SW) * BB);
-#pragma unroll
-        for (int k = 0; k < IPU; ++k) {
-            const uint32_t rr = std::min(r0 + std::min(prow[k], glast), rlast);
-            const uint32_t pc16 = pcol[k] % (16u * PC);
-            const uint32_t col = std::min(c0 + pcol[k] - pc16, lastcol) + pc16;
-            stg[k] = ld_u32x4(w + ((uint64_t)rr * row_bytes + col));
-        }
+    // unit (slice sl, group index i): one uniform base and a 32-bit offset per
+    // lane, so the next unit's loads go out one v_min after the slot stores.
+    // A unit wholly past the row end re-reads the row's last blocks (cache
+    // hits); blocks past the end of a unit that starts inside the row, and
+    // rows past the matrix, read what follows (no result uses them), clamped
+    // to the matrix's last piece.
+    const uint64_t wlast = (uint64_t)n * row_bytes - 16;
+    const uint32_t lastcol = (uint32_t)std::max(bpr - CB, 0) * BB;
+    struct UnitAddr {
+        const uint8_t *base;
+        uint32_t lim;
     };
-    gload(0, 0);  // the first unit before any schedule arithmetic
+    // a group index past the last group (the work-group's last slots) re-reads
+    // the last group; no result of it is stored
+    const int groups = (n + gr - 1) / gr;
+    auto uaddr = [&](int sl, int i) __attribute__((always_inline)) -> UnitAddr {
+        const uint32_t c = (uint32_t)((wb0 + sl * SW) * BB);
+        const uint32_t grp = (uint32_t)std::min(bx + i * G, groups - 1);
+        const uint64_t b0 = (uint64_t)(grp * (uint32_t)gr) * row_bytes + (c < (uint32_t)row_bytes ? c : lastcol);
+        return UnitAddr{w + b0, (uint32_t)std::min<uint64_t>(wlast - b0, 0xFFFFFFF0ull)};
+    };
+    u32x4 stg[IPU];
+    auto gload_u = [&](const UnitAddr &a) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < IPU; ++k) stg[k] = ld_u32x4(a.base + std::min(poff[k], a.lim));
+    };
+    gload_u(uaddr(0, 0));  // the first unit before any schedule arithmetic
     const int slices = (kb1 - kb0 + SW - 1) / SW;
     const int U = slices * gpw;
-    const int groups = (n + gr - 1) / gr;
 
     const BatchedWs Lw = batched_ws(bpr, SETS);
     const int n16 = lane & 15, g = lane >> 4, hsel = g >> 1;
@@ -558,16 +567,15 @@ __global__ __launch_bounds__(NW * 64) void gemv_batched_wave_kernel(const uint8_
     };
     int csl = 0, ci = 0;  // compute position
     for (int u = 0; u < U; ++u) {
+        // the next unit (past the last one: the last again, a cache hit), its
+        // base worked out before the slot stores wait for this unit's data
+        const bool new_slice = li == 0 && lsl < slices;
+        const int next_sl = lsl;
+        const UnitAddr na = lsl < slices ? uaddr(lsl, li) : uaddr(slices - 1, gpw - 1);
 #pragma unroll
         for (int k = 0; k < IPU; ++k) *reinterpret_cast<u32x4 *>(slot + plds[k]) = stg[k];
         __asm__ volatile("" ::: "memory");  // the unit's reads follow its stores (in-order LDS)
-        // the next unit (past the last one: the last again, a cache hit)
-        const bool new_slice = li == 0 && lsl < slices;
-        const int next_sl = lsl;
-        if (lsl < slices)
-            gload(lsl, li);
-        else
-            gload(slices - 1, gpw - 1);
+        gload_u(na);
         advance(lsl, li);
 
         const int jb0 = wb0 + csl * SW;

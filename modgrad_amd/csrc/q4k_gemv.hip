@@ -377,7 +377,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         uint32_t lim, tcol;
     };
     auto uaddr = [&](uint32_t r0, uint32_t tcol, const uint8_t *wm) -> UnitAddr {
-        uint64_t b0 = (uint64_t)r0 * row_bytes;
+        uint64_t b0 = (uint64_t)std::min(r0, (uint32_t)(n - 1)) * row_bytes;
         if constexpr (WV) {
             const uint32_t c = tcol + (uint32_t)(cbu * BB);
             b0 += c < (uint32_t)row_bytes ? c : lastcol;
@@ -966,7 +966,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
     const uint32_t lastcol = (uint32_t)std::max(bpr - (R == 32 ? 1 : 2), 0) * BB;
     auto unit_b0 = [&](uint32_t r0, uint32_t tcol) {
         const uint32_t c = tcol + (uint32_t)(cb0 * BB);
-        return (uint64_t)r0 * row_bytes + (c < (uint32_t)row_bytes ? c : lastcol);
+        return (uint64_t)std::min(r0, (uint32_t)(n - 1)) * row_bytes + (c < (uint32_t)row_bytes ? c : lastcol);
     };
     auto unit_lim = [&](uint64_t b0) { return (uint32_t)std::min<uint64_t>(wlast - b0, 0xFFFFFFF0ull); };
     auto gload_b = [&](uint64_t b0, uint32_t lim) {
