@@ -483,32 +483,43 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_wave_long_kernel(const uint8
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     uint8_t *slot = lds + Lo.stage + (uint32_t)wave * q6w::SLOT;
     const long RB = (long)bpr * BB;
-    const u32x4 *wc = reinterpret_cast<const u32x4 *>(w);
-    const long last_chunk = (long)n * RB / 16 - 1;
+    const uint64_t last_off = ((uint64_t)n * RB / 16 - 1) * 16;  // the last whole chunk
 
-    // chunk p of a unit: row p / CH, chunk p % CH of its segment
-    int prow[IPU], pch[IPU];
-    uint32_t plds[IPU];
+    // chunk p of a unit: row p / CH, chunk p % CH of its segment (the 16-byte
+    // chunks that hold the row's 210 bytes of the block)
+    uint32_t prb[IPU], pc16[IPU], plds[IPU];
 #pragma unroll
     for (int k = 0; k < IPU; ++k) {
         const int p = min(k * 64 + lane, UP - 1);
-        prow[k] = p / CH;
-        pch[k] = p - prow[k] * CH;
-        plds[k] = (uint32_t)((prow[k] * PITCH + pch[k]) * 16);
+        const int row = p / CH, ch = p - row * CH;
+        prb[k] = (uint32_t)row * (uint32_t)RB;
+        pc16[k] = (uint32_t)(16 * ch);
+        plds[k] = (uint32_t)((row * PITCH + ch) * 16);
     }
     u32x4 stg[IPU];
-    // the unit (group row0, block b): row segments clamped to the last row,
-    // chunks to the tensor end
-    auto gload = [&](int row0, int b) {
+    // the unit (group row0, block b): the chunk-aligned start of its first row
+    // segment as a uniform base, and per lane its row's chunk offset from it,
+    // so a unit's loads go out a few VALU after the previous unit's slot
+    // stores; chunks past the tensor's last whole chunk (rows past n, which
+    // no result uses) read that chunk
+    struct UnitAddr {
+        const uint8_t *base;
+        uint32_t mis, lim;
+    };
+    auto uaddr = [&](int row0, int b) -> UnitAddr {
+        const uint64_t s = (uint64_t)row0 * RB + (uint64_t)b * BB, s16 = s & ~15ull;
+        return UnitAddr{w + s16, (uint32_t)(s & 15), (uint32_t)min(last_off - s16, (uint64_t)0xFFFFFFF0u)};
+    };
+    auto gload_u = [&](const UnitAddr &a) {
 #pragma unroll
         for (int k = 0; k < IPU; ++k) {
-            const long s = (long)min(row0 + prow[k], n - 1) * RB + (long)b * BB;
-            stg[k] = wc[min((s >> 4) + pch[k], last_chunk)];
+            const uint32_t o = ((a.mis + prb[k]) & ~15u) + pc16[k];
+            stg[k] = ld_u32x4(a.base + min(o, a.lim));
         }
     };
     // this wavefront's blocks per group: w, w + NW, ...
     const int nb = wave < bpr ? (bpr - wave + NW - 1) / NW : 0;
-    gload((int)blockIdx.x * R, min(wave, bpr - 1));  // group 0 of every schedule is blockIdx.x
+    gload_u(uaddr((int)blockIdx.x * R, min(wave, bpr - 1)));  // group 0 of every schedule is blockIdx.x
     const int groups = (n + R - 1) / R;
     const int my_groups = sched_count(sch, (int)blockIdx.x, (int)gridDim.x, groups);
     const int U = my_groups * nb;
@@ -557,23 +568,22 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_wave_long_kernel(const uint8
     float yacc = 0.0f;
     int q = 0, k = 0;  // group index and block index (of nb) of unit u
     for (int u = 0; u < U; ++u) {
+        // the next unit (past the last one: the last again, a cache hit), its
+        // base worked out before the slot stores wait for this unit's data
+        int q1 = q, k1 = k + 1;
+        if (k1 == nb) {
+            k1 = 0;
+            q1 = q + 1;
+        }
+        if (q1 >= my_groups) {
+            q1 = my_groups - 1;
+            k1 = nb - 1;
+        }
+        const UnitAddr na = uaddr(sched_group(sch, (int)blockIdx.x, (int)gridDim.x, q1) * R, wave + k1 * NW);
 #pragma unroll
         for (int i = 0; i < IPU; ++i) *reinterpret_cast<u32x4 *>(slot + plds[i]) = stg[i];
         __asm__ volatile("" ::: "memory");  // the unit's reads follow its stores (in-order LDS)
-        {
-            // the next unit (past the last one: the last again, a cache hit),
-            // unconditional so the load-counter waits stay exact
-            int q1 = q, k1 = k + 1;
-            if (k1 == nb) {
-                k1 = 0;
-                q1 = q + 1;
-            }
-            if (q1 >= my_groups) {
-                q1 = my_groups - 1;
-                k1 = nb - 1;
-            }
-            gload(sched_group(sch, (int)blockIdx.x, (int)gridDim.x, q1) * R, wave + k1 * NW);
-        }
+        gload_u(na);  // unconditional, so the load-counter waits stay exact
         const int b = wave + k * NW;
         const int row = min(sched_group(sch, (int)blockIdx.x, (int)gridDim.x, q) * R + n16, n - 1);
         const uint32_t rb = (uint32_t)(n16 * PITCH * 16) + (uint32_t)(((long)row * RB + (long)b * BB) & 15);
