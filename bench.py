@@ -951,7 +951,7 @@ def other_configs(torch, q4k, steps: int) -> dict:
     wl = Workload(torch, layer_shapes(), copies=10)
     out["config2"] = {"workload": "layer: q,k,v,o,gate,up,down of one 7B layer, unfused, "
                                   "10 rotating weight copies, one graph per shape",
-                      "kernel": "mgq::gemv_wave_kernel (gate, up, down) + mgq::gemv_mfma_kernel",
+                      "kernel": "mgq::gemv_wave_kernel (q, k, v, o: direct register loads)",
                       "per_shape": shape_times(torch, q4k, wl),
                       "parity": check_parity(torch, wl)}
     del wl
@@ -1106,11 +1106,10 @@ def main() -> int:
         # launch is the step, its bytes the step's
         kernel, avg_s, avg_b = "mgq::chain_kernel<2>", ms * 1e-3, wl.bytes_per_pass
     else:
-        # back-to-back GEMV launches (one graph per step): the kernels' average
-        # launch duration is the step time over its launches (gate|up, down and
-        # lm_head on the wave-private kernel, qkv and o on the staged one)
-        kernel, avg_s, avg_b = ("mgq::gemv_wave_kernel + mgq::gemv_mfma_kernel", ms * 1e-3 / nl,
-                                wl.bytes_per_pass / nl)
+        # back-to-back GEMV launches (one graph per step): the kernel's average
+        # launch duration is the step time over its launches (every matvec on
+        # the wave-private kernel: qkv and o with direct register loads)
+        kernel, avg_s, avg_b = ("mgq::gemv_wave_kernel", ms * 1e-3 / nl, wl.bytes_per_pass / nl)
     achieved = avg_b / avg_s / 1e9
     log(f"kernel {kernel} avg {avg_s * 1e6:.3f} us per launch, {achieved:.1f} GB/s")
 

@@ -1374,6 +1374,7 @@ hipError_t gemv_prepare() {
     if (e == hipSuccess) e = wave_prepare<16, 14, 7>();
     if (e == hipSuccess) e = wave_prepare<16, 20, 10>();
     if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<16, 14, 7, 1, true>);
+    if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<32, 14, 14, 1, true>);
     if (e == hipSuccess) e = prepare_swave<true, 0>();
     if (e == hipSuccess) e = prepare_swave<true, kFuseQuant>();
     if (e == hipSuccess) e = prepare_swave<false, kFmtQ5K>();
@@ -1424,16 +1425,22 @@ static hipError_t mfma_dispatch(const uint8_t *w, const GemvAct &a, float *y, in
         // lane's pieces straight into registers (DIRECT): o 4.47 -> 4.30 us
         // per launch in chains, decode step 1.138-1.140 -> 1.132-1.133 ms;
         // with LDS slots they measured 0.1 us slower than the staged kernel.
-        // qkv's 32-row groups keep the staged kernel (direct: 5.59 -> 5.63).
-        // MGQ_GEMV_WAVE=0 turns the wave-private kernel off, MGQ_GEMV_DIRECT=0
-        // the direct loads.
+        // qkv's groups of ceil(N / #CUs) rows in 32-row tiles (cfg 8) load
+        // directly too: 5.76 -> 5.61-5.66 us per launch, decode step 1114 ->
+        // 1108 us (once the wave kernel's per-unit divisions were gone; before,
+        // 5.59 -> 5.63). MGQ_GEMV_WAVE=0 turns the wave-private kernel off,
+        // MGQ_GEMV_DIRECT=0 the direct loads for o, MGQ_GEMV_QKV_DIRECT=0 for
+        // qkv.
         static const int wave_env = env_int("MGQ_GEMV_WAVE", 1);
         static const int direct_env = env_int("MGQ_GEMV_DIRECT", 1);
+        static const int qkv_direct_env = env_int("MGQ_GEMV_QKV_DIRECT", 1);
         const bool multi = (long)(n + 15) / 16 > 2 * device_cus();
         if (wave_env && force < 0) {
             if (cfg == 6 && multi) e = launch_wave<16, 14, 7>(w, a.x, y, n, bpr, stream, true);
             else if (cfg == 2) e = launch_wave<16, 20, 10>(w, a.x, y, n, bpr, stream, false);
             else if (cfg == 6 && direct_env) e = launch_wave_direct<16, 14, 7>(w, a.x, y, n, bpr, stream, 0);
+            else if (cfg == 8 && qkv_direct_env)
+                e = launch_wave_direct<32, 14, 14>(w, a.x, y, n, bpr, stream, gr);
         }
     }
     if constexpr (Q8 || FUSE != 0) {
