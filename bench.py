@@ -916,7 +916,7 @@ def run_kquant(torch, q4k, args):
             "mgq::gemv_q6k_mfma_kernel + mgq::gemv_q6k_mfma_long_kernel"}
 
 
-TRAFFIC_PROFILES = {"decode7b": "gemv_mfma_decode7b_pmc.txt",
+TRAFFIC_PROFILES = {"decode7b": "gemv_wave_decode7b_pmc.txt",
                     "prefill": "gemm_q4k_f16_prefill_pmc.txt"}
 
 
