@@ -108,12 +108,16 @@ def test_matvec_random_bytes_wide_dynamic_range(L, orc):
 
 
 @pytest.mark.parametrize("n,bpr", [(24576 + 17, 2), (30000, 14), (16, 40), (17, 29),
-                                   (4100, 17), (4200, 74), (5000, 112), (300, 100)])
+                                   (4100, 17), (4200, 74), (5000, 112), (300, 100),
+                                   (20005, 13), (16009, 7), (3590, 75), (4609, 14)])
 def test_matvec_random_bytes_all_configs(L, orc, n, bpr):
     # shapes that select each launch configuration (many / few row groups,
     # single- and multi-stage K, ragged last stage and row group) and each
     # count of activation chunks per lane (1, 2, 4, 8), including the
-    # single-buffered fallback when the double-buffered stages do not fit
+    # single-buffered fallback when the double-buffered stages do not fit;
+    # odd blocks per row on the persistent and the long-row wave kernels
+    # (a unit half past the row end, units wholly past it) with a partial
+    # last row group, and one-group-per-CU rows with a ragged last group
     note(f"matvec random bytes n={n} bpr={bpr}")
     rng = np.random.default_rng(n + bpr)
     w = random_q4k_bytes(rng, n * bpr)
@@ -626,7 +630,8 @@ def assert_dp4a_close(y, y_ref, absterm, tol=1e-5):
 
 
 @pytest.mark.parametrize("n,bpr", [(1, 1), (17, 3), (64, 14), (3584, 14), (700, 74), (4100, 17),
-                                   (30000, 14), (300, 100), (4608, 14), (6000, 5)])
+                                   (30000, 14), (300, 100), (4608, 14), (6000, 5),
+                                   (20005, 13), (701, 75)])
 def test_dp4a_matvec_matches_oracle(L, orc, n, bpr):
     # shapes that take each launch configuration of the matrix-core kernel's
     # Q8 mode (few/many row groups, one/several stages, fallback to
