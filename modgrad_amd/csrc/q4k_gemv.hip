@@ -40,8 +40,10 @@
 //    its own unit through its own LDS slot, so stages need no work-group
 //    barrier; used for plain f32 matvecs whose work-groups stream several
 //    stages (gate|up, lm_head, down). With DIRECT (one unit per wavefront:
-//    o and other single-stage 16-row launches) each lane loads the pieces it
-//    multiplies straight into registers.
+//    o, qkv's one group per CU and other single-stage launches) each lane
+//    loads the pieces it multiplies straight into registers. A unit's loads
+//    go out from a uniform base with one clamped 32-bit offset per lane,
+//    the next unit's base worked out before the current unit's slot stores.
 //
 // 4. gemv_batched_kernel -- vector-ALU batched GEMV (up to 16 activation rows).
 #include "q4k_device.hpp"
