@@ -589,16 +589,30 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         if (lane == 0) reinterpret_cast<float *>(lds + Lo.normp)[wave] = ssq;
     }
   }
-    // the base of stage q (past the last one: the last again, a cache hit)
-    auto qaddr = [&](int q) -> UnitAddr {
-        q = std::min(q, Q - 1);
-        const int vg = q / stages;  // pass index: row group vg / VM, matrix vg % VM
-        const uint32_t r0 =
-            (uint32_t)sched_group(sch, (int)blockIdx.x, (int)gridDim.x, vg / VM) * (uint32_t)gr;
-        const uint8_t *wm = (VM == 2 && (vg & 1)) ? fz.w2 : w;
-        return uaddr(r0, (uint32_t)((q % stages) * C * BB), wm);
+    // Stage q's position: column t = q % stages and pass vg = q / stages (row
+    // group vg / VM, matrix vg % VM). The stage loop keeps it in counters, so
+    // no step divides by the (run-time) stage count.
+    struct StagePos {
+        int t, vg;
     };
-    auto gload = [&](int q, u32x4(&dst)[IPW]) { gload_u(qaddr(q), dst); };
+    auto pos_of = [&](int q) { return StagePos{q % stages, q / stages}; };
+    auto advance = [&](StagePos p, int k) {
+        for (int i = 0; i < k; ++i)
+            if (++p.t == stages) {
+                p.t = 0;
+                ++p.vg;
+            }
+        return p;
+    };
+    // the base of the stage at p
+    auto paddr = [&](StagePos p) -> UnitAddr {
+        const uint32_t r0 =
+            (uint32_t)sched_group(sch, (int)blockIdx.x, (int)gridDim.x, p.vg / VM) * (uint32_t)gr;
+        const uint8_t *wm = (VM == 2 && (p.vg & 1)) ? fz.w2 : w;
+        return uaddr(r0, (uint32_t)(p.t * C * BB), wm);
+    };
+    // stage q (past the last one: the last again, a cache hit)
+    auto gload = [&](int q, u32x4(&dst)[IPW]) { gload_u(paddr(pos_of(std::min(q, Q - 1))), dst); };
 #pragma unroll
     for (int f = 1; f < PF; ++f) gload(f, stg[f]);
     // (the barrier before the first stage is computed also orders the table)
@@ -680,11 +694,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     // One stage: compute it, then (when `more`) move stage q+1 from its
     // register set into the other LDS buffer and refill that set with stage
     // q+1+PF. F = q % PF is a compile-time constant at every call site.
-    auto step = [&](const int q, auto fc, const bool more) {
+    // stage q at position pq; pn: the position of the refill, stage
+    // min(q + 1 + PF, Q - 1)
+    auto step = [&](const int q, const StagePos pq, const StagePos pn, auto fc, const bool more) {
         constexpr int F = decltype(fc)::value;
-        const int t = q % stages;
+        const int t = pq.t;
         // the refill's base, worked out before the stage's loads are waited for
-        const UnitAddr na = qaddr(q + 1 + PF);
+        const UnitAddr na = paddr(pn);
         const uint8_t *sbuf = lds + Lo.stage + (dbuf ? (q & 1) * Lo.stage_bytes : 0u);
         for (int u = wave; u < UNITS; u += NW) {
             // tile A = (rows rowA.., block cbA), tile B = (rows rowB.., block cbB)
@@ -770,7 +786,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         // barrier of its step, while the first R threads may still be reading
         // this group's: the buffer they read is the other one, and reusing it
         // two groups later is ordered by the barrier between.
-        float *auxg = aux + (WV ? (q / stages) : ((q / stages) & 1)) * (NW * 32);
+        float *auxg = aux + (WV ? pq.vg : (pq.vg & 1)) * (NW * 32);
         if (group_end) {
             // sum the 4 lanes (g = 0..3) of each row, then one value per row
             // and tile into aux (free after the prologue)
@@ -808,7 +824,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
             if (tid < R) {
                 float sum = 0.0f;
                 for (int wv = 0; wv < NW; ++wv) sum += auxg[wv * 32 + tid];
-                reinterpret_cast<float *>(lds + Lo.ybuf)[(q / stages) * R + tid] = sum;
+                reinterpret_cast<float *>(lds + Lo.ybuf)[pq.vg * R + tid] = sum;
             }
             yaccA = 0.0f;
             yaccB = 0.0f;
@@ -818,21 +834,41 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     // unconditional and the compiler waits only for the set being stored
     // (the loop is entered, and loops back, with the same load order).
     int q0 = 0;
+    StagePos p0{0, 0};                                        // stage q0
+    const StagePos qlast_pos = pos_of(std::max(Q - 1, 0));        // the last stage
+    auto refill_pos = [&](int q, StagePos pq) {               // stage min(q + 1 + PF, Q - 1)
+        return q + 1 + PF < Q ? advance(pq, 1 + PF) : qlast_pos;
+    };
     if (Q > PF) {
         gload(PF, stg[0]);
         __syncthreads();
         for (; q0 + PF < Q; q0 += PF) {
-            step(q0, std::integral_constant<int, 0>{}, true);
-            if constexpr (PF > 1) step(q0 + 1, std::integral_constant<int, 1 % PF>{}, true);
-            if constexpr (PF > 2) step(q0 + 2, std::integral_constant<int, 2 % PF>{}, true);
+            step(q0, p0, refill_pos(q0, p0), std::integral_constant<int, 0>{}, true);
+            if constexpr (PF > 1) {
+                const StagePos p1 = advance(p0, 1);
+                step(q0 + 1, p1, refill_pos(q0 + 1, p1), std::integral_constant<int, 1 % PF>{}, true);
+            }
+            if constexpr (PF > 2) {
+                const StagePos p2 = advance(p0, 2);
+                step(q0 + 2, p2, refill_pos(q0 + 2, p2), std::integral_constant<int, 2 % PF>{}, true);
+            }
+            p0 = advance(p0, PF);
         }
     } else {
         __syncthreads();
     }
     // Tail: the last <= PF stages.
-    if (q0 < Q) step(q0, std::integral_constant<int, 0>{}, q0 + 1 < Q);
-    if constexpr (PF > 1) if (q0 + 1 < Q) step(q0 + 1, std::integral_constant<int, 1 % PF>{}, q0 + 2 < Q);
-    if constexpr (PF > 2) if (q0 + 2 < Q) step(q0 + 2, std::integral_constant<int, 2 % PF>{}, q0 + 3 < Q);
+    if (q0 < Q) step(q0, p0, refill_pos(q0, p0), std::integral_constant<int, 0>{}, q0 + 1 < Q);
+    if constexpr (PF > 1)
+        if (q0 + 1 < Q) {
+            const StagePos p1 = advance(p0, 1);
+            step(q0 + 1, p1, refill_pos(q0 + 1, p1), std::integral_constant<int, 1 % PF>{}, q0 + 2 < Q);
+        }
+    if constexpr (PF > 2)
+        if (q0 + 2 < Q) {
+            const StagePos p2 = advance(p0, 2);
+            step(q0 + 2, p2, refill_pos(q0 + 2, p2), std::integral_constant<int, 2 % PF>{}, q0 + 3 < Q);
+        }
     __syncthreads();
     float rstd = 1.0f;
     if constexpr (NORM) {
