@@ -937,6 +937,8 @@ static int env_int(const char *name, int dflt) {
 // row sums of each row group go to LDS (one slot per group and wavefront)
 // and are reduced across wavefronts once, after the stream, in the same
 // order as gemv_mfma_kernel (identical results).
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
 struct WaveLayout {
     uint32_t meta, slots, aux;
     size_t total;
@@ -956,7 +958,7 @@ __host__ __device__ inline WaveLayout wave_layout(int bpr, int rounds) {
 // DIRECT (one unit per wavefront: a single stage, one group per work-group):
 // every lane loads the three pieces it computes with (block header, quant
 // pieces 1+g and 5+g of its row) straight into registers, with no LDS slot.
-template <int R, int C, int NW, int XIT, bool DIRECT = false>
+template <int R, int C, int NW, int XIT, bool DIRECT = false, bool I8 = false>
 __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__restrict__ w,
                                                             const float *__restrict__ x,
                                                             float *__restrict__ y, int n, int bpr,
@@ -1076,13 +1078,49 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
         sum += quad_xor<1>(sum);
         sum += quad_xor<2>(sum);
         if (i >= nitems) continue;
+        const int b = i >> 5, sb = (i >> 2) & 7, j = i & 3;
+        if constexpr (I8) {
+            // x * 2^e = X, an integer of at most 21 bits (|X| <= 2^20), as three
+            // signed 7-bit digits X = d2 2^14 + d1 2^7 + d0 (A rows 3 slot + digit)
+            int e = 0;
+            float corr = 1.0f;
+            if (amax > 0.0f && amax <= 3.402823466e38f) {
+                int ex;
+                frexpf(amax, &ex);
+                e = std::min(std::max(20 - ex, -100), 140);
+                corr = ldexpf(1.0f, -e);
+            } else if (!(amax == 0.0f)) {
+                corr = amax;  // Inf or NaN: the row sums come out non-finite
+            }
+            if (j == 0) {
+                meta[b * 16 + sb] = corr;
+                meta[b * 16 + 8 + sb] = sum;
+            }
+            const float xs[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            uint32_t dw[3][2] = {{0u, 0u}, {0u, 0u}, {0u, 0u}};
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int X = (int)__builtin_rintf(ldexpf(xs[q], e));
+                const int d0 = __builtin_amdgcn_sbfe(X, 0, 7);
+                const int X1 = (X - d0) >> 7;
+                const int d1 = __builtin_amdgcn_sbfe(X1, 0, 7);
+                const int d2 = (X1 - d1) >> 7;
+                dw[0][q >> 2] |= ((uint32_t)d0 & 0xFFu) << (8 * (q & 3));
+                dw[1][q >> 2] |= ((uint32_t)d1 & 0xFFu) << (8 * (q & 3));
+                dw[2][q >> 2] |= ((uint32_t)d2 & 0xFFu) << (8 * (q & 3));
+            }
+#pragma unroll
+            for (int dg = 0; dg < 3; ++dg)
+                *reinterpret_cast<u32x2 *>(lds + (size_t)b * 1040 + (size_t)(((sb * 3 + dg) * 2 + (j >> 1)) * 16 + (j & 1) * 8)) =
+                    u32x2{dw[dg][0], dw[dg][1]};
+            continue;
+        }
         int e = 0;
         if (amax > 0.0f && amax <= 3.402823466e38f) {
             int ex;
             frexpf(amax, &ex);
             e = std::min(std::max(14 - ex, -90), 140);
         }
-        const int b = i >> 5, sb = (i >> 2) & 7, j = i & 3;
         if (j == 0) {
             meta[b * 16 + sb] = ldexpf(1.0f, ((sb & 1) ? 20 : 24) - e);
             meta[b * 16 + 8 + sb] = sum;
@@ -1116,6 +1154,21 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
         const bool hit = (n16 >> 1) == sb;
         aoff[c] = hit ? (uint32_t)((c * 4 + g) * 32 + (n16 & 1) * 16) : 1024u;
     }
+    // I8: MFMA c4 = low / high nibbles (c4 & 1) of qs pieces 1+g (c4 < 2) or
+    // 5+g: lane group g's 16 bytes are sub-block pair jp = 2 (c4 >> 1) + (g >> 1)
+    // at elements 16 (g & 1) ..; A row m = 4 jp + digit holds that pair's low
+    // (c4 even) or high sub-block's digits. The low-nibble MFMAs accumulate
+    // into one accumulator and the high-nibble ones into the other, so lane
+    // group G holds sub-blocks 2G and 2G + 1, as in the f16 form (same decode).
+    uint32_t aoff8[4];
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) {
+        const int hi = c4 & 1, jp = 2 * (c4 >> 1) + (g >> 1), sbc = 2 * jp + hi;
+        const bool hit = (n16 >> 2) == jp && (n16 & 3) < 3;
+        aoff8[c4] = hit ? (uint32_t)(((sbc * 3 + (n16 & 3)) * 2 + (g & 1)) * 16) : 1024u;
+    }
+    // the three digit sums, exactly (|each| < 2^15)
+    auto digits = [](const i32x4 &a) -> float { return (float)((a[2] << 14) + (a[1] << 7) + a[0]); };
     auto decode = [&](const u32x4 &hd, int b, float s0, float s1) -> float {
         const float d = half_bits_finite(hd[0]), dmin = half_bits_finite(hd[0] >> 16);
         const uint32_t scs = jq ? hd[3] : hd[1], mns = jq ? (hd[3] >> 4) : hd[2];
@@ -1165,6 +1218,29 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
             const u32x4 qb1 = DIRECT ? dreg[5] : piece(rowB + n16, cbB, 5 + g);
             const u32x4 hdA = DIRECT ? dreg[0] : piece(n16, 0, 0);
             const u32x4 hdB = DIRECT ? dreg[3] : piece(rowB + n16, cbB, 0);
+          if constexpr (I8) {
+            auto tile8 = [&](const u32x4 &hd, int b, const u32x4 &q0, const u32x4 &q1) -> float {
+                i32x4 alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0};
+                const uint8_t *tb = lds + (uint32_t)b * 1040u;
+#pragma unroll
+                for (int c4 = 0; c4 < 4; ++c4) {
+                    const u32x4 src = c4 < 2 ? q0 : q1;
+                    const u32x4 bq = (c4 & 1) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
+                    const i32x4 av = *reinterpret_cast<const i32x4 *>(tb + aoff8[c4]);
+                    if (c4 & 1) ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, __builtin_bit_cast(i32x4, bq), ahi, 0, 0, 0);
+                    else alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, __builtin_bit_cast(i32x4, bq), alo, 0, 0, 0);
+                }
+                return decode(hd, b, digits(alo), digits(ahi));
+            };
+            const float cA = tile8(hdA, bA, qa0, qa1);
+            const float cB = tile8(hdB, bBc, qb0, qb1);
+            if (R == 32) {
+                yaccA += cA;
+                yaccB += cB;
+            } else {
+                yaccA += hasB ? cA + cB : cA;
+            }
+          } else {
             f32x4 accA = {0.f, 0.f, 0.f, 0.f}, accB = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
@@ -1190,6 +1266,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
             } else {
                 yaccA += hasB ? cA + cB : cA;
             }
+          }
         }
         if (t == stages - 1) {
             // this wavefront's sums of the group's rows, to its own slot
@@ -1221,10 +1298,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
     }
 }
 
-template <int R, int C, int NW, int XIT, bool DIRECT = false>
+template <int R, int C, int NW, int XIT, bool DIRECT = false, bool I8 = false>
 static hipError_t launch_wave_xit(const uint8_t *w, const float *x, float *y, int n, int bpr,
                                   hipStream_t stream, bool persistent, int gr) {
-    auto kern = gemv_wave_kernel<R, C, NW, XIT, DIRECT>;
+    auto kern = gemv_wave_kernel<R, C, NW, XIT, DIRECT, I8>;
     // DIRECT: one unit per wavefront (a single stage, one group per work-group)
     if (DIRECT && (persistent || bpr > C)) return hipErrorNotSupported;
     const hipError_t attr = allow_full_lds_by_addr((const void *)kern);
@@ -1255,21 +1332,33 @@ static hipError_t wave_prepare() {
     if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<R, C, NW, 2>);
     if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<R, C, NW, 4>);
     if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<R, C, NW, 8>);
+    if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<R, C, NW, 1, false, true>);
+    if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<R, C, NW, 2, false, true>);
+    if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<R, C, NW, 4, false, true>);
+    if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<R, C, NW, 8, false, true>);
     return e;
 }
 
 // one unit per wavefront with direct register loads (single-stage rows)
 template <int R, int C, int NW>
 static hipError_t launch_wave_direct(const uint8_t *w, const float *x, float *y, int n, int bpr,
-                                     hipStream_t stream, int gr) {
+                                     hipStream_t stream, int gr, bool i8) {
     if (bpr * 32 > NW * 64) return hipErrorNotSupported;
+    if (i8) return launch_wave_xit<R, C, NW, 1, true, true>(w, x, y, n, bpr, stream, false, gr);
     return launch_wave_xit<R, C, NW, 1, true>(w, x, y, n, bpr, stream, false, gr);
 }
 
 template <int R, int C, int NW>
 static hipError_t launch_wave(const uint8_t *w, const float *x, float *y, int n, int bpr,
-                              hipStream_t stream, bool persistent, int gr = 0) {
+                              hipStream_t stream, bool persistent, bool i8, int gr = 0) {
     const int need = (bpr * 32 + NW * 64 - 1) / (NW * 64);
+    if (i8) {
+        if (need <= 1) return launch_wave_xit<R, C, NW, 1, false, true>(w, x, y, n, bpr, stream, persistent, gr);
+        if (need <= 2) return launch_wave_xit<R, C, NW, 2, false, true>(w, x, y, n, bpr, stream, persistent, gr);
+        if (need <= 4) return launch_wave_xit<R, C, NW, 4, false, true>(w, x, y, n, bpr, stream, persistent, gr);
+        if (need <= 8) return launch_wave_xit<R, C, NW, 8, false, true>(w, x, y, n, bpr, stream, persistent, gr);
+        return hipErrorNotSupported;
+    }
     if (need <= 1) return launch_wave_xit<R, C, NW, 1>(w, x, y, n, bpr, stream, persistent, gr);
     if (need <= 2) return launch_wave_xit<R, C, NW, 2>(w, x, y, n, bpr, stream, persistent, gr);
     if (need <= 4) return launch_wave_xit<R, C, NW, 4>(w, x, y, n, bpr, stream, persistent, gr);
@@ -1412,6 +1501,8 @@ hipError_t gemv_prepare() {
     if (e == hipSuccess) e = wave_prepare<16, 14, 7>();
     if (e == hipSuccess) e = wave_prepare<16, 20, 10>();
     if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<16, 14, 7, 1, true>);
+    if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<16, 14, 7, 1, true, true>);
+    if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<32, 14, 14, 1, true, true>);
     if (e == hipSuccess) e = allow_full_lds_by_addr((const void *)gemv_wave_kernel<32, 14, 14, 1, true>);
     if (e == hipSuccess) e = prepare_swave<true, 0>();
     if (e == hipSuccess) e = prepare_swave<true, kFuseQuant>();
@@ -1472,13 +1563,15 @@ static hipError_t mfma_dispatch(const uint8_t *w, const GemvAct &a, float *y, in
         static const int wave_env = env_int("MGQ_GEMV_WAVE", 1);
         static const int direct_env = env_int("MGQ_GEMV_DIRECT", 1);
         static const int qkv_direct_env = env_int("MGQ_GEMV_QKV_DIRECT", 1);
+        static const int i8_env = env_int("MGQ_GEMV_I8", 1);
         const bool multi = (long)(n + 15) / 16 > 2 * device_cus();
         if (wave_env && force < 0) {
-            if (cfg == 6 && multi) e = launch_wave<16, 14, 7>(w, a.x, y, n, bpr, stream, true);
-            else if (cfg == 2) e = launch_wave<16, 20, 10>(w, a.x, y, n, bpr, stream, false);
-            else if (cfg == 6 && direct_env) e = launch_wave_direct<16, 14, 7>(w, a.x, y, n, bpr, stream, 0);
+            if (cfg == 6 && multi) e = launch_wave<16, 14, 7>(w, a.x, y, n, bpr, stream, true, i8_env >= 1);
+            else if (cfg == 2) e = launch_wave<16, 20, 10>(w, a.x, y, n, bpr, stream, false, i8_env >= 2);
+            else if (cfg == 6 && direct_env)
+                e = launch_wave_direct<16, 14, 7>(w, a.x, y, n, bpr, stream, 0, i8_env >= 2);
             else if (cfg == 8 && qkv_direct_env)
-                e = launch_wave_direct<32, 14, 14>(w, a.x, y, n, bpr, stream, gr);
+                e = launch_wave_direct<32, 14, 14>(w, a.x, y, n, bpr, stream, gr, i8_env >= 1);
         }
     }
     if constexpr (Q8 || FUSE != 0) {
