@@ -84,7 +84,7 @@ __device__ __forceinline__ int split_exponent(float amax) {
     if (amax > 0.0f && amax <= 3.402823466e38f) {
         int ex;
         frexpf(amax, &ex);
-        e = std::min(std::max(14 - ex, -90), 120);
+        e = std::min(std::max(14 - ex, -103), 120);  // 2^(20 - e) stays finite
     }
     return e;
 }

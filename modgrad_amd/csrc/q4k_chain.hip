@@ -359,7 +359,7 @@ __global__ __launch_bounds__(pc::NT) void chain_kernel(const ChainTask *__restri
             if (amax > 0.0f && amax <= 3.402823466e38f) {
                 int ex;
                 frexpf(amax, &ex);
-                e = std::min(std::max(14 - ex, -90), 140);
+                e = std::min(std::max(14 - ex, -103), 140);  // 2^(24 - e) stays finite
             }
             const int bl = i >> 5, sb = (i >> 2) & 7, jj = i & 3;
             if (jj == 0) {

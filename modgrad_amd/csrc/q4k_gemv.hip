@@ -553,7 +553,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         if (amax > 0.0f && amax <= 3.402823466e38f) {
             int ex;
             frexpf(amax, &ex);  // amax in [2^(ex-1), 2^ex)
-            e = std::min(std::max(14 - ex, -90), 140);
+            e = std::min(std::max(14 - ex, -103), 140);  // 2^(24 - e) stays finite
         }
         const int b = i >> 5, sb = (i >> 2) & 7, j = i & 3;
         if (j == 0) {
@@ -936,7 +936,13 @@ static int env_int(const char *name, int dflt) {
 // stages: a wavefront starts on its unit as soon as its own pieces land. Its
 // row sums of each row group go to LDS (one slot per group and wavefront)
 // and are reduced across wavefronts once, after the stream, in the same
-// order as gemv_mfma_kernel (identical results).
+// order as gemv_mfma_kernel (identical results in the f16 form).
+// I8 (the int8 form): each 32-value sub-block of x is scaled by its own
+// power of two to integers |X| <= 2^22 held as three signed 8-bit digits,
+// the nibbles are the int8 B operand as they sit in the qs bytes (masked,
+// not spread), and v_mfma_i32_16x16x64_i8 sums 64 products exactly: half
+// the MFMAs, A-operand reads and nibble masks of the f16 form, whose x is
+// split into two f16 halves (22 bits) times 16-bit B operands.
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 struct WaveLayout {
@@ -1080,14 +1086,16 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
         if (i >= nitems) continue;
         const int b = i >> 5, sb = (i >> 2) & 7, j = i & 3;
         if constexpr (I8) {
-            // x * 2^e = X, an integer of at most 21 bits (|X| <= 2^20), as three
-            // signed 7-bit digits X = d2 2^14 + d1 2^7 + d0 (A rows 3 slot + digit)
+            // x 2^e rounded to an integer X, |X| < 2^22, as three signed 8-bit
+            // digits: the bytes of Y = X + 128 (1 + 256 + 65536) with their top
+            // bits flipped (byte - 128), so X = sum (byte_i - 128) 256^i. Adding
+            // 1.5 2^23 rounds x 2^e to an integer in the mantissa's low bits.
             int e = 0;
             float corr = 1.0f;
             if (amax > 0.0f && amax <= 3.402823466e38f) {
                 int ex;
                 frexpf(amax, &ex);
-                e = std::min(std::max(20 - ex, -100), 140);
+                e = std::min(22 - ex, 140);  // ex <= 128: e >= -106
                 corr = ldexpf(1.0f, -e);
             } else if (!(amax == 0.0f)) {
                 corr = amax;  // Inf or NaN: the row sums come out non-finite
@@ -1097,29 +1105,32 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
                 meta[b * 16 + 8 + sb] = sum;
             }
             const float xs[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-            uint32_t dw[3][2] = {{0u, 0u}, {0u, 0u}, {0u, 0u}};
+            uint32_t yv[8];
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const int X = (int)__builtin_rintf(ldexpf(xs[q], e));
-                const int d0 = __builtin_amdgcn_sbfe(X, 0, 7);
-                const int X1 = (X - d0) >> 7;
-                const int d1 = __builtin_amdgcn_sbfe(X1, 0, 7);
-                const int d2 = (X1 - d1) >> 7;
-                dw[0][q >> 2] |= ((uint32_t)d0 & 0xFFu) << (8 * (q & 3));
-                dw[1][q >> 2] |= ((uint32_t)d1 & 0xFFu) << (8 * (q & 3));
-                dw[2][q >> 2] |= ((uint32_t)d2 & 0xFFu) << (8 * (q & 3));
-            }
+            for (int q = 0; q < 8; ++q)
+                yv[q] = __builtin_bit_cast(uint32_t, ldexpf(xs[q], e) + 12582912.0f) - (0x4B400000u - 0x808080u);
 #pragma unroll
-            for (int dg = 0; dg < 3; ++dg)
+            for (int dg = 0; dg < 3; ++dg) {
+                // byte dg of values 4h .. 4h + 3 (v_perm: selector k picks byte k of
+                // the second operand, 4 + k of the first; 0x0C a zero byte)
+                const uint32_t sel = (uint32_t)dg | ((4u + dg) << 8) | 0x0C0C0000u;
+                uint32_t dw[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t lo = __builtin_amdgcn_perm(yv[4 * h + 1], yv[4 * h], sel);
+                    const uint32_t hi = __builtin_amdgcn_perm(yv[4 * h + 3], yv[4 * h + 2], sel);
+                    dw[h] = __builtin_amdgcn_perm(hi, lo, 0x05040100u) ^ 0x80808080u;
+                }
                 *reinterpret_cast<u32x2 *>(lds + (size_t)b * 1040 + (size_t)(((sb * 3 + dg) * 2 + (j >> 1)) * 16 + (j & 1) * 8)) =
-                    u32x2{dw[dg][0], dw[dg][1]};
+                    u32x2{dw[0], dw[1]};
+            }
             continue;
         }
         int e = 0;
         if (amax > 0.0f && amax <= 3.402823466e38f) {
             int ex;
             frexpf(amax, &ex);
-            e = std::min(std::max(14 - ex, -90), 140);
+            e = std::min(std::max(14 - ex, -103), 140);  // 2^(24 - e) stays finite
         }
         if (j == 0) {
             meta[b * 16 + sb] = ldexpf(1.0f, ((sb & 1) ? 20 : 24) - e);
@@ -1167,8 +1178,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
         const bool hit = (n16 >> 2) == jp && (n16 & 3) < 3;
         aoff8[c4] = hit ? (uint32_t)(((sbc * 3 + (n16 & 3)) * 2 + (g & 1)) * 16) : 1024u;
     }
-    // the three digit sums, exactly (|each| < 2^15)
-    auto digits = [](const i32x4 &a) -> float { return (float)((a[2] << 14) + (a[1] << 7) + a[0]); };
+    // the three digit sums (|each| < 2^16): a0 + 256 a1 exactly, then + 65536 a2
+    auto digits = [](const i32x4 &a) -> float { return (float)a[2] * 65536.0f + (float)((a[1] << 8) + a[0]); };
     auto decode = [&](const u32x4 &hd, int b, float s0, float s1) -> float {
         const float d = half_bits_finite(hd[0]), dmin = half_bits_finite(hd[0] >> 16);
         const uint32_t scs = jq ? hd[3] : hd[1], mns = jq ? (hd[3] >> 4) : hd[2];
@@ -1560,18 +1571,22 @@ static hipError_t mfma_dispatch(const uint8_t *w, const GemvAct &a, float *y, in
         // 5.59 -> 5.63). MGQ_GEMV_WAVE=0 turns the wave-private kernel off,
         // MGQ_GEMV_DIRECT=0 the direct loads for o, MGQ_GEMV_QKV_DIRECT=0 for
         // qkv.
+        // The int8 matrix-core form (I8) on every wave launch, against the
+        // f16 form, alternating on one box: decode step 1119 -> 1077 us
+        // (qkv 5.81 -> 5.46, o 4.33 -> 4.20, gate|up 17.6 -> 15.8, down
+        // 11.93 -> 11.77 us per launch in chains). MGQ_GEMV_I8=0 turns it off.
         static const int wave_env = env_int("MGQ_GEMV_WAVE", 1);
         static const int direct_env = env_int("MGQ_GEMV_DIRECT", 1);
         static const int qkv_direct_env = env_int("MGQ_GEMV_QKV_DIRECT", 1);
-        static const int i8_env = env_int("MGQ_GEMV_I8", 1);
+        static const bool i8 = env_int("MGQ_GEMV_I8", 1) != 0;
         const bool multi = (long)(n + 15) / 16 > 2 * device_cus();
         if (wave_env && force < 0) {
-            if (cfg == 6 && multi) e = launch_wave<16, 14, 7>(w, a.x, y, n, bpr, stream, true, i8_env >= 1);
-            else if (cfg == 2) e = launch_wave<16, 20, 10>(w, a.x, y, n, bpr, stream, false, i8_env >= 2);
+            if (cfg == 6 && multi) e = launch_wave<16, 14, 7>(w, a.x, y, n, bpr, stream, true, i8);
+            else if (cfg == 2) e = launch_wave<16, 20, 10>(w, a.x, y, n, bpr, stream, false, i8);
             else if (cfg == 6 && direct_env)
-                e = launch_wave_direct<16, 14, 7>(w, a.x, y, n, bpr, stream, 0, i8_env >= 2);
+                e = launch_wave_direct<16, 14, 7>(w, a.x, y, n, bpr, stream, 0, i8);
             else if (cfg == 8 && qkv_direct_env)
-                e = launch_wave_direct<32, 14, 14>(w, a.x, y, n, bpr, stream, gr, i8_env >= 1);
+                e = launch_wave_direct<32, 14, 14>(w, a.x, y, n, bpr, stream, gr, i8);
         }
     }
     if constexpr (Q8 || FUSE != 0) {

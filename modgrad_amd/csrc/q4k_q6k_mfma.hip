@@ -107,7 +107,7 @@ __device__ __forceinline__ void q6m_item(uint8_t *lds, float *meta, int i, bool 
     if (amax > 0.0f && amax <= 3.402823466e38f) {
         int ex;
         frexpf(amax, &ex);
-        e = std::min(std::max(14 - ex, -90), 140);
+        e = std::min(std::max(14 - ex, -103), 140);  // 2^(24 - e) stays finite
     }
     const int b = i >> 5, j = (i >> 2) & 7, kg = i & 3;
     // sub-blocks 2, 3, 6, 7 (high nibbles) arrive as 16q: their corr is / 16

@@ -351,6 +351,55 @@ def test_matvec_one_group_per_cu_shapes(L, orc, n, bpr):
     assert_gemv_close(y, y_ref, a)
 
 
+# Each 32-value sub-block of x at its own power of two, from float32's
+# denormals to 2^110, on the shapes of each wave launch (qkv's one group per
+# CU, o, the persistent gate|up, the long-row down, a ragged persistent one):
+# the matrix-core forms scale each sub-block of x by a power of two of their
+# own before splitting it into digits, and that scale must cover every
+# exponent (a sub-block at 2^110 dominates each row's bound and pins it).
+# Much larger activations can overflow float32 in a sub-block's partial
+# products sc * sum(q x) and m * sum(x), which the kernels round before they
+# multiply by d and dmin, as the sum of 32 values near 2^127 itself can.
+@pytest.mark.parametrize("n,bpr", [(4608, 14), (3584, 14), (37888, 14), (3584, 74), (20005, 13)])
+def test_matvec_per_subblock_magnitudes(L, orc, n, bpr):
+    note(f"matvec per-sub-block magnitudes n={n} bpr={bpr}")
+    rng = np.random.default_rng(n * 13 + bpr)
+    k = bpr * 256
+    w = random_q4k_bytes(rng, n * bpr, d_scale=1e-5)
+    ex = rng.integers(-140, 100, size=k // 32)
+    ex[0], ex[1], ex[2] = 110, -149, 0
+    x = (rng.standard_normal((k // 32, 32)) * np.exp2(ex.astype(np.float64))[:, None])
+    x = x.astype(np.float32).ravel()
+    y = run_gemv(L, w, x, n, bpr)
+    y_ref, a = orc.gemv(w, x, n, bpr)
+    assert np.all(np.isfinite(y_ref))
+    assert_gemv_close(y, y_ref, a)
+    # the same vector without the 2^110 sub-block: the next largest (up to
+    # 2^99) then sets the bound
+    x[0:32] = 0.0
+    y = run_gemv(L, w, x, n, bpr)
+    y_ref, a = orc.gemv(w, x, n, bpr)
+    assert_gemv_close(y, y_ref, a)
+
+
+def test_matvec_f16_wave_forms_under_switch():
+    # MGQ_GEMV_I8=0 (read once per process) puts every wave launch on the
+    # f16 matrix-core form: the wave-launch matvec cases above again, in one
+    # child process with the switch set
+    import os
+    import subprocess
+    note("matvec f16 wave forms (child process, MGQ_GEMV_I8=0)")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    cases = ("matvec_random_bytes_all_configs or per_subblock or baseline_layer_shapes or "
+             "one_group_per_cu or lm_head_full_size or matvec_small_shapes")
+    r = subprocess.run([sys.executable, "-m", "pytest", os.path.abspath(__file__), "-m", "gpu", "-x",
+                        "-q", "-p", "no:cacheprovider", "-k", cases],
+                       env=dict(os.environ, MGQ_GEMV_I8="0"), cwd=root, capture_output=True,
+                       text=True, timeout=110)
+    assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-2000:]
+    assert " passed" in r.stdout and "deselected" in r.stdout
+
+
 # --------------------------------------------------------------------- GEMM --
 # (70000, 1, 16): 547 tiles of 128 rows but 438 of 160 for 512 resident
 # slots, so the 160-row tile runs; the others, ragged tiles of either height
