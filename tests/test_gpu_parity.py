@@ -109,7 +109,7 @@ def test_matvec_random_bytes_wide_dynamic_range(L, orc):
 
 @pytest.mark.parametrize("n,bpr", [(24576 + 17, 2), (30000, 14), (16, 40), (17, 29),
                                    (4100, 17), (4200, 74), (5000, 112), (300, 100),
-                                   (20005, 13), (16009, 7), (3590, 75), (4609, 14)])
+                                   (20005, 13), (16009, 7), (3590, 75), (4609, 14), (2047, 20)])
 def test_matvec_random_bytes_all_configs(L, orc, n, bpr):
     # shapes that select each launch configuration (many / few row groups,
     # single- and multi-stage K, ragged last stage and row group) and each
