@@ -234,7 +234,9 @@ struct MfmaLayout {
 // stream, in the same order (results identical to the barrier-staged kernel
 // of the same stage width). Needs one unit per wavefront and stage, one
 // stage in flight and a single stage buffer.
-constexpr int kFuseNorm = 1, kFuseGlu = 2, kFuseQuant = 4, kFmtQ5K = 8, kStageWave = 16;
+// kI8 (with kStageWave, Q4_K f32 activations): the int8 matrix-core form of
+// the wave-private kernel (i8_table_entry, i8_tile).
+constexpr int kFuseNorm = 1, kFuseGlu = 2, kFuseQuant = 4, kFmtQ5K = 8, kStageWave = 16, kI8 = 32;
 __host__ __device__ constexpr int block_pieces(int fuse) { return (fuse & kFmtQ5K) ? 11 : 9; }
 struct GemvFuse {
     const uint8_t *w2;  // kFuseGlu: the up matrix
@@ -293,6 +295,87 @@ __host__ __device__ inline MfmaLayout mfma_layout(int bpr, int R, int C, int NW,
 // (row, sub-block) pairs per lane.
 // DB: double-buffered LDS stage (one barrier per stage) or a single buffer
 // (two barriers per stage, half the LDS, so more work-groups fit per CU).
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// The int8 form's activation table (one 1040-byte entry per block, as the
+// f16 form's): item j (x values 8j .. 8j + 7) of sub-block sb of block b.
+// x 2^e rounded to an integer X, |X| < 2^22, as three signed 8-bit digits:
+// the bytes of Y = X + 128 (1 + 256 + 65536) with their top bits flipped
+// (byte - 128), so X = sum (byte_i - 128) 256^i. Adding 1.5 2^23 rounds
+// x 2^e to an integer in the mantissa's low bits. Digit dg of the item sits
+// at ((sb 3 + dg) 2 + j / 2) 16 + (j % 2) 8: A row m = 4 (sub-block pair) +
+// digit reads 16 bytes (two items) of one sub-block. meta[b 16 + sb] = 2^-e,
+// meta[b 16 + 8 + sb] = the sub-block's sum.
+__device__ __forceinline__ void i8_table_entry(uint8_t *lds, float *meta, int b, int sb, int j,
+                                               const f32x4 &v0, const f32x4 &v1, float amax,
+                                               float sum) {
+    int e = 0;
+    float corr = 1.0f;
+    if (amax > 0.0f && amax <= 3.402823466e38f) {
+        int ex;
+        frexpf(amax, &ex);
+        e = std::min(22 - ex, 140);  // ex <= 128: e >= -106
+        corr = ldexpf(1.0f, -e);
+    } else if (!(amax == 0.0f)) {
+        corr = amax;  // Inf or NaN: the row sums come out non-finite
+    }
+    if (j == 0) {
+        meta[b * 16 + sb] = corr;
+        meta[b * 16 + 8 + sb] = sum;
+    }
+    const float xs[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+    uint32_t yv[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+        yv[q] = __builtin_bit_cast(uint32_t, ldexpf(xs[q], e) + 12582912.0f) - (0x4B400000u - 0x808080u);
+#pragma unroll
+    for (int dg = 0; dg < 3; ++dg) {
+        // byte dg of values 4h .. 4h + 3 (v_perm: selector k picks byte k of
+        // the second operand, 4 + k of the first; 0x0C a zero byte)
+        const uint32_t sel = (uint32_t)dg | ((4u + dg) << 8) | 0x0C0C0000u;
+        uint32_t dw[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t lo = __builtin_amdgcn_perm(yv[4 * h + 1], yv[4 * h], sel);
+            const uint32_t hi = __builtin_amdgcn_perm(yv[4 * h + 3], yv[4 * h + 2], sel);
+            dw[h] = __builtin_amdgcn_perm(hi, lo, 0x05040100u) ^ 0x80808080u;
+        }
+        *reinterpret_cast<u32x2 *>(lds + (size_t)b * 1040 + (size_t)(((sb * 3 + dg) * 2 + (j >> 1)) * 16 + (j & 1) * 8)) =
+            u32x2{dw[0], dw[1]};
+    }
+}
+
+// int8 form: MFMA c4 = low / high nibbles (c4 & 1) of qs pieces 1+g (c4 < 2)
+// or 5+g: lane group g's 16 bytes are sub-block pair jp = 2 (c4 >> 1) +
+// (g >> 1) at elements 16 (g & 1) ..; A row m = 4 jp + digit holds that
+// pair's low (c4 even) or high sub-block's digits. The low-nibble MFMAs
+// accumulate into one accumulator and the high-nibble ones into the other,
+// so lane group G holds sub-blocks 2G and 2G + 1, as in the f16 form (same
+// decode). Lanes whose row m takes no data read the block's zero slot.
+__device__ __forceinline__ uint32_t i8_aoff(int c4, int n16, int g) {
+    const int hi = c4 & 1, jp = 2 * (c4 >> 1) + (g >> 1), sbc = 2 * jp + hi;
+    const bool hit = (n16 >> 2) == jp && (n16 & 3) < 3;
+    return hit ? (uint32_t)(((sbc * 3 + (n16 & 3)) * 2 + (g & 1)) * 16) : 1024u;
+}
+
+// The scaled q*x sums s0, s1 (sub-blocks 2g, 2g + 1 of row n16) of one block
+// (table entry tb) from its qs pieces q0 (1 + g) and q1 (5 + g): the three
+// digit sums of each (|each| < 2^16) as a0 + 256 a1 exactly, then + 65536 a2.
+__device__ __forceinline__ void i8_tile(const uint8_t *tb, const uint32_t (&aoff8)[4], const u32x4 &q0,
+                                        const u32x4 &q1, float &s0, float &s1) {
+    i32x4 alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0};
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) {
+        const u32x4 src = c4 < 2 ? q0 : q1;
+        const u32x4 bq = (c4 & 1) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
+        const i32x4 av = *reinterpret_cast<const i32x4 *>(tb + aoff8[c4]);
+        if (c4 & 1) ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, __builtin_bit_cast(i32x4, bq), ahi, 0, 0, 0);
+        else alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, __builtin_bit_cast(i32x4, bq), alo, 0, 0, 0);
+    }
+    s0 = (float)alo[2] * 65536.0f + (float)((alo[1] << 8) + alo[0]);
+    s1 = (float)ahi[2] * 65536.0f + (float)((ahi[1] << 8) + ahi[0]);
+}
+
 // Q8: the dp4a matvec of kernels/matvec_q4k_dp4a.hip:52-106 on the same
 // weight stream: activations arrive as int8 xq with per-sub-block scale xd and
 // sum xsum; each lane dots its 32 qs bytes (4 sub-block halves) with
@@ -307,7 +390,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
                                                             float *__restrict__ y, int n,
                                                             int bpr, int rounds, GemvFuse fz,
                                                             GemvSched sch, int gr) {
-    constexpr int FM = FUSE & ~kStageWave;  // the mode bits
+    constexpr int FM = FUSE & ~(kStageWave | kI8);  // the mode bits
     static_assert(Q8 ? (FM == 0 || FM == kFuseQuant) : (FM & kFuseQuant) == 0,
                   "fused glue runs on f32 activations; quantization only in Q8 mode");
     static_assert(!(FM & kFmtQ5K) || FM == kFmtQ5K, "Q5_K weights: plain f32 matvec only");
@@ -315,6 +398,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     constexpr bool Q5 = (FUSE & kFmtQ5K) != 0;
     constexpr bool WV = (FUSE & kStageWave) != 0;
     static_assert(!WV || (PF == 1 && !DB), "kStageWave: one stage in flight, one stage buffer");
+    constexpr bool I8 = (FUSE & kI8) != 0;
+    static_assert(!I8 || (WV && !Q8 && !Q5), "kI8: Q4_K f32 activations on kStageWave only");
     constexpr int BP = block_pieces(FUSE);  // 16-byte pieces per block
     constexpr int BB = BP * 16;              // block bytes
     constexpr bool NORM = (FUSE & kFuseNorm) != 0;
@@ -549,6 +634,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         sum += quad_xor<1>(sum);
         sum += quad_xor<2>(sum);
         if (i >= nitems) continue;
+        if constexpr (I8) {
+            i8_table_entry(lds, meta, i >> 5, (i >> 2) & 7, i & 3, v0, v1, amax, sum);
+            continue;
+        }
         int e = 0;  // x*2^e puts the sub-block's largest |x| in [2^13, 2^14)
         if (amax > 0.0f && amax <= 3.402823466e38f) {
             int ex;
@@ -638,6 +727,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
         const bool hit = (n16 >> 1) == sb;  // A lane m = n16 = 2*sb + part
         aoff[c] = hit ? (uint32_t)((c * 4 + g) * 32 + (n16 & 1) * 16) : 1024u;
     }
+    uint32_t aoff8[4];  // I8: the int8 A operands (i8_aoff)
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) aoff8[c4] = i8_aoff(c4, n16, g);
     // y contribution of one tile: sub-blocks 2g, 2g+1 of W row n16 in block b,
     // from their q*x sums s0, s1 (scaled by corr) and the block header hd.
     auto decode = [&](const u32x4 &hd, int b, float s0, float s1) -> float {
@@ -721,6 +813,18 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
           if constexpr (Q8) {
             const float cA = decode_q8(hdA, bA, qa0, qa1);
             const float cB = decode_q8(hdB, bBc, qb0, qb1);
+            if (R == 32) {
+                yaccA += cA;
+                yaccB += cB;
+            } else {
+                yaccA += hasB ? cA + cB : cA;
+            }
+          } else if constexpr (I8) {
+            float sa0, sa1, sb0, sb1;
+            i8_tile(lds + (uint32_t)bA * 1040u, aoff8, qa0, qa1, sa0, sa1);
+            i8_tile(lds + (uint32_t)bBc * 1040u, aoff8, qb0, qb1, sb0, sb1);
+            const float cA = decode(hdA, bA, sa0, sa1);
+            const float cB = decode(hdB, bBc, sb0, sb1);
             if (R == 32) {
                 yaccA += cA;
                 yaccB += cB;
@@ -943,7 +1047,6 @@ static int env_int(const char *name, int dflt) {
 // not spread), and v_mfma_i32_16x16x64_i8 sums 64 products exactly: half
 // the MFMAs, A-operand reads and nibble masks of the f16 form, whose x is
 // split into two f16 halves (22 bits) times 16-bit B operands.
-typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 struct WaveLayout {
     uint32_t meta, slots, aux;
@@ -1086,44 +1189,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
         if (i >= nitems) continue;
         const int b = i >> 5, sb = (i >> 2) & 7, j = i & 3;
         if constexpr (I8) {
-            // x 2^e rounded to an integer X, |X| < 2^22, as three signed 8-bit
-            // digits: the bytes of Y = X + 128 (1 + 256 + 65536) with their top
-            // bits flipped (byte - 128), so X = sum (byte_i - 128) 256^i. Adding
-            // 1.5 2^23 rounds x 2^e to an integer in the mantissa's low bits.
-            int e = 0;
-            float corr = 1.0f;
-            if (amax > 0.0f && amax <= 3.402823466e38f) {
-                int ex;
-                frexpf(amax, &ex);
-                e = std::min(22 - ex, 140);  // ex <= 128: e >= -106
-                corr = ldexpf(1.0f, -e);
-            } else if (!(amax == 0.0f)) {
-                corr = amax;  // Inf or NaN: the row sums come out non-finite
-            }
-            if (j == 0) {
-                meta[b * 16 + sb] = corr;
-                meta[b * 16 + 8 + sb] = sum;
-            }
-            const float xs[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-            uint32_t yv[8];
-#pragma unroll
-            for (int q = 0; q < 8; ++q)
-                yv[q] = __builtin_bit_cast(uint32_t, ldexpf(xs[q], e) + 12582912.0f) - (0x4B400000u - 0x808080u);
-#pragma unroll
-            for (int dg = 0; dg < 3; ++dg) {
-                // byte dg of values 4h .. 4h + 3 (v_perm: selector k picks byte k of
-                // the second operand, 4 + k of the first; 0x0C a zero byte)
-                const uint32_t sel = (uint32_t)dg | ((4u + dg) << 8) | 0x0C0C0000u;
-                uint32_t dw[2];
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const uint32_t lo = __builtin_amdgcn_perm(yv[4 * h + 1], yv[4 * h], sel);
-                    const uint32_t hi = __builtin_amdgcn_perm(yv[4 * h + 3], yv[4 * h + 2], sel);
-                    dw[h] = __builtin_amdgcn_perm(hi, lo, 0x05040100u) ^ 0x80808080u;
-                }
-                *reinterpret_cast<u32x2 *>(lds + (size_t)b * 1040 + (size_t)(((sb * 3 + dg) * 2 + (j >> 1)) * 16 + (j & 1) * 8)) =
-                    u32x2{dw[0], dw[1]};
-            }
+            i8_table_entry(lds, meta, b, sb, j, v0, v1, amax, sum);
             continue;
         }
         int e = 0;
@@ -1165,21 +1231,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
         const bool hit = (n16 >> 1) == sb;
         aoff[c] = hit ? (uint32_t)((c * 4 + g) * 32 + (n16 & 1) * 16) : 1024u;
     }
-    // I8: MFMA c4 = low / high nibbles (c4 & 1) of qs pieces 1+g (c4 < 2) or
-    // 5+g: lane group g's 16 bytes are sub-block pair jp = 2 (c4 >> 1) + (g >> 1)
-    // at elements 16 (g & 1) ..; A row m = 4 jp + digit holds that pair's low
-    // (c4 even) or high sub-block's digits. The low-nibble MFMAs accumulate
-    // into one accumulator and the high-nibble ones into the other, so lane
-    // group G holds sub-blocks 2G and 2G + 1, as in the f16 form (same decode).
-    uint32_t aoff8[4];
+    uint32_t aoff8[4];  // I8: the int8 A operands (i8_aoff)
 #pragma unroll
-    for (int c4 = 0; c4 < 4; ++c4) {
-        const int hi = c4 & 1, jp = 2 * (c4 >> 1) + (g >> 1), sbc = 2 * jp + hi;
-        const bool hit = (n16 >> 2) == jp && (n16 & 3) < 3;
-        aoff8[c4] = hit ? (uint32_t)(((sbc * 3 + (n16 & 3)) * 2 + (g & 1)) * 16) : 1024u;
-    }
-    // the three digit sums (|each| < 2^16): a0 + 256 a1 exactly, then + 65536 a2
-    auto digits = [](const i32x4 &a) -> float { return (float)a[2] * 65536.0f + (float)((a[1] << 8) + a[0]); };
+    for (int c4 = 0; c4 < 4; ++c4) aoff8[c4] = i8_aoff(c4, n16, g);
     auto decode = [&](const u32x4 &hd, int b, float s0, float s1) -> float {
         const float d = half_bits_finite(hd[0]), dmin = half_bits_finite(hd[0] >> 16);
         const uint32_t scs = jq ? hd[3] : hd[1], mns = jq ? (hd[3] >> 4) : hd[2];
@@ -1231,17 +1285,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_wave_kernel(const uint8_t *__res
             const u32x4 hdB = DIRECT ? dreg[3] : piece(rowB + n16, cbB, 0);
           if constexpr (I8) {
             auto tile8 = [&](const u32x4 &hd, int b, const u32x4 &q0, const u32x4 &q1) -> float {
-                i32x4 alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0};
-                const uint8_t *tb = lds + (uint32_t)b * 1040u;
-#pragma unroll
-                for (int c4 = 0; c4 < 4; ++c4) {
-                    const u32x4 src = c4 < 2 ? q0 : q1;
-                    const u32x4 bq = (c4 & 1) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
-                    const i32x4 av = *reinterpret_cast<const i32x4 *>(tb + aoff8[c4]);
-                    if (c4 & 1) ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, __builtin_bit_cast(i32x4, bq), ahi, 0, 0, 0);
-                    else alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, __builtin_bit_cast(i32x4, bq), alo, 0, 0, 0);
-                }
-                return decode(hd, b, digits(alo), digits(ahi));
+                float s0, s1;
+                i8_tile(lds + (uint32_t)b * 1040u, aoff8, q0, q1, s0, s1);
+                return decode(hd, b, s0, s1);
             };
             const float cA = tile8(hdA, bA, qa0, qa1);
             const float cB = tile8(hdB, bBc, qb0, qb1);
@@ -1521,6 +1567,9 @@ hipError_t gemv_prepare() {
     if (e == hipSuccess) e = prepare_swave<false, kFuseNorm>();
     if (e == hipSuccess) e = prepare_swave<false, kFuseGlu>();
     if (e == hipSuccess) e = prepare_swave<false, kFuseNorm | kFuseGlu>();
+    if (e == hipSuccess) e = prepare_swave<false, kFuseNorm | kI8>();
+    if (e == hipSuccess) e = prepare_swave<false, kFuseGlu | kI8>();
+    if (e == hipSuccess) e = prepare_swave<false, kFuseNorm | kFuseGlu | kI8>();
     if (e == hipSuccess) e = batched_prepare();
     return e;
 }
@@ -1599,6 +1648,16 @@ static hipError_t mfma_dispatch(const uint8_t *w, const GemvAct &a, float *y, in
         // MGQ_GEMV_SWAVE=0 turns it off.
         static const int swave_env = env_int("MGQ_GEMV_SWAVE", 1);
         const bool multi = (long)(n + 15) / 16 > 2 * device_cus();
+        if constexpr (!Q8 && (FUSE & kFmtQ5K) == 0) {
+            // the fused Q4_K modes in the int8 form (MGQ_GEMV_I8=0: f16)
+            static const bool i8f = env_int("MGQ_GEMV_I8", 1) != 0;
+            if (swave_env && i8f && force < 0 && e == hipErrorNotSupported) {
+                if (cfg == 6 && multi)
+                    e = launch_cfg<16, 14, 7, 1, false, Q8, FUSE | kStageWave | kI8>(w, a, fz, y, n, bpr, stream, true);
+                else if (cfg == 2)
+                    e = launch_cfg<16, 16, 8, 1, false, Q8, FUSE | kStageWave | kI8>(w, a, fz, y, n, bpr, stream, false);
+            }
+        }
         if (swave_env && force < 0 && e == hipErrorNotSupported) {
             if (cfg == 6 && multi)
                 e = launch_cfg<16, 14, 7, 1, false, Q8, FUSE | kStageWave>(w, a, fz, y, n, bpr, stream, true);
