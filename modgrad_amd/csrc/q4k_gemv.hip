@@ -1568,6 +1568,7 @@ hipError_t gemv_prepare() {
     if (e == hipSuccess) e = prepare_swave<false, kFuseGlu>();
     if (e == hipSuccess) e = prepare_swave<false, kFuseNorm | kFuseGlu>();
     if (e == hipSuccess) e = prepare_swave<false, kFuseNorm | kI8>();
+    if (e == hipSuccess) e = lds_attr_all<32, 14, 14, 1, false, false, kFuseNorm | kStageWave | kI8>();
     if (e == hipSuccess) e = prepare_swave<false, kFuseGlu | kI8>();
     if (e == hipSuccess) e = prepare_swave<false, kFuseNorm | kFuseGlu | kI8>();
     if (e == hipSuccess) e = batched_prepare();
@@ -1656,6 +1657,12 @@ static hipError_t mfma_dispatch(const uint8_t *w, const GemvAct &a, float *y, in
                     e = launch_cfg<16, 14, 7, 1, false, Q8, FUSE | kStageWave | kI8>(w, a, fz, y, n, bpr, stream, true);
                 else if (cfg == 2)
                     e = launch_cfg<16, 16, 8, 1, false, Q8, FUSE | kStageWave | kI8>(w, a, fz, y, n, bpr, stream, false);
+                else if constexpr (FUSE == kFuseNorm) {
+                    // qkv with its RMSNorm: one group of gr rows per CU, 32-row tiles
+                    if (cfg == 8)
+                        e = launch_cfg<32, 14, 14, 1, false, Q8, FUSE | kStageWave | kI8>(w, a, fz, y, n, bpr,
+                                                                                          stream, false, gr);
+                }
             }
         }
         if (swave_env && force < 0 && e == hipErrorNotSupported) {

@@ -91,7 +91,7 @@ def _weights(orc, seed, n, bpr):
 
 # (n, bpr): persistent whole-row (cfg 3), small-N (cfg 1), long K small-N
 # (cfg 2), long K persistent (cfg 0), ragged row groups
-FUSED_SHAPES = [(4608, 14), (3584, 14), (300, 3), (64, 74), (5000, 74), (33, 1)]
+FUSED_SHAPES = [(4608, 14), (3584, 14), (300, 3), (64, 74), (5000, 74), (33, 1), (4609, 14)]
 
 
 @pytest.mark.parametrize("n,bpr", FUSED_SHAPES)
