@@ -361,13 +361,23 @@ __device__ __forceinline__ uint32_t i8_aoff(int c4, int n16, int g) {
 // The scaled q*x sums s0, s1 (sub-blocks 2g, 2g + 1 of row n16) of one block
 // (table entry tb) from its qs pieces q0 (1 + g) and q1 (5 + g): the three
 // digit sums of each (|each| < 2^16) as a0 + 256 a1 exactly, then + 65536 a2.
+// Q5K: the qs pieces are 3 + g and 7 + g, and bit j (sub-block j) of the
+// qh byte of each qs byte (hq: qh piece 1 + (g & 1)) is the weight's fifth
+// bit, q = nibble + 16 bit (a digit sum over 32 values stays below 2^17 in
+// magnitude: exact in int32; its f32 combination rounds as an f32 sum does).
+template <bool Q5K = false>
 __device__ __forceinline__ void i8_tile(const uint8_t *tb, const uint32_t (&aoff8)[4], const u32x4 &q0,
-                                        const u32x4 &q1, float &s0, float &s1) {
+                                        const u32x4 &q1, float &s0, float &s1,
+                                        const u32x4 &hq = u32x4{0u, 0u, 0u, 0u}, int g = 0) {
     i32x4 alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0};
 #pragma unroll
     for (int c4 = 0; c4 < 4; ++c4) {
         const u32x4 src = c4 < 2 ? q0 : q1;
-        const u32x4 bq = (c4 & 1) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
+        u32x4 bq = (c4 & 1) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
+        if constexpr (Q5K) {
+            const uint32_t j = (uint32_t)(2 * (2 * (c4 >> 1) + (g >> 1)) + (c4 & 1));
+            bq |= ((hq >> j) & 0x01010101u) << 4u;
+        }
         const i32x4 av = *reinterpret_cast<const i32x4 *>(tb + aoff8[c4]);
         if (c4 & 1) ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, __builtin_bit_cast(i32x4, bq), ahi, 0, 0, 0);
         else alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, __builtin_bit_cast(i32x4, bq), alo, 0, 0, 0);
@@ -399,7 +409,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
     constexpr bool WV = (FUSE & kStageWave) != 0;
     static_assert(!WV || (PF == 1 && !DB), "kStageWave: one stage in flight, one stage buffer");
     constexpr bool I8 = (FUSE & kI8) != 0;
-    static_assert(!I8 || (WV && !Q8 && !Q5), "kI8: Q4_K f32 activations on kStageWave only");
+    static_assert(!I8 || (WV && !Q8), "kI8: Q4_K / Q5_K f32 activations on kStageWave only");
     constexpr int BP = block_pieces(FUSE);  // 16-byte pieces per block
     constexpr int BB = BP * 16;              // block bytes
     constexpr bool NORM = (FUSE & kFuseNorm) != 0;
@@ -821,8 +831,15 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(const uint8_t *__res
             }
           } else if constexpr (I8) {
             float sa0, sa1, sb0, sb1;
-            i8_tile(lds + (uint32_t)bA * 1040u, aoff8, qa0, qa1, sa0, sa1);
-            i8_tile(lds + (uint32_t)bBc * 1040u, aoff8, qb0, qb1, sb0, sb1);
+            if constexpr (Q5) {
+                const u32x4 hqa = piece(rowA + n16, cbA, 1 + (g & 1));
+                const u32x4 hqb = piece(rowB + n16, cbB, 1 + (g & 1));
+                i8_tile<true>(lds + (uint32_t)bA * 1040u, aoff8, qa0, qa1, sa0, sa1, hqa, g);
+                i8_tile<true>(lds + (uint32_t)bBc * 1040u, aoff8, qb0, qb1, sb0, sb1, hqb, g);
+            } else {
+                i8_tile(lds + (uint32_t)bA * 1040u, aoff8, qa0, qa1, sa0, sa1);
+                i8_tile(lds + (uint32_t)bBc * 1040u, aoff8, qb0, qb1, sb0, sb1);
+            }
             const float cA = decode(hdA, bA, sa0, sa1);
             const float cB = decode(hdB, bBc, sb0, sb1);
             if (R == 32) {
@@ -1568,6 +1585,7 @@ hipError_t gemv_prepare() {
     if (e == hipSuccess) e = prepare_swave<false, kFuseGlu>();
     if (e == hipSuccess) e = prepare_swave<false, kFuseNorm | kFuseGlu>();
     if (e == hipSuccess) e = prepare_swave<false, kFuseNorm | kI8>();
+    if (e == hipSuccess) e = prepare_swave<false, kFmtQ5K | kI8>();
     if (e == hipSuccess) e = lds_attr_all<32, 14, 14, 1, false, false, kFuseNorm | kStageWave | kI8>();
     if (e == hipSuccess) e = prepare_swave<false, kFuseGlu | kI8>();
     if (e == hipSuccess) e = prepare_swave<false, kFuseNorm | kFuseGlu | kI8>();
@@ -1649,8 +1667,8 @@ static hipError_t mfma_dispatch(const uint8_t *w, const GemvAct &a, float *y, in
         // MGQ_GEMV_SWAVE=0 turns it off.
         static const int swave_env = env_int("MGQ_GEMV_SWAVE", 1);
         const bool multi = (long)(n + 15) / 16 > 2 * device_cus();
-        if constexpr (!Q8 && (FUSE & kFmtQ5K) == 0) {
-            // the fused Q4_K modes in the int8 form (MGQ_GEMV_I8=0: f16)
+        if constexpr (!Q8) {
+            // the fused Q4_K and the Q5_K modes in the int8 form (MGQ_GEMV_I8=0: f16)
             static const bool i8f = env_int("MGQ_GEMV_I8", 1) != 0;
             if (swave_env && i8f && force < 0 && e == hipErrorNotSupported) {
                 if (cfg == 6 && multi)

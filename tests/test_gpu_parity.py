@@ -383,17 +383,18 @@ def test_matvec_per_subblock_magnitudes(L, orc, n, bpr):
 
 
 def test_matvec_f16_wave_forms_under_switch():
-    # MGQ_GEMV_I8=0 (read once per process) puts every wave launch and the
-    # fused RMSNorm / GLU matvecs on the f16 matrix-core form: the matvec
-    # cases above and the fused ones again, in one child process with the
-    # switch set
+    # MGQ_GEMV_I8=0 (read once per process) puts every wave launch, the
+    # fused RMSNorm / GLU matvecs and the Q5_K matvec on the f16 matrix-core
+    # form: the matvec, Q5_K / Q6_K and fused cases again, in one child
+    # process with the switch set
     import os
     import subprocess
     note("matvec f16 wave forms (child process, MGQ_GEMV_I8=0)")
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     cases = ("matvec_random_bytes_all_configs or per_subblock or baseline_layer_shapes or "
              "one_group_per_cu or lm_head_full_size or matvec_small_shapes or "
-             "matvec_rmsnorm_matches_norm_then_matvec or matvec_glu_matches_unfused_chain")
+             "matvec_rmsnorm_matches_norm_then_matvec or matvec_glu_matches_unfused_chain or "
+             "kquant_matvec_matches_oracle")
     glue = os.path.join(os.path.dirname(os.path.abspath(__file__)), "test_gpu_glue.py")
     r = subprocess.run([sys.executable, "-m", "pytest", os.path.abspath(__file__), glue, "-m", "gpu",
                         "-x", "-q", "-p", "no:cacheprovider", "-k", cases],
