@@ -34,9 +34,12 @@
 //        of the one being computed.
 //    Per 32 rows x 1 block a wave issues 16 MFMAs and about 220 VALU ops.
 //    Its kStageWave variant stages per wavefront (below) for the Q8 / dp4a,
-//    fused RMSNorm / GLU and Q5_K modes.
+//    fused RMSNorm / GLU and Q5_K modes; with kI8 the fused and Q5_K modes
+//    multiply in the int8 form described under 3.
 //
-// 3. gemv_wave_kernel -- the same arithmetic with every wavefront staging
+// 3. gemv_wave_kernel -- the same arithmetic (by default in its int8 form:
+//    x as three signed 8-bit digits per value, the nibbles as int8 operands,
+//    v_mfma_i32_16x16x64_i8) with every wavefront staging
 //    its own unit through its own LDS slot, so stages need no work-group
 //    barrier; used for plain f32 matvecs whose work-groups stream several
 //    stages (gate|up, lm_head, down). With DIRECT (one unit per wavefront:
